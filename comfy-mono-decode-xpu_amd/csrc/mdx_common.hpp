@@ -1,0 +1,107 @@
+// Shared host/device helpers of libmdx (gfx950, wave64).
+//
+// Every floating-point step whose rounding is part of an operator's contract is written out
+// here as an explicit IEEE single operation (no contraction): bf16 rounding is the software
+// round-to-nearest-even of the top 16 bits, fp32 sums and products are separate
+// __fadd_rn / __fmul_rn calls, so the CPU oracle can restate each result bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/mdx.h"
+
+namespace mdx {
+
+// ---- error reporting (thread-local message, returned as a status code) ----------------------
+void set_error(const char* fmt, ...);
+#define MDX_CHECK(cond, ...)                 \
+    do {                                     \
+        if (!(cond)) {                       \
+            ::mdx::set_error(__VA_ARGS__);   \
+            return MDX_EINVAL;               \
+        }                                    \
+    } while (0)
+#define MDX_HIP(call)                                                               \
+    do {                                                                            \
+        hipError_t e_ = (call);                                                     \
+        if (e_ != hipSuccess) {                                                     \
+            ::mdx::set_error("%s failed: %s", #call, hipGetErrorString(e_));        \
+            return MDX_EHIP;                                                        \
+        }                                                                           \
+    } while (0)
+#define MDX_LAUNCHED()                                                              \
+    do {                                                                            \
+        hipError_t e_ = hipGetLastError();                                          \
+        if (e_ != hipSuccess) {                                                     \
+            ::mdx::set_error("kernel launch failed: %s", hipGetErrorString(e_));    \
+            return MDX_EHIP;                                                        \
+        }                                                                           \
+    } while (0)
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---- scalar conversions (device) ---------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// round-to-nearest-even fp32 -> bf16; NaN becomes the canonical quiet NaN 0x7FC0
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ float fp16_to_f32(uint16_t h) {
+    return float(__builtin_bit_cast(_Float16, h));
+}
+
+// OCP float8 e4m3fn (bias 7, no infinities, S.1111.111 = NaN) -> fp32, exact
+__device__ __forceinline__ float fp8_to_f32(uint8_t b) {
+    const uint32_t s = uint32_t(b >> 7) << 31, e = (b >> 3) & 15u, m = b & 7u;
+    if (e == 15u && m == 7u) return __uint_as_float(s | 0x7FC00000u);
+    if (e == 0u) {
+        const float v = float(m) * 0.001953125f;  // m * 2^-9
+        return s ? -v : v;
+    }
+    return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+__device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i) {
+    if (dtype == MDX_DT_F32) return reinterpret_cast<const float*>(s)[i];
+    if (dtype == MDX_DT_F16) return fp16_to_f32(reinterpret_cast<const uint16_t*>(s)[i]);
+    return fp8_to_f32(reinterpret_cast<const uint8_t*>(s)[i]);
+}
+
+// ---- wave64 helpers -----------------------------------------------------------------------------
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <typename T>
+__device__ __forceinline__ T shfl_down(T v, int d) { return __shfl_down(v, d, 64); }
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int d) { return __shfl_xor(v, d, 64); }
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, shfl_xor(v, d));
+    return v;
+}
+
+// fused_scaleback: (float(acc) * xs) * sc, each product rounded on its own
+__device__ __forceinline__ float scaleback(int32_t acc, float xs, float sc) {
+    float f = float(acc);
+    f = __fmul_rn(f, xs);
+    f = __fmul_rn(f, sc);
+    return f;
+}
+
+}  // namespace mdx
+
+namespace mdx {
+// Raise a kernel's dynamic LDS limit above the 64 KiB default (gfx950 has 160 KiB per CU).
+inline void allow_smem(const void* fn, size_t bytes) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+    (void)hipGetLastError();
+}
+}  // namespace mdx

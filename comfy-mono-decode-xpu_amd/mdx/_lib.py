@@ -1,0 +1,85 @@
+"""ctypes binding of libmdx.so (the C ABI declared in include/mdx.h).
+
+torch is imported first on purpose: torch ships its own HIP runtime (soname libamdhip64.so.7), and
+loading it before libmdx makes the dynamic loader bind libmdx to that same runtime, so torch's
+streams and device pointers are valid inside libmdx.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see above)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmdx.so")
+
+MDX_OK, MDX_EINVAL, MDX_EHIP = 0, 1, 2
+DT_F32, DT_F16, DT_FP8E4M3, DT_BF16 = 0, 1, 2, 3
+LAYOUT_ROW, LAYOUT_TILE = 0, 1
+DECODE_EXACT, DECODE_AUTO = 0, 1
+ROT_NONE, ROT_H256, ROT_MATRIX = 0, 1, 2
+
+c_void_p, c_int32, c_int64, c_size_t = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+
+
+class MdxW4(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("s_rel", c_void_p), ("s_channel", c_void_p), ("codebook", c_void_p),
+                ("n", c_int64), ("k", c_int64), ("group_size", c_int64),
+                ("s_dtype", c_int32), ("layout", c_int32), ("decode", c_int32), ("reserved", c_int32)]
+
+
+W4P = ctypes.POINTER(MdxW4)
+
+# name -> (restype, argtypes); every symbol declared in include/mdx.h
+SIGNATURES = {
+    "mdx_last_error": (ctypes.c_char_p, []),
+    "mdx_version": (ctypes.c_int, []),
+    "mdx_w4a8_decode_linear": (ctypes.c_int, [c_void_p, c_void_p, W4P, c_void_p, c_void_p, c_int32, c_int64, c_void_p]),
+    "mdx_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "mdx_mono_mlp_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "mdx_mono_mlp": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int32, c_void_p, W4P, W4P, W4P,
+                                    c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+    "mdx_stream_gemv": (ctypes.c_int, [c_void_p, c_void_p, ctypes.POINTER(W4P), c_int32, c_int32,
+                                       ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p), c_int32, c_void_p, c_int64,
+                                       c_void_p]),
+    "mdx_rms_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p, c_int32, c_void_p,
+                                         c_void_p, c_int64, c_int64, c_void_p]),
+}
+
+_lib = None
+
+
+class MdxError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (raises if it was not built: there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MdxError(f"libmdx.so not built ({LIB_PATH}); run comfy-mono-decode-xpu_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc != MDX_OK:
+        msg = lib().mdx_last_error().decode(errors="replace")
+        raise MdxError(f"{name}: {msg}")
+    return rc
+
+
+def stream_of(t: torch.Tensor):
+    return c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t):
+    return None if t is None else c_void_p(t.data_ptr())

@@ -1,0 +1,283 @@
+"""CPU oracle: a numpy restatement of the reference operator chain of the W4A8 decode path.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker / the timed CPU baseline -- never as a product path.
+
+Every function cites the reference file:line it restates (comfy-mono-decode-xpu). Floating-point
+steps are single IEEE operations on numpy float32 / float64 scalars or arrays (round to nearest
+even, no fused multiply-add), bf16 is the round-to-nearest-even of the top 16 bits with NaN ->
+0x7FC0. Where the reference's own order is not portable (Intel DPAS accumulation, the EU rsqrt),
+the library's canonical order is restated instead; each such place says so.
+
+Pinning (tests/test_oracle.py): bf16 / fp16 / fp8 conversions against torch's independent
+conversions; the int8-grid decode against its closed forms (integral scales, half-even ties,
+clamp, NaN); the int32 dot against an exact float64 matmul; the rotation against exact rational
+arithmetic on the Kronecker matrix; RMSNorm against float64; top-k rank keys against brute-force
+sorts; the accept walk against an independent tree walk.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------------------------
+# scalar formats
+# ---------------------------------------------------------------------------------------------
+
+
+def bf16_to_f32(b):
+    """bf16 bit patterns (uint16) -> float32 (exact)."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f):
+    """float32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (library convention)."""
+    u = np.asarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, np.uint16(0x7FC0), r).astype(np.uint16)
+
+
+def bfround(f):
+    return bf16_to_f32(f32_to_bf16(f))
+
+
+def fp8e4m3_to_f32(b):
+    """OCP float8 e4m3fn bytes -> float32 (bias 7, subnormals m * 2^-9, 0x7F/0xFF NaN)."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    s = np.where(b >> 7, -1.0, 1.0)
+    e = (b >> 3) & 15
+    m = b & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return (s * v).astype(np.float32)
+
+
+def scales_to_f32(s, dtype):
+    """s_rel storage (raw numpy array of the given dtype name) -> float32."""
+    if dtype == "f32":
+        return np.asarray(s, dtype=np.float32)
+    if dtype == "f16":
+        return np.asarray(s).view(np.float16).astype(np.float32)
+    if dtype == "fp8":
+        return fp8e4m3_to_f32(np.asarray(s).view(np.uint8))
+    raise ValueError(dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# A1: W4A8 decode linear -- csrc/w4a8_decode.sycl:4-11 (contract), :33-45 (decode4), :139-166
+# ---------------------------------------------------------------------------------------------
+
+
+def unpack_codes(packed):
+    """packed [N, K/2] -> codes [N, K]: byte b holds k = 2b (low nibble), 2b + 1 (high)
+    (csrc/w4a8_decode.sycl:33-45: code i of a word is bits 4i..4i+3)."""
+    b = np.asarray(packed).view(np.uint8)
+    out = np.empty((b.shape[0], b.shape[1] * 2), dtype=np.int64)
+    out[:, 0::2] = b & 15
+    out[:, 1::2] = b >> 4
+    return out
+
+
+def decode_w8(packed, s_rel_f32, codebook=None, group_size=128):
+    """w8[n, k] = isnan(r) ? 0 : clamp(r, -127, 127), r = rint(float(cb[code]) * s_rel[n, k / G])
+    in float32 (csrc/w4a8_decode.sycl:35-45; default codebook i - 8, :82). Returns int8 [N, K]."""
+    packed = np.asarray(packed)
+    s_rel_f32 = np.asarray(s_rel_f32, dtype=np.float32)
+    cb = (np.arange(16, dtype=np.float32) - 8) if codebook is None else np.asarray(codebook, dtype=np.float32)
+    n = packed.shape[0]
+    out = np.empty((n, packed.shape[1] * 2), dtype=np.int8)
+    for r0 in range(0, n, 1024):  # row blocks bound the temporaries
+        codes = unpack_codes(packed[r0:r0 + 1024])
+        sc = np.repeat(s_rel_f32[r0:r0 + 1024], group_size, axis=1)
+        with np.errstate(invalid="ignore", over="ignore"):
+            r = np.rint(cb[codes] * sc)  # float32 product (one rounding), then round-half-even
+            r = np.where(np.isnan(r), 0.0, np.clip(r, -127, 127))
+        out[r0:r0 + 1024] = r.astype(np.int8)
+    return out
+
+
+def int32_wrap(a):
+    return ((np.asarray(a, dtype=np.int64) + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int64)
+
+
+def w4a8_acc(x, w8):
+    """acc[m, n] = sum_k x[m, k] * w8[n, k] modulo 2^32 (csrc/w4a8_decode.sycl:8-9, 130-133).
+    Computed as float64 matmuls of the integer values: exact, since |x| <= 128, |w8| <= 127 and
+    K <= 2^20 keep every partial sum below 2^53 (checked)."""
+    x = np.asarray(x, dtype=np.int64)
+    assert x.shape[1] <= 1 << 20
+    xf = x.astype(np.float64)
+    w8 = np.asarray(w8)
+    acc = np.empty((x.shape[0], w8.shape[0]), dtype=np.int64)
+    for r0 in range(0, w8.shape[0], 2048):
+        acc[:, r0:r0 + 2048] = (xf @ w8[r0:r0 + 2048].astype(np.float64).T).astype(np.int64)
+    return int32_wrap(acc)
+
+
+def w4a8_acc_int64(x, w8):
+    """The same sum in int64 arithmetic (the bit-exact path, used to pin w4a8_acc)."""
+    return int32_wrap(np.asarray(x, dtype=np.int64) @ np.asarray(w8, dtype=np.int64).T)
+
+
+def scaleback(acc, xs, sch):
+    """f = (float(acc) * xs[m]) * sch[n], each product rounded on its own
+    (csrc/w4a8_decode.sycl:155-157; fused_scaleback, csrc/mono_common.hpp:510-516)."""
+    f = np.asarray(acc, dtype=np.int64).astype(np.float32)
+    f = (f * np.asarray(xs, dtype=np.float32).reshape(-1, 1)).astype(np.float32)
+    return (f * np.asarray(sch, dtype=np.float32).reshape(1, -1)).astype(np.float32)
+
+
+def w4a8_linear(x, xs, packed, s_rel_f32, sch, codebook=None, group_size=128, residual=None, out="bf16"):
+    """The fused linear (csrc/w4a8_decode.sycl:139-166): bf16 bits or float32 out; with residual,
+    cast(float(residual) + float(cast(f)))."""
+    acc = w4a8_acc(x, decode_w8(packed, s_rel_f32, codebook, group_size))
+    f = scaleback(acc, xs, sch)
+    if out == "bf16":
+        if residual is None:
+            return f32_to_bf16(f)
+        return f32_to_bf16(bf16_to_f32(residual) + bfround(f))
+    if residual is None:
+        return f
+    return (np.asarray(residual, dtype=np.float32) + f).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------
+# A2: rot_quant -- csrc/act_prep.sycl:4-10, 70-91 (mono_common.hpp:419-441)
+# ---------------------------------------------------------------------------------------------
+H4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.int64)
+
+
+def fwht256_f64(x):
+    """x [..., 256] float64 -> x . kron(H4, H4, H4, H4) (no 1/16), as the library computes it:
+    radix-4 stages along strides 1, 4, 16, 64, butterfly out = ((a0+a1)+a2)-a3,
+    ((a0+a1)-a2)+a3, ((a0-a1)+a2)+a3, ((a1-a0)+a2)+a3 (H4 rows, csrc/draft_fused.sycl:59-64).
+    Canonical order of this library: the reference's bf16 DPAS accumulation is not portable."""
+    a = np.array(x, dtype=np.float64)
+    for st in (1, 4, 16, 64):
+        v = a.reshape(a.shape[:-1] + (256 // (4 * st), 4, st))
+        a0, a1, a2, a3 = v[..., 0, :], v[..., 1, :], v[..., 2, :], v[..., 3, :]
+        o = np.stack([((a0 + a1) + a2) - a3, ((a0 + a1) - a2) + a3, ((a0 - a1) + a2) + a3, ((a1 - a0) + a2) + a3],
+                     axis=-2)
+        a = o.reshape(a.shape)
+    return a
+
+
+def rotate_rows(xf, rot, h=None):
+    """x_rot = bf16(x_group . H) per 256-group. rot: 'none' | 'h256' | 'matrix' (h: bf16 bits
+    [256, 256]). fp64 sums (fixed order), one rounding to fp32, one to bf16."""
+    xf = np.asarray(xf, dtype=np.float32)
+    if rot == "none":
+        return xf.copy()
+    g = xf.reshape(xf.shape[0], -1, 256).astype(np.float64)
+    if rot == "h256":
+        r = fwht256_f64(g) * 0.0625
+    else:
+        hf = bf16_to_f32(h).reshape(256, 256).astype(np.float64)
+        r = np.zeros_like(g)
+        for k in range(256):  # sequential fp64 sum of exact products
+            r = r + g[..., k:k + 1] * hf[k][None, None, :]
+    return bfround(r.astype(np.float32).reshape(xf.shape))
+
+
+def quantize_rows(xr):
+    """scale = max(amax / 127, 1e-30) (f32), sb = bf16(scale) (0 -> 0x0080),
+    q = int8(clamp(rint(float(bf16(xr / sb))), -128, 127)) (csrc/act_prep.sycl:175-195)."""
+    xr = np.asarray(xr, dtype=np.float32)
+    amax = np.fmax.reduce(np.abs(xr), axis=1, initial=np.float32(0)).astype(np.float32)
+    scale = np.maximum((amax / np.float32(127.0)).astype(np.float32), np.float32(1e-30)).astype(np.float32)
+    sb = f32_to_bf16(scale)
+    sb = np.where((sb & 0x7FFF) == 0, np.uint16(0x0080), sb)
+    sbf = bf16_to_f32(sb)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        d = bfround((xr / sbf[:, None]).astype(np.float32))
+        q = np.clip(np.rint(d), -128, 127)
+    q = np.where(np.isnan(q), 0, q)
+    return q.astype(np.int8), scale
+
+
+def rot_quant(x_bits, rot="h256", h=None):
+    """rot_quant(x, h) on bf16 bits [rows, K] -> (int8 [rows, K], f32 scale [rows])."""
+    return quantize_rows(rotate_rows(bf16_to_f32(x_bits), rot, h))
+
+
+# ---------------------------------------------------------------------------------------------
+# A5: RMSNorm (library canonical order; the reference's OmniXPU tree + EU rsqrt,
+# csrc/mono_common.hpp:452-505, is not portable)
+# ---------------------------------------------------------------------------------------------
+
+
+def rmsnorm_factor(xf, eps):
+    """r = 1 / sqrt(ss / K + eps) for float32 rows [rows, K]. ss: 256 partials, partial t sums
+    the squares of its elements in increasing order, its elements being the 8-element blocks
+    b = t + 256 j (elements 8 b .. 8 b + 7); then the halving tree p[t] + p[t + 128], + 64, .., + 1
+    (all float32). This is the library's canonical order."""
+    xf = np.asarray(xf, dtype=np.float32)
+    rows, K = xf.shape
+    sq = (xf * xf).astype(np.float32)
+    nb = K // 8
+    blk = sq.reshape(rows, nb, 8)
+    p = None
+    for j in range(-(-nb // 256)):
+        part = blk[:, 256 * j:256 * (j + 1), :]
+        if part.shape[1] < 256:  # threads without a block in this round keep their partial
+            pad = np.zeros((rows, 256 - part.shape[1], 8), np.float32)
+            part = np.concatenate([part, pad], axis=1)
+            valid = np.arange(256) < blk.shape[1] - 256 * j
+        else:
+            valid = np.ones(256, bool)
+        for e in range(8):
+            term = part[:, :, e]
+            if p is None:
+                p = np.where(valid[None, :], term, np.float32(0)).astype(np.float32)
+            else:
+                p = np.where(valid[None, :], (p + term).astype(np.float32), p)
+    n = 256
+    while n > 1:
+        n //= 2
+        p = (p[:, :n] + p[:, n:2 * n]).astype(np.float32)
+    ss = p[:, 0]
+    mean = (ss / np.float32(K)).astype(np.float32)
+    return (np.float32(1.0) / np.sqrt((mean + np.float32(eps)).astype(np.float32))).astype(np.float32)
+
+
+def rmsnorm(x_bits, w_bits, eps):
+    """y = bf16((x * r) * w) (mono_common.hpp:497-502 form), r from rmsnorm_factor."""
+    x = bf16_to_f32(x_bits).astype(np.float32)
+    r = rmsnorm_factor(x, eps)
+    w = bf16_to_f32(w_bits)
+    return f32_to_bf16(((x * r[:, None]).astype(np.float32) * w[None, :]).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------------------------
+# A4: mono_mlp -- csrc/mono_mlp.sycl:109-167
+# ---------------------------------------------------------------------------------------------
+
+
+def silu_mul(g_f32, u_f32, lut_bits):
+    """h = bf16(float(lut[bf16(g)]) * float(bf16(u))) (csrc/mono_mlp.sycl:130-138)."""
+    gb = f32_to_bf16(g_f32)
+    act = bf16_to_f32(np.asarray(lut_bits, dtype=np.uint16)[gb])
+    return f32_to_bf16((act * bfround(u_f32)).astype(np.float32))
+
+
+def mono_mlp(xn_bits, rot, h, lut_bits, gate, up, down):
+    """gate/up/down: dicts with packed, s (f32 array), sch, cb, G (row-major contract tensors);
+    a dict may carry its decoded "w8" to skip the decode."""
+    def w8(d):
+        if "w8" not in d:
+            d["w8"] = decode_w8(d["packed"], d["s"], d["cb"], d["G"])
+        return d["w8"]
+    q1, s1 = rot_quant(xn_bits, rot, h)
+    accg = w4a8_acc(q1, w8(gate))
+    accu = w4a8_acc(q1, w8(up))
+    hb = silu_mul(scaleback(accg, s1, gate["sch"]), scaleback(accu, s1, up["sch"]), lut_bits)
+    q2, s2 = rot_quant(hb, rot, h)
+    accd = w4a8_acc(q2, w8(down))
+    return f32_to_bf16(scaleback(accd, s2, down["sch"]))
+
+
+def silu_lut_f64():
+    """A float64 SiLU over every bf16 pattern (a pin for torch's table, not the table itself)."""
+    x = bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16)).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return x / (1.0 + np.exp(-x))

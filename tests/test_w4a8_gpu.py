@@ -1,0 +1,206 @@
+"""W4A8 linear, rot_quant and the fused MLP on the GPU against the CPU oracle: int8 / int32-derived
+outputs bit for bit (bf16 outputs are bf16 roundings of bit-exact fp32 epilogues, so they are
+compared bit for bit too). Reference tests mirrored: tests/test_w4a8_linear.py,
+tests/test_rot_quant.py, tests/test_mono_mlp.py."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bits_equal, bits
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def random_w4(N, K, g, fmt):
+    """Packed W4 weights in one of the scale formats:
+    fp8g16   -- the reference checkpoint format (tests/test_w4a8_linear.py:9-16): random bytes,
+                fp8 e4m3 G16 scale bytes 0x18..0x57, codebook i - 8
+    gptq     -- GPTQ int4 / fp16 G128 scales ~U(0.005, 0.02) through the integral packer
+    gptq_rint-- the same through the non-integral packer (per-weight rint decode)
+    f32g32   -- float32 G32 scales with a random codebook (general decode)"""
+    from mdx import layout
+    if fmt == "fp8g16":
+        q = torch.randint(-128, 128, (N, K // 2), generator=g, dtype=torch.int8)
+        s = torch.randint(0x18, 0x58, (N, K // 16), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn)
+        c = torch.rand(N, generator=g) * 1e-3 + 1e-4
+        cb = torch.arange(-8, 8, dtype=torch.float32)
+        return q, s, c, cb, 16
+    if fmt in ("gptq", "gptq_rint"):
+        qi = torch.randint(-8, 8, (N, K), generator=g)
+        sg = (torch.rand(N, K // 128, generator=g) * 0.015 + 0.005).half()
+        packed, s_rel, sch, _ = layout.gptq_pack(qi, sg, 128, integral=fmt == "gptq")
+        return packed, s_rel, sch, None, 128
+    if fmt == "f32g32":
+        q = torch.randint(-128, 128, (N, K // 2), generator=g, dtype=torch.int8)
+        s = torch.rand(N, K // 32, generator=g) * 30
+        c = torch.rand(N, generator=g) * 1e-3 + 1e-4
+        cb = torch.randn(16, generator=g)
+        return q, s, c, cb, 32
+    raise ValueError(fmt)
+
+
+def s_f32(s):
+    if s.dtype == torch.float8_e4m3fn:
+        return ref.fp8e4m3_to_f32(s.view(torch.uint8).numpy())
+    return s.float().numpy()
+
+
+def oracle_linear(x, xs, w, residual=None, out="bf16"):
+    q, s, c, cb, G = w
+    return ref.w4a8_linear(x.numpy(), xs.numpy(), q.numpy(), s_f32(s), c.numpy(),
+                           None if cb is None else cb.numpy(), G,
+                           None if residual is None else bits(residual), out)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (12288, 4096), (4096, 12288)])
+@pytest.mark.parametrize("fmt", ["fp8g16", "gptq", "gptq_rint", "f32g32"])
+def test_w4a8_decode_linear_matches_oracle(C, dev, N, K, fmt):
+    g = torch.Generator().manual_seed(N + K + len(fmt))
+    w = random_w4(N, K, g, fmt)
+    wd = [t.to(dev) if t is not None else None for t in w[:4]]
+    for M in (1, 2, 3, 8, 16):
+        print(f"case N={N} K={K} fmt={fmt} M={M}", flush=True)
+        x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+        out = C.w4a8_decode_linear(x.to(dev), xs.to(dev), *wd, None, w[4], 2, 0, False)
+        assert_bits_equal(bits(out), oracle_linear(x, xs, w), f"{fmt} M={M}")
+
+
+@pytest.mark.parametrize("fmt", ["fp8g16", "gptq"])
+def test_w4a8_residual_and_f32_out(C, dev, fmt):
+    g = torch.Generator().manual_seed(11)
+    N, K = 1024, 4096
+    w = random_w4(N, K, g, fmt)
+    wd = [t.to(dev) if t is not None else None for t in w[:4]]
+    for M in (1, 5):
+        x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+        res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+        out = C.w4a8_decode_linear(x.to(dev), xs.to(dev), *wd, res.to(dev), w[4], 2, 0, False)
+        assert_bits_equal(bits(out), oracle_linear(x, xs, w, res), "bf16 residual")
+        out32 = C.w4a8_decode_linear(x.to(dev), xs.to(dev), *wd, None, w[4], 0, 0, False)
+        assert_bits_equal(bits(out32), oracle_linear(x, xs, w, None, "f32").view(np.uint32), "f32 out")
+
+
+def test_w4a8_rejects_bad_contracts(C, dev):
+    x = torch.zeros(1, 4096, dtype=torch.int8, device=dev)
+    xs = torch.ones(1, device=dev)
+    q = torch.zeros(64, 2048, dtype=torch.int8, device=dev)
+    s = torch.ones(64, 256, device=dev)
+    c = torch.ones(64, device=dev)
+    with pytest.raises(RuntimeError):
+        C.w4a8_decode_linear(torch.zeros(17, 4096, dtype=torch.int8, device=dev), xs, q, s, c, None, None, 16)
+    with pytest.raises(RuntimeError):
+        C.w4a8_decode_linear(x, xs, q, s, c, None, None, 32)  # group size disagrees with the scales
+    with pytest.raises(RuntimeError):
+        C.w4a8_decode_linear(x, xs, q[:, :1000], s, c, None, None, 16)
+
+
+def _rows(kind, M, K, g):
+    x = torch.randn(M, K, generator=g)
+    if kind == "outlier":
+        x[:, torch.randint(0, K, (8,), generator=g)] *= 300
+    if kind == "wide":
+        x = x * torch.exp(torch.randn(M, K, generator=g) * 3)
+    if kind == "tiny":
+        x = x * 1e-36
+    if kind == "zero":
+        x = x * 0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("K", [4096, 12288])
+@pytest.mark.parametrize("rot", ["h256", "none", "matrix"])
+def test_rot_quant_matches_oracle(C, dev, K, rot):
+    from mdx import layout
+    g = torch.Generator().manual_seed(K + len(rot))
+    if rot == "h256":
+        h = layout.regular_hadamard()
+    elif rot == "none":
+        h = torch.eye(256).to(torch.bfloat16)
+    else:
+        h = (torch.randn(256, 256, generator=g) / 16).to(torch.bfloat16)
+    hd = h.to(dev)
+    for M in (1, 3, 8):
+        for kind in ("normal", "outlier", "wide", "tiny", "zero"):
+            print(f"case K={K} rot={rot} M={M} kind={kind}", flush=True)
+            x = _rows(kind, M, K, g)
+            q, s = C.rot_quant(x.to(dev), hd, 3)
+            wq, ws = ref.rot_quant(bits(x), "none" if rot == "none" else rot, bits(h))
+            assert_bits_equal(bits(q), wq, f"q {kind}")
+            assert_bits_equal(bits(s.view(-1)), ws.view(np.uint32), f"scale {kind}")
+
+
+def _mlp_weights(g, fmt, dev, tiled):
+    from mdx import layout
+    ws = [random_w4(12288, 4096, g, fmt), random_w4(12288, 4096, g, fmt), random_w4(4096, 12288, g, fmt)]
+    cb = ws[0][3]
+    ws = [(q, s, c, cb, G) for q, s, c, _, G in ws]
+    args = []
+    for q, s, c, cbv, G in ws:
+        if tiled:
+            q = layout.tile_major_codes(q)
+        cbt = cbv if cbv is not None else torch.arange(-8, 8, dtype=torch.float32)
+        args += [q.to(dev), s.to(dev), c.to(dev), cbt.to(dev)]
+    return ws, args
+
+
+def _oracle_dicts(ws):
+    return [dict(packed=q.numpy(), s=s_f32(s), sch=c.numpy(), cb=None if cb is None else cb.numpy(), G=G)
+            for q, s, c, cb, G in ws]
+
+
+@pytest.mark.parametrize("fmt,tiled,rot", [("gptq", True, "none"), ("gptq", False, "h256"),
+                                           ("fp8g16", True, "h256"), ("fp8g16", False, "none")])
+def test_mono_mlp_matches_oracle(C, dev, fmt, tiled, rot):
+    from mdx import layout
+    g = torch.Generator().manual_seed(21)
+    ws, args = _mlp_weights(g, fmt, dev, tiled)
+    h = layout.regular_hadamard() if rot == "h256" else torch.eye(256).to(torch.bfloat16)
+    lut = layout.silu_lut()
+    d = _oracle_dicts(ws)
+    for M in (1, 3, 8, 16):
+        print(f"case mlp fmt={fmt} tiled={tiled} rot={rot} M={M}", flush=True)
+        xn = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        out = C.mono_mlp(xn.to(dev), h.to(dev), lut.to(dev), *args, 0, 4, tiled)
+        want = ref.mono_mlp(bits(xn), rot, bits(h), bits(lut), *d)
+        assert_bits_equal(bits(out), want, f"M={M}")
+
+
+@pytest.mark.parametrize("K", [4096, 12288])
+def test_rms_rot_quant_matches_oracle(C, dev, K):
+    from mdx import _lib, layout
+    g = torch.Generator().manual_seed(K + 5)
+    w = (1 + torch.randn(K, generator=g) * 0.02).to(torch.bfloat16)
+    for M in (1, 3, 8):
+        for kind in ("normal", "outlier", "wide", "zero"):
+            print(f"case rms K={K} M={M} kind={kind}", flush=True)
+            x = _rows(kind, M, K, g)
+            xn = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+            for rot, name in ((_lib.ROT_NONE, "none"), (_lib.ROT_H256, "h256")):
+                h = layout.regular_hadamard(dev)
+                q, s = C.rms_rot_quant(x.to(dev), w.to(dev), 1e-6, rot, h, xn)
+                wxn = ref.rmsnorm(bits(x), bits(w), 1e-6)
+                assert_bits_equal(bits(xn), wxn, f"xn {kind}")
+                wq, ws = ref.rot_quant(wxn, name)
+                assert_bits_equal(bits(q), wq, f"q {kind} {name}")
+                assert_bits_equal(bits(s), ws.view(np.uint32), f"scale {kind} {name}")
+
+
+def test_mlp_with_norm_matches_oracle(C, dev):
+    from mdx import _lib, layout
+    g = torch.Generator().manual_seed(33)
+    ws, _ = _mlp_weights(g, "gptq", dev, True)
+    handles = [layout.W4(layout.tile_major_codes(q).to(dev), s.to(dev), c.to(dev), None, _lib.LAYOUT_TILE)
+               for q, s, c, _, _ in ws]
+    lut = layout.silu_lut()
+    nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    d = _oracle_dicts(ws)
+    for M in (1, 4, 8):
+        print(f"case norm-mlp M={M}", flush=True)
+        x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        out = C.mono_mlp_w4(x.to(dev), _lib.ROT_NONE, None, lut.to(dev), *handles, norm_w=nw.to(dev), eps=1e-6)
+        xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
+        want = ref.mono_mlp(xn, "none", None, bits(lut), *d)
+        assert_bits_equal(bits(out), want, f"M={M}")
