@@ -34,6 +34,9 @@
 //
 // Split-K partial sums of the waves of a work-group are int32 and are added through LDS:
 // integer addition is associative, so every split gives the same bits.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "mdx_common.hpp"
 
 namespace mdx {
@@ -277,6 +280,7 @@ struct GemvArgs {
     int rows;
     int KS, TPW;          // K slices per tile, tiles per work-group
     int xglobal;          // MFMA only: activation too large for LDS, A fragments read from global
+    int force_exact;      // MDX_DECODE_EXACT: never take the integral form
     int epi;
     void* out[3];
     const void* res[3];
@@ -342,40 +346,12 @@ __device__ __forceinline__ float rd_scale(const uint8_t* p) {
     return fp8_to_f32(*p);
 }
 
-// LDS staging of the activation: de-interleaved int8 rows + 8 * (sum of each 32-k block)
-__device__ void stage_activation(const GemvArgs& a, uint8_t* xl, int32_t* xs8) {
-    const int K = a.K;
-    const int nblk = K / 32;
-    const int total = a.rows * nblk;
-    for (int u = threadIdx.x; u < total; u += blockDim.x) {
-        const int r = u / nblk, b = u - r * nblk;
-        const uint4* src = reinterpret_cast<const uint4*>(a.xq + r * K + b * 32);
-        const uint4 v0 = src[0], v1 = src[1];
-        const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        uint32_t o[8];
-        int sum = 0;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            o[2 * h] = __builtin_amdgcn_perm(d[2 * h + 1], d[2 * h], 0x06040200u);
-            o[2 * h + 1] = __builtin_amdgcn_perm(d[2 * h + 1], d[2 * h], 0x07050301u);
-            sum = sdot4(int(d[2 * h]), 0x01010101, sum);
-            sum = sdot4(int(d[2 * h + 1]), 0x01010101, sum);
-        }
-        if (!a.xglobal) {
-            uint4* dst = reinterpret_cast<uint4*>(xl + r * K + b * 32);
-            dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-            dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
-        }
-        xs8[u] = 8 * sum;
-    }
-}
-
 // -------------------------------------------------------------------------------------------------
 // epilogue
 // -------------------------------------------------------------------------------------------------
-__device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, int r, int32_t acc) {
+__device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, int r, int32_t acc, float xs, float sc) {
     const MatArg& m = a.m[mi];
-    const float f = scaleback(acc, a.xs[r], m.sch[n]);
+    const float f = scaleback(acc, xs, sc);
     const int o = r * m.n + n;
     if (a.out_dt == MDX_DT_BF16) {
         uint16_t v = f2bf(f);
@@ -388,9 +364,10 @@ __device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, int 
     }
 }
 
-__device__ __forceinline__ void store_silu(const GemvArgs& a, int n, int r, int32_t ag, int32_t au) {
-    const uint16_t g = f2bf(scaleback(ag, a.xs[r], a.m[0].sch[n]));
-    const uint16_t u = f2bf(scaleback(au, a.xs[r], a.m[1].sch[n]));
+__device__ __forceinline__ void store_silu(const GemvArgs& a, int n, int r, int32_t ag, int32_t au, float xs, float scg,
+                                           float scu) {
+    const uint16_t g = f2bf(scaleback(ag, xs, scg));
+    const uint16_t u = f2bf(scaleback(au, xs, scu));
     const float act = bf2f(a.lut[g]);
     reinterpret_cast<uint16_t*>(a.out[0])[r * a.m[0].n + n] = f2bf(__fmul_rn(act, bf2f(u)));
 }
@@ -407,14 +384,16 @@ __device__ __forceinline__ int32_t reduced(const GemvArgs& a, const int32_t* red
 }
 
 template <bool MFMA>
-__device__ void epilogue(const GemvArgs& a, const int32_t* red) {
+__device__ void epilogue(const GemvArgs& a, const int32_t* red, const float* prml) {
     const int wg = blockIdx.x;
     const int per = 16 * a.rows;
+    const float* xsl = prml + a.TPW * 16;
     if (a.epi == EPI_SILU) {
         for (int e = threadIdx.x; e < per; e += blockDim.x) {
             const int r = e >> 4, c = e & 15;
             const int n = wg * 16 + c;  // pair: work-group wg owns gate tile wg and up tile wg
-            store_silu(a, n, r, reduced<MFMA>(a, red, 0, r, c), reduced<MFMA>(a, red, 1, r, c));
+            store_silu(a, n, r, reduced<MFMA>(a, red, 0, r, c), reduced<MFMA>(a, red, 1, r, c), xsl[r], prml[c],
+                       prml[16 + c]);
         }
         return;
     }
@@ -423,29 +402,46 @@ __device__ void epilogue(const GemvArgs& a, const int32_t* red) {
         int tile;
         const int mi = which_mat(a, wg * a.TPW + ts, tile);
         if (tile >= a.m[mi].tiles) continue;
-        store_out(a, mi, tile * 16 + c, r, reduced<MFMA>(a, red, ts, r, c));
+        store_out(a, mi, tile * 16 + c, r, reduced<MFMA>(a, red, ts, r, c), xsl[r], prml[ts * 16 + c]);
     }
 }
 
 // -------------------------------------------------------------------------------------------------
 // the kernel
 // -------------------------------------------------------------------------------------------------
-constexpr int RING = 4;
+// natural-order code bytes of a code dword: [c0 c1 c2 c3], [c4 c5 c6 c7] from its low / high nibbles
+__device__ __forceinline__ void nat_order(uint32_t lo, uint32_t hi, uint32_t& n0, uint32_t& n1) {
+    n0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+    n1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+}
 
-template <bool MFMA, int R, int SDT, int DEC>
+#define MDX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Copy `bytes` (a multiple of 16) from global to LDS with direct-to-LDS loads: one wave instruction
+// moves 64 x 16 contiguous bytes, no registers involved. The caller waits and barriers.
+__device__ __forceinline__ void dma_to_lds(const uint8_t* src, uint8_t* dst, int bytes) {
+    const int lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE, w = threadIdx.x / WAVE;
+    for (int off = w * 1024; off < bytes; off += nw * 1024) {
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(src + off + lane * 16, MDX_LDS(dst + off), 16, 0, 0);
+    }
+}
+
+template <bool MFMA, int R, int SDT, int RING>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
-    extern __shared__ uint8_t lds[];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
     const int K = a.K;
-    const int nblk = K / 32;
     const int ng = K >> a.lgG;
-    uint8_t* xl = lds;                                                               // rows * K (unless xglobal)
-    int32_t* xs8 = reinterpret_cast<int32_t*>(lds + (a.xglobal ? 0 : a.rows * K));  // rows * K/32
-    int32_t* red = xs8 + a.rows * nblk;
-    float* cbl = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
-    uint8_t* sl = reinterpret_cast<uint8_t*>(cbl + 16);                               // [TPW][16][ng] raw scales
+    const int per_tile = 16 * ng * ESZ;
+    // LDS: activation rows (natural order) | scale blocks [TPW][16][ng] | reduction | parameters
+    uint8_t* xl = lds;
+    uint8_t* sl = xl + ((a.rows * K + 1023) & ~1023);
+    int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * per_tile + 1023) & ~1023));
+    float* prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
 
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int t = threadIdx.x;
+    const int wave = t / WAVE, lane = t % WAVE;
     const int ts = wave / a.KS, slice = wave - ts * a.KS;
     int tile;
     const int mi = which_mat(a, blockIdx.x * a.TPW + ts, tile);
@@ -458,8 +454,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     const int klane = 32 * kq;
     const int lgG = a.lgG;
 
-    // per-lane code stream (32-bit offsets); loads past the slice re-read its last chunk so every
-    // iteration issues the same number of loads (a static wait count)
+    // weight ring first (registers): every slot issues one load; reads past the slice repeat its
+    // last chunk so the wait counts are static
     const uint8_t* wp;
     int wstride;
     if (a.layout == MDX_LAYOUT_TILE) {
@@ -472,94 +468,93 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     const int last = nch > 0 ? nch - 1 : 0;
     uint4 buf[RING];
 #pragma unroll
-    for (int p = 0; p < RING; ++p) buf[p] = live ? ldg_stream(wp + min(p, last) * wstride) : make_uint4(0, 0, 0, 0);
+    for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
 
-    // stage the work-group's group scales: a tile's 16 scale rows [16][K/G] are one contiguous block
-    {
-        const int per_tile = 16 * ng * ESZ;  // a multiple of 16 bytes (checked on the host)
-        for (int tsi = 0; tsi < a.TPW; ++tsi) {
-            int tl;
-            const int mm = which_mat(a, blockIdx.x * a.TPW + tsi, tl);
-            const uint8_t* src = (mm == 0 ? a.m[0].s : (mm == 1 ? a.m[1].s : a.m[2].s)) + tl * per_tile;
-            const int tiles = mm == 0 ? a.m[0].tiles : (mm == 1 ? a.m[1].tiles : a.m[2].tiles);
-            if (tl < tiles)
-                for (int i = threadIdx.x * 16; i < per_tile; i += blockDim.x * 16)
-                    *reinterpret_cast<uint4*>(sl + tsi * per_tile + i) = *reinterpret_cast<const uint4*>(src + i);
-        }
+    // then the one-shot operands straight into LDS: activation rows, the tiles' scale blocks
+    dma_to_lds(reinterpret_cast<const uint8_t*>(a.xq), xl, a.rows * K);
+    for (int tsi = 0; tsi < a.TPW; ++tsi) {
+        int tl;
+        const int mm = which_mat(a, blockIdx.x * a.TPW + tsi, tl);
+        const uint8_t* sb = mm == 0 ? a.m[0].s : (mm == 1 ? a.m[1].s : a.m[2].s);
+        const int tiles = mm == 0 ? a.m[0].tiles : (mm == 1 ? a.m[1].tiles : a.m[2].tiles);
+        if (tl < tiles) dma_to_lds(sb + tl * per_tile, sl + tsi * per_tile, per_tile);
     }
-    if (threadIdx.x < 16) cbl[threadIdx.x] = a.cb ? a.cb[threadIdx.x] : float(int(threadIdx.x) - 8);
-    stage_activation(a, xl, xs8);
-    __syncthreads();
+    float prm = 0.f;
+    if (t < a.TPW * 16) {
+        int tl;
+        const int mm = which_mat(a, blockIdx.x * a.TPW + t / 16, tl);
+        const float* sc = mm == 0 ? a.m[0].sch : (mm == 1 ? a.m[1].sch : a.m[2].sch);
+        const int tiles = mm == 0 ? a.m[0].tiles : (mm == 1 ? a.m[1].tiles : a.m[2].tiles);
+        prm = sc[(tl < tiles ? tl : 0) * 16 + (t & 15)];
+    } else if (t < a.TPW * 16 + a.rows) {
+        prm = a.xs[t - a.TPW * 16];
+    }
     float cb[16];
     bool cbdef = true;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        cb[i] = cbl[i];
+        cb[i] = a.cb ? a.cb[i] : float(i - 8);
         cbdef = cbdef && cb[i] == float(i - 8);
     }
-    // the integral form needs one scale per lane chunk (VALU) or per column chunk (MFMA)
-    const bool can_int = DEC == MDX_DECODE_AUTO && cbdef && (lgG >= (MFMA ? 7 : 5));
+    const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
+    if (t < a.TPW * 16 + a.rows) prml[t] = prm;
+    __syncthreads();
     const uint8_t* scol = sl + (ts * 16 + c) * ng * ESZ;
-    auto scale_of = [&](int ch, int dk) { return rd_scale<SDT>(scol + ((ch * CHUNK_K + klane + dk) >> lgG) * ESZ); };
 
     if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
         int32_t tot[4] = {0, 0, 0, 0};  // integral chunks: sum of s * (chunk dot - 8 sum x)
-        const int arow = lane & 15;
-        const bool arow_live = arow < a.rows;
-        const uint8_t* xrow = a.xglobal ? reinterpret_cast<const uint8_t*>(a.xq) + arow * K + klane : xl + arow * K + klane;
+        const bool xlive = (lane & 15) < a.rows;
+        const uint8_t* xrow = xl + (xlive ? (lane & 15) : 0) * K + klane;
         for (int i0 = 0; i0 < nch; i0 += RING) {
 #pragma unroll
             for (int p = 0; p < RING; ++p) {
                 const int i = i0 + p;
-                const uint4 w = buf[p];
-                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                 if (i < nch) {
+                    const uint4 w = buf[p];
+                    buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                     const int ch = c0 + i;
-                    const float s0 = scale_of(ch, 0);
+                    const int k0 = ch * CHUNK_K + klane;
+                    const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
                     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                    long aop[4] = {0, 0, 0, 0};
-                    if (arow_live) {
-                        const uint4* xp = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
-                        const uint4 xa = xp[0], xb = xp[1];
-                        uint32_t d[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                        if (a.xglobal) {
+                    const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
+                    const uint4 xa = x4[0], xb = x4[1];
+                    uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                    if (!xlive)
 #pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                const uint32_t e = __builtin_amdgcn_perm(d[2 * j + 1], d[2 * j], 0x06040200u);
-                                const uint32_t o = __builtin_amdgcn_perm(d[2 * j + 1], d[2 * j], 0x07050301u);
-                                d[2 * j] = e;
-                                d[2 * j + 1] = o;
-                            }
-                        }
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) aop[j] = long(uint64_t(d[2 * j]) | (uint64_t(d[2 * j + 1]) << 32));
-                    }
+                        for (int j = 0; j < 8; ++j) xd[j] = 0;
                     const bool integ = can_int && __all(s0 == rintf(s0) && fabsf(s0) <= 15.f);
                     if (integ) {
                         v4i dacc = {0, 0, 0, 0};
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
-                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[j], long(uint64_t(lo) | (uint64_t(hi) << 32)), dacc, 0, 0, 0);
+                            uint32_t n0, n1;
+                            nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, n0, n1);
+                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                         long(uint64_t(n0) | (uint64_t(n1) << 32)), dacc, 0, 0, 0);
                         }
+                        // 8 * sum of the chunk's activation per row: own 32 bytes, then the 4 quarters
+                        int xsum = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) xsum = sdot4(int(xd[j]), 0x01010101, xsum);
+                        xsum += shfl_xor(xsum, 16);
+                        xsum += shfl_xor(xsum, 32);
                         const int sv = int(s0);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int row = kq * 4 + r;
-                            int corr = 0;
-                            if (row < a.rows) {
-                                const int4 xb = *reinterpret_cast<const int4*>(xs8 + row * nblk + ch * 4);
-                                corr = xb.x + xb.y + xb.z + xb.w;
-                            }
+                            const int corr = 8 * __shfl(xsum, kq * 4 + r, 64);
                             tot[r] += __mul24(sv, dacc[r] - corr);
                         }
                     } else {
                         uint32_t lo[4], hi[4];
-                        decode_exact(wd, s0, scale_of(ch, 16), cb, lo, hi);
+                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            accE = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[j], long(uint64_t(lo[j]) | (uint64_t(hi[j]) << 32)), accE, 0, 0, 0);
+                        for (int j = 0; j < 4; ++j) {
+                            uint32_t n0, n1;
+                            nat_order(lo[j], hi[j], n0, n1);
+                            accE = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                         long(uint64_t(n0) | (uint64_t(n1) << 32)), accE, 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -575,38 +570,39 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int p = 0; p < RING; ++p) {
                 const int i = i0 + p;
-                const uint4 w = buf[p];
-                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                 if (i < nch) {
+                    const uint4 w = buf[p];
+                    buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                     const int ch = c0 + i;
-                    const float s0 = scale_of(ch, 0);
+                    const int k0 = ch * CHUNK_K + klane;
+                    const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
                     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                    uint32_t lo[4], hi[4];
+                    uint32_t nat[8];
                     const bool integ = can_int && __all(s0 == rintf(s0) && fabsf(s0) <= 15.f);
                     if (integ) {
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            lo[j] = wd[j] & 0x0F0F0F0Fu;
-                            hi[j] = (wd[j] >> 4) & 0x0F0F0F0Fu;
-                        }
+                        for (int j = 0; j < 4; ++j) nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, nat[2 * j], nat[2 * j + 1]);
                     } else {
-                        decode_exact(wd, s0, scale_of(ch, 16), cb, lo, hi);
+                        uint32_t lo[4], hi[4];
+                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], nat[2 * j], nat[2 * j + 1]);
                     }
                     const int sv = integ ? int(s0) : 1;
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         if (r < a.rows) {
-                            const uint4* xp = reinterpret_cast<const uint4*>(xl + r * K + ch * CHUNK_K + klane);
-                            const uint4 xa = xp[0], xb = xp[1];
+                            const uint4* x4 = reinterpret_cast<const uint4*>(xl + r * K + ch * CHUNK_K + klane);
+                            const uint4 xa = x4[0], xb = x4[1];
                             const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                            int d = 0;
+                            int d = 0, xsum = 0;
 #pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                d = sdot4(int(lo[j]), int(xv[2 * j]), d);
-                                d = sdot4(int(hi[j]), int(xv[2 * j + 1]), d);
+                            for (int j = 0; j < 8; ++j) d = sdot4(int(nat[j]), int(xv[j]), d);
+                            if (integ) {
+#pragma unroll
+                                for (int j = 0; j < 8; ++j) xsum = sdot4(int(xv[j]), 0x01010101, xsum);
                             }
-                            const int corr = integ ? xs8[r * nblk + ch * 4 + kq] : 0;
-                            tot[r] += __mul24(sv, d - corr);
+                            tot[r] += __mul24(sv, d - 8 * xsum);
                         }
                     }
                 }
@@ -626,47 +622,44 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
                 if (r < a.rows) red[((ts * a.KS + slice) * 16 + lane) * a.rows + r] = tot[r];
     }
     __syncthreads();
-    epilogue<MFMA>(a, red);
+    epilogue<MFMA>(a, red, prml);
 }
 
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) {
-    const int K = a.K;
-    size_t s = (a.xglobal ? 0 : size_t(a.rows) * K) + size_t(a.rows) * (K / 32) * 4;
+    const size_t per_tile = size_t(16) * (a.K >> a.lgG) * esz;
+    size_t s = ((size_t(a.rows) * a.K + 1023) & ~size_t(1023)) + ((a.TPW * per_tile + 1023) & ~size_t(1023));
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
-    s += 16 * 4;
-    s += size_t(a.TPW) * 16 * (K >> a.lgG) * esz;
-    return s;
+    return s + 64 * 4;
 }
 
 int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1); }
 
-template <bool MFMA, int R, int SDT, int DEC>
+template <bool MFMA, int R, int SDT, int RING>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
     const size_t smem = gemv_smem(a, MFMA, esz_of(SDT));
-    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, DEC>);
+    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING>);
     if (smem > 64 * 1024) allow_smem(fn, smem);
     const int threads = a.TPW * a.KS * WAVE;
-    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, DEC>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
+    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
 
-template <int SDT, int DEC>
+template <int SDT, int RING>
 int launch_gemv_s(const GemvArgs& a, bool mfma, int wgs, hipStream_t st) {
-    if (mfma) return launch_gemv_t<true, 4, SDT, DEC>(a, wgs, st);
-    if (a.rows == 1) return launch_gemv_t<false, 1, SDT, DEC>(a, wgs, st);
-    return launch_gemv_t<false, 2, SDT, DEC>(a, wgs, st);
+    if (mfma) return launch_gemv_t<true, 4, SDT, RING>(a, wgs, st);
+    return launch_gemv_t<false, 1, SDT, RING>(a, wgs, st);
 }
 
-template <int DEC>
+template <int RING>
 int launch_gemv_d(const GemvArgs& a, int sdt, bool mfma, int wgs, hipStream_t st) {
-    if (sdt == MDX_DT_F32) return launch_gemv_s<MDX_DT_F32, DEC>(a, mfma, wgs, st);
-    if (sdt == MDX_DT_F16) return launch_gemv_s<MDX_DT_F16, DEC>(a, mfma, wgs, st);
-    return launch_gemv_s<MDX_DT_FP8E4M3, DEC>(a, mfma, wgs, st);
+    if (sdt == MDX_DT_F32) return launch_gemv_s<MDX_DT_F32, RING>(a, mfma, wgs, st);
+    if (sdt == MDX_DT_F16) return launch_gemv_s<MDX_DT_F16, RING>(a, mfma, wgs, st);
+    return launch_gemv_s<MDX_DT_FP8E4M3, RING>(a, mfma, wgs, st);
 }
 
-// Rows at which the MFMA path takes over from the VALU dot path (the VALU path handles 1..2).
-constexpr int MFMA_MIN_ROWS = 3;
+// Rows at which the MFMA path takes over from the VALU dot path (the VALU path handles one row).
+constexpr int MFMA_MIN_ROWS = 2;
 
 int ilog2(int64_t v) {
     int l = 0;
@@ -694,6 +687,21 @@ int check_w4(const mdx_w4* w, const char* what) {
 int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
              void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st) {
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
+    // the activation rows live in LDS: above 128 KiB, run the rows in two halves
+    if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
+        const int ra = 8, rb = rows - 8;
+        int rc = run_gemv(ws, nm, pair, xq, xs, ra, epi, outs, res, out_dt, lut, st);
+        if (rc) return rc;
+        const int esz = out_dt == MDX_DT_F32 ? 4 : 2;
+        void* o2[3];
+        const void* r2[3];
+        for (int i = 0; i < nm; ++i) {
+            o2[i] = static_cast<uint8_t*>(outs[i]) + size_t(ra) * ws[pair ? 0 : i]->n * esz;
+            r2[i] = res && res[i] ? static_cast<const uint8_t*>(res[i]) + size_t(ra) * ws[i]->n * esz : nullptr;
+        }
+        if (pair) o2[1] = o2[0];
+        return run_gemv(ws, nm, pair, xq + size_t(ra) * ws[0]->k, xs + ra, rb, epi, o2, r2, out_dt, lut, st);
+    }
     MDX_CHECK(aligned(xq, 16), "x must be 16-byte aligned");
     const mdx_w4& w0 = *ws[0];
     for (int i = 0; i < nm; ++i) {
@@ -728,23 +736,31 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     a.out_dt = out_dt;
     a.lut = lut;
     const bool mfma = rows >= MFMA_MIN_ROWS;
-    // geometry: TPW tiles per work-group, KS K-slices per tile, at most 16 waves per work-group
+    // geometry: TPW tiles per work-group, KS K-slices per tile (at most 16 waves per work-group):
+    // the smallest split that puts >= 3072 waves on the chip (12 per CU), measured best on MI355X
+    // for the 8-52 MB matrices of this model (longer streams per wave beat more, shorter waves)
     a.TPW = pair ? 2 : 1;
     const int NC = a.K / CHUNK_K;
     const int wgs = (total + a.TPW - 1) / a.TPW;
-    int waves = wgs >= 256 ? 8 : 16;
-    a.KS = waves / a.TPW;
-    while (a.KS > 1 && (NC % a.KS != 0 || (NC / a.KS) % RING != 0)) a.KS >>= 1;
-    if (a.KS > NC) a.KS = NC;
+    const int maxks = 16 / a.TPW;
+    a.KS = 1;
+    for (int d = 1; d <= maxks && d <= NC; ++d) {
+        if (NC % d) continue;
+        a.KS = d;
+        if (int64_t(total) * d >= 3072) break;
+    }
+    // MDX_GEMV_KS overrides the split (tuning sweeps)
+    if (const char* env = getenv("MDX_GEMV_KS")) {
+        const int ks = atoi(env);
+        if (ks >= 1 && ks <= maxks && NC % ks == 0) a.KS = ks;
+    }
     a.xglobal = 0;
     const int esz = esz_of(w0.s_dtype);
-    if (mfma && gemv_smem(a, mfma, esz) > 128 * 1024) a.xglobal = 1;
     MDX_CHECK((16 * (a.K >> a.lgG) * esz) % 16 == 0, "a tile's scale block must be a multiple of 16 bytes");
     for (int i = 0; i < nm; ++i) MDX_CHECK(aligned(ws[i]->s_rel, 16), "s_rel must be 16-byte aligned");
-    const size_t smem = gemv_smem(a, mfma, esz);
-    MDX_CHECK(smem <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
-    if (w0.decode == MDX_DECODE_AUTO) return launch_gemv_d<MDX_DECODE_AUTO>(a, w0.s_dtype, mfma, wgs, st);
-    return launch_gemv_d<MDX_DECODE_EXACT>(a, w0.s_dtype, mfma, wgs, st);
+    MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
+    a.force_exact = w0.decode == MDX_DECODE_EXACT;
+    return launch_gemv_d<4>(a, w0.s_dtype, mfma, wgs, st);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
