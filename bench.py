@@ -207,13 +207,28 @@ def bench_linear(args, dev):
     }
 
 
+def bench_copy(args, dev):
+    """Calibration workload: a plain device copy of 256 MiB (read 256 MiB, write 256 MiB). Its
+    FETCH_SIZE / WRITE_SIZE counters give the scale factor of the traffic figures."""
+    import torch
+    n = 256 * 2 ** 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    reps = max(1, args.steps // 100)
+    t = graph_time(lambda: dst.copy_(src), reps, args.warmup)
+    return {"metric": "device copy GB/s (read + write)", "value": round(2 * n / t / 1e9, 2), "unit": "GB/s",
+            "n_gpus": 1, "steps": reps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": "copy of 256 MiB (traffic calibration)", "bytes_read": n, "bytes_written": n}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1)
-    ap.add_argument("--workload", choices=["mlp", "linear"], default="mlp")
+    ap.add_argument("--workload", choices=["mlp", "linear", "copy"], default="mlp")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -225,7 +240,7 @@ def main():
         print(json.dumps({"error": "no ROCm device"}))
         sys.exit(1)
     dev = torch.device("cuda", 0)
-    res = bench_mlp(args, dev) if args.workload == "mlp" else bench_linear(args, dev)
+    res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy}[args.workload](args, dev)
     print(json.dumps(res), flush=True)
 
 

@@ -75,6 +75,10 @@ __device__ __forceinline__ float load_scale(const void* s, int dtype, int64_t i)
     return fp8_to_f32(reinterpret_cast<const uint8_t*>(s)[i]);
 }
 
+// correctly rounded fp32 square root (HIP's __fsqrt_rn maps to the approximate hardware sqrt unless
+// the OCML rounded-operation mode is on; llvm.sqrt.f32 is lowered with the rounding correction)
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 // ---- wave64 helpers -----------------------------------------------------------------------------
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

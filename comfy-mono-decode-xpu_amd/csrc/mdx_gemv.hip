@@ -139,7 +139,7 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
         }
         const float ss = tree256(p, red);
         const float mean = __fdiv_rn(ss, float(K));
-        const float r = __fdiv_rn(1.f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+        const float r = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(mean, a.eps)));
 #pragma unroll
         for (int j = 0; j < PREP_BLK; ++j) {
             const int b = t + PREP_THREADS * j;

@@ -145,3 +145,118 @@ def mono_mlp(xn, hadamard, silu_lut, gq, gs, gsc, gcb, uq, us, usc, ucb, dq, ds,
     _check(silu_lut.dtype == torch.bfloat16 and silu_lut.numel() == 65536, "silu_lut bf16 [65536]")
     out = mono_mlp_w4(xn.reshape(rows, K1), classify_rotation(hadamard), hadamard, silu_lut, g, u, d)
     return out.reshape(*xn.shape[:-1], d.n)
+
+
+def _bf16_heads(t, what):
+    _dev(t, what)
+    _check(t.dtype == torch.bfloat16 and t.stride(-1) == 1, f"{what}: bf16 with a contiguous last dim")
+
+
+def _rope(qn, kn, vn, wq, wk, freqs, key, value, position, epsq, epsk, rd):
+    # q/k/v as [S, H, D] or [1, S, H, D] views (a gated q is the query half of [.., H, 2 D])
+    qn, kn, vn = (t[0] if t.dim() == 4 else t for t in (qn, kn, vn))
+    for t, n in ((qn, "q"), (kn, "k"), (vn, "v")):
+        _bf16_heads(t, n)
+        _check(t.dim() == 3, f"{n}: [S, H, D] or [1, S, H, D]")
+    S, Hq, D = qn.shape
+    Hk = kn.shape[1]
+    _check(kn.shape == (S, Hk, D) and vn.shape == (S, Hk, D), "k/v shapes")
+    _check(key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16 and key.is_contiguous()
+           and value.is_contiguous() and key.dim() == 4 and key.shape[0] == 1 and key.shape[1] == Hk
+           and key.shape[3] == D and value.shape == key.shape, "bf16 [1, Hk, cap, D] cache")
+    _check(freqs.dtype == torch.float32 and freqs.shape[-1] == 2 and freqs.shape[-2] == 2
+           and freqs.shape[-3] == rd // 2 and freqs.stride(-1) == 1 and freqs.stride(-2) == 2
+           and freqs.stride(-3) == 4 and freqs.numel() // (rd // 2 * 4) == S, "freqs [.., S, rd/2, 2, 2] f32")
+    _check(position.dtype == torch.int64 and position.is_contiguous() and position.numel() >= S,
+           "int64 positions [>= S]")
+    fs = freqs.stride(-4) if freqs.dim() >= 4 else rd // 2 * 4
+    if wq is not None:
+        for w, n in ((wq, "weight_q"), (wk, "weight_k")):
+            _check(w.dtype == torch.bfloat16 and w.is_contiguous() and w.numel() == D, f"{n}: bf16 [D]")
+    q = torch.empty(1, Hq, S, D, dtype=torch.bfloat16, device=qn.device)
+    k = torch.empty(1, Hk, S, D, dtype=torch.bfloat16, device=qn.device)
+    _lib.call("mdx_qk_norm_rope_kv", _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
+              kn.stride(1), _lib.ptr(vn), vn.stride(0), vn.stride(1), _lib.ptr(wq), _lib.ptr(wk), float(epsq),
+              float(epsk), _lib.ptr(freqs), fs, _lib.ptr(key), _lib.ptr(value), _lib.ptr(position), _lib.ptr(q),
+              _lib.ptr(k), S, Hq, Hk, D, key.shape[2], rd, _lib.stream_of(qn))
+    return [q, k]
+
+
+def rope_kv(qn, kn, vn, freqs, key, value, position, rd):
+    """Reference csrc/rope_kv.sycl:58-114: partial split-half RoPE on q and k + the KV cache write.
+    Returns [q [1, Hq, S, D], k [1, Hk, S, D]]."""
+    return _rope(qn, kn, vn, None, None, freqs, key, value, position, 1.0, 1.0, rd)
+
+
+def qk_norm_rope_kv(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd):
+    """Reference csrc/rope_kv.sycl:120-245: per-head Q/K RMSNorm, then rope_kv. The norm's reduction
+    order is the library's own (per-lane partials in element order, then a 64-lane halving tree)."""
+    _check(weightq is not None and weightk is not None, "norm weights")
+    _check(epsq > 0 and epsk > 0, "positive eps")
+    return _rope(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd)
+
+
+def _i64(t, what):
+    _dev(t, what)
+    _check(t.dtype == torch.int64 and t.is_contiguous(), f"{what}: contiguous int64 device tensor")
+
+
+def mtp_prep_draft(st, k, ftab, freqs, mpos, mseq):
+    """Reference csrc/mtp_loop.sycl:29-53: draft k's rope row and MTP KV positions from st."""
+    _i64(st, "st")
+    _i64(mpos, "mtp position")
+    _check(mseq.dtype == torch.int32 and mseq.numel() >= 1, "mtp seqlen int32")
+    _check(ftab.dtype == torch.float32 and ftab.is_contiguous() and freqs.dtype == torch.float32
+           and freqs.is_contiguous() and ftab.dim() >= 3 and freqs.dim() == ftab.dim() and freqs.shape[2] == 1,
+           "rope table [.., .., cap, ...] / row [.., .., 1, ...] float")
+    n, cap = freqs.numel(), ftab.shape[2]
+    _check(ftab.numel() == cap * n, "rope table row size")
+    _lib.call("mdx_mtp_prep_draft", _lib.ptr(st), int(k), _lib.ptr(ftab), cap, n, _lib.ptr(freqs), _lib.ptr(mpos),
+              mpos.numel(), _lib.ptr(mseq), _lib.stream_of(st))
+
+
+def _slots_of(ctl):
+    _check(ctl.dtype == torch.int32 and ctl.is_contiguous() and (ctl.numel() - 2) % 3 == 0, "ctl int32 [2 + 3 slots]")
+    slots = (ctl.numel() - 2) // 3
+    _check(slots in (8, 16), "8 or 16 slots")
+    return slots
+
+
+def mtp_prep_verify(st, apos, aseq, vpos, tree_pos, ctl, tree_ctl, parity, rope_offset):
+    """Reference csrc/mtp_loop.sycl:55-84: verify positions, ctl parity and the tree program."""
+    for t, n in ((st, "st"), (apos, "attention position"), (vpos, "verify positions"), (tree_pos, "tree positions")):
+        _i64(t, n)
+    _check(aseq.dtype == torch.int32, "attention seqlen int32")
+    slots = _slots_of(ctl)
+    _check(tree_ctl.dtype == torch.int32 and tree_ctl.numel() == 2 * slots and tree_ctl.is_contiguous(),
+           "tree program int32 [2 slots]")
+    rows = vpos.numel()
+    _check(tree_pos.numel() == rows and 1 <= rows <= slots and apos.numel() <= 64, "rows")
+    _lib.call("mdx_mtp_prep_verify", _lib.ptr(st), _lib.ptr(apos), apos.numel(), _lib.ptr(aseq), _lib.ptr(vpos),
+              _lib.ptr(tree_pos), rows, _lib.ptr(ctl), _lib.ptr(tree_ctl), slots, int(parity), int(rope_offset),
+              _lib.stream_of(st))
+
+
+def mtp_accept(st, toks, vtok, cand, children, rows, depth, x, nt_buf, h_buf, ctl, kv_ptrs, kv_heads, kv_cap,
+               head_dim, result):
+    """Reference csrc/mtp_loop.sycl:86-196: the accept walk, record, counters, ctl, next token and
+    hidden row, and the KV slot moves of an off-chain path."""
+    for t, n in ((st, "st"), (result, "result"), (nt_buf, "next token"), (vtok, "verify tokens")):
+        _i64(t, n)
+    slots = _slots_of(ctl)
+    _check(toks.dtype == torch.int64 and toks.numel() >= rows and toks.stride(-1) == 1 and toks.is_contiguous(),
+           "sampled tokens int64 [1, rows]")
+    _check(1 <= rows <= slots and 0 <= depth < rows, "rows / depth")
+    _check(children.dtype == torch.int32 and children.numel() == slots * slots and children.is_contiguous(),
+           "children int32 [slots][slots]")
+    has_cand = cand is not None and cand.numel() > 0
+    _check(not has_cand or (cand.dtype == torch.int64 and cand.is_contiguous() and cand.numel() >= 7 * max(depth, 7)),
+           "auto candidates int64 [max(depth, 7), 7]")
+    _check(x.is_contiguous() and h_buf.is_contiguous() and x.dtype == torch.bfloat16 and h_buf.dtype == torch.bfloat16
+           and x.numel() >= rows * h_buf.numel(), "hidden rows bf16")
+    _check(kv_ptrs.dtype == torch.int64 and kv_ptrs.is_contiguous(), "kv pointer table")
+    _check(result.numel() >= slots + 24, "result slot")
+    _lib.call("mdx_mtp_accept", _lib.ptr(st), _lib.ptr(toks), _lib.ptr(vtok), _lib.ptr(cand) if has_cand else None,
+              _lib.ptr(children), int(rows), int(depth), slots, _lib.ptr(x), h_buf.numel(), _lib.ptr(nt_buf),
+              _lib.ptr(h_buf), _lib.ptr(ctl), _lib.ptr(kv_ptrs), kv_ptrs.numel(), int(kv_heads), int(kv_cap),
+              int(head_dim), _lib.ptr(result), _lib.stream_of(st))

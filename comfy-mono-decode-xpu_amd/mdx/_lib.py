@@ -45,6 +45,17 @@ SIGNATURES = {
                                        c_void_p]),
     "mdx_rms_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p, c_int32, c_void_p,
                                          c_void_p, c_int64, c_int64, c_void_p]),
+    "mdx_qk_norm_rope_kv": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                           c_int64, c_void_p, c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
+                                           c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                           c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_mtp_prep_draft": (ctypes.c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                          c_void_p, c_void_p]),
+    "mdx_mtp_prep_verify": (ctypes.c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
+                                           c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_mtp_accept": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+                                      c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                      c_int64, c_int64, c_void_p, c_void_p]),
 }
 
 _lib = None

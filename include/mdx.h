@@ -115,6 +115,55 @@ int mdx_stream_gemv(const int8_t* x, const float* x_scale, const mdx_w4* const* 
 int mdx_rms_rot_quant(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* xn_out, const uint16_t* h,
                       int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
 
+/* Q/K RMSNorm (optional) + partial split-half RoPE + KV cache write, one launch.
+ * Replaces: _C.rope_kv (csrc/rope_kv.sycl:58-114; weight_q = weight_k = NULL) and
+ * _C.qk_norm_rope_kv (csrc/rope_kv.sycl:120-245; both weights given), bindings.cpp:84-90.
+ *   [t = bf16((x * r) * w), r = 1 / sqrt(sum(x^2) / D + eps), per head, in the library's fixed order]
+ *   pair j < rd/2, f = freqs[s, j] = [[f00, f01], [f10, f11]]:
+ *   o[j] = bf16(t[j] * f00 + t[j + rd/2] * f01), o[j + rd/2] = bf16(t[j + rd/2] * f11 + t[j] * f10),
+ *   each product rounded to fp32 on its own; lanes d >= rd pass through.
+ * q/k/v bf16 rows s of stride *_row_stride and heads of stride *_head_stride (elements; the last dim
+ * contiguous: a gated q is the first half of each [query, gate] head); freqs f32 [S, rd/2, 2, 2] with
+ * row stride freqs_row_stride; key/value bf16 [Hk, cap, D]: rows position[s] are written with k
+ * (rotated) and v; q_out [Hq, S, D], k_out [Hk, S, D]. 1 <= S <= 16, D in {64, 128, 192, 256}.
+ * The caller owns in-range positions (0 <= position[s] < cap). */
+int mdx_qk_norm_rope_kv(const uint16_t* q, int64_t q_row_stride, int64_t q_head_stride, const uint16_t* k,
+                        int64_t k_row_stride, int64_t k_head_stride, const uint16_t* v, int64_t v_row_stride,
+                        int64_t v_head_stride, const uint16_t* weight_q, const uint16_t* weight_k, float eps_q,
+                        float eps_k, const float* freqs, int64_t freqs_row_stride, uint16_t* key, uint16_t* value,
+                        const int64_t* position, uint16_t* q_out, uint16_t* k_out, int64_t S, int64_t Hq,
+                        int64_t Hk, int64_t D, int64_t cap, int64_t rd, void* stream);
+
+/* MTP draft k's rope row and MTP KV positions from the device loop state st (int64 [4]:
+ * st[0] committed length, st[1] MTP KV length).
+ * Replaces: _C.mtp_prep_draft, csrc/mtp_loop.sycl:29-53.
+ *   p = st[0] + k; freqs = ftab[min(p, ftab_rows - 1)] (row_elems floats); mpos[i] = st[1] + k + i;
+ *   mseq[0] = st[1] + k + 1. */
+int mdx_mtp_prep_draft(const int64_t* st, int64_t k, const float* ftab, int64_t ftab_rows, int64_t row_elems,
+                       float* freqs, int64_t* mpos, int64_t npos, int32_t* mseq, void* stream);
+
+/* Verify-step positions and the deferred-delta ctl program.
+ * Replaces: _C.mtp_prep_verify, csrc/mtp_loop.sycl:55-84.
+ *   apos[i] = st[0] + i; aseq = st[0]; vpos[r] = tree_pos[r] + st[0] + rope_offset; ctl[1] = parity;
+ *   ctl[2 + slots + i] = tree_ctl[i] for i < 2 slots (parents, programs). ctl int32 [2 + 3 slots]. */
+int mdx_mtp_prep_verify(const int64_t* st, int64_t* apos, int64_t npos, int32_t* aseq, int64_t* vpos,
+                        const int64_t* tree_pos, int64_t rows, int32_t* ctl, const int32_t* tree_ctl, int64_t slots,
+                        int64_t parity, int64_t rope_offset, void* stream);
+
+/* The accept walk of one verify step, on the device.
+ * Replaces: _C.mtp_accept, csrc/mtp_loop.sycl:86-196.
+ *   path = [0]; extend by the first child c (children[cur][j], -1 terminated) with vtok[c] == toks[cur].
+ *   result int64 [slots + 24] = [n, commit[slots], row, on_chain, nranks, ranks[7], pos, kept, ...];
+ *   st[0] += n; st[1] += kept; ctl[0] = n; ctl[2 + i] = path[i] (i < n) else i; nt = toks[row];
+ *   hbuf = x[row]; an off-chain path moves KV slot (pos + path[k]) % cap to (pos + k) % cap in every
+ *   table of kv_ptrs (bf16 [kv_heads, cap, head_dim] each), k ascending.
+ * cand: int64 [max(depth, 7)][7] draft candidates of the chain nodes for the rank record, or NULL.
+ * slots in {8, 16}; kv_cap > slots. */
+int mdx_mtp_accept(int64_t* st, const int64_t* toks, const int64_t* vtok, const int64_t* cand,
+                   const int32_t* children, int64_t rows, int64_t depth, int64_t slots, const uint16_t* x,
+                   int64_t hidden, int64_t* nt, uint16_t* hbuf, int32_t* ctl, const int64_t* kv_ptrs, int64_t nkv,
+                   int64_t kv_heads, int64_t kv_cap, int64_t head_dim, int64_t* result, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -281,3 +281,147 @@ def silu_lut_f64():
     x = bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16)).astype(np.float64)
     with np.errstate(over="ignore", invalid="ignore"):
         return x / (1.0 + np.exp(-x))
+
+
+# ---------------------------------------------------------------------------------------------
+# RoPE + KV write (csrc/rope_kv.sycl)
+# ---------------------------------------------------------------------------------------------
+
+
+def head_rmsnorm(x_bits, w_bits, eps):
+    """Per-head RMSNorm of qk_norm_rope_kv in the library's fixed order (the reference's Q tree of
+    two 128-lane torch partials and its K tree with the EU rsqrt, csrc/rope_kv.sycl:193-219, are not
+    portable): 64 lanes, lane l owns d = l + 64 j and sums x[d]^2 over j in order (fp32); the lanes are
+    added by a halving tree (offsets 32, 16, .., 1); r = 1 / sqrt(ss / D + eps) with IEEE sqrt and
+    divide; t = bf16((x * r) * w) (csrc/rope_kv.sycl:225-227). x_bits [..., D] bf16 bits."""
+    x = bf16_to_f32(x_bits)
+    D = x.shape[-1]
+    lanes = x.reshape(x.shape[:-1] + (D // 64, 64))
+    sq = (lanes * lanes).astype(np.float32)
+    part = sq[..., 0, :]
+    for j in range(1, D // 64):
+        part = (part + sq[..., j, :]).astype(np.float32)
+    off = 32
+    while off >= 1:
+        part = part.copy()
+        part[..., :off] = (part[..., :off] + part[..., off:2 * off]).astype(np.float32)
+        off //= 2
+    ss = part[..., 0]
+    r = (np.float32(1) / np.sqrt((ss / np.float32(D)).astype(np.float32) + np.float32(eps))).astype(np.float32)
+    w = bf16_to_f32(w_bits)
+    return f32_to_bf16(((x * r[..., None]).astype(np.float32) * w).astype(np.float32))
+
+
+def rope_rows(t_bits, freqs, rd):
+    """Partial split-half RoPE (csrc/rope_kv.sycl:5-11,44-52, tests/test_rope_kv.py:9-23).
+    t_bits [S, H, D] bf16 bits; freqs f32 [S, rd/2, 2, 2]. For j < rd/2 with h = rd/2:
+    o[j] = bf16(fl(t[j] * f00) + fl(t[j+h] * f01)), o[j+h] = bf16(fl(t[j+h] * f11) + fl(t[j] * f10))."""
+    t = bf16_to_f32(t_bits)
+    h = rd // 2
+    f = np.asarray(freqs, dtype=np.float32)[:, None]  # [S, 1, h, 2, 2]
+    lo, hi = t[..., :h], t[..., h:rd]
+    o0 = (lo * f[..., 0, 0]).astype(np.float32) + (hi * f[..., 0, 1]).astype(np.float32)
+    o1 = (hi * f[..., 1, 1]).astype(np.float32) + (lo * f[..., 1, 0]).astype(np.float32)
+    out = np.array(t_bits, dtype=np.uint16, copy=True)
+    out[..., :h] = f32_to_bf16(o0.astype(np.float32))
+    out[..., h:rd] = f32_to_bf16(o1.astype(np.float32))
+    return out
+
+
+def rope_kv(q_bits, k_bits, v_bits, freqs, key_bits, value_bits, pos, rd, wq=None, wk=None, epsq=1e-6, epsk=1e-6):
+    """rope_kv / qk_norm_rope_kv (csrc/rope_kv.sycl:58-114,120-245): returns q [Hq, S, D], k [Hk, S, D]
+    and the updated caches key/value [Hk, cap, D] (rows pos[s] <- rotated k / v)."""
+    if wq is not None:
+        q_bits, k_bits = head_rmsnorm(q_bits, wq, epsq), head_rmsnorm(k_bits, wk, epsk)
+    rq, rk = rope_rows(q_bits, freqs, rd), rope_rows(k_bits, freqs, rd)
+    key, value = np.array(key_bits, copy=True), np.array(value_bits, copy=True)
+    for s, p in enumerate(np.asarray(pos)):
+        key[:, p] = rk[s]
+        value[:, p] = v_bits[s]
+    return rq.transpose(1, 0, 2).copy(), rk.transpose(1, 0, 2).copy(), key, value
+
+
+# ---------------------------------------------------------------------------------------------
+# MTP loop bookkeeping (csrc/mtp_loop.sycl, comfy_mono_decode_xpu/mtp_loop.py)
+# ---------------------------------------------------------------------------------------------
+
+
+def accept_walk(children, toks, dr, depth, cand=None):
+    """The host accept walk (comfy_mono_decode_xpu/mtp_loop.py:117-136): from the root, step to the
+    first child whose draft token equals the token the verify chose at the current node.
+    children: list of child lists. Returns path, commit, ranks, row, on_chain, kept."""
+    path = [0]
+    while True:
+        cur = path[-1]
+        nxt = [c for c in children[cur] if dr[c] == toks[cur]]
+        if not nxt:
+            break
+        path.append(nxt[0])
+    ranks = []
+    if cand is not None:
+        for node in path:
+            if node >= depth:
+                break
+            row7 = list(cand[7 * node:7 * node + 7])
+            ranks.append(row7.index(toks[node]) if toks[node] in row7 else 7)
+    commit = [dr[r] for r in path[1:]] + [toks[path[-1]]]
+    row = path[-1]
+    on_chain = row == len(path) - 1
+    kept = min(len(path) if on_chain else len(path) - 1, depth)
+    return path, commit, ranks, row, on_chain, kept
+
+
+def accept_record(slots, path, commit, ranks, row, on_chain, kept, pos):
+    """The int64 result record of mtp_accept (csrc/mtp_loop.sycl:143-161), slots generalised:
+    [n, commit[slots] (-1 padded), row, on_chain, nranks, ranks[7], pos, kept]; at most 7 ranks are
+    recorded (the first 7 chain nodes of a deeper 16-slot tree)."""
+    ranks = ranks[:7]
+    r = [len(path)] + commit + [-1] * (slots - len(commit)) + [row, int(on_chain), len(ranks)]
+    r += ranks + [0] * (7 - len(ranks)) + [pos, kept]
+    return r
+
+
+def commit_path(cache, path, on_chain, pos):
+    """FixedKVState.commit_path's slot moves (csrc/mtp_loop.sycl:177-192, tests/test_mtp_accept.py:95-102):
+    for an off-chain path, slot (pos + k) % cap <- slot (pos + path[k]) % cap, k ascending, applied in
+    sequence on cache [Hk, cap, D]."""
+    out = np.array(cache, copy=True)
+    cap = out.shape[1]
+    if not on_chain:
+        for k, src in enumerate(path[1:], 1):
+            if src != k:
+                out[:, (pos + k) % cap] = out[:, (pos + src) % cap]
+    return out
+
+
+def tree_from_spec(spec, rows):
+    """VerifyTree parent / children / depth / chain of a nested child-list spec (qwen35 tree order:
+    depth-first, first child is the chain; tests/test_mtp_accept.py:15-36)."""
+    parent, children, depth = [], [], []
+
+    def add(node, p):
+        r = len(parent)
+        parent.append(p)
+        children.append([])
+        depth.append(0 if p < 0 else depth[p] + 1)
+        if p >= 0:
+            children[p].append(r)
+        for child in node:
+            add(child, r)
+    add(spec, -1)
+    chain = 0
+    while children[chain]:
+        chain = children[chain][0]
+    while len(parent) < rows:
+        parent.append(-1)
+        children.append([])
+        depth.append(0)
+    return parent, children, depth, chain
+
+
+def spec_of_widths(widths):
+    """qwen35.tree_spec: a chain with (width - 1) leaf siblings at each depth."""
+    node = []
+    for width in reversed(widths):
+        node = [node] + [[] for _ in range(width - 1)]
+    return node
