@@ -1,0 +1,317 @@
+// Exact top-k of long rows in torch's XPU order, one launch: fast_topk / fast_pick (one bf16 row,
+// k <= 8, optional argmax) and topk_rows (up to 16 fp32 or bf16 rows, k <= 64).
+//
+// Reference semantics (comfy-mono-decode-xpu): csrc/fast_topk.sycl:4-40 (bf16 radix key, argmax rank,
+// gather order of 1024 threads x 4 loads of 8), csrc/fast_topk.sycl:145-157 (index back-mapping),
+// csrc/topk_rows.sycl:7-11,33-43 (fp32 radix key, gather order of 1024 threads x 8 loads of 4).
+// Every element gets a unique 64-bit rank (radix key in the high word, the complement of its gather
+// position in the low word); the k largest ranks, in descending order, are the result.
+//
+// Launch: rows x nseg work-groups of 256 (4 waves), each owning a contiguous segment of its row.
+//   1. every thread streams its elements (stride 256) and keeps its largest rank;
+//   2. theta = the k-th largest of the 256 thread maxima (each thread counts the maxima above its own;
+//      ranks are unique, so exactly one thread sees k - 1). Every element >= theta belongs to one of
+//      the k threads whose maximum is >= theta, so at most k * ceil(seg / 256) elements qualify and
+//      the candidate buffer in LDS never overflows, ties or not;
+//   3. the candidates are ranked by counting (position = number of larger candidates); the segment's
+//      top-k goes to the workspace as a descending, zero-padded list;
+//   4. the row's last work-group (device-scope counter, reset by that work-group) merges the nseg
+//      lists: an entry's final position is its own position plus, for every other list, the number of
+//      entries above it (binary search).
+// Ranks are never 0 (the radix key of a non-NaN value is nonzero, and a NaN's rank has a nonzero
+// gather word), so 0 marks an empty slot.
+#include <algorithm>
+
+#include "mdx_common.hpp"
+
+namespace mdx {
+namespace {
+
+constexpr int TK_T = 256;
+constexpr int TK_MAXK = 64;
+constexpr int TK_MAXR = 16;
+constexpr int TK_MAXSEG = 64;
+
+enum Order : int {
+    ORDER_BF16 = 0,    // torch XPU topk of one bf16 row: bf16 radix key, gather 1024 x 4 loads x 8
+    ORDER_ARGMAX = 1,  // torch XPU argmax of a bf16 row: NaN first, -0 == +0, smallest index
+    ORDER_F32 = 2,     // torch XPU topk of fp32 rows: fp32 radix key, gather 1024 x 8 loads x 4
+};
+
+// Position of element i in the gather order of a sweep of 1024 threads, each issuing `loads` vector
+// loads of `width` elements per 32768-element iteration: (iteration, thread, load, lane).
+template <int LOADS, int WIDTH>
+__device__ __forceinline__ uint32_t gather_pos(uint32_t i) {
+    const uint32_t it = i >> 15, off = i & 32767u;
+    const uint32_t load = off / (1024u * WIDTH), thread = (off % (1024u * WIDTH)) / WIDTH, lane = off % WIDTH;
+    return (it << 15) | (thread * (LOADS * WIDTH)) | (load * WIDTH) | lane;
+}
+template <int LOADS, int WIDTH>
+__device__ __forceinline__ uint32_t gather_index(uint32_t g) {
+    const uint32_t it = g >> 15, rem = g & 32767u;
+    const uint32_t thread = rem / (LOADS * WIDTH), load = (rem / WIDTH) % LOADS, lane = rem % WIDTH;
+    return (it << 15) | (load * 1024u * WIDTH) | (thread * WIDTH) | lane;
+}
+
+// radix keys: larger key = earlier in torch's descending order
+__device__ __forceinline__ uint32_t key_bf16(uint16_t b) {
+    if ((b & 0x7FFFu) > 0x7F80u) return 0xFFFFu;  // NaN on top
+    return (b & 0x8000u) ? uint32_t(b ^ 0xFFFFu) : uint32_t(b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t key_f32(uint32_t u) {  // +NaN on top, -NaN at the bottom
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t key_argmax(uint16_t b) {
+    if ((b & 0x7FFFu) > 0x7F80u) return 0xFFFFFFFFu;
+    if ((b & 0x7FFFu) == 0) b = 0;  // -0 == +0
+    return (b & 0x8000u) ? 0x7FFFu - (b & 0x7FFFu) : 0x8000u + b;
+}
+
+template <int ORD>
+__device__ __forceinline__ uint64_t rank_of(const void* row, uint32_t i, bool f32) {
+    if (ORD == ORDER_BF16)
+        return (uint64_t(key_bf16(static_cast<const uint16_t*>(row)[i])) << 32) |
+               (0xFFFFFFFFu - gather_pos<4, 8>(i));
+    if (ORD == ORDER_ARGMAX)
+        return (uint64_t(key_argmax(static_cast<const uint16_t*>(row)[i])) << 32) | (0xFFFFFFFFu - i);
+    const uint32_t u = f32 ? static_cast<const uint32_t*>(row)[i] : uint32_t(static_cast<const uint16_t*>(row)[i]) << 16;
+    return (uint64_t(key_f32(u)) << 32) | (0xFFFFFFFFu - gather_pos<8, 4>(i));
+}
+
+template <int ORD>
+__device__ __forceinline__ uint32_t index_of(uint64_t r) {
+    const uint32_t g = 0xFFFFFFFFu - uint32_t(r);
+    if (ORD == ORDER_BF16) return gather_index<4, 8>(g);
+    if (ORD == ORDER_ARGMAX) return g;
+    return gather_index<8, 4>(g);
+}
+
+struct TopkArgs {
+    const void* x;       // [rows, n] bf16 or fp32
+    int64_t n;
+    int rows, k, nseg, seg, f32;
+    int pick;            // also the argmax (ORDER_ARGMAX rank) of the row
+    void* values;        // [rows, k]: bf16 (ORDER_BF16 / ORDER_ARGMAX) or fp32 (ORDER_F32)
+    int64_t* indices;    // [rows, k]
+    int64_t* argmax;     // [rows] when pick
+    uint64_t* lists;     // workspace: [rows][nseg][k] ranks, [rows][nseg] argmax ranks
+    uint64_t* amax;
+    unsigned* counter;   // [rows], zero between launches
+};
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint64_t o = __shfl_xor(v, d, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+template <int ORD>
+__global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
+    extern __shared__ __align__(16) uint64_t sm[];
+    uint64_t* tmax = sm;             // [256] thread maxima
+    uint64_t* cand = sm + TK_T;      // candidates (k * ceil(seg / 256)) or, in the merge, nseg * k lists
+    __shared__ uint64_t theta_s, am_s[TK_T / 64];
+    __shared__ unsigned ncand, last_s;
+    const int t = threadIdx.x;
+    const int row = blockIdx.x / a.nseg, sg = blockIdx.x % a.nseg;
+    const int K = a.k;
+    const bool f32 = a.f32;
+    const void* xr = f32 ? static_cast<const void*>(static_cast<const uint32_t*>(a.x) + row * a.n)
+                         : static_cast<const void*>(static_cast<const uint16_t*>(a.x) + row * a.n);
+    const uint32_t lo = uint32_t(sg) * uint32_t(a.seg);
+    const int64_t end = int64_t(lo) + a.seg;
+    const uint32_t hi = uint32_t(end < a.n ? end : a.n);
+
+    // 1. thread maxima (and the argmax rank for a pick)
+    uint64_t mx = 0, am = 0;
+    for (uint32_t i = lo + t; i < hi; i += TK_T) {
+        const uint64_t r = rank_of<ORD>(xr, i, f32);
+        mx = r > mx ? r : mx;
+        if (a.pick) {
+            const uint64_t q = rank_of<ORDER_ARGMAX>(xr, i, false);
+            am = q > am ? q : am;
+        }
+    }
+    tmax[t] = mx;
+    if (t == 0) ncand = 0;
+    if (a.pick) {
+        am = wave_max_u64(am);
+        if ((t & 63) == 0) am_s[t >> 6] = am;
+    }
+    __syncthreads();
+    // 2. theta: the k-th largest thread maximum (or the smallest nonzero one if fewer than k)
+    const int nz = __syncthreads_count(mx != 0);
+    if (nz <= K) {
+        if (t == 0) theta_s = 1;
+    } else if (mx != 0) {
+        int above = 0;
+        for (int q = 0; q < TK_T; ++q) above += tmax[q] > mx;
+        if (above == K - 1) theta_s = mx;
+    }
+    __syncthreads();
+    const uint64_t theta = theta_s;
+    // 3. candidates >= theta, ranked by counting
+    if (mx >= theta)
+        for (uint32_t i = lo + t; i < hi; i += TK_T) {
+            const uint64_t r = rank_of<ORD>(xr, i, f32);
+            if (r >= theta) cand[atomicAdd(&ncand, 1u)] = r;
+        }
+    __syncthreads();
+    const int nc = int(ncand);
+    uint64_t* mylist = a.lists + (int64_t(row) * a.nseg + sg) * K;
+    for (int j = t; j < nc; j += TK_T) {
+        const uint64_t v = cand[j];
+        int pos = 0;
+        for (int q = 0; q < nc; ++q) pos += cand[q] > v;
+        if (pos < K) mylist[pos] = v;
+    }
+    for (int j = nc + t; j < K; j += TK_T) mylist[j] = 0;
+    if (a.pick && t == 0) {
+        uint64_t b = am_s[0];
+        for (int w = 1; w < TK_T / 64; ++w) b = am_s[w] > b ? am_s[w] : b;
+        a.amax[int64_t(row) * a.nseg + sg] = b;
+    }
+    // 4. the row's last work-group merges
+    __threadfence();
+    __syncthreads();
+    if (t == 0)
+        last_s = __hip_atomic_fetch_add(a.counter + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+                 unsigned(a.nseg - 1);
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+    const int total = a.nseg * K;
+    const uint64_t* rl = a.lists + int64_t(row) * a.nseg * K;
+    for (int e = t; e < total; e += TK_T)
+        cand[e] = __hip_atomic_load(rl + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    for (int e = t; e < total; e += TK_T) {
+        const uint64_t v = cand[e];
+        if (v == 0) continue;
+        const int mine = e / K;
+        int pos = e % K;
+        for (int w = 0; w < a.nseg && pos < K; ++w) {
+            if (w == mine) continue;
+            const uint64_t* l = cand + w * K;
+            int b0 = 0, b1 = K;  // first entry of list w not above v (lists descend, zero-padded)
+            while (b0 < b1) {
+                const int m = (b0 + b1) >> 1;
+                if (l[m] > v) b0 = m + 1;
+                else b1 = m;
+            }
+            pos += b0;
+        }
+        if (pos < K) {
+            const uint32_t idx = index_of<ORD>(v);
+            a.indices[int64_t(row) * K + pos] = idx;
+            if (ORD == ORDER_F32) {
+                const uint32_t u = f32 ? static_cast<const uint32_t*>(xr)[idx]
+                                       : uint32_t(static_cast<const uint16_t*>(xr)[idx]) << 16;
+                static_cast<float*>(a.values)[int64_t(row) * K + pos] = __uint_as_float(u);
+            } else {
+                static_cast<uint16_t*>(a.values)[int64_t(row) * K + pos] = static_cast<const uint16_t*>(xr)[idx];
+            }
+        }
+    }
+    if (a.pick && t == 0) {
+        uint64_t b = 0;
+        for (int w = 0; w < a.nseg; ++w) {
+            const uint64_t q = __hip_atomic_load(a.amax + int64_t(row) * a.nseg + w, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            b = q > b ? q : b;
+        }
+        a.argmax[row] = index_of<ORDER_ARGMAX>(b);
+    }
+    if (t == 0) __hip_atomic_store(a.counter + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// segments: about 2 x 256 work-groups over all rows, at least 1024 elements each
+void plan(int64_t rows, int64_t n, int& nseg, int& seg) {
+    int64_t s = std::max<int64_t>(1, std::min<int64_t>(TK_MAXSEG, 512 / rows));
+    s = std::min<int64_t>(s, std::max<int64_t>(1, n / 1024));
+    int64_t len = (n + s - 1) / s;
+    len = (len + 63) / 64 * 64;
+    nseg = int((n + len - 1) / len);
+    seg = int(len);
+}
+
+size_t lds_bytes(int k, int nseg, int seg) {
+    const size_t cand = size_t(k) * size_t((seg + TK_T - 1) / TK_T);
+    return (TK_T + std::max(cand, size_t(nseg) * k)) * sizeof(uint64_t);
+}
+
+size_t workspace_bytes(int64_t rows) {
+    return size_t(rows) * TK_MAXSEG * (TK_MAXK + 1) * sizeof(uint64_t) + 256;
+}
+
+int launch(const void* x, bool f32, int ord, int64_t rows, int64_t n, int64_t k, bool pick, void* values,
+           int64_t* indices, int64_t* argmax, void* ws, size_t ws_bytes, hipStream_t stream) {
+    MDX_CHECK(ws && aligned(ws, 256) && ws_bytes >= workspace_bytes(rows), "workspace: %zu bytes, 256-byte aligned",
+              workspace_bytes(rows));
+    int nseg, seg;
+    plan(rows, n, nseg, seg);
+    TopkArgs a{};
+    a.x = x;
+    a.n = n;
+    a.rows = int(rows);
+    a.k = int(k);
+    a.nseg = nseg;
+    a.seg = seg;
+    a.f32 = f32;
+    a.pick = pick;
+    a.values = values;
+    a.indices = indices;
+    a.argmax = argmax;
+    a.counter = static_cast<unsigned*>(ws);
+    a.lists = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + 256);
+    a.amax = a.lists + size_t(rows) * TK_MAXSEG * TK_MAXK;
+    const size_t lds = lds_bytes(int(k), nseg, seg);
+    MDX_CHECK(lds <= 64 * 1024, "top-k LDS plan %zu bytes exceeds 64 KiB", lds);
+    const dim3 grid(unsigned(rows * nseg)), block(TK_T);
+    if (ord == ORDER_BF16)
+        hipLaunchKernelGGL(topk_kernel<ORDER_BF16>, grid, block, lds, stream, a);
+    else if (ord == ORDER_ARGMAX)
+        hipLaunchKernelGGL(topk_kernel<ORDER_ARGMAX>, grid, block, lds, stream, a);
+    else
+        hipLaunchKernelGGL(topk_kernel<ORDER_F32>, grid, block, lds, stream, a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
+}  // namespace
+}  // namespace mdx
+
+using namespace mdx;
+
+extern "C" size_t mdx_topk_workspace(int64_t rows) { return workspace_bytes(std::max<int64_t>(rows, 1)); }
+
+extern "C" int mdx_fast_topk(const uint16_t* x, int64_t V, int64_t k, int32_t argmax_order, uint16_t* values,
+                             int64_t* indices, void* workspace, size_t workspace_bytes, void* stream) {
+    MDX_CHECK(x && values && indices, "null pointer");
+    MDX_CHECK(k >= 1 && k <= 8, "1 <= k <= 8");
+    MDX_CHECK(!argmax_order || k == 1, "argmax order takes k = 1");
+    MDX_CHECK(V >= 32768 && V < (int64_t(1) << 31), "one long row (32768 <= V < 2^31)");
+    return launch(x, false, argmax_order ? ORDER_ARGMAX : ORDER_BF16, 1, V, k, false, values, indices, nullptr,
+                  workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_fast_pick(const uint16_t* x, int64_t V, int64_t k, uint16_t* values, int64_t* indices,
+                             int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream) {
+    MDX_CHECK(x && values && indices && argmax, "null pointer");
+    MDX_CHECK(k >= 1 && k <= 8, "1 <= k <= 8");
+    MDX_CHECK(V >= 32768 && V < (int64_t(1) << 31), "one long row (32768 <= V < 2^31)");
+    return launch(x, false, ORDER_BF16, 1, V, k, true, values, indices, argmax, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
+                             int64_t* indices, void* workspace, size_t workspace_bytes, void* stream) {
+    MDX_CHECK(x && values && indices, "null pointer");
+    MDX_CHECK(x_dtype == MDX_DT_F32 || x_dtype == MDX_DT_BF16, "x: fp32 or bf16");
+    MDX_CHECK(rows >= 1 && rows <= TK_MAXR, "1 <= rows <= 16");
+    MDX_CHECK(k >= 1 && k <= TK_MAXK && n >= 4096 && n < (int64_t(1) << 31), "1 <= k <= 64, 4096 <= N < 2^31");
+    return launch(x, x_dtype == MDX_DT_F32, ORDER_F32, rows, n, k, false, values, indices, nullptr, workspace,
+                  workspace_bytes, static_cast<hipStream_t>(stream));
+}

@@ -260,3 +260,68 @@ def mtp_accept(st, toks, vtok, cand, children, rows, depth, x, nt_buf, h_buf, ct
               _lib.ptr(children), int(rows), int(depth), slots, _lib.ptr(x), h_buf.numel(), _lib.ptr(nt_buf),
               _lib.ptr(h_buf), _lib.ptr(ctl), _lib.ptr(kv_ptrs), kv_ptrs.numel(), int(kv_heads), int(kv_cap),
               int(head_dim), _lib.ptr(result), _lib.stream_of(st))
+
+
+_TOPK_WS = {}
+
+
+def _topk_ws(dev):
+    """The per-device top-k workspace (zeroed once; the kernels leave their counters at zero)."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device())
+    ws = _TOPK_WS.get(key)
+    if ws is None:
+        ws = torch.zeros(_lib.lib().mdx_topk_workspace(16), dtype=torch.uint8, device=dev)
+        _TOPK_WS[key] = ws
+    return ws
+
+
+def _bf16_row(x):
+    _dev(x, "x")
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous(), "bf16 contiguous")
+    V = x.shape[-1]
+    _check(x.numel() == V and 32768 <= V < 2 ** 31, "one long row")
+    return V
+
+
+def fast_topk(x, k, argmax_order=False):
+    """Reference csrc/fast_topk.sycl:164-170: exact top-k (k <= 8) of one bf16 row in torch XPU order,
+    or its argmax (argmax_order, k = 1). Returns [values bf16 [1, k], indices int64 [1, k]]."""
+    V = _bf16_row(x)
+    _check(1 <= k <= 8, "1 <= k <= 8")
+    values = torch.empty(1, k, dtype=torch.bfloat16, device=x.device)
+    indices = torch.empty(1, k, dtype=torch.int64, device=x.device)
+    ws = _topk_ws(x.device)
+    _lib.call("mdx_fast_topk", _lib.ptr(x), V, int(k), int(bool(argmax_order)), _lib.ptr(values), _lib.ptr(indices),
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    return [values, indices]
+
+
+def fast_pick(x, k):
+    """Reference csrc/fast_topk.sycl:172-175: top-k (topk order) and the argmax of the same row in one
+    launch. Returns [values [1, k], indices [1, k], argmax int64 [1]]."""
+    V = _bf16_row(x)
+    _check(1 <= k <= 8, "1 <= k <= 8")
+    values = torch.empty(1, k, dtype=torch.bfloat16, device=x.device)
+    indices = torch.empty(1, k, dtype=torch.int64, device=x.device)
+    am = torch.empty(1, dtype=torch.int64, device=x.device)
+    ws = _topk_ws(x.device)
+    _lib.call("mdx_fast_pick", _lib.ptr(x), V, int(k), _lib.ptr(values), _lib.ptr(indices), _lib.ptr(am),
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    return [values, indices, am]
+
+
+def topk_rows(x, k):
+    """Reference csrc/topk_rows.sycl:223-246: exact top-k (k <= 64) of 1..16 fp32 or bf16 rows in torch
+    XPU fp32 order. Returns [values f32 [R, k], indices int64 [R, k]]."""
+    _dev(x, "x")
+    _check(x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous() and x.dim() == 2,
+           "x: contiguous fp32 / bf16 [R, N]")
+    R, N = x.shape
+    _check(1 <= R <= 16, "1 <= rows <= 16")
+    _check(1 <= k <= 64 and 4096 <= N < 2 ** 31, "1 <= k <= 64, 4096 <= N")
+    values = torch.empty(R, k, dtype=torch.float32, device=x.device)
+    indices = torch.empty(R, k, dtype=torch.int64, device=x.device)
+    ws = _topk_ws(x.device)
+    _lib.call("mdx_topk_rows", _lib.ptr(x), _lib.DT_F32 if x.dtype == torch.float32 else _lib.DT_BF16, R, N, int(k),
+              _lib.ptr(values), _lib.ptr(indices), _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    return [values, indices]

@@ -56,6 +56,13 @@ SIGNATURES = {
     "mdx_mtp_accept": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                       c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                       c_int64, c_int64, c_void_p, c_void_p]),
+    "mdx_topk_workspace": (c_size_t, [c_int64]),
+    "mdx_fast_topk": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t,
+                                     c_void_p]),
+    "mdx_fast_pick": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                     c_void_p]),
+    "mdx_topk_rows": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                                     c_size_t, c_void_p]),
 }
 
 _lib = None

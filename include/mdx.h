@@ -164,6 +164,34 @@ int mdx_mtp_accept(int64_t* st, const int64_t* toks, const int64_t* vtok, const 
                    int64_t hidden, int64_t* nt, uint16_t* hbuf, int32_t* ctl, const int64_t* kv_ptrs, int64_t nkv,
                    int64_t kv_heads, int64_t kv_cap, int64_t head_dim, int64_t* result, void* stream);
 
+/* Bytes of device workspace the top-k entry points need for `rows` rows. The workspace must be zeroed
+ * once when allocated; every launch leaves its counters at zero again. Launches that share one
+ * workspace must be ordered (one stream). */
+size_t mdx_topk_workspace(int64_t rows);
+
+/* Exact top-k (k <= 8) of one bf16 row in torch's XPU topk order, or (argmax_order, k = 1) its argmax.
+ * Replaces: _C.fast_topk, csrc/fast_topk.sycl:67-170 (bindings.cpp:91-92).
+ *   topk rank: (bf16 radix key: NaN on top, -0 below +0; then earlier gather position of a sweep of
+ *   1024 threads x 4 loads of 8 per 32768 elements); argmax rank: NaN first, -0 == +0, smallest index.
+ * x bf16 [V], 32768 <= V < 2^31 (LDS bounds the practical V to a few million); values bf16 [k] = x[idx],
+ * indices int64 [k], descending rank. */
+int mdx_fast_topk(const uint16_t* x, int64_t V, int64_t k, int32_t argmax_order, uint16_t* values,
+                  int64_t* indices, void* workspace, size_t workspace_bytes, void* stream);
+
+/* fast_topk in topk order plus the argmax of the same row, one launch.
+ * Replaces: _C.fast_pick, csrc/fast_topk.sycl:172-175. argmax: int64 [1]. */
+int mdx_fast_pick(const uint16_t* x, int64_t V, int64_t k, uint16_t* values, int64_t* indices, int64_t* argmax,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Exact top-k (k <= 64) of 1..16 rows in torch's XPU fp32 topk order (bf16 rows: of their fp32 values).
+ * Replaces: _C.topk_rows, csrc/topk_rows.sycl:223-246.
+ *   rank: (fp32 radix key, the sign-flipped bits: +NaN on top, -NaN at the bottom, -0 below +0; then
+ *   earlier gather position of a sweep of 1024 threads x 8 loads of 4 per 32768 elements).
+ * x [rows, n] of x_dtype (MDX_DT_F32 or MDX_DT_BF16), 4096 <= n < 2^31; values f32 [rows, k],
+ * indices int64 [rows, k]. */
+int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
+                  int64_t* indices, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

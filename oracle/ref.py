@@ -425,3 +425,70 @@ def spec_of_widths(widths):
     for width in reversed(widths):
         node = [node] + [[] for _ in range(width - 1)]
     return node
+
+
+# ---------------------------------------------------------------------------------------------
+# exact top-k in torch's XPU order (csrc/fast_topk.sycl, csrc/topk_rows.sycl)
+# ---------------------------------------------------------------------------------------------
+
+
+def gather_pos(i, loads, width):
+    """Position of element i in the gather order of torch XPU's topk sweep: per 32768-element iteration,
+    1024 threads each issue `loads` vector loads of `width` elements; order (iteration, thread, load,
+    lane) (csrc/fast_topk.sycl:4-9: loads 4 x width 8 for bf16; csrc/topk_rows.sycl:7-11: 8 x 4 for fp32)."""
+    i = np.asarray(i, dtype=np.int64)
+    it, off = i >> 15, i & 32767
+    load, thread, lane = off // (1024 * width), (off % (1024 * width)) // width, off % width
+    return (it << 15) + thread * (loads * width) + load * width + lane
+
+
+def key_bf16(b):
+    """bf16 radix key (csrc/fast_topk.sycl:22-26): NaN on top, -0 below +0, larger key first."""
+    b = np.asarray(b, dtype=np.uint16).astype(np.int64)
+    nan = (b & 0x7FFF) > 0x7F80
+    return np.where(nan, 0xFFFF, np.where(b & 0x8000, b ^ 0xFFFF, b | 0x8000))
+
+
+def key_f32(u):
+    """fp32 radix key (csrc/topk_rows.sycl:33): sign-flipped bits, +NaN on top, -NaN at the bottom."""
+    u = np.asarray(u, dtype=np.uint32).astype(np.int64)
+    return np.where(u & 0x80000000, u ^ 0xFFFFFFFF, u | 0x80000000)
+
+
+def key_argmax(b):
+    """argmax rank key (csrc/fast_topk.sycl:31-40): NaN first, -0 == +0."""
+    b = np.asarray(b, dtype=np.uint16).astype(np.int64)
+    nan = (b & 0x7FFF) > 0x7F80
+    b = np.where((b & 0x7FFF) == 0, 0, b)
+    return np.where(nan, 0xFFFFFFFF, np.where(b & 0x8000, 0x7FFF - (b & 0x7FFF), 0x8000 + b))
+
+
+def _topk_by(key, second, k):
+    """Indices of the k best by (key desc, second asc)."""
+    order = np.lexsort((second, -key))
+    return order[:k]
+
+
+def fast_topk(x_bits, k, argmax_order=False):
+    """fast_topk (csrc/fast_topk.sycl:67-170): one bf16 row -> (values bits [k], indices [k])."""
+    x_bits = np.asarray(x_bits, dtype=np.uint16).reshape(-1)
+    i = np.arange(x_bits.size, dtype=np.int64)
+    if argmax_order:
+        idx = _topk_by(key_argmax(x_bits), i, k)
+    else:
+        idx = _topk_by(key_bf16(x_bits), gather_pos(i, 4, 8), k)
+    return x_bits[idx], idx
+
+
+def argmax_bf16(x_bits):
+    return int(fast_topk(x_bits, 1, True)[1][0])
+
+
+def topk_rows(x, k):
+    """topk_rows (csrc/topk_rows.sycl:104-246): fp32 values [R, N] (or bf16 bits as uint16) ->
+    (values f32 [R, k], indices [R, k]) in torch XPU fp32 order."""
+    x = np.asarray(x)
+    u = (x.astype(np.uint32) << 16) if x.dtype == np.uint16 else x.astype(np.float32).view(np.uint32)
+    g = gather_pos(np.arange(u.shape[1], dtype=np.int64), 8, 4)
+    idx = np.stack([_topk_by(key_f32(row), g, k) for row in u])
+    return np.take_along_axis(u, idx, 1).view(np.float32), idx
