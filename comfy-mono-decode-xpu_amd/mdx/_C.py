@@ -325,3 +325,45 @@ def topk_rows(x, k):
     _lib.call("mdx_topk_rows", _lib.ptr(x), _lib.DT_F32 if x.dtype == torch.float32 else _lib.DT_BF16, R, N, int(k),
               _lib.ptr(values), _lib.ptr(indices), _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     return [values, indices]
+
+
+_ATTN_WS = {}
+
+
+def _attn_ws(dev, nbytes):
+    """Per-device attention workspace, grown on demand (zeroed when allocated; launches keep their
+    counters at zero). Growing happens outside graph capture: warm up once per shape before capturing."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _ATTN_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _ATTN_WS[key] = ws
+    return ws
+
+
+def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0):
+    """Reference csrc/attn_dpas.sycl:269-342: decode attention of the tree-verify rows (mask int32 [S])
+    or the draft row (empty mask, S = 1) over the cache prefix [0, seqlen[0]) and the admitted tree rows.
+    q bf16 [1, H, S, D]; key/value bf16 [1, Hk, cap, D]; xk/xv bf16 [1, Hk, S, D]. Returns bf16
+    [1, S, H * D]. chunks_hint is accepted and ignored (the split is planned on the device)."""
+    for t, n in ((q, "q"), (key, "key"), (value, "value"), (xk, "xk"), (xv, "xv")):
+        _dev(t, n)
+        _check(t.dtype == torch.bfloat16 and t.dim() == 4 and t.shape[0] == 1 and t.stride(3) == 1, f"{n}: bf16 [1, ., ., D]")
+    _, H, S, D = q.shape
+    _check(key.is_contiguous() and value.is_contiguous() and key.shape == value.shape and key.shape[3] == D,
+           "cache bf16 [1, Hk, cap, D]")
+    Hk, cap = key.shape[1], key.shape[2]
+    _check(seqlen.dtype == torch.int32 and seqlen.numel() >= 1, "int32 seqlen")
+    _check(mask.dtype == torch.int32 and mask.is_contiguous(), "int32 mask")
+    merge = mask.numel() > 0
+    _check(1 <= S <= 16 and H % Hk == 0 and (mask.numel() == S if merge else S == 1), "batch 1, 1..16 rows")
+    _check(xk.shape == xv.shape and xk.shape[1] == Hk and xk.shape[2] == S and xk.shape[3] == D
+           and xk.stride() == xv.stride(), "xk / xv [1, Hk, S, D]")
+    _check((H // Hk) * S <= 64, "at most 64 query rows per kv head")
+    out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=q.device)
+    need = _lib.lib().mdx_attn_workspace(H, Hk, S, D, cap)
+    ws = _attn_ws(q.device, need)
+    _lib.call("mdx_attn_decode", _lib.ptr(q), q.stride(1), q.stride(2), _lib.ptr(key), _lib.ptr(value), _lib.ptr(seqlen),
+              _lib.ptr(xk), _lib.ptr(xv), xk.stride(1), xk.stride(2), _lib.ptr(mask) if merge else None, _lib.ptr(out),
+              H, Hk, S, D, cap, _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+    return out

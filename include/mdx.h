@@ -192,6 +192,26 @@ int mdx_fast_pick(const uint16_t* x, int64_t V, int64_t k, uint16_t* values, int
 int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
                   int64_t* indices, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of device workspace mdx_attn_decode needs for H query heads, Hk kv heads, S rows, head_dim D
+ * and cache capacity cap. Zero it once when allocated: every launch leaves its counters at zero. */
+size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap);
+
+/* Decode attention of tree-verify rows (mask != NULL) or the MTP draft row (mask == NULL, S == 1).
+ * Replaces: _C.attn_dpas, csrc/attn_dpas.sycl:269-342 (and the attn_core contract, layer.py:406-435).
+ *   For query head h and row s (kv head kh = h / (H / Hk)): softmax over the scores
+ *   q[h, s] . K[kh, t] / sqrt(D) of the cached tokens t in [0, L), L = clamp(seqlen[0], 0, cap), and of
+ *   the tree rows t' with bit t' of mask[s] set (keys xk[kh, t'], values xv[kh, t']); out[s, h] =
+ *   bf16(sum p V / sum p), or 0 if the row admits no token. P is rounded to bf16 for the P.V product;
+ *   partial softmax states merge in fp32 (tolerance parity against a float64 reference).
+ * q bf16 [H, S, D] (head / row strides in elements, rows contiguous); key/value bf16 [Hk, cap, D]
+ * contiguous; xk/xv bf16 [Hk, S, D] (strides as given); mask int32 [S]; out bf16 [S, H, D].
+ * D in {64, 128, 256}; 1 <= S <= 16; (H / Hk) * S <= 64. seqlen is read on the device. */
+int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
+                    const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, const uint16_t* xv,
+                    int64_t x_head_stride, int64_t x_row_stride, const int32_t* mask, uint16_t* out, int64_t H,
+                    int64_t Hk, int64_t S, int64_t D, int64_t cap, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -492,3 +492,39 @@ def topk_rows(x, k):
     g = gather_pos(np.arange(u.shape[1], dtype=np.int64), 8, 4)
     idx = np.stack([_topk_by(key_f32(row), g, k) for row in u])
     return np.take_along_axis(u, idx, 1).view(np.float32), idx
+
+
+# ---------------------------------------------------------------------------------------------
+# tree-verify decode attention (csrc/attn_dpas.sycl; tests/test_attn_dpas.py:11-29)
+# ---------------------------------------------------------------------------------------------
+
+
+def tree_mask(parents):
+    """Row s admits its ancestors and itself (tests/test_attn_dpas.py:11-15)."""
+    m = []
+    for r, p in enumerate(parents):
+        m.append((m[p] if p >= 0 else 0) | (1 << r))
+    return m
+
+
+def attention_f64(q, k, v, L, xk, xv, mask, dtype=np.float64):
+    """Softmax attention of each (head h, row s) over the cache prefix [0, L) and the tree rows its mask
+    admits, in `dtype` (float64: the reference bound; float32: the fp32 chain whose error sets the
+    tolerance). q [H, S, D], k/v [Hk, cap, D], xk/xv [Hk, S, D] as float arrays; mask list or None.
+    Returns [S, H, D] in dtype (unrounded)."""
+    H, S, D = q.shape
+    Hk = k.shape[0]
+    out = np.zeros((S, H, D), dtype=dtype)
+    scale = dtype(1.0) / np.sqrt(dtype(D))
+    for h in range(H):
+        kh = h // (H // Hk)
+        for s in range(S):
+            rows = [t for t in range(S) if mask is not None and (mask[s] >> t) & 1]
+            K = np.concatenate([k[kh, :L], xk[kh, rows]]).astype(dtype)
+            V = np.concatenate([v[kh, :L], xv[kh, rows]]).astype(dtype)
+            if K.shape[0] == 0:
+                continue
+            sc = (K @ q[h, s].astype(dtype)) * scale
+            e = np.exp(sc - sc.max())
+            out[s, h] = (e / e.sum()) @ V
+    return out
