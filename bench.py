@@ -207,6 +207,81 @@ def bench_linear(args, dev):
     }
 
 
+def _ring_count(per_call_bytes):
+    """Copies cycled per replay so the working set exceeds 2x the 256 MB Infinity Cache."""
+    return max(1, -(-2 * 256 * 2 ** 20 // per_call_bytes) + 1) if per_call_bytes < 2 * 256 * 2 ** 20 else 1
+
+
+def _line(args, value, unit, t, steps, dtype, data, config, roofline=None):
+    res = {"metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+           "ms_per_step": round(t * 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": dtype, "data": data, "config": config}
+    if roofline:
+        res["roofline"] = roofline
+    return res
+
+
+def bench_lmhead(args, dev):
+    """bf16 lm_head of the hybrid stack: vocab 151936 x hidden 4096, `rows` decode rows."""
+    import torch
+    from mdx import _C, layout
+    gen = torch.Generator(device=dev).manual_seed(5)
+    V, H, M = 151936, 4096, args.rows
+    per = V * H * 2 + M * H * 2 + M * V * 2
+    w = layout.tile_major_bf16((torch.randn(V, H, generator=gen, device=dev) * 0.02).bfloat16())
+    x = torch.randn(M, H, generator=gen, device=dev).bfloat16()
+    out = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    reps = max(1, args.steps // 10)
+    t = graph_time(lambda: _C.bf16_linear(x, w, tiled=True, out=out), reps, args.warmup)
+    gbs = per / t / 1e9
+    return _line(args, round(gbs, 2), "GB/s", t, reps, "bf16 x bf16 -> fp32 acc, bf16 out",
+                 "synthetic (seeded N(0, 0.02) weights, N(0,1) rows)",
+                 {"workload": f"bf16 lm_head 151936x4096, rows={M}, tile-major", "rows": M,
+                  "algorithmic_bytes_per_step": per},
+                 {"bound": "hbm", "kernel": "bf16_linear_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                  "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                  "avg_launch_us": round(t * 1e6, 3)})
+
+
+def bench_attn(args, dev):
+    """Tree-verify decode attention of the hybrid stack's attention layer: 32 q / 8 kv heads, head_dim
+    128, 16 tree rows, context `--ctx` tokens; KV caches cycled in a ring."""
+    import torch
+    from mdx import _C
+    sys.path.insert(0, ROOT)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    H, Hk, D, S, L = 32, 8, 128, 16, args.ctx
+    cap = L + 64
+    per = 2 * Hk * L * D * 2 + H * S * D * 2 * 2 + 2 * Hk * S * D * 2
+    ring_n = _ring_count(per)
+    caches = [((torch.randn(1, Hk, cap, D, generator=gen, device=dev)).bfloat16(),
+               (torch.randn(1, Hk, cap, D, generator=gen, device=dev)).bfloat16()) for _ in range(ring_n)]
+    q = torch.randn(1, H, S, D, generator=gen, device=dev).bfloat16()
+    xk = torch.randn(1, Hk, S, D, generator=gen, device=dev).bfloat16()
+    xv = torch.randn(1, Hk, S, D, generator=gen, device=dev).bfloat16()
+    parents = [-1, 0, 1, 2, 3, 4, 5, 6, 0, 8, 1, 10, 2, 12, 3, 14]
+    m = []
+    for r, p in enumerate(parents):
+        m.append((m[p] if p >= 0 else 0) | (1 << r))
+    mask = torch.tensor(m, dtype=torch.int32, device=dev)
+    sl = torch.tensor([L], dtype=torch.int32, device=dev)
+
+    def all_ring():
+        for k, v in caches:
+            _C.attn_dpas(q, k, v, sl, xk, xv, mask, 0)
+
+    reps = max(1, args.steps // ring_n)
+    t = graph_time(all_ring, reps, args.warmup) / ring_n
+    gbs = per / t / 1e9
+    return _line(args, round(gbs, 2), "GB/s", t, reps * ring_n, "bf16 x bf16 -> fp32 (MFMA), bf16 out",
+                 "synthetic (seeded N(0,1) KV cache and rows)",
+                 {"workload": f"tree-verify decode attention, 32q/8kv heads, head_dim 128, 16 rows, ctx={L}, "
+                              f"{ring_n}-copy KV ring", "ctx": L, "rows": S, "algorithmic_bytes_per_step": per},
+                 {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                  "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                  "avg_launch_us": round(t * 1e6, 3)})
+
+
 def bench_copy(args, dev):
     """Calibration workload: a plain device copy of 256 MiB (read 256 MiB, write 256 MiB). Its
     FETCH_SIZE / WRITE_SIZE counters give the scale factor of the traffic figures."""
@@ -228,7 +303,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1)
-    ap.add_argument("--workload", choices=["mlp", "linear", "copy"], default="mlp")
+    ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn"], default="mlp")
+    ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,7 +316,8 @@ def main():
         print(json.dumps({"error": "no ROCm device"}))
         sys.exit(1)
     dev = torch.device("cuda", 0)
-    res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy}[args.workload](args, dev)
+    res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
+           "attn": bench_attn}[args.workload](args, dev)
     print(json.dumps(res), flush=True)
 
 

@@ -1,5 +1,5 @@
 // Tree-verify / draft decode attention over a bf16 KV cache, split along the context (flash decoding)
-// with bf16 MFMA on gfx950, and the chunk merge in the same launch.
+// with bf16 MFMA on gfx950, then a wide merge of the chunk partials.
 //
 // Reference semantics (comfy-mono-decode-xpu): csrc/attn_dpas.sycl:269-342 (contract: rows of one kv
 // head attend the committed prefix [0, L) of the cache and, for tree verify, the tree rows their mask
@@ -16,10 +16,11 @@
 //   O^T += V^T P^T   A = V^T from LDS (the wave transposes its 32 x D V tile into [dim][token] order,
 //                 tokens permuted so a lane's 8 k-slots are the 8 tokens its S^T accumulators hold),
 //                 B = bf16(P^T) straight from the S^T registers -- no shuffle of P.
-// The 4 waves merge in LDS; the work-group's partial (m, l, O) goes to the workspace; the last
-// work-group of a (kv head, row tile) (device-scope counter, reset by it) merges the chunks and writes
-// the bf16 rows. Every work-group increments the counter, also those whose chunk is empty for the
-// current context length (read from device memory, so a captured graph replays for any length).
+// Each wave prefetches its next step's K and V into a second register set while the current step
+// computes (head_dim <= 128). The 4 waves merge in LDS; the work-group's partial (m, l, O) goes to
+// the workspace; attn_merge_kernel (one work-group per query row, one thread per dim) combines the
+// chunks and the tree-row partial and writes bf16. The context split is recomputed on the device
+// from seqlen in both kernels, so a captured graph replays for any context length.
 // Work-group ids are laid out so the row tiles of one (kv head, chunk) share an XCD (ids are dealt
 // round-robin over the 8 XCDs): the 4x re-read of a K/V chunk hits that XCD's L2.
 #include <math.h>
@@ -36,7 +37,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int AT_WAVES = 4;
 constexpr int AT_STEP = 32;        // tokens per MFMA step
 constexpr int AT_VT_ROW = 72;      // bytes per [dim] row of the transposed V tile (64 + 8: conflict-free writes)
-constexpr int AT_MIN_TPW = 128;    // at least this many tokens per wave per chunk
+constexpr int AT_MIN_TPW = 128;    // default: at least this many tokens per wave per chunk
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -51,8 +52,8 @@ struct AttnArgs {
     const int32_t* mask;     // [S] or null (draft row)
     uint16_t* out;           // [S, H, D]
     float* part;             // [Hk][RT][C + 1][2 * 16 + 16 * D]
-    unsigned* counter;       // [Hk * RT]
     int H, Hk, S, cap, groups, rows, RT, C;
+    int min_tpw;             // a chunk gives each wave at least this many tokens
     float zscale;            // 1/sqrt(D) * log2(e)
 };
 
@@ -68,23 +69,22 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
 // {4g..4g+3} (first S^T tile) and {16+4g..16+4g+3} (second tile), stored contiguously at 8g
 __device__ __forceinline__ int vt_col(int t) { return t < 16 ? 8 * (t >> 2) + (t & 3) : 8 * ((t - 16) >> 2) + 4 + (t & 3); }
 
-// per-device context split: chunks of at least AT_MIN_TPW tokens per wave
-__device__ __forceinline__ void split(int L, int C, int& tpw, int& active) {
-    int c = (L + AT_WAVES * AT_MIN_TPW - 1) / (AT_WAVES * AT_MIN_TPW);
+// per-device context split: at most C chunks of at least min_tpw tokens per wave
+__device__ __forceinline__ void split(int L, int C, int min_tpw, int& tpw, int& active) {
+    int c = (L + AT_WAVES * min_tpw - 1) / (AT_WAVES * min_tpw);
     c = c < 1 ? 1 : (c > C ? C : c);
     tpw = (L + AT_WAVES * c - 1) / (AT_WAVES * c);
     tpw = (tpw + AT_STEP - 1) / AT_STEP * AT_STEP;
     active = L > 0 ? (L + AT_WAVES * tpw - 1) / (AT_WAVES * tpw) : 0;
 }
 
-template <int D>
+template <int D, bool PINGPONG>
 __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
     constexpr int KK = D / 32;   // MFMA k-steps over the head dim
     constexpr int DT = D / 16;   // 16-dim output tiles
     constexpr int NV = D / 16;   // 16-byte V loads per lane per step
     constexpr int WREG = 72 * D; // LDS bytes per wave: the transposed V tile, later the wave's (m, l, O)
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int last_s;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
     const int units = a.Hk * (a.C + 1);
     const int bid = blockIdx.x;
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
     int L = a.seqlen[0];
     L = L < 0 ? 0 : (L > a.cap ? a.cap : L);
     int tpw, active;
-    split(L, a.C, tpw, active);
+    split(L, a.C, a.min_tpw, tpw, active);
 
     // this lane's query row: the column of S^T and O^T it holds
     const int r = rt * 16 + c16;
@@ -137,21 +137,8 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
     float m = -INFINITY, l = 0.f;
     unsigned char* vt = smem + w * WREG;
 
-    for (int t0 = t_begin; t0 < t_end; t0 += AT_STEP) {
-        // K rows (A of S^T) and this lane's V pieces, clamped into the wave's range
-        u32x4 kf[2][KK], vr[NV];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int tok = min(t0 + 16 * tt + c16, t_end - 1);
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) kf[tt][kk] = ld16(kb + tok * kstride + 32 * kk + 8 * g);
-        }
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int tok = min(t0 + 2 * c16 + (j & 1), t_end - 1);
-            vr[j] = ld16(vb + tok * vstride + 8 * (4 * (j >> 1) + g));
-        }
-        // S^T: lane holds tokens t0 + 16 tt + 4 g + i of query row c16
+    // one 32-token step: S^T, online softmax, V^T through LDS, O^T
+    auto step = [&](int t0, const u32x4 (&kf)[2][KK], const u32x4 (&vr)[NV]) {
         f32x4 st[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -216,6 +203,40 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // K rows (A of S^T) and this lane's V pieces of the step at t0, clamped into the wave's range
+    // (loads past the range repeat its last token, so every load is unconditional)
+    auto load = [&](int t0, u32x4 (&kf)[2][KK], u32x4 (&vr)[NV]) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int tok = max(min(t0 + 16 * tt + c16, t_end - 1), 0);
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) kf[tt][kk] = ld16(kb + tok * kstride + 32 * kk + 8 * g);
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int tok = max(min(t0 + 2 * c16 + (j & 1), t_end - 1), 0);
+            vr[j] = ld16(vb + tok * vstride + 8 * (4 * (j >> 1) + g));
+        }
+    };
+    if (t_begin < t_end) {
+        u32x4 kA[2][KK], vA[NV];
+        load(t_begin, kA, vA);
+        if (PINGPONG) {
+            // two register sets: the next step's loads are in flight while this step computes
+            u32x4 kB[2][KK], vB[NV];
+            for (int t0 = t_begin; t0 < t_end; t0 += 2 * AT_STEP) {
+                load(t0 + AT_STEP, kB, vB);
+                step(t0, kA, vA);
+                load(t0 + 2 * AT_STEP, kA, vA);
+                if (t0 + AT_STEP < t_end) step(t0 + AT_STEP, kB, vB);
+            }
+        } else {
+            for (int t0 = t_begin; t0 < t_end; t0 += AT_STEP) {
+                if (t0 > t_begin) load(t0, kA, vA);
+                step(t0, kA, vA);
+            }
+        }
     }
 
     // merge the 4 waves in LDS: per wave m[16], l[16], O[16][D]
@@ -252,46 +273,55 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
             }
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last_s = __hip_atomic_fetch_add(a.counter + kh * a.RT + rt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-                 unsigned(a.C);
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-    // the last work-group of (kv head, row tile): merge the chunks and the tree partial, write bf16 rows
-    const float* base = a.part + int64_t(kh * a.RT + rt) * (a.C + 1) * (32 + 16 * D);
-    const bool use_tree = a.mask != nullptr;
-    for (int e = threadIdx.x; e < 16 * D; e += 64 * AT_WAVES) {
-        const int row = e / D, d = e % D;
-        const int rr2 = rt * 16 + row;
-        if (rr2 >= a.rows) continue;
-        float M = -INFINITY;
-        for (int c = 0; c <= a.C; ++c) {
-            if (c < a.C ? c >= active : !use_tree) continue;
-            M = fmaxf(M, base[c * (32 + 16 * D) + row]);
-        }
-        float o = 0.f, s = 0.f;
-        for (int c = 0; c <= a.C; ++c) {
-            if (c < a.C ? c >= active : !use_tree) continue;
-            const float* rc = base + c * (32 + 16 * D);
-            const float mc = rc[row];
-            const float f = mc == -INFINITY ? 0.f : exp2f(mc - M);
-            o += rc[32 + e] * f;
-            s += rc[16 + row] * f;
-        }
-        const int h = kh * a.groups + rr2 / a.S, sr = rr2 % a.S;
-        a.out[(int64_t(sr) * a.H + h) * D + d] = f2bf(s > 0.f ? __fdiv_rn(o, s) : 0.f);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(a.counter + kh * a.RT + rt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-int plan_chunks(int Hk, int RT, int cap) {
+// Merge of the chunk partials and the tree partial: one work-group per (kv head, row tile, row), one
+// thread per output dim; the partials' weights are computed once in LDS, the O loads are independent.
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float wgt[72], lsum[72];
+    __shared__ float Ms;
+    const int row = blockIdx.x % 16, rt = (blockIdx.x / 16) % a.RT, kh = blockIdx.x / (16 * a.RT);
+    const int r = rt * 16 + row;
+    if (r >= a.rows) return;
+    int L = a.seqlen[0];
+    L = L < 0 ? 0 : (L > a.cap ? a.cap : L);
+    int tpw, active;
+    split(L, a.C, a.min_tpw, tpw, active);
+    const bool use_tree = a.mask != nullptr;
+    const int np = active + (use_tree ? 1 : 0);
+    const float* base = a.part + int64_t(kh * a.RT + rt) * (a.C + 1) * (32 + 16 * D);
+    auto slot = [&](int i) { return i < active ? i : a.C; };
+    const int t = threadIdx.x;
+    for (int i = t; i < np; i += D) {
+        wgt[i] = base[slot(i) * (32 + 16 * D) + row];
+        lsum[i] = base[slot(i) * (32 + 16 * D) + 16 + row];
+    }
+    __syncthreads();
+    if (t == 0) {
+        float M = -INFINITY;
+        for (int i = 0; i < np; ++i) M = fmaxf(M, wgt[i]);
+        Ms = M;
+    }
+    __syncthreads();
+    for (int i = t; i < np; i += D) wgt[i] = wgt[i] == -INFINITY ? 0.f : exp2f(wgt[i] - Ms);
+    __syncthreads();
+    float o = 0.f, s = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < np; ++i) {
+        o += base[slot(i) * (32 + 16 * D) + 32 + row * D + t] * wgt[i];
+        s += lsum[i] * wgt[i];
+    }
+    const int h = kh * a.groups + r / a.S, sr = r % a.S;
+    a.out[(int64_t(sr) * a.H + h) * D + t] = f2bf(s > 0.f ? __fdiv_rn(o, s) : 0.f);
+}
+
+int plan_chunks(int Hk, int RT, int cap, int hint) {
+    if (hint > 0) return hint > 64 ? 64 : hint;
     int c = (512 + Hk * RT - 1) / (Hk * RT);
     const int by_cap = (cap + AT_WAVES * AT_MIN_TPW - 1) / (AT_WAVES * AT_MIN_TPW);
     c = c > by_cap ? by_cap : c;
-    return c < 1 ? 1 : (c > 64 ? 64 : c);
+    return c < 1 ? 1 : (c > 64 ? 64 : c);  // the merge holds at most 64 + 1 partial weights
 }
 
 size_t workspace_bytes(int Hk, int RT, int C, int D) {
@@ -300,11 +330,14 @@ size_t workspace_bytes(int Hk, int RT, int C, int D) {
 
 template <int D>
 int launch(const AttnArgs& a, hipStream_t st) {
+    constexpr bool PP = D <= 128;  // register ping-pong fits below 256 VGPRs up to head_dim 128
     const int units = a.Hk * (a.C + 1);
     const int grid = (units + 7) / 8 * 8 * a.RT;
     const size_t lds = size_t(AT_WAVES) * 72 * D;
-    allow_smem(reinterpret_cast<const void*>(&attn_kernel<D>), lds);
-    hipLaunchKernelGGL(attn_kernel<D>, dim3(grid), dim3(64 * AT_WAVES), lds, st, a);
+    allow_smem(reinterpret_cast<const void*>(&attn_kernel<D, PP>), lds);
+    hipLaunchKernelGGL((attn_kernel<D, PP>), dim3(grid), dim3(64 * AT_WAVES), lds, st, a);
+    MDX_LAUNCHED();
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.Hk * a.RT * 16), dim3(D), 0, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
@@ -314,17 +347,17 @@ int launch(const AttnArgs& a, hipStream_t st) {
 
 using namespace mdx;
 
-extern "C" size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap) {
+extern "C" size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint) {
     if (Hk <= 0 || H % Hk != 0 || S <= 0) return 0;
     const int RT = int((H / Hk * S + 15) / 16);
-    return workspace_bytes(int(Hk), RT, plan_chunks(int(Hk), RT, int(cap)), int(D));
+    return workspace_bytes(int(Hk), RT, plan_chunks(int(Hk), RT, int(cap), int(chunks_hint)), int(D));
 }
 
 extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
                                const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, const uint16_t* xv,
                                int64_t x_head_stride, int64_t x_row_stride, const int32_t* mask, uint16_t* out,
-                               int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, void* workspace,
-                               size_t workspace_bytes_, void* stream) {
+                               int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint,
+                               void* workspace, size_t workspace_bytes_, void* stream) {
     MDX_CHECK(q && key && value && seqlen && xk && xv && out, "null pointer");
     MDX_CHECK(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
     MDX_CHECK(Hk >= 1 && H % Hk == 0 && S >= 1 && S <= 16, "heads / 1..16 rows");
@@ -335,7 +368,7 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
                   q_head_stride % 8 == 0 && q_row_stride % 8 == 0 && x_head_stride % 8 == 0 && x_row_stride % 8 == 0,
               "16-byte aligned rows");
     const int RT = int((H / Hk * S + 15) / 16);
-    const int C = plan_chunks(int(Hk), RT, int(cap));
+    const int C = plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
     MDX_CHECK(workspace && aligned(workspace, 256) && workspace_bytes_ >= workspace_bytes(int(Hk), RT, C, int(D)),
               "workspace: %zu bytes, 256-byte aligned, zeroed once", workspace_bytes(int(Hk), RT, C, int(D)));
     AttnArgs a{};
@@ -351,7 +384,6 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.xs = a.vs = x_row_stride;
     a.mask = mask;
     a.out = out;
-    a.counter = static_cast<unsigned*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
     a.H = int(H);
     a.Hk = int(Hk);
@@ -361,8 +393,8 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.rows = int(H / Hk * S);
     a.RT = RT;
     a.C = C;
+    a.min_tpw = chunks_hint > 0 ? AT_STEP : AT_MIN_TPW;
     a.zscale = float(1.0 / sqrt(double(D)) * 1.4426950408889634);
-    MDX_CHECK(Hk * RT <= 64, "counter table");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (D == 64) return launch<64>(a, st);
     if (D == 128) return launch<128>(a, st);

@@ -1,0 +1,128 @@
+// bf16 decode linear for 1..16 rows: out[m, n] = bf16(sum_k x[m, k] * W[n, k]) with fp32 accumulation,
+// optional bf16 residual (out = bf16(float(res) + float(bf16(acc)))). Serves the lm_head and the bf16
+// projections of the MTP draft block.
+//
+// Reference: the lm_head is a library F.linear in the reference's loop (comfy_mono_decode_xpu/
+// mtp_loop.py:221-225; draft_head.py:214-232 for the draft's head and block GEMMs); tolerance parity
+// against float64 (bf16 outputs within 1e-2 relative).
+//
+// Every product is one v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k (one 16-byte load per
+// lane: 1 KiB of the tile-major weight stream per wave instruction), B = the activation rows as
+// columns (rows >= `rows` are zero), D = 16 outputs x 16 rows. A wave owns a 16-row tile of W and a
+// K slice; slices of one tile (split-K when there are few tiles) add up in LDS in slice order.
+// Weights stream through a register ring of RING loads per lane with clamped addresses (no branches
+// in the loop, static wait counts).
+//
+// Tile-major weights: [N/16][K/32][64 lanes][8 bf16], lane 16 g + c holding row 16 t + c, k in
+// [32 j + 8 g, 32 j + 8 g + 8) of block (t, j). Row-major [N, K] weights are read in place.
+#include <algorithm>
+
+#include "mdx_common.hpp"
+
+namespace mdx {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BF_RING = 8;
+
+struct Bf16Args {
+    const uint16_t* x;     // [rows, K]
+    const uint16_t* w;
+    const uint16_t* res;   // [rows, N] or null
+    uint16_t* out;         // [rows, N]
+    int N, K, rows, KS, TPW, tiles, layout;
+};
+
+__device__ __forceinline__ u32x4 ldnt(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+template <int RING>
+__global__ __launch_bounds__(1024) void bf16_linear_kernel(Bf16Args a) {
+    extern __shared__ __align__(16) float red[];  // [TPW][KS][64][4]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ts = wave / a.KS, slice = wave % a.KS;
+    const int tile = blockIdx.x * a.TPW + ts;
+    const bool live = tile < a.tiles;
+    const int NC = a.K / 32;
+    const int c0 = live ? slice * NC / a.KS : 0, c1 = live ? (slice + 1) * NC / a.KS : 0;
+    const int nch = c1 - c0, last = nch > 0 ? nch - 1 : 0;
+    const int g = lane >> 4, c = lane & 15;
+    const uint16_t* wp;
+    int wstride;
+    if (a.layout == MDX_LAYOUT_TILE) {
+        wp = a.w + (int64_t(live ? tile : 0) * NC + c0) * 512 + lane * 8;
+        wstride = 512;
+    } else {
+        wp = a.w + int64_t((live ? tile : 0) * 16 + c) * a.K + c0 * 32 + 8 * g;
+        wstride = 32;
+    }
+    u32x4 ring[RING];
+#pragma unroll
+    for (int p = 0; p < RING; ++p) ring[p] = ldnt(wp + min(p, last) * wstride);
+    const bool xlive = c < a.rows;
+    const uint16_t* xp = a.x + (xlive ? c : 0) * a.K + c0 * 32 + 8 * g;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < nch; i0 += RING) {
+#pragma unroll
+        for (int p = 0; p < RING; ++p) {
+            const int i = i0 + p;
+            if (i < nch) {
+                const u32x4 wv = ring[p];
+                ring[p] = ldnt(wp + min(i + RING, last) * wstride);
+                u32x4 xv = *reinterpret_cast<const u32x4*>(xp + i * 32);
+                if (!xlive) xv = u32x4{0u, 0u, 0u, 0u};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv),
+                                                              __builtin_bit_cast(bf16x8, xv), acc, 0, 0, 0);
+            }
+        }
+    }
+    // D: lane holds outputs n = 16 tile + 4 g + i of row c
+    *reinterpret_cast<f32x4*>(red + ((ts * a.KS + slice) * 64 + lane) * 4) = acc;
+    __syncthreads();
+    if (slice != 0 || !live || c >= a.rows) return;
+    f32x4 s = acc;
+    for (int k = 1; k < a.KS; ++k) s += *reinterpret_cast<const f32x4*>(red + ((ts * a.KS + k) * 64 + lane) * 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t o = int64_t(c) * a.N + tile * 16 + 4 * g + i;
+        uint16_t v = f2bf(s[i]);
+        if (a.res) v = f2bf(__fadd_rn(bf2f(a.res[o]), bf2f(v)));
+        a.out[o] = v;
+    }
+}
+
+}  // namespace
+}  // namespace mdx
+
+using namespace mdx;
+
+extern "C" int mdx_bf16_linear(const uint16_t* x, const uint16_t* w, int32_t layout, const uint16_t* residual,
+                               uint16_t* out, int64_t rows, int64_t N, int64_t K, void* stream) {
+    MDX_CHECK(x && w && out, "null pointer");
+    MDX_CHECK(rows >= 1 && rows <= 16, "1 <= rows <= 16");
+    MDX_CHECK(N >= 16 && N % 16 == 0 && K >= 32 && K % 32 == 0 && N < (int64_t(1) << 31) && K <= 65536,
+              "N % 16 == 0, K % 32 == 0");
+    MDX_CHECK(layout == MDX_LAYOUT_ROW || layout == MDX_LAYOUT_TILE, "layout");
+    MDX_CHECK(aligned(x, 16) && aligned(w, 16), "16-byte aligned x / w");
+    const int tiles = int(N / 16), NC = int(K / 32);
+    // split K until about 12 waves per CU are in flight (slices must divide the chunk count)
+    int KS = 1;
+    for (int d = 1; d <= 16; ++d)
+        if (NC % d == 0) {
+            KS = d;
+            if (int64_t(tiles) * d >= 3072) break;
+        }
+    const int TPW = std::max(1, 4 / KS);
+    Bf16Args a{x, w, residual, out, int(N), int(K), int(rows), KS, TPW, tiles, layout};
+    const int wgs = (tiles + TPW - 1) / TPW;
+    const size_t lds = size_t(TPW) * KS * 64 * 4 * sizeof(float);
+    allow_smem(reinterpret_cast<const void*>(&bf16_linear_kernel<BF_RING>), lds);
+    hipLaunchKernelGGL(bf16_linear_kernel<BF_RING>, dim3(wgs), dim3(64 * TPW * KS), lds,
+                       static_cast<hipStream_t>(stream), a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}

@@ -345,7 +345,7 @@ def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0):
     """Reference csrc/attn_dpas.sycl:269-342: decode attention of the tree-verify rows (mask int32 [S])
     or the draft row (empty mask, S = 1) over the cache prefix [0, seqlen[0]) and the admitted tree rows.
     q bf16 [1, H, S, D]; key/value bf16 [1, Hk, cap, D]; xk/xv bf16 [1, Hk, S, D]. Returns bf16
-    [1, S, H * D]. chunks_hint is accepted and ignored (the split is planned on the device)."""
+    [1, S, H * D]. chunks_hint: 0 plans the context split; n > 0 caps it at n chunks per kv head."""
     for t, n in ((q, "q"), (key, "key"), (value, "value"), (xk, "xk"), (xv, "xv")):
         _dev(t, n)
         _check(t.dtype == torch.bfloat16 and t.dim() == 4 and t.shape[0] == 1 and t.stride(3) == 1, f"{n}: bf16 [1, ., ., D]")
@@ -361,9 +361,29 @@ def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0):
            and xk.stride() == xv.stride(), "xk / xv [1, Hk, S, D]")
     _check((H // Hk) * S <= 64, "at most 64 query rows per kv head")
     out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=q.device)
-    need = _lib.lib().mdx_attn_workspace(H, Hk, S, D, cap)
+    need = _lib.lib().mdx_attn_workspace(H, Hk, S, D, cap, int(chunks_hint))
     ws = _attn_ws(q.device, need)
     _lib.call("mdx_attn_decode", _lib.ptr(q), q.stride(1), q.stride(2), _lib.ptr(key), _lib.ptr(value), _lib.ptr(seqlen),
               _lib.ptr(xk), _lib.ptr(xv), xk.stride(1), xk.stride(2), _lib.ptr(mask) if merge else None, _lib.ptr(out),
-              H, Hk, S, D, cap, _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+              H, Hk, S, D, cap, int(chunks_hint), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
+    return out
+
+
+def bf16_linear(x, w, tiled=True, residual=None, out=None):
+    """bf16 decode linear (lm_head / draft block GEMMs; the reference's F.linear at
+    comfy_mono_decode_xpu/mtp_loop.py:221-225): bf16(x . W^T) with fp32 accumulation, 1..16 rows.
+    w: [N, K] bf16, tile-major (layout.tile_major_bf16) when tiled, else row-major."""
+    _dev(x, "x")
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2, "x: contiguous bf16 [rows, K]")
+    _check(w.dtype == torch.bfloat16 and w.is_contiguous() and w.dim() == 2 and w.shape[1] == x.shape[1],
+           "w: contiguous bf16 [N, K]")
+    rows, N = x.shape[0], w.shape[0]
+    if out is None:
+        out = torch.empty(rows, N, dtype=torch.bfloat16, device=x.device)
+    _check(out.dtype == torch.bfloat16 and out.is_contiguous() and out.shape == (rows, N), "out bf16 [rows, N]")
+    if residual is not None:
+        _check(residual.dtype == torch.bfloat16 and residual.is_contiguous() and residual.shape == (rows, N),
+               "residual bf16 [rows, N]")
+    _lib.call("mdx_bf16_linear", _lib.ptr(x), _lib.ptr(w), _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW,
+              _lib.ptr(residual), _lib.ptr(out), rows, N, x.shape[1], _lib.stream_of(x))
     return out

@@ -63,10 +63,12 @@ SIGNATURES = {
                                      c_void_p]),
     "mdx_topk_rows": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_size_t, c_void_p]),
-    "mdx_attn_workspace": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "mdx_attn_workspace": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mdx_attn_decode": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-                                       c_int64, c_void_p, c_size_t, c_void_p]),
+                                       c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
+    "mdx_bf16_linear": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+                                       c_void_p]),
 }
 
 _lib = None

@@ -179,3 +179,11 @@ def silu_lut(device=None) -> torch.Tensor:
 
 def sigmoid_lut(device=None) -> torch.Tensor:
     return torch.sigmoid(bf16_all(device)).contiguous()
+
+
+def tile_major_bf16(w: torch.Tensor) -> torch.Tensor:
+    """bf16 [N, K] -> the bf16 linear's tile-major order [N/16][K/32][64 lanes][8] (lane 16 g + c holds
+    row 16 t + c, k in [32 j + 8 g, 32 j + 8 g + 8) of block (t, j)), returned as [N, K]."""
+    N, K = w.shape
+    assert N % 16 == 0 and K % 32 == 0
+    return w.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous().reshape(N, K)

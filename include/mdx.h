@@ -194,7 +194,7 @@ int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64
 
 /* Bytes of device workspace mdx_attn_decode needs for H query heads, Hk kv heads, S rows, head_dim D
  * and cache capacity cap. Zero it once when allocated: every launch leaves its counters at zero. */
-size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap);
+size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint);
 
 /* Decode attention of tree-verify rows (mask != NULL) or the MTP draft row (mask == NULL, S == 1).
  * Replaces: _C.attn_dpas, csrc/attn_dpas.sycl:269-342 (and the attn_core contract, layer.py:406-435).
@@ -205,12 +205,25 @@ size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t c
  *   partial softmax states merge in fp32 (tolerance parity against a float64 reference).
  * q bf16 [H, S, D] (head / row strides in elements, rows contiguous); key/value bf16 [Hk, cap, D]
  * contiguous; xk/xv bf16 [Hk, S, D] (strides as given); mask int32 [S]; out bf16 [S, H, D].
- * D in {64, 128, 256}; 1 <= S <= 16; (H / Hk) * S <= 64. seqlen is read on the device. */
+ * D in {64, 128, 256}; 1 <= S <= 16; (H / Hk) * S <= 64. seqlen is read on the device.
+ * chunks_hint: 0 plans the context split (chunks of >= 128 tokens per wave); n > 0 splits the context
+ * into at most n chunks per kv head of >= 32 tokens per wave (as the reference's chunks_hint steers
+ * its split). */
 int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
                     const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, const uint16_t* xv,
                     int64_t x_head_stride, int64_t x_row_stride, const int32_t* mask, uint16_t* out, int64_t H,
-                    int64_t Hk, int64_t S, int64_t D, int64_t cap, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* bf16 decode linear for 1..16 rows: out = bf16(x . W^T) with fp32 accumulation (MFMA), optional
+ * bf16 residual (out = bf16(float(residual) + float(bf16(acc)))).
+ * Replaces: the lm_head F.linear of the device loop (comfy_mono_decode_xpu/mtp_loop.py:221-225) and the
+ * bf16 GEMMs of the MTP draft block (comfy_mono_decode_xpu/draft_head.py:179-232).
+ * x bf16 [rows, K] contiguous; W bf16 [N, K] row-major (MDX_LAYOUT_ROW) or tile-major (MDX_LAYOUT_TILE:
+ * [N/16][K/32][64][8], lane 16 g + c holding row 16 t + c, k in [32 j + 8 g, + 8) of block (t, j));
+ * out / residual bf16 [rows, N]. N % 16 == 0, K % 32 == 0. */
+int mdx_bf16_linear(const uint16_t* x, const uint16_t* w, int32_t layout, const uint16_t* residual, uint16_t* out,
+                    int64_t rows, int64_t N, int64_t K, void* stream);
 
 #ifdef __cplusplus
 }

@@ -528,3 +528,16 @@ def attention_f64(q, k, v, L, xk, xv, mask, dtype=np.float64):
             e = np.exp(sc - sc.max())
             out[s, h] = (e / e.sum()) @ V
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# bf16 linear (lm_head; comfy_mono_decode_xpu/mtp_loop.py:221-225)
+# ---------------------------------------------------------------------------------------------
+
+
+def bf16_linear_f64(x_bits, w_bits):
+    """x . W^T in float64 of bf16 inputs (the tolerance reference), and sum |x| . |W|^T (the scale of
+    the fp32 accumulation error)."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    w = bf16_to_f32(w_bits).astype(np.float64)
+    return x @ w.T, np.abs(x) @ np.abs(w).T

@@ -1,0 +1,62 @@
+"""bf16 decode linear (lm_head and draft-block GEMMs) on the GPU against float64: bf16 outputs within
+2^-8 relative plus the fp32 accumulation bound (2^-16 x sum |x||w|); the tile-major and row-major
+layouts give identical bits (same products, same order)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bits_equal, bits
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, x, w, cols=None, res=None):
+    xb, wb = bits(x), bits(w)
+    if cols is not None:
+        wb = wb[cols]
+        got = got[:, cols]
+    want, scale = ref.bf16_linear_f64(xb, wb)
+    acc = np.abs(want)
+    if res is not None:  # out = bf16(res + bf16(acc)): the product's own rounding adds 2^-9 |acc|
+        r = ref.bf16_to_f32(bits(res)).astype(np.float64)
+        want = want + (r if cols is None else r[:, cols])
+    g = got.float().cpu().numpy().astype(np.float64)
+    err = np.abs(g - want)
+    bound = np.abs(want) * 2 ** -8 + (acc * 2 ** -8 if res is not None else 0) + scale * 2 ** -16 + 1e-30
+    assert (err <= bound).all(), (err / bound).max()
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (12288, 4096), (4096, 12288), (1024, 8192), (48, 64)])
+@pytest.mark.parametrize("rows", [1, 3, 8, 16])
+def test_bf16_linear_matches_f64(C, dev, N, K, rows):
+    from mdx import layout
+    g = torch.Generator().manual_seed(N + K + rows)
+    x = torch.randn(rows, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    xd, wd = x.to(dev), w.to(dev)
+    out_t = C.bf16_linear(xd, layout.tile_major_bf16(wd), tiled=True)
+    out_r = C.bf16_linear(xd, wd, tiled=False)
+    assert_bits_equal(bits(out_t), bits(out_r), "tile vs row layout")
+    _check(out_t.cpu(), x, w)
+    res = torch.randn(rows, N, generator=g).bfloat16()
+    out_res = C.bf16_linear(xd, wd, tiled=False, residual=res.to(dev))
+    _check(out_res.cpu(), x, w, res=res)
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_lm_head_151936(C, dev, rows):
+    """The bf16 lm_head of the hybrid stack (vocab 151936, hidden 4096), checked on 4096 sampled
+    vocabulary rows, plus the top-20 of the logits against the oracle's exact rank order."""
+    from mdx import layout
+    g = torch.Generator(device=dev).manual_seed(5)
+    V, H = 151936, 4096
+    w = (torch.randn(V, H, generator=g, device=dev) * 0.02).bfloat16()
+    x = torch.randn(rows, H, generator=g, device=dev).bfloat16()
+    wt = layout.tile_major_bf16(w)
+    logits = C.bf16_linear(x, wt, tiled=True)
+    cols = np.random.default_rng(0).choice(V, 4096, replace=False)
+    _check(logits.cpu(), x.cpu(), w.cpu(), cols=cols)
+    v, i = C.topk_rows(logits, 20)
+    wv, wi = ref.topk_rows(bits(logits), 20)
+    assert np.array_equal(i.cpu().numpy(), wi)
