@@ -1,0 +1,314 @@
+// Gated-DeltaNet decode core with deferred replay, for 1..16 tree-verify rows: the causal conv over
+// tree ancestors, the gates, the q/k sums of squares, the delta-rule state update (replay of the
+// previous step's accepted rows, then this step's verify program) and the gated RMSNorm.
+//
+// Reference semantics (comfy-mono-decode-xpu): csrc/mono_gdn.sycl:313-374 (conv), :424-450 (gates),
+// :459-479 (sums), :398-571 (entries: replay of ctl's accepted slots from the previous parity, always
+// committed; verify entries prog & 15 = slot, prog & 32 = commit; the persistent state keeps the replay
+// only), :574-607 (gated RMSNorm). Tolerance parity against a float64 restatement (the reference's
+// own arithmetic is Kitchen's fast-math build, not portable); the control walk (entry list, slots,
+// ancestry, the buffers of the next step) is exact.
+//
+// Buffers (per layer): conv_state bf16 [C, 3]; pb, qb bf16 [2 parities][slots][C] (projections and
+// conv outputs of each step, kept for the next step's replay); rec f32 [HV][128][128] (row-major
+// [head][k row][v col]); gates f32 [2][slots][HV][2] (decay, beta); sums f32 [2][slots][HK][2]
+// (q, k sum of squares); ctl int32 [2 + 3 slots] = pending, parity, accepted slots, parents, program.
+// Channels of proj / qb: q [0, KD), k [KD, 2 KD), v [2 KD, 2 KD + HV 128), KD = HK 128.
+//
+// Launches: gdn_conv_kernel (one thread per channel: owns its conv history), then gdn_head_kernel (one
+// work-group of 512 per value head: thread (row group rg, column col) holds state rows
+// 32 rg .. 32 rg + 31 of column col in registers).
+#include <math.h>
+
+#include "mdx_common.hpp"
+
+namespace mdx {
+namespace {
+
+constexpr int DH = 128, CW = 3, RG = 4, RPG = DH / RG, GT = RG * DH;
+constexpr int MAXS = 16;
+
+struct GdnArgs {
+    const uint16_t* proj;   // [R, C]
+    const uint16_t* z;      // [R, HV * 128]
+    const uint16_t* ab;     // [R, 2 HV]: a then b
+    const uint16_t* conv_w; // [C, 4]
+    uint16_t* conv_state;   // [C, 3]
+    uint16_t* pb;           // [2][slots][C]
+    uint16_t* qb;           // [2][slots][C]
+    const int32_t* ctl;
+    const float* dt_bias;   // [HV]
+    const float* g_decay;   // [HV]
+    float* rec;             // [HV][128][128]
+    float* gates;           // [2][slots][HV][2]
+    float* sums;            // [2][slots][HK][2]
+    const uint16_t* gnorm_w;// [128]
+    float eps, qscale;
+    uint16_t* core;         // [R, HV * 128]
+    int R, HK, HV, C, slots;
+};
+
+__device__ __forceinline__ bool ctl_ok(const GdnArgs& a) {
+    const int pending = a.ctl[0], p = a.ctl[1];
+    return p >= 0 && p <= 1 && pending >= 0 && pending <= a.slots;
+}
+
+__global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= a.C || !ctl_ok(a)) return;
+    const int S = a.slots, pending = a.ctl[0], p = a.ctl[1];
+    const int* acc = a.ctl + 2;
+    const int* parent = a.ctl + 2 + S;
+    const int64_t C = a.C;
+    uint16_t old[CW], hist[CW];
+#pragma unroll
+    for (int r = 0; r < CW; ++r) old[r] = a.conv_state[c * CW + r];
+    // the history shifted by the previous step's accepted rows
+#pragma unroll
+    for (int r = 0; r < CW; ++r) {
+        const int j = pending + r;
+        if (j < CW) {
+            hist[r] = old[j < 0 ? 0 : (j > CW - 1 ? CW - 1 : j)];
+        } else {
+            int slot = acc[j - CW];
+            slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
+            hist[r] = a.pb[((1 - p) * S + slot) * C + c];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < CW; ++r) a.conv_state[c * CW + r] = hist[r];
+    float w[CW + 1];
+#pragma unroll
+    for (int d = 0; d <= CW; ++d) w[d] = bf2f(a.conv_w[c * (CW + 1) + d]);
+    for (int ts = 0; ts < S; ++ts) {
+        uint16_t out = 0, pr = 0;
+        if (ts < a.R) {
+            pr = a.proj[ts * C + c];
+            int anc = ts, miss = 0;
+            float sum = 0.f;
+#pragma unroll
+            for (int d = 0; d <= CW; ++d) {
+                if (d > 0) {
+                    anc = anc >= 0 ? parent[anc] : -1;
+                    anc = anc >= a.R ? -1 : anc;  // a parent is an earlier row of this step
+                    miss += anc < 0;
+                }
+                const float v = anc >= 0 ? bf2f(a.proj[anc * C + c]) : bf2f(hist[CW - miss]);
+                sum = fmaf(v, w[CW - d], sum);
+            }
+            const float y = bfround(sum);
+            out = f2bf(__fdiv_rn(y, __fadd_rn(1.f, expf(-y))));
+        }
+        a.qb[(p * S + ts) * C + c] = out;
+        a.pb[(p * S + ts) * C + c] = pr;
+    }
+}
+
+__global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
+    __shared__ float kvec[2 * MAXS][DH], qvec[MAXS][DH], vvec[2 * MAXS][DH], rawb[MAXS][DH];
+    __shared__ float mbuf[2][RG][DH], rbuf[2][RG][DH];
+    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], csum[MAXS][2], rss[MAXS];
+    __shared__ int ectl[2 + 3 * MAXS];
+    if (!ctl_ok(a)) return;
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
+    const int kh = h / (HV / HK);
+    const int64_t C = a.C;
+    if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
+    __syncthreads();
+    const int pending = ectl[0], p = ectl[1];
+    const int* acc = ectl + 2;
+    const int* prog = ectl + 2 + 2 * S;
+    int E0 = 0;
+    while (E0 < pending && acc[E0] >= 0 && acc[E0] < S) ++E0;
+    const bool replayed = E0 == pending;
+    int E1 = 0;
+    if (replayed)
+        while (E1 < R && prog[E1] >= 0 && (prog[E1] & 15) < R) ++E1;
+    const int E = E0 + E1;
+    auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
+
+    // this step's gates and sums (parity p)
+    if (t < S) {
+        float decay = 0.f, beta = 0.f;
+        if (t < R) {
+            const float av = __fadd_rn(bf2f(a.ab[t * 2 * HV + h]), a.dt_bias[h]);
+            const float bv = bf2f(a.ab[t * 2 * HV + HV + h]);
+            const float sp = av > 20.f ? av : log1pf(expf(av));
+            decay = expf(__fmul_rn(a.g_decay[h], sp));
+            beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bv))));
+        }
+        a.gates[((p * S + t) * HV + h) * 2] = decay;
+        a.gates[((p * S + t) * HV + h) * 2 + 1] = beta;
+        cgate[t][0] = decay;
+        cgate[t][1] = beta;
+    } else if (t >= 64 && t < 64 + 2 * S) {
+        const int which = (t - 64) / S, ts = (t - 64) % S;
+        float s2 = 0.f;
+        if (ts < R) {
+            const uint16_t* src = a.qb + (p * S + ts) * C + which * KD + kh * DH;
+            for (int d = 0; d < DH; ++d) {
+                const float v = bf2f(src[d]);
+                s2 = fmaf(v, v, s2);
+            }
+        }
+        // the heads of one key head write identical values
+        a.sums[((p * S + ts) * HK + kh) * 2 + which] = s2;
+        csum[ts][which] = s2;
+    }
+    __syncthreads();
+    // the entries' inputs: k * ki, (q * scale) * qi, v, decay, beta
+    if (t < E) {
+        const int e = t, ts = slot_of(e);
+        if (e < E0) {
+            egate[e][0] = a.gates[(((1 - p) * S + ts) * HV + h) * 2];
+            egate[e][1] = a.gates[(((1 - p) * S + ts) * HV + h) * 2 + 1];
+        } else {
+            egate[e][0] = cgate[ts][0];
+            egate[e][1] = cgate[ts][1];
+        }
+    }
+    for (int i = t; i < E * DH; i += GT) {
+        const int e = i / DH, d = i % DH, ts = slot_of(e);
+        const bool verify = e >= E0;
+        const int par = verify ? p : 1 - p;
+        const uint16_t* src = a.qb + (par * S + ts) * C;
+        const float sk = verify ? csum[ts][1] : a.sums[((par * S + ts) * HK + kh) * 2 + 1];
+        const float ki = __fdiv_rn(1.f, fmaxf(sqrt_rn(sk), 1e-12f));
+        kvec[e][d] = __fmul_rn(bf2f(src[KD + kh * DH + d]), ki);
+        vvec[e][d] = bf2f(src[2 * KD + h * DH + d]);
+        if (verify) {
+            const float qi = __fdiv_rn(1.f, fmaxf(sqrt_rn(csum[ts][0]), 1e-12f));
+            qvec[e - E0][d] = __fmul_rn(__fmul_rn(bf2f(src[kh * DH + d]), a.qscale), qi);
+        }
+    }
+    // the state: rows 32 rg + r of column col
+    const int col = t % DH, rg = t / DH;
+    float st[RPG];
+    float* rs = a.rec + (int64_t(h) * DH + rg * RPG) * DH + col;
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) st[r] = rs[r * DH];
+    __syncthreads();
+    for (int e = 0; e < E; ++e) {
+        const bool verify = e >= E0;
+        const bool commit = !verify || (prog[e - E0] & 32);
+        const float decay = egate[e][0], beta = egate[e][1];
+        const float* kk = kvec[e] + rg * RPG;
+        float mem = 0.f;
+        if (commit) {
+#pragma unroll
+            for (int r = 0; r < RPG; ++r) {
+                st[r] = __fmul_rn(st[r], decay);
+                mem = fmaf(st[r], kk[r], mem);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RPG; ++r) mem = fmaf(__fmul_rn(st[r], decay), kk[r], mem);
+        }
+        mbuf[e & 1][rg][col] = mem;
+        __syncthreads();  // the one barrier per entry (mbuf / rbuf alternate)
+        const float kv = __fadd_rn(__fadd_rn(__fadd_rn(mbuf[e & 1][0][col], mbuf[e & 1][1][col]), mbuf[e & 1][2][col]),
+                                   mbuf[e & 1][3][col]);
+        const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
+        float res = 0.f;
+        const float* qq = verify ? qvec[e - E0] + rg * RPG : nullptr;
+        if (commit) {
+#pragma unroll
+            for (int r = 0; r < RPG; ++r) {
+                st[r] = fmaf(kk[r], delta, st[r]);
+                if (verify) res = fmaf(st[r], qq[r], res);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RPG; ++r) res = fmaf(fmaf(kk[r], delta, __fmul_rn(st[r], decay)), qq[r], res);
+        }
+        if (verify) rbuf[e & 1][rg][col] = res;
+        if (e == E0 - 1 && replayed)
+#pragma unroll
+            for (int r = 0; r < RPG; ++r) rs[r * DH] = st[r];
+        // the previous verify entry's output row (its partials are complete after this barrier)
+        if (e > E0 && rg == 0) {
+            const int pe = e - 1;
+            rawb[slot_of(pe)][col] = bfround(__fadd_rn(__fadd_rn(__fadd_rn(rbuf[pe & 1][0][col], rbuf[pe & 1][1][col]),
+                                                                 rbuf[pe & 1][2][col]), rbuf[pe & 1][3][col]));
+        }
+    }
+    __syncthreads();
+    if (E1 > 0 && rg == 0) {
+        const int pe = E - 1;
+        rawb[slot_of(pe)][col] = bfround(__fadd_rn(__fadd_rn(__fadd_rn(rbuf[pe & 1][0][col], rbuf[pe & 1][1][col]),
+                                                             rbuf[pe & 1][2][col]), rbuf[pe & 1][3][col]));
+    }
+    unsigned written = 0;
+    for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
+    __syncthreads();
+    // gated RMSNorm: one wave per row: lane l sums columns l and l + 64, then a halving tree
+    const int lane = t & 63, wv = t >> 6;
+    for (int ts = wv; ts < R; ts += GT / 64) {
+        if (!((written >> ts) & 1)) continue;
+        const float x0 = rawb[ts][lane], x1 = rawb[ts][lane + 64];
+        float s2 = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
+        for (int off = 32; off >= 1; off >>= 1) s2 = __fadd_rn(s2, shfl_down(s2, off));
+        if (lane == 0) rss[ts] = s2;
+    }
+    __syncthreads();
+    const float gw = bf2f(a.gnorm_w[col]);
+    for (int ts = rg; ts < R; ts += RG) {
+        uint16_t outv = 0;
+        if ((written >> ts) & 1) {
+            const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(rss[ts], float(DH)), a.eps)));
+            const float normed = bfround(__fmul_rn(__fmul_rn(rawb[ts][col], gw), rsq));
+            const float zz = bf2f(a.z[ts * HV * DH + h * DH + col]);
+            const float gz = bfround(__fdiv_rn(zz, __fadd_rn(1.f, expf(-zz))));
+            outv = f2bf(__fmul_rn(normed, gz));
+        }
+        a.core[ts * HV * DH + h * DH + col] = outv;
+    }
+}
+
+}  // namespace
+}  // namespace mdx
+
+using namespace mdx;
+
+extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* ab, const uint16_t* conv_w,
+                            uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
+                            const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums,
+                            const uint16_t* gnorm_w, float gnorm_eps, float qscale, uint16_t* core, int64_t rows,
+                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    MDX_CHECK(proj && z && ab && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
+                  rec_state && gates && sums && gnorm_w && core,
+              "null pointer");
+    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
+    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
+    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV <= 1024, "heads");
+    GdnArgs a{};
+    a.proj = proj;
+    a.z = z;
+    a.ab = ab;
+    a.conv_w = conv_w;
+    a.conv_state = conv_state;
+    a.pb = proj_buf;
+    a.qb = qkv_buf;
+    a.ctl = ctl;
+    a.dt_bias = dt_bias;
+    a.g_decay = g_decay;
+    a.rec = rec_state;
+    a.gates = gates;
+    a.sums = sums;
+    a.gnorm_w = gnorm_w;
+    a.eps = gnorm_eps;
+    a.qscale = qscale;
+    a.core = core;
+    a.R = int(rows);
+    a.HK = int(HK);
+    a.HV = int(HV);
+    a.C = int(2 * HK * DH + HV * DH);
+    a.slots = int(slots);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256), dim3(256), 0, st, a);
+    MDX_LAUNCHED();
+    hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV), dim3(GT), 0, st, a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}

@@ -387,3 +387,32 @@ def bf16_linear(x, w, tiled=True, residual=None, out=None):
     _lib.call("mdx_bf16_linear", _lib.ptr(x), _lib.ptr(w), _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW,
               _lib.ptr(residual), _lib.ptr(out), rows, N, x.shape[1], _lib.stream_of(x))
     return out
+
+
+def gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
+             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None):
+    """The Gated-DeltaNet core of csrc/mono_gdn.sycl:313-607 (layer_gdn phases P3-P5; layer_gdn_core's
+    output): deferred conv, gates, sums, replay + verify delta rule, gated RMSNorm. Buffers are updated
+    in place; returns core bf16 [R, HV * 128]."""
+    for t, n in ((proj, "proj"), (z, "z"), (ab, "ab"), (conv_w, "conv_w"), (conv_state, "conv_state"),
+                 (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf"), (gnorm_w, "gnorm_w")):
+        _dev(t, n)
+        _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
+    for t, n in ((dt_bias, "dt_bias"), (g_decay, "g_decay"), (rec_state, "rec_state"), (gates_buf, "gates"),
+                 (sums_buf, "sums")):
+        _check(t.dtype == torch.float32 and t.is_contiguous(), f"{n}: contiguous f32")
+    slots = _slots_of(ctl)
+    R, C = proj.shape[-2], proj.shape[-1]
+    HV = rec_state.shape[-3]
+    _check(rec_state.shape[-2:] == (128, 128) and C == 2 * hk * 128 + HV * 128, "GDN shapes")
+    _check(z.shape[-1] == HV * 128 and ab.shape[-1] == 2 * HV and conv_w.numel() == C * 4
+           and conv_state.numel() == C * 3, "GDN operand shapes")
+    _check(proj_buf.numel() == 2 * slots * C and qkv_buf.numel() == 2 * slots * C, "proj / qkv buffers [2, slots, C]")
+    _check(gates_buf.numel() == 2 * slots * HV * 2 and sums_buf.numel() == 2 * slots * hk * 2, "gates / sums buffers")
+    if core is None:
+        core = torch.empty(R, HV * 128, dtype=torch.bfloat16, device=proj.device)
+    _lib.call("mdx_gdn_core", _lib.ptr(proj), _lib.ptr(z), _lib.ptr(ab), _lib.ptr(conv_w), _lib.ptr(conv_state),
+              _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias), _lib.ptr(g_decay),
+              _lib.ptr(rec_state), _lib.ptr(gates_buf), _lib.ptr(sums_buf), _lib.ptr(gnorm_w), float(gnorm_eps),
+              float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(proj))
+    return core

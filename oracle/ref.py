@@ -541,3 +541,164 @@ def bf16_linear_f64(x_bits, w_bits):
     x = bf16_to_f32(x_bits).astype(np.float64)
     w = bf16_to_f32(w_bits).astype(np.float64)
     return x @ w.T, np.abs(x) @ np.abs(w).T
+
+
+# ---------------------------------------------------------------------------------------------
+# Gated-DeltaNet decode step with deferred replay (csrc/mono_gdn.sycl:313-374,398-607)
+# ---------------------------------------------------------------------------------------------
+GDN_DH = 128
+GDN_CW = 3
+
+
+def _rnd(v, dtype, bf=True):
+    """bf16 rounding in the float32 chain; identity in float64 (the exact reference)."""
+    if dtype == np.float64 or not bf:
+        return np.asarray(v, dtype=dtype)
+    return bfround(np.asarray(v, dtype=np.float32))
+
+
+def gdn_conv(state, proj, conv_w, ctl, R, slots, dtype=np.float64):
+    """The deferred causal conv (kernel 4) over tree ancestors (csrc/mono_gdn.sycl:313-374).
+    state: dict with conv_state [C, 3], pb [2, slots, C] (bf16 values as float). proj [R, C].
+    ctl = [pending, parity, accepted[slots], parents[slots], prog[slots]].
+    Updates conv_state (shifted by the previous step's accepted rows) and pb[parity]; returns the conv
+    outputs qb [slots, C] (SiLU(bf16(sum)) rounded to bf16; rows >= R zero)."""
+    pending, p = ctl[0], ctl[1]
+    acc_slots = ctl[2:2 + slots]
+    parents = ctl[2 + slots:2 + 2 * slots]
+    C = proj.shape[1]
+    old = state["conv_state"].astype(dtype)
+    prev = state["pb"][1 - p].astype(dtype)
+    hist = np.empty((C, GDN_CW), dtype=dtype)
+    for r in range(GDN_CW):
+        j = pending + r
+        hist[:, r] = old[:, j] if j < GDN_CW else prev[acc_slots[j - GDN_CW]]
+    w = conv_w.astype(dtype)
+    out = np.zeros((slots, C), dtype=dtype)
+    for ts in range(R):
+        anc = [ts]
+        miss = [0]
+        for d in range(1, GDN_CW + 1):
+            a = parents[anc[-1]] if anc[-1] >= 0 else -1
+            anc.append(a)
+            miss.append(miss[-1] + (a < 0))
+        s = np.zeros(C, dtype=dtype)
+        for d in range(GDN_CW + 1):
+            v = proj[anc[d]].astype(dtype) if anc[d] >= 0 else hist[:, GDN_CW - miss[d]]
+            s = s + v * w[:, GDN_CW - d] if dtype == np.float64 else (s + (v * w[:, GDN_CW - d]).astype(np.float32)).astype(np.float32)
+        y = _rnd(s, dtype)
+        out[ts] = _rnd(y / (1 + np.exp(-y)), dtype)
+    state["conv_state"] = hist.astype(state["conv_state"].dtype)
+    pbn = np.zeros((slots, C), dtype=state["pb"].dtype)
+    pbn[:R] = proj
+    state["pb"][p] = pbn
+    return out
+
+
+def gdn_gates(a, b, dt_bias, g_decay, dtype=np.float64):
+    """decay = exp(g_decay * softplus(a + dt_bias)) (softplus(x) = x above 20), beta = bf16(sigmoid(b))
+    (csrc/mono_gdn.sycl:441-450). a, b: [R, HV] bf16 values."""
+    av = a.astype(dtype) + dt_bias.astype(dtype)
+    sp = np.where(av > 20, av, np.log1p(np.exp(np.minimum(av, 20))))
+    decay = np.exp(g_decay.astype(dtype) * sp)
+    beta = _rnd(1 / (1 + np.exp(-b.astype(dtype))), dtype)
+    return decay, beta
+
+
+def gdn_step(state, proj, z, a, b, conv_w, dt_bias, g_decay, gnorm_w, eps, qscale, ctl, R, HK, slots,
+             dtype=np.float64):
+    """One deferred GDN step. state: conv_state [C, 3], pb / qb [2, slots, C], rec [HV, 128, 128],
+    gates [2, slots, HV, 2], sums [2, slots, HK, 2] (mutated). Returns core [R, HV * 128] (float;
+    rows not produced by a verify entry are 0).
+    Entries: first the previous step's accepted slots (parity 1 - p, always committed), then this
+    step's verify program (prog & 15 = slot, prog & 32 = commit); the persistent state keeps only the
+    replayed entries; verify entries update a working copy when they commit."""
+    DH = GDN_DH
+    pending, p = int(ctl[0]), int(ctl[1])
+    HV = state["rec"].shape[0]
+    KD = HK * DH
+    qb = gdn_conv(state, proj, conv_w, ctl, R, slots, dtype)
+    state["qb"][p] = qb.astype(state["qb"].dtype)
+    decay, beta = gdn_gates(a, b, dt_bias, g_decay, dtype)
+    gates = np.zeros((slots, HV, 2))
+    gates[:R, :, 0] = decay
+    gates[:R, :, 1] = beta
+    state["gates"][p] = gates
+    sums = np.zeros((slots, HK, 2))
+    for ts in range(R):
+        for kh in range(HK):
+            for which in range(2):
+                v = qb[ts, which * KD + kh * DH:which * KD + (kh + 1) * DH].astype(dtype)
+                sums[ts, kh, which] = np.sum(v * v)
+    state["sums"][p] = sums
+    acc_slots = [int(s) for s in ctl[2:2 + slots]]
+    prog = [int(s) for s in ctl[2 + 2 * slots:2 + 3 * slots]]
+    E0 = 0
+    while E0 < pending and 0 <= acc_slots[E0] < slots:
+        E0 += 1
+    replayed = E0 == pending
+    E1 = 0
+    if replayed:
+        while E1 < R and prog[E1] >= 0 and (prog[E1] & 15) < R:
+            E1 += 1
+    core = np.zeros((R, HV * DH), dtype=np.float64)
+    for h in range(HV):
+        kh = h // (HV // HK)
+        S = state["rec"][h].astype(dtype)
+        raw = {}
+        for e in range(E0 + E1):
+            verify = e >= E0
+            par = p if verify else 1 - p
+            ts = (prog[e - E0] & 15) if verify else acc_slots[e]
+            commit = (not verify) or bool(prog[e - E0] & 32)
+            src = qb if verify else state["qb"][1 - p].astype(dtype)
+            sq = state["sums"][par][ts, kh] if not verify else sums[ts, kh]
+            dec, bet = (state["gates"][par][ts, h] if not verify else gates[ts, h])
+            q = src[ts, kh * DH:(kh + 1) * DH].astype(dtype)
+            k = src[ts, KD + kh * DH:KD + (kh + 1) * DH].astype(dtype)
+            v = src[ts, 2 * KD + h * DH:2 * KD + (h + 1) * DH].astype(dtype)
+            kn = k / max(np.sqrt(sq[1]), 1e-12)
+            qn = (q * qscale) / max(np.sqrt(sq[0]), 1e-12)
+            Sd = S * dtype(dec)
+            kv = kn @ Sd                      # [col]
+            delta = (v - kv) * dtype(bet)
+            Su = Sd + np.outer(kn, delta)
+            if verify:
+                raw[ts] = _rnd(qn @ Su, dtype)
+            if commit:
+                S = Su
+            if e == E0 - 1:
+                state["rec"][h] = S.astype(state["rec"].dtype)
+        if E0 == 0 and replayed:
+            pass
+        for ts, rv in raw.items():
+            ss = np.sum(rv.astype(dtype) ** 2)
+            rsq = 1 / np.sqrt(ss / DH + eps)
+            normed = _rnd(rv * gnorm_w.astype(dtype) * rsq, dtype)
+            zz = z[ts, h * DH:(h + 1) * DH].astype(dtype)
+            gz = _rnd(zz / (1 + np.exp(-zz)), dtype)
+            core[ts, h * DH:(h + 1) * DH] = _rnd(normed * gz, dtype)
+    return core
+
+
+def verify_program(parents, R):
+    """A verify program for a chain-with-leaf-siblings tree (qwen35 tree_spec shape): nodes in an order
+    where each node sees the state after exactly its ancestors; chain nodes commit (bit 32), leaves do
+    not. Returns prog [R]."""
+    children = [[] for _ in range(R)]
+    for r in range(R):
+        if parents[r] >= 0:
+            children[parents[r]].append(r)
+    order, node = [], 0
+    while True:
+        order.append((node, True))
+        kids = children[node]
+        for leaf in kids[1:]:
+            assert not children[leaf], "only the first child may have children"
+            order.append((leaf, False))
+        if not kids:
+            break
+        node = kids[0]
+    order[-1] = (order[-1][0], False) if order[-1][1] else order[-1]
+    assert len(order) == R
+    return [n | (32 if c else 0) for n, c in order]
