@@ -72,6 +72,12 @@ struct PrepArgs {
     int8_t* q;             // int8 [rows, K]
     float* scale;          // f32 [rows]
     int K;
+    // optional sigmoid gate: x[i] <- bf16(x[i] * sig[gate[row * g_row + (i / g_head) * g_hstride + g_off +
+    // i % g_head]]) before the rotation (the gated attention output of layer_post)
+    const uint16_t* gate = nullptr;
+    const uint16_t* sig = nullptr;
+    int64_t g_row = 0;
+    int g_head = 0, g_hstride = 0, g_off = 0;
 };
 
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
@@ -121,6 +127,23 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
     for (int j = 0; j < PREP_BLK; ++j) {
         const int b = t + PREP_THREADS * j;
         if (b < nb) unpack8(raw[j], v[j]);
+    }
+    if (a.gate) {
+#pragma unroll
+        for (int j = 0; j < PREP_BLK; ++j) {
+            const int b = t + PREP_THREADS * j;
+            if (b < nb) {
+                const int i0 = 8 * b;
+                const uint16_t* gp = a.gate + row * a.g_row + (i0 / a.g_head) * a.g_hstride + a.g_off + i0 % a.g_head;
+                const uint4 gv = *reinterpret_cast<const uint4*>(gp);
+                const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t gb = uint16_t(gw[e >> 1] >> (16 * (e & 1)));
+                    v[j][e] = bfround(__fmul_rn(v[j][e], bf2f(a.sig[gb])));
+                }
+            }
+        }
     }
     if (a.nw) {
         // canonical RMSNorm: thread t's partial sums its own elements in increasing order
@@ -810,13 +833,35 @@ extern "C" int mdx_rms_rot_quant(const uint16_t* x, const uint16_t* norm_w, floa
     return launch_prep(a, rows, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64_t gate_row_stride, int64_t gate_head,
+                                  int64_t gate_head_stride, int64_t gate_offset, const uint16_t* sig_lut,
+                                  const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K,
+                                  void* stream) {
+    MDX_CHECK(y && gate && sig_lut && q && scale, "null pointer");
+    int rc = prep_checks(rows, K, rot, h);
+    if (rc) return rc;
+    MDX_CHECK(gate_head >= 8 && gate_head % 8 == 0 && K % gate_head == 0 && gate_head_stride % 8 == 0 &&
+                  gate_offset % 8 == 0 && gate_row_stride % 8 == 0 && aligned(gate, 16),
+              "gate rows: 16-byte aligned runs of whole heads");
+    if (rows == 0) return MDX_OK;
+    PrepArgs a{y, nullptr, 0.f, nullptr, h, rot, q, scale, int(K)};
+    a.gate = gate;
+    a.sig = sig_lut;
+    a.g_row = gate_row_stride;
+    a.g_head = int(gate_head);
+    a.g_hstride = int(gate_head_stride);
+    a.g_off = int(gate_offset);
+    return launch_prep(a, rows, static_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1) {
     return align256(size_t(rows) * K1) + align256(size_t(rows) * N1) + align256(64 * 4) + align256(size_t(rows) * N1 * 2);
 }
 
 extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
                             const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
-                            uint16_t* out, int64_t rows, void* workspace, size_t workspace_bytes, void* stream) {
+                            const uint16_t* residual, uint16_t* out, int64_t rows, void* workspace,
+                            size_t workspace_bytes, void* stream) {
     MDX_CHECK(xn && silu_lut && gate && up && down && out && workspace, "null pointer");
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16");
     const int64_t K1 = gate->k, N1 = gate->n;
@@ -844,7 +889,8 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     if ((rc = launch_prep(pb, rows, st))) return rc;
     const mdx_w4* dn[1] = {down};
     void* o2[1] = {out};
-    return run_gemv(dn, 1, false, q2, s + 32, int(rows), EPI_STORE, o2, nullptr, MDX_DT_BF16, nullptr, st);
+    const void* r2[1] = {residual};
+    return run_gemv(dn, 1, false, q2, s + 32, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st);
 }
 
 extern "C" int mdx_stream_gemv(const int8_t* x, const float* x_scale, const mdx_w4* const* mats, int32_t nmats,

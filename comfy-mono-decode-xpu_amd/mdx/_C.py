@@ -89,8 +89,10 @@ def quant_rows(x):
     return q, scale
 
 
-def mono_mlp_w4(xn, rot, h, silu_lut, gate: W4, up: W4, down: W4, norm_w=None, eps=1e-6, out=None, ws=None):
-    """mono_mlp on prepared W4 handles (the library's own callers); norm_w: RMSNorm the input first."""
+def mono_mlp_w4(xn, rot, h, silu_lut, gate: W4, up: W4, down: W4, norm_w=None, eps=1e-6, out=None, ws=None,
+                residual=None):
+    """mono_mlp on prepared W4 handles (the library's own callers); norm_w: RMSNorm the input first;
+    residual: out = bf16(residual + bf16(down))."""
     K1 = xn.shape[-1]
     rows = xn.numel() // K1
     if out is None:
@@ -99,8 +101,8 @@ def mono_mlp_w4(xn, rot, h, silu_lut, gate: W4, up: W4, down: W4, norm_w=None, e
     if ws is None:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xn.device)
     _lib.call("mdx_mono_mlp", _lib.ptr(xn), _lib.ptr(norm_w), float(eps), _lib.ptr(h), rot, _lib.ptr(silu_lut),
-              gate.struct(), up.struct(), down.struct(), _lib.ptr(out), rows, _lib.ptr(ws), ws.numel(),
-              _lib.stream_of(xn))
+              gate.struct(), up.struct(), down.struct(), _lib.ptr(residual), _lib.ptr(out), rows, _lib.ptr(ws),
+              ws.numel(), _lib.stream_of(xn))
     return out
 
 
@@ -416,3 +418,173 @@ def gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g
               _lib.ptr(rec_state), _lib.ptr(gates_buf), _lib.ptr(sums_buf), _lib.ptr(gnorm_w), float(gnorm_eps),
               float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(proj))
     return core
+
+
+
+# ---------------------------------------------------------------------------------------------------
+# decoder-layer segments (csrc/mono_layer.sycl, csrc/mono_gdn.sycl)
+# ---------------------------------------------------------------------------------------------------
+_SCRATCH = {}
+
+
+def _scratch(dev):
+    """Per-device buffers of the layer segments (stable addresses for graph capture), 16 rows."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    sc = _SCRATCH.get(key)
+    if sc is None:
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        sc = _SCRATCH[key] = dict(
+            q1=torch.empty(16, 16384, dtype=torch.int8, device=dev), s=torch.empty(64, dtype=torch.float32, device=dev),
+            xn=torch.empty(16, 4096, **bf), x1=torch.empty(16, 4096, **bf), proj=torch.empty(16, 16384, **bf),
+            z=torch.empty(16, 8192, **bf), ab=torch.empty(16, 256, **bf), core=torch.empty(16, 8192, **bf),
+            mlp_ws=torch.empty(_lib.lib().mdx_mono_mlp_workspace(16, 4096, 16384), dtype=torch.uint8, device=dev),
+            wab={})
+    return sc
+
+
+def _buf(t, R, N):
+    """A contiguous [R, N] view at the start of a scratch buffer."""
+    return t.view(-1)[:R * N].view(R, N)
+
+
+def _w4_list(mats, tiled):
+    _check(len(mats) % 4 == 0 and len(mats) >= 4, "W4 matrices as (q, s, sc, cb) groups")
+    ws = [_w4(mats[i], mats[i + 1], mats[i + 2], mats[i + 3], tiled) for i in range(0, len(mats), 4)]
+    for w in ws[1:]:
+        w.cb = ws[0].cb if (w.cb is not None and ws[0].cb is not None and torch.equal(w.cb, ws[0].cb)) else w.cb
+    return ws
+
+
+def _rows_of(x):
+    _dev(x, "x")
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[-1] == 4096, "x bf16 [..., 4096]")
+    R = x.numel() // 4096
+    _check(1 <= R <= 16, "1..16 rows")
+    return R
+
+
+def gate_rot_quant(y, gate, sig_lut, hadamard, q=None, scale=None):
+    """bf16(y * sig_lut[gate]) -> rot_quant (layer_post's first phase, csrc/mono_layer.sycl:243-256).
+    gate: [R, 2 K] interleaved per 256-head ([query | gate]) or [R, K]."""
+    K = y.shape[-1]
+    R = y.numel() // K
+    inter = gate.numel() == 2 * R * K
+    _check(gate.dtype == torch.bfloat16 and gate.is_contiguous() and (inter or gate.numel() == R * K), "gate bf16")
+    if q is None:
+        q = torch.empty(R, K, dtype=torch.int8, device=y.device)
+        scale = torch.empty(R, dtype=torch.float32, device=y.device)
+    g = (2 * K, 256, 512, 256) if inter else (K, K, K, 0)
+    _lib.call("mdx_gate_rot_quant", _lib.ptr(y), _lib.ptr(gate), *g, _lib.ptr(sig_lut), _lib.ptr(hadamard),
+              classify_rotation(hadamard), _lib.ptr(q), _lib.ptr(scale), R, K, _lib.stream_of(y))
+    return q, scale
+
+
+def layer_pre(x, norm_w, eps, hadamard, mats, nwg=0, tiled=True):
+    """Reference csrc/mono_layer.sycl:69-155: xn = RMSNorm(x), q = rot_quant(xn), then 1..3 W4
+    projections of q in one engine launch. Returns [xn, out_0, ...] (bf16)."""
+    R = _rows_of(x)
+    _check(norm_w.dtype == torch.bfloat16 and norm_w.numel() == 4096, "norm weight bf16 [4096]")
+    ws = _w4_list(mats, tiled)
+    _check(len(ws) <= 3 and all(w.k == 4096 for w in ws), "1..3 W4 matrices with K = hidden")
+    xn = torch.empty(R, 4096, dtype=torch.bfloat16, device=x.device)
+    q, s = rms_rot_quant(x.reshape(R, 4096), norm_w, eps, classify_rotation(hadamard), hadamard, xn_out=xn)
+    outs = [torch.empty(R, w.n, dtype=torch.bfloat16, device=x.device) for w in ws]
+    stream_gemv(q, s, ws, outs)
+    return [xn] + outs
+
+
+def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop):
+    R = _rows_of(x)
+    _check(stop >= 6, "only the full post block (stop >= 6) is supported")
+    _check(y.dtype == torch.bfloat16 and y.is_contiguous() and y.numel() == R * 4096, "y bf16 [R, 4096]")
+    sc = _scratch(x.device)
+    x2 = x.view(R, 4096)
+    rot = classify_rotation(hadamard)
+    q, s = _buf(sc["q1"], R, 4096), sc["s"][:R]
+    if gate is not None:
+        gate_rot_quant(y.view(R, 4096), gate, sig_lut, hadamard, q, s)
+    else:
+        _lib.call("mdx_rot_quant", _lib.ptr(y), _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R, 4096,
+                  _lib.stream_of(y))
+    x1 = _buf(sc["x1"], R, 4096)
+    stream_gemv(q, s, [O], [x1], residuals=[x2])
+    mono_mlp_w4(x1, rot, hadamard, silu_lut, G, U, D, norm_w=norm_w, eps=eps, out=x2, ws=sc["mlp_ws"], residual=x1)
+    return x
+
+
+def layer_post(x, y, gate, sig_lut, oq, os_, osc, ocb, norm_w, eps, hadamard, silu_lut, gq, gs, gsc, gcb, uq, us, usc,
+               ucb, dq, ds, dsc, dcb, nwg=0, stop=6, tiled=True):
+    """Reference csrc/mono_layer.sycl:157-318: y' = bf16(y * sigmoid(gate)) (optional), x1 = x +
+    o_proj(rot_quant(y')), x = x1 + mlp(RMSNorm(x1)); x is updated in place and returned."""
+    O, G, U, D = (_w4(*w, tiled) for w in ((oq, os_, osc, ocb), (gq, gs, gsc, gcb), (uq, us, usc, ucb),
+                                           (dq, ds, dsc, dcb)))
+    U.cb = D.cb = G.cb
+    return _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop)
+
+
+def expand_compact_h(h16):
+    """The full H256 from layer_post_h16's [2, 16, 16] (+H16, -H16): block (kb, cb) is -H16 when the
+    base-4 digits of kb ^ cb hold an odd number of 3s (comfy_mono_decode_xpu/layer.py:74-90)."""
+    b = torch.arange(16, device=h16.device)
+    d = b[:, None] ^ b[None, :]
+    d = d & (d >> 1) & 5
+    neg = ((d & 1) ^ (d >> 2)).bool()
+    return torch.where(neg[:, None, :, None], h16[1][None, :, None, :], h16[0][None, :, None, :]).reshape(256, 256)
+
+
+def layer_post_h16(x, y, gate, sig_lut, oq, os_, osc, ocb, norm_w, eps, hadamard, *rest):
+    """Reference layer_post_h16 (csrc/mono_layer.sycl:157-318 with CompactH): the rotation given as its
+    [2, 16, 16] compact form."""
+    _check(hadamard.dim() == 3 and tuple(hadamard.shape) == (2, 16, 16), "compact Hadamard [2, 16, 16]")
+    sc = _scratch(x.device)
+    key = ("h16", hadamard.data_ptr(), hadamard._version)
+    full = sc["wab"].get(key)
+    if full is None or full[0] is not hadamard:
+        full = sc["wab"][key] = (hadamard, expand_compact_h(hadamard).contiguous())
+    return layer_post(x, y, gate, sig_lut, oq, os_, osc, ocb, norm_w, eps, full[1], *rest)
+
+
+def _wab(sc, wa, wb):
+    key = ("ab", wa.data_ptr(), wb.data_ptr(), wa._version, wb._version)
+    hit = sc["wab"].get(key)
+    if hit is None or hit[0] is not wa or hit[1] is not wb:
+        if len(sc["wab"]) > 128:
+            sc["wab"].clear()
+        hit = sc["wab"][key] = (wa, wb, torch.cat([wa, wb]).contiguous())
+    return hit[2]
+
+
+def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
+              rec_state, gates_buf, sums_buf, gnorm_w, gnorm_eps, qscale, hk, norm_post, eps_post, silu_lut, nwg=0,
+              stop=11, tiled=True):
+    """Reference csrc/mono_gdn.sycl:87-699: x += out_proj(GDN(RMSNorm(x))); x += mlp(RMSNorm(x)) for
+    1..16 tree-verify rows, in place. w4: qkv, z, out, gate, up, down as (q, s, sc, cb) groups (24
+    tensors). stop 5: only the GDN core (read it with layer_gdn_core); stop >= 6: the whole layer."""
+    R = _rows_of(x)
+    _check(len(w4) == 24, "W4: qkv, z, out, gate, up, down (q, s, sc, cb each)")
+    QKV, Z, O, G, U, D = _w4_list(w4, tiled)
+    HV = rec_state.shape[-3]
+    _check(wa.dtype == torch.bfloat16 and wa.shape == (HV, 4096) and wb.shape == wa.shape, "w_a / w_b bf16 [HV, 4096]")
+    sc = _scratch(x.device)
+    x2 = x.view(R, 4096)
+    rot = classify_rotation(hadamard)
+    xn, q, s = _buf(sc["xn"], R, 4096), _buf(sc["q1"], R, 4096), sc["s"][:R]
+    _lib.call("mdx_rms_rot_quant", _lib.ptr(x2), _lib.ptr(norm_in), float(eps_in), _lib.ptr(xn), _lib.ptr(hadamard), rot,
+              _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(x))
+    ab = _buf(sc["ab"], R, 2 * HV)
+    bf16_linear(xn, _wab(sc, wa, wb), tiled=False, out=ab)
+    proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
+    stream_gemv(q, s, [QKV, Z], [proj, z])
+    core = _buf(sc["core"], R, HV * 128)
+    gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
+             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=core)
+    if stop >= 6:
+        U.cb = D.cb = G.cb
+        _layer_post(x, core, None, None, O, norm_post, eps_post, hadamard, silu_lut, G, U, D, 6)
+    return x
+
+
+def layer_gdn_core(like, rows):
+    """Reference csrc/mono_gdn.sycl:702-704: the GDN core output of the last layer_gdn on this device
+    (rows 0..rows-1), valid until the next call."""
+    return _buf(_scratch(like.device)["core"], rows, 4096)

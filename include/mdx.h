@@ -93,11 +93,14 @@ size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1);
  *   g, u = bf16 scaleback of the gate / up accumulators; h = bf16(float(silu_lut[g]) * float(u));
  *   q2, s2 = rot_quant(h); out = bf16((float(acc_down) * s2) * s_channel_down).
  * xn bf16 [rows, K1]; silu_lut bf16 [65536] (F.silu of every bf16 bit pattern); out bf16 [rows, N2].
- * gate/up: N1 x K1, down: N2 x N1; one codebook for all three; 1 <= rows <= 16.
+ * gate/up: N1 x K1, down: N2 x N1; one codebook for all three; 1 <= rows <= 16. With residual (bf16
+ * [rows, N2], may equal xn): out = bf16(float(residual) + float(bf16(down))) (layer_post's last phase,
+ * csrc/mono_layer.sycl:303-313).
  * workspace: >= mdx_mono_mlp_workspace(rows, K1, N1) bytes, 256-byte aligned. */
 int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
-                 const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down, uint16_t* out,
-                 int64_t rows, void* workspace, size_t workspace_bytes, void* stream);
+                 const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
+                 const uint16_t* residual, uint16_t* out, int64_t rows, void* workspace, size_t workspace_bytes,
+                 void* stream);
 
 /* One launch of the stream GEMV engine over up to three W4 matrices sharing K (outputs per matrix),
  * or a gate/up pair with the SiLU-multiply epilogue into outs[0].
@@ -248,6 +251,15 @@ int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* ab, co
                  const float* g_decay, float* rec_state, float* gates, float* sums, const uint16_t* gnorm_w,
                  float gnorm_eps, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
                  void* stream);
+
+/* Sigmoid-gated rotation + row quantisation: y' = bf16(y * sig_lut[gate]), then rot_quant(y').
+ * Replaces: the first phase of _C.layer_post (csrc/mono_layer.sycl:243-256: the gated attention output,
+ * gate interleaved in q_proj's output as [head][query 256 | gate 256], or a separate [rows, K] gate).
+ * Gate element of row r, column i: gate[r * gate_row_stride + (i / gate_head) * gate_head_stride +
+ * gate_offset + i % gate_head] (interleaved: 8192, 256, 512, 256; separate: K, K, K, 0). */
+int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64_t gate_row_stride, int64_t gate_head,
+                       int64_t gate_head_stride, int64_t gate_offset, const uint16_t* sig_lut, const uint16_t* h,
+                       int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
 
 #ifdef __cplusplus
 }

@@ -702,3 +702,45 @@ def verify_program(parents, R):
     order[-1] = (order[-1][0], False) if order[-1][1] else order[-1]
     assert len(order) == R
     return [n | (32 if c else 0) for n, c in order]
+
+
+# ---------------------------------------------------------------------------------------------
+# decoder-layer segments (csrc/mono_layer.sycl:69-318)
+# ---------------------------------------------------------------------------------------------
+
+
+def gate_mul(y_bits, gate_bits, sig_lut_bits):
+    """y' = bf16(float(y) * float(sig[gate])) (csrc/mono_layer.sycl:243-252, bf16_mul)."""
+    sig = bf16_to_f32(np.asarray(sig_lut_bits, dtype=np.uint16)[np.asarray(gate_bits, dtype=np.uint16)])
+    return f32_to_bf16((bf16_to_f32(y_bits) * sig).astype(np.float32))
+
+
+def interleaved_gate(q_out_bits, K=4096, head=256):
+    """The gate half of q_proj's [head][query | gate] output rows (csrc/mono_layer.sycl:248)."""
+    q = np.asarray(q_out_bits).reshape(q_out_bits.shape[0], K // head, 2 * head)
+    return q[:, :, head:].reshape(q_out_bits.shape[0], K)
+
+
+def add_bf16(res_bits, f_bits):
+    """bf16(float(res) + float(f)) (the residual rule of every epilogue)."""
+    return f32_to_bf16((bf16_to_f32(res_bits) + bf16_to_f32(f_bits)).astype(np.float32))
+
+
+def layer_pre(x_bits, norm_w_bits, eps, rot, h, mats):
+    """xn = RMSNorm(x); q = rot_quant(xn); outs = W4 linears (csrc/mono_layer.sycl:69-155).
+    mats: dicts as for mono_mlp."""
+    xn = rmsnorm(x_bits, norm_w_bits, eps)
+    q, s = rot_quant(xn, rot, h)
+    outs = [f32_to_bf16(scaleback(w4a8_acc(q, decode_w8(m["packed"], m["s"], m["cb"], m["G"])), s, m["sch"]))
+            for m in mats]
+    return xn, outs
+
+
+def layer_post(x_bits, y_bits, gate_bits, sig_bits, o, norm_w_bits, eps, rot, h, lut_bits, g, u, d):
+    """x1 = x + o_proj(rot_quant(gate_mul(y))); x = x1 + mlp(RMSNorm(x1)) (csrc/mono_layer.sycl:157-318)."""
+    yy = y_bits if gate_bits is None else gate_mul(y_bits, gate_bits, sig_bits)
+    q, s = rot_quant(yy, rot, h)
+    x1 = f32_to_bf16(bf16_to_f32(x_bits) + bfround(scaleback(w4a8_acc(q, decode_w8(o["packed"], o["s"], o["cb"],
+                                                                                      o["G"])), s, o["sch"])))
+    mlp = mono_mlp(rmsnorm(x1, norm_w_bits, eps), rot, h, lut_bits, g, u, d)
+    return add_bf16(x1, mlp), x1

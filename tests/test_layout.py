@@ -11,3 +11,9 @@ def test_tile_major_bf16_layout():
         g_, c = lane >> 4, lane & 15
         assert torch.equal(t[lane * 8:lane * 8 + 8], w[c, 8 * g_:8 * g_ + 8])
     assert torch.equal(torch.sort(t.float()).values, torch.sort(w.float().view(-1)).values)
+
+
+def test_compact_h_expands_to_h256():
+    from mdx import _C, layout
+    h = layout.regular_hadamard()
+    assert torch.equal(_C.expand_compact_h(torch.stack((h[:16, :16], -h[:16, :16]))).view(torch.int16), h.view(torch.int16))
