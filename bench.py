@@ -282,6 +282,43 @@ def bench_attn(args, dev):
                   "avg_launch_us": round(t * 1e6, 3)})
 
 
+def bench_stack(args, dev):
+    """The full synthetic 32-layer hybrid stack (3 GDN : 1 attention, hidden 4096, MLP 12288, W4A8
+    GPTQ G128), 1-layer bf16 MTP draft block, bf16 lm_head over 151936, tree_spec (4, 3) (8 rows, 2
+    drafts per step), top-k 20 sampling; a seeded random prompt is prefilled (not timed), then each
+    decode step is one replayed HIP graph. value = accepted tokens per second."""
+    import torch
+    from mdx import hybrid
+    steps, warm = args.steps, max(args.warmup, 2)
+    cap = args.prompt + 8 * (steps + warm + 4) + 64
+    cfg = hybrid.HybridConfig(cap=cap)
+    t0 = time.perf_counter()
+    m = hybrid.HybridModel(cfg, dev, seed=5)
+    prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
+    m.prefill(prompt)
+    m.capture()
+    m.replay(warm)
+    torch.cuda.synchronize()
+    setup = time.perf_counter() - t0
+    st0 = int(m.st[0].item())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    m.replay(steps)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3
+    tokens = int(m.st[0].item()) - st0
+    per_step = t / steps
+    return _line(args, round(tokens / t, 2), "tok/s", per_step, steps, "W4A8 int8 x int4 -> int32; bf16 draft, lm_head",
+                 "synthetic (random-init weights, seeded random prompt)",
+                 {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936, "
+                              f"MTP draft, tree (4, 3), top-k 20, prompt {args.prompt}, {steps} decode steps",
+                  "prompt": args.prompt, "steps": steps, "tokens": tokens,
+                  "accepted_per_step": round(tokens / steps, 3), "ms_per_step": round(per_step * 1e3, 4),
+                  "setup_s": round(setup, 1)})
+
+
 def bench_copy(args, dev):
     """Calibration workload: a plain device copy of 256 MiB (read 256 MiB, write 256 MiB). Its
     FETCH_SIZE / WRITE_SIZE counters give the scale factor of the traffic figures."""
@@ -303,7 +340,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1)
-    ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn"], default="mlp")
+    ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn", "stack"], default="mlp")
+    ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -317,7 +355,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
-           "attn": bench_attn}[args.workload](args, dev)
+           "attn": bench_attn, "stack": bench_stack}[args.workload](args, dev)
     print(json.dumps(res), flush=True)
 
 

@@ -354,8 +354,9 @@ extern "C" size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D
 }
 
 extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
-                               const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, const uint16_t* xv,
-                               int64_t x_head_stride, int64_t x_row_stride, const int32_t* mask, uint16_t* out,
+                               const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, int64_t xk_head_stride,
+                               int64_t xk_row_stride, const uint16_t* xv, int64_t xv_head_stride, int64_t xv_row_stride,
+                               const int32_t* mask, uint16_t* out,
                                int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint,
                                void* workspace, size_t workspace_bytes_, void* stream) {
     MDX_CHECK(q && key && value && seqlen && xk && xv && out, "null pointer");
@@ -365,7 +366,8 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     MDX_CHECK(H / Hk * S <= 64, "at most 64 query rows per kv head");
     MDX_CHECK(cap >= 1 && cap < (int64_t(1) << 30) / D, "cache capacity");
     MDX_CHECK(aligned(q, 16) && aligned(key, 16) && aligned(value, 16) && aligned(xk, 16) && aligned(xv, 16) &&
-                  q_head_stride % 8 == 0 && q_row_stride % 8 == 0 && x_head_stride % 8 == 0 && x_row_stride % 8 == 0,
+                  q_head_stride % 8 == 0 && q_row_stride % 8 == 0 && xk_head_stride % 8 == 0 &&
+                  xk_row_stride % 8 == 0 && xv_head_stride % 8 == 0 && xv_row_stride % 8 == 0,
               "16-byte aligned rows");
     const int RT = int((H / Hk * S + 15) / 16);
     const int C = plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
@@ -380,8 +382,10 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.seqlen = seqlen;
     a.xk = xk;
     a.xv = xv;
-    a.xh = a.vh = x_head_stride;
-    a.xs = a.vs = x_row_stride;
+    a.xh = xk_head_stride;
+    a.xs = xk_row_stride;
+    a.vh = xv_head_stride;
+    a.vs = xv_row_stride;
     a.mask = mask;
     a.out = out;
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);

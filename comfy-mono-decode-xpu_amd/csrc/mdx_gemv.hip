@@ -34,6 +34,7 @@
 //
 // Split-K partial sums of the waves of a work-group are int32 and are added through LDS:
 // integer addition is associative, so every split gives the same bits.
+#include <algorithm>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -178,6 +179,7 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
             }
         }
     }
+    if (!a.q) return;  // RMSNorm only (xn_out)
     if (a.rot != MDX_ROT_NONE) {
 #pragma unroll
         for (int j = 0; j < PREP_BLK; ++j) {
@@ -852,6 +854,34 @@ extern "C" int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64
     a.g_hstride = int(gate_head_stride);
     a.g_off = int(gate_offset);
     return launch_prep(a, rows, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* out, int64_t rows, int64_t K,
+                           void* stream) {
+    MDX_CHECK(x && norm_w && out, "null pointer");
+    MDX_CHECK(rows >= 0 && rows <= 65535 && K % 8 == 0 && K >= 8 && K <= 8 * PREP_THREADS * PREP_BLK,
+              "rows / K (K % 8 == 0, K <= %d)", 8 * PREP_THREADS * PREP_BLK);
+    MDX_CHECK(aligned(x, 16) && aligned(norm_w, 16) && aligned(out, 16), "16-byte aligned rows");
+    if (rows == 0) return MDX_OK;
+    PrepArgs a{x, norm_w, eps, out, nullptr, MDX_ROT_NONE, nullptr, nullptr, int(K)};
+    return launch_prep(a, rows, static_cast<hipStream_t>(stream));
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, const uint16_t* lut,
+                                                       uint16_t* out, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+        out[i] = f2bf(__fmul_rn(bf2f(lut[g[i]]), bf2f(u[i])));
+}
+
+extern "C" int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t* silu_lut, uint16_t* out, int64_t n,
+                            void* stream) {
+    MDX_CHECK(g && u && silu_lut && out && n >= 0, "null pointer / size");
+    if (n == 0) return MDX_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), g, u,
+                       silu_lut, out, n);
+    MDX_LAUNCHED();
+    return MDX_OK;
 }
 
 extern "C" size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1) {

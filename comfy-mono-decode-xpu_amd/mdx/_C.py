@@ -154,7 +154,7 @@ def _bf16_heads(t, what):
     _check(t.dtype == torch.bfloat16 and t.stride(-1) == 1, f"{what}: bf16 with a contiguous last dim")
 
 
-def _rope(qn, kn, vn, wq, wk, freqs, key, value, position, epsq, epsk, rd):
+def _rope(qn, kn, vn, wq, wk, freqs, key, value, position, epsq, epsk, rd, outs=None):
     # q/k/v as [S, H, D] or [1, S, H, D] views (a gated q is the query half of [.., H, 2 D])
     qn, kn, vn = (t[0] if t.dim() == 4 else t for t in (qn, kn, vn))
     for t, n in ((qn, "q"), (kn, "k"), (vn, "v")):
@@ -175,8 +175,13 @@ def _rope(qn, kn, vn, wq, wk, freqs, key, value, position, epsq, epsk, rd):
     if wq is not None:
         for w, n in ((wq, "weight_q"), (wk, "weight_k")):
             _check(w.dtype == torch.bfloat16 and w.is_contiguous() and w.numel() == D, f"{n}: bf16 [D]")
-    q = torch.empty(1, Hq, S, D, dtype=torch.bfloat16, device=qn.device)
-    k = torch.empty(1, Hk, S, D, dtype=torch.bfloat16, device=qn.device)
+    if outs is None:
+        q = torch.empty(1, Hq, S, D, dtype=torch.bfloat16, device=qn.device)
+        k = torch.empty(1, Hk, S, D, dtype=torch.bfloat16, device=qn.device)
+    else:
+        q, k = outs
+        _check(q.is_contiguous() and k.is_contiguous() and q.numel() == Hq * S * D and k.numel() == Hk * S * D,
+               "outputs [1, Hq, S, D], [1, Hk, S, D]")
     _lib.call("mdx_qk_norm_rope_kv", _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
               kn.stride(1), _lib.ptr(vn), vn.stride(0), vn.stride(1), _lib.ptr(wq), _lib.ptr(wk), float(epsq),
               float(epsk), _lib.ptr(freqs), fs, _lib.ptr(key), _lib.ptr(value), _lib.ptr(position), _lib.ptr(q),
@@ -190,12 +195,12 @@ def rope_kv(qn, kn, vn, freqs, key, value, position, rd):
     return _rope(qn, kn, vn, None, None, freqs, key, value, position, 1.0, 1.0, rd)
 
 
-def qk_norm_rope_kv(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd):
+def qk_norm_rope_kv(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd, outs=None):
     """Reference csrc/rope_kv.sycl:120-245: per-head Q/K RMSNorm, then rope_kv. The norm's reduction
     order is the library's own (per-lane partials in element order, then a 64-lane halving tree)."""
     _check(weightq is not None and weightk is not None, "norm weights")
     _check(epsq > 0 and epsk > 0, "positive eps")
-    return _rope(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd)
+    return _rope(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd, outs)
 
 
 def _i64(t, what):
@@ -343,7 +348,7 @@ def _attn_ws(dev, nbytes):
     return ws
 
 
-def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0):
+def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0, out=None):
     """Reference csrc/attn_dpas.sycl:269-342: decode attention of the tree-verify rows (mask int32 [S])
     or the draft row (empty mask, S = 1) over the cache prefix [0, seqlen[0]) and the admitted tree rows.
     q bf16 [1, H, S, D]; key/value bf16 [1, Hk, cap, D]; xk/xv bf16 [1, Hk, S, D]. Returns bf16
@@ -359,14 +364,17 @@ def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0):
     _check(mask.dtype == torch.int32 and mask.is_contiguous(), "int32 mask")
     merge = mask.numel() > 0
     _check(1 <= S <= 16 and H % Hk == 0 and (mask.numel() == S if merge else S == 1), "batch 1, 1..16 rows")
-    _check(xk.shape == xv.shape and xk.shape[1] == Hk and xk.shape[2] == S and xk.shape[3] == D
-           and xk.stride() == xv.stride(), "xk / xv [1, Hk, S, D]")
+    _check(xk.shape == xv.shape and xk.shape[1] == Hk and xk.shape[2] == S and xk.shape[3] == D,
+           "xk / xv [1, Hk, S, D]")
     _check((H // Hk) * S <= 64, "at most 64 query rows per kv head")
-    out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=q.device)
+    if out is None:
+        out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=q.device)
+    _check(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == S * H * D, "out bf16 [1, S, H * D]")
     need = _lib.lib().mdx_attn_workspace(H, Hk, S, D, cap, int(chunks_hint))
     ws = _attn_ws(q.device, need)
     _lib.call("mdx_attn_decode", _lib.ptr(q), q.stride(1), q.stride(2), _lib.ptr(key), _lib.ptr(value), _lib.ptr(seqlen),
-              _lib.ptr(xk), _lib.ptr(xv), xk.stride(1), xk.stride(2), _lib.ptr(mask) if merge else None, _lib.ptr(out),
+              _lib.ptr(xk), xk.stride(1), xk.stride(2), _lib.ptr(xv), xv.stride(1), xv.stride(2),
+              _lib.ptr(mask) if merge else None, _lib.ptr(out),
               H, Hk, S, D, cap, int(chunks_hint), _lib.ptr(ws), ws.numel(), _lib.stream_of(q))
     return out
 
@@ -588,3 +596,23 @@ def layer_gdn_core(like, rows):
     """Reference csrc/mono_gdn.sycl:702-704: the GDN core output of the last layer_gdn on this device
     (rows 0..rows-1), valid until the next call."""
     return _buf(_scratch(like.device)["core"], rows, 4096)
+
+
+def rmsnorm(x, w, eps, out=None):
+    """bf16 RMSNorm of rows in the library's fixed order (the draft block's norms)."""
+    K = x.shape[-1]
+    rows = x.numel() // K
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and w.numel() == K, "x bf16 [.., K], w bf16 [K]")
+    if out is None:
+        out = torch.empty_like(x)
+    _lib.call("mdx_rmsnorm", _lib.ptr(x), _lib.ptr(w), float(eps), _lib.ptr(out), rows, K, _lib.stream_of(x))
+    return out
+
+
+def silu_mul(g, u, silu_lut, out=None):
+    """bf16(silu_lut[g] * u) elementwise (the draft block's SwiGLU)."""
+    _check(g.dtype == torch.bfloat16 and u.dtype == torch.bfloat16 and g.numel() == u.numel(), "bf16 g / u")
+    if out is None:
+        out = torch.empty_like(g)
+    _lib.call("mdx_silu_mul", _lib.ptr(g), _lib.ptr(u), _lib.ptr(silu_lut), _lib.ptr(out), g.numel(), _lib.stream_of(g))
+    return out

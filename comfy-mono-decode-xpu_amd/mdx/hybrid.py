@@ -1,0 +1,387 @@
+"""A synthetic Qwen3.5-style W4A8 hybrid model decoded with MTP tree verification on one MI355X.
+
+Shape (defaults): 32 layers, every 4th full attention (32 q / 8 kv heads, head_dim 128, partial RoPE
+theta 1e7, Q/K RMSNorm), the rest Gated-DeltaNet (16 key / 32 value heads of 128, conv 4); hidden
+4096, SwiGLU MLP 12288; random GPTQ int4 weights (G128 fp16 scales, tile-major); a 1-layer bf16 MTP
+draft block; a bf16 lm_head over vocab 151936; an 8-row draft tree (tree_spec (4, 3): two drafts per
+step); top-k 20 sampling.
+
+One decode step (comfy_mono_decode_xpu/mtp_loop.py:187-489, graph_step.py:62-127):
+  drafts   for depth k: mtp_prep_draft -> MTP block (embed + hidden norms, fc, attention layer, MLP)
+           -> final norm -> lm_head -> fast_topk(width_k): the tree's children at depth k + 1;
+  verify   mtp_prep_verify -> 32 layers over the tree rows (layer_pre / qk_norm_rope_kv / attn_dpas /
+           layer_post for attention layers, layer_gdn for GDN layers) -> final norm -> lm_head ->
+           topk_rows(20) -> Gumbel-max sampling -> mtp_accept (counters, ctl, next token, hidden row,
+           KV slot moves).
+Every counter lives on the device, so a step is one captured HIP graph; two graphs alternate the
+replay parity of the GDN buffers. The host only replays graphs.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _C, _lib, _tree, layout
+
+
+@dataclass
+class HybridConfig:
+    layers: int = 32
+    hidden: int = 4096
+    inter: int = 12288
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    rotary: int = 64
+    theta: float = 1e7
+    gdn_key_heads: int = 16
+    gdn_value_heads: int = 32
+    vocab: int = 151936
+    widths: tuple = (4, 3)
+    slots: int = 16
+    top_k: int = 20
+    temperature: float = 1.0
+    greedy: bool = False          # take the top-1 instead of sampling
+    eps: float = 1e-6
+    cap: int = 2048
+
+    def attention(self, i):
+        return i % 4 == 3
+
+
+def _gptq(N, K, gen, dev):
+    q = torch.randint(-8, 8, (N, K), generator=gen, device=dev, dtype=torch.int8)
+    s = (torch.rand(N, K // 128, generator=gen, device=dev) * 0.015 + 0.005).half()
+    packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=True)
+    del q
+    return layout.W4(layout.tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE)
+
+
+def _norm(n, gen, dev, spread=0.02):
+    return (1 + spread * torch.randn(n, generator=gen, device=dev)).bfloat16()
+
+
+def _bf16w(N, K, gen, dev, std):
+    return layout.tile_major_bf16((torch.randn(N, K, generator=gen, device=dev) * std).bfloat16())
+
+
+def tree_tensors(widths, slots, dev):
+    """Parents, depths, verify program, ancestor masks, children table and, per depth, the rows that
+    receive the draft's candidates (chain child first) of tree_spec(widths)."""
+    parents, children, depth, chain = _tree.tree_from_spec(_tree.spec_of_widths(widths), slots)
+    R = 1 + sum(widths)
+    prog = _tree.verify_program(parents[:R], R)
+    mask = []
+    for r in range(R):
+        p = parents[r]
+        mask.append((mask[p] if p >= 0 else 0) | (1 << r))
+    ch = torch.full((slots, slots), -1, dtype=torch.int32)
+    for r, cs in enumerate(children[:slots]):
+        for j, c in enumerate(cs):
+            ch[r, j] = c
+    chain_nodes = [0]
+    while children[chain_nodes[-1]]:
+        chain_nodes.append(children[chain_nodes[-1]][0])
+    fill = [torch.tensor(children[chain_nodes[k]], dtype=torch.int64, device=dev) for k in range(len(widths))]
+    tree_ctl = torch.tensor(parents[:R] + [-1] * (slots - R) + prog + [0] * (slots - R), dtype=torch.int32, device=dev)
+    return dict(R=R, depth=chain, parents=parents[:R], prog=prog,
+                mask=torch.tensor(mask, dtype=torch.int32, device=dev), children=ch.reshape(-1).to(dev),
+                tree_pos=torch.tensor(depth[:R], dtype=torch.int64, device=dev), tree_ctl=tree_ctl, fill=fill)
+
+
+def rope_table(cfg, dev):
+    """[cap, rd/2, 2, 2] rotation matrices [[cos, -sin], [sin, cos]] of each position."""
+    half = cfg.rotary // 2
+    inv = cfg.theta ** (-torch.arange(half, dtype=torch.float64) * 2 / cfg.rotary)
+    ang = torch.arange(cfg.cap, dtype=torch.float64)[:, None] * inv[None, :]
+    c, s = torch.cos(ang), torch.sin(ang)
+    return torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2).float().contiguous().to(dev)
+
+
+class HybridModel:
+    """Random-init weights of the hybrid stack and its decode state on one device."""
+
+    def __init__(self, cfg: HybridConfig, device, seed=5):
+        self.cfg = c = cfg
+        dev = self.dev = torch.device(device)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        H, I = c.hidden, c.inter
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        hk, hv = c.gdn_key_heads, c.gdn_value_heads
+        self.gdn_ch = 2 * hk * 128 + hv * 128
+        self.embed = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.5).bfloat16()
+        self.lm_head = _bf16w(c.vocab, H, gen, dev, 0.02)
+        self.final_norm = _norm(H, gen, dev)
+        self.h256 = layout.regular_hadamard(dev)
+        self.silu = layout.silu_lut(dev)
+        self.sig = torch.sigmoid(layout.bf16_all(dev)).contiguous()
+        self.layers = []
+        for i in range(c.layers):
+            L = dict(norm_in=_norm(H, gen, dev), norm_post=_norm(H, gen, dev), g=_gptq(I, H, gen, dev),
+                     u=_gptq(I, H, gen, dev), d=_gptq(H, I, gen, dev))
+            L["u"].cb = L["d"].cb = L["g"].cb
+            if c.attention(i):
+                L.update(q=_gptq(qd, H, gen, dev), k=_gptq(kd, H, gen, dev), v=_gptq(kd, H, gen, dev),
+                         o=_gptq(H, qd, gen, dev), qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1))
+            else:
+                L.update(qkv=_gptq(self.gdn_ch, H, gen, dev), z=_gptq(hv * 128, H, gen, dev), o=_gptq(H, hv * 128, gen, dev),
+                         wab=(torch.randn(2 * hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
+                         conv_w=(torch.randn(self.gdn_ch, 4, generator=gen, device=dev) * 0.5).bfloat16(),
+                         dt_bias=torch.rand(hv, generator=gen, device=dev) * 2 - 1,
+                         g_decay=-torch.exp(torch.rand(hv, generator=gen, device=dev) * 1.5 - 1),
+                         gnorm=_norm(128, gen, dev, 0.1))
+            self.layers.append(L)
+        # the MTP draft block (bf16)
+        self.mtp = dict(norm_e=_norm(H, gen, dev), norm_h=_norm(H, gen, dev), fc=_bf16w(H, 2 * H, gen, dev, 0.02),
+                        norm_in=_norm(H, gen, dev), qkv=_bf16w(qd + 2 * kd, H, gen, dev, 0.02),
+                        qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1),
+                        o=_bf16w(H, qd, gen, dev, 0.02), norm_post=_norm(H, gen, dev),
+                        gu=_bf16w(2 * I, H, gen, dev, 0.02), d=_bf16w(H, I, gen, dev, 0.02), norm_f=_norm(H, gen, dev))
+        self.ftab = rope_table(c, dev)
+        self._state(gen)
+
+    # ---- decode state --------------------------------------------------------------------------
+    def _state(self, gen):
+        c, dev = self.cfg, self.dev
+        S = c.slots
+        self.tree = tree_tensors(c.widths, S, dev)
+        R = self.R = self.tree["R"]
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.kv = [None] * c.layers
+        self.gdn = [None] * c.layers
+        for i in range(c.layers):
+            if c.attention(i):
+                self.kv[i] = (torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf),
+                              torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf))
+            else:
+                hv, hk = c.gdn_value_heads, c.gdn_key_heads
+                self.gdn[i] = dict(conv=torch.zeros(self.gdn_ch, 3, **bf), pb=torch.zeros(2, S, self.gdn_ch, **bf),
+                                   qb=torch.zeros(2, S, self.gdn_ch, **bf),
+                                   rec=torch.randn(hv, 128, 128, generator=gen, device=dev) * 0.1,
+                                   gates=torch.zeros(2, S, hv, 2, device=dev), sums=torch.zeros(2, S, hk, 2, device=dev))
+        self.mkv = (torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf),
+                    torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf))
+        ptrs = []
+        for kv in self.kv:
+            if kv is not None:
+                ptrs += [kv[0].data_ptr(), kv[1].data_ptr()]
+        self.kv_ptrs = torch.tensor([p - (1 << 64) if p >= (1 << 63) else p for p in ptrs], dtype=torch.int64, device=dev)
+        i64 = dict(dtype=torch.int64, device=dev)
+        self.st = torch.zeros(4, **i64)
+        self.ctl = torch.zeros(2 + 3 * S, dtype=torch.int32, device=dev)
+        self.result = torch.zeros(S + 24, **i64)
+        self.nt = torch.zeros(1, 1, **i64)
+        self.hbuf = torch.zeros(1, c.hidden, **bf)
+        self.vtok = torch.zeros(1, R, **i64)
+        self.toks = torch.zeros(1, R, **i64)
+        self.apos = torch.zeros(R, **i64)
+        self.aseq = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.vpos = torch.zeros(1, R, **i64)
+        self.vfreqs = torch.zeros(R, c.rotary // 2, 2, 2, device=dev)
+        self.x = torch.zeros(R, c.hidden, **bf)
+        self.logits = torch.zeros(R, c.vocab, **bf)
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        # MTP block buffers (up to `slots` rows: one per draft, a chain of rows in the prefill)
+        self.dfreqs = torch.zeros(1, 1, 1, c.rotary // 2, 2, 2, device=dev)
+        self.mpos = torch.zeros(S, **i64)
+        self.mseq = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.dh = torch.zeros(S, c.hidden, **bf)
+        self.dcat = torch.zeros(S, 2 * c.hidden, **bf)
+        self.dx = torch.zeros(S, c.hidden, **bf)
+        self.dxn = torch.zeros(S, c.hidden, **bf)
+        self.dqkv = torch.zeros(S, qd + 2 * kd, **bf)
+        self.dy = torch.zeros(S, qd, **bf)
+        self.dx1 = torch.zeros(S, c.hidden, **bf)
+        self.dgu = torch.zeros(S, 2 * c.inter, **bf)
+        self.dact = torch.zeros(S, c.inter, **bf)
+        self.dg = torch.zeros(S, c.inter, **bf)
+        self.du = torch.zeros(S, c.inter, **bf)
+        self.dlogits = torch.zeros(1, c.vocab, **bf)
+        self.empty_mask = torch.empty(0, dtype=torch.int32, device=dev)
+        self.graphs = {}
+
+    # ---- the pieces of a step ------------------------------------------------------------------
+    def _attn_layer(self, i, x, R, mask, seq, pos, freqs):
+        c, L = self.cfg, self.layers[i]
+        key, value = self.kv[i]
+        xn = torch.empty(R, c.hidden, dtype=torch.bfloat16, device=self.dev)
+        q, s = _C.rms_rot_quant(x, L["norm_in"], c.eps, _lib.ROT_NONE, None, xn_out=xn)
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        qkv = [torch.empty(R, n, dtype=torch.bfloat16, device=self.dev) for n in (qd, kd, kd)]
+        _C.stream_gemv(q, s, [L["q"], L["k"], L["v"]], qkv)
+        qv = qkv[0].view(1, R, c.heads, c.head_dim)
+        kv_ = qkv[1].view(1, R, c.kv_heads, c.head_dim)
+        vv = qkv[2].view(1, R, c.kv_heads, c.head_dim)
+        qo = torch.empty(1, c.heads, R, c.head_dim, dtype=torch.bfloat16, device=self.dev)
+        ko = torch.empty(1, c.kv_heads, R, c.head_dim, dtype=torch.bfloat16, device=self.dev)
+        _C.qk_norm_rope_kv(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, outs=(qo, ko))
+        y = torch.empty(1, R, qd, dtype=torch.bfloat16, device=self.dev)
+        _C.attn_dpas(qo, key, value, seq, ko, vv.transpose(1, 2), mask, 0, out=y)
+        _C._layer_post(x, y.view(R, qd), None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"],
+                       L["d"], 6)
+
+    def _gdn_layer(self, i, x, R):
+        c, L, G = self.cfg, self.layers[i], self.gdn[i]
+        sc = _C._scratch(self.dev)
+        xn, q, s = _C._buf(sc["xn"], R, c.hidden), _C._buf(sc["q1"], R, c.hidden), sc["s"][:R]
+        _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn), None,
+                  _lib.ROT_NONE, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
+        hv = c.gdn_value_heads
+        ab = _C._buf(sc["ab"], R, 2 * hv)
+        _C.bf16_linear(xn, L["wab"], tiled=False, out=ab)
+        proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
+        _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
+        core = _C._buf(sc["core"], R, hv * 128)
+        _C.gdn_core(proj, z, ab, L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
+                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core)
+        _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6)
+
+    def verify_layers(self, x, R, mask, seq, pos, freqs):
+        for i in range(self.cfg.layers):
+            if self.cfg.attention(i):
+                self._attn_layer(i, x, R, mask, seq, pos, freqs)
+            else:
+                self._gdn_layer(i, x, R)
+
+    def mtp_block(self, n, tok, h, freqs, kvpos, seq, mask):
+        """The MTP block over n rows (tokens `tok` [n], hidden rows `h` [n, H]): writes the MTP KV at
+        kvpos, attends the MTP cache prefix [0, seq) (and, with a mask, the block's own rows); leaves
+        the output hidden rows in self.dh[:n]."""
+        c, M = self.cfg, self.mtp
+        H = c.hidden
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        cat = _C._buf(self.dcat, n, 2 * H)
+        e = torch.index_select(self.embed, 0, tok.view(-1))
+        ca = cat.view(n, 2, H)
+        ea, hb = torch.empty(n, H, dtype=torch.bfloat16, device=self.dev), torch.empty(n, H, dtype=torch.bfloat16,
+                                                                                        device=self.dev)
+        _C.rmsnorm(e, M["norm_e"], c.eps, out=ea)
+        _C.rmsnorm(h, M["norm_h"], c.eps, out=hb)
+        ca[:, 0].copy_(ea)
+        ca[:, 1].copy_(hb)
+        x = _C._buf(self.dx, n, H)
+        xn = _C._buf(self.dxn, n, H)
+        _C.bf16_linear(cat, M["fc"], out=x)
+        _C.rmsnorm(x, M["norm_in"], c.eps, out=xn)
+        qkv = _C._buf(self.dqkv, n, qd + 2 * kd)
+        _C.bf16_linear(xn, M["qkv"], out=qkv)
+        qv = qkv[:, :qd].view(1, n, c.heads, c.head_dim)
+        kv_ = qkv[:, qd:qd + kd].view(1, n, c.kv_heads, c.head_dim)
+        vv = qkv[:, qd + kd:].view(1, n, c.kv_heads, c.head_dim)
+        mk, mv = self.mkv
+        qo = torch.empty(1, c.heads, n, c.head_dim, dtype=torch.bfloat16, device=self.dev)
+        ko = torch.empty(1, c.kv_heads, n, c.head_dim, dtype=torch.bfloat16, device=self.dev)
+        _C.qk_norm_rope_kv(qv, kv_, vv, M["qn"], M["kn"], freqs, mk, mv, kvpos, c.eps, c.eps, c.rotary, outs=(qo, ko))
+        y = _C._buf(self.dy, n, qd)
+        _C.attn_dpas(qo, mk, mv, seq, ko, vv.transpose(1, 2), self.empty_mask if mask is None else mask, 0,
+                     out=y.view(1, n, qd))
+        x1 = _C._buf(self.dx1, n, H)
+        _C.bf16_linear(y, M["o"], residual=x, out=x1)
+        _C.rmsnorm(x1, M["norm_post"], c.eps, out=xn)
+        gu = _C._buf(self.dgu, n, 2 * c.inter)
+        _C.bf16_linear(xn, M["gu"], out=gu)
+        act = _C._buf(self.dact, n, c.inter)
+        g_, u_ = _C._buf(self.dg, n, c.inter), _C._buf(self.du, n, c.inter)
+        g_.copy_(gu[:, :c.inter])
+        u_.copy_(gu[:, c.inter:])
+        _C.silu_mul(g_, u_, self.silu, out=act)
+        _C.bf16_linear(act, M["d"], residual=x1, out=_C._buf(self.dh, n, H))
+
+    def draft(self, k, tok, h, width):
+        """Draft depth k: the MTP block on the chain token `tok` [1] and hidden row `h` [1, H] at the
+        device positions of mtp_prep_draft, then the final norm, the lm_head and the top-`width`."""
+        c = self.cfg
+        _C.mtp_prep_draft(self.st, k, self.ftab.view(1, 1, c.cap, c.rotary // 2, 2, 2), self.dfreqs, self.mpos, self.mseq)
+        self.mtp_block(1, tok, h, self.dfreqs.view(1, c.rotary // 2, 2, 2), self.mpos[:1], self.mseq, None)
+        xf = _C.rmsnorm(self.dh[:1], self.mtp["norm_f"], c.eps)
+        _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
+        return _C.fast_topk(self.dlogits, width, False)[1]
+
+    def step(self, parity):
+        """One decode step on the device (drafts, verify, sampling, accept)."""
+        c, T = self.cfg, self.tree
+        R = self.R
+        # drafts: depth k proposes the children of chain node k
+        tok, h = self.nt.view(-1), self.hbuf
+        self.vtok[0, 0:1].copy_(self.nt.view(-1))
+        for k, w in enumerate(c.widths):
+            top = self.draft(k, tok, h, w)
+            self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
+            tok, h = top.view(-1)[:1], self.dh[:1]
+        # verify
+        _C.mtp_prep_verify(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0)
+        torch.index_select(self.ftab, 0, self.vpos.view(-1), out=self.vfreqs)
+        torch.index_select(self.embed, 0, self.vtok.view(-1), out=self.x)
+        self.verify_layers(self.x, R, T["mask"], self.aseq, self.apos, self.vfreqs)
+        xf = _C.rmsnorm(self.x, self.final_norm, c.eps)
+        _C.bf16_linear(xf, self.lm_head, out=self.logits)
+        vals, idx = _C.topk_rows(self.logits, c.top_k)
+        if c.greedy:
+            self.toks.copy_(idx[:, :1].reshape(1, R))
+        else:
+            # Gumbel-max over the top-k: a sample of softmax(vals / T) restricted to the top k
+            g = -torch.log(-torch.log(torch.rand(R, c.top_k, device=self.dev).clamp_(1e-20, 1.0)))
+            pick = torch.argmax(vals / c.temperature + g, dim=1, keepdim=True)
+            self.toks.copy_(torch.gather(idx, 1, pick).view(1, R))
+        _C.mtp_accept(self.st, self.toks, self.vtok, None, T["children"], R, T["depth"], self.x, self.nt,
+                      self.hbuf.view(1, 1, -1), self.ctl, self.kv_ptrs, c.kv_heads, c.cap, c.head_dim, self.result)
+
+    # ---- prefill (not timed) -------------------------------------------------------------------
+    def prefill(self, prompt):
+        """Feed prompt[:-1] through the verify path as chains of up to `slots` rows, each committed in
+        full (the next chain replays it), and the MTP block over the same chains (hidden row of
+        position p with token p + 1). The last prompt token is the first decode step's root row."""
+        c = self.cfg
+        S = c.slots
+        dev = self.dev
+        prompt = prompt.to(dev)
+        body = prompt[:-1]
+        n0, parity = 0, 0
+        while n0 < body.numel():
+            n = min(S, body.numel() - n0)
+            chain_ctl = torch.tensor(list(range(-1, n - 1)) + [-1] * (S - n) + [r | 32 for r in range(n)] + [0] * (S - n),
+                                     dtype=torch.int32, device=dev)
+            tpos = torch.arange(n, dtype=torch.int64, device=dev)
+            apos = torch.empty(n, dtype=torch.int64, device=dev)
+            vpos = torch.empty(1, n, dtype=torch.int64, device=dev)
+            _C.mtp_prep_verify(self.st, apos, self.aseq, vpos, tpos, self.ctl, chain_ctl, parity, 0)
+            freqs = torch.index_select(self.ftab, 0, vpos.view(-1))
+            x = torch.index_select(self.embed, 0, body[n0:n0 + n])
+            mask = torch.tensor([(1 << (r + 1)) - 1 for r in range(n)], dtype=torch.int32, device=dev)
+            self.verify_layers(x, n, mask, self.aseq, apos, freqs)
+            # the MTP block over the chain: hidden of position p with token p + 1
+            st1 = int(self.st[1].item())
+            kvpos = torch.arange(st1, st1 + n, dtype=torch.int64, device=dev)
+            seq = torch.tensor([st1], dtype=torch.int32, device=dev)
+            self.mtp_block(n, prompt[n0 + 1:n0 + 1 + n], x, freqs, kvpos, seq, mask)
+            self.st[1] += n
+            # commit the whole chain: the next step replays it
+            self.st[0] += n
+            self.ctl[0] = n
+            self.ctl[2:2 + S] = torch.arange(S, dtype=torch.int32, device=dev)
+            parity ^= 1
+            self.hbuf.copy_(x[n - 1:n])
+            n0 += n
+        self.nt.fill_(int(prompt[-1].item()))
+        self.parity = parity
+
+    # ---- graphs ----------------------------------------------------------------------------------
+    def capture(self):
+        """Capture one step per parity (after an eager warm-up of each)."""
+        s = torch.cuda.Stream(self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            for p in (self.parity, self.parity ^ 1):
+                self.step(p)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        for p in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.step(p)
+            self.graphs[p] = g
+
+    def replay(self, steps):
+        for _ in range(steps):
+            self.graphs[self.parity].replay()
+            self.parity ^= 1

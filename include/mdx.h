@@ -207,14 +207,16 @@ size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t c
  *   bf16(sum p V / sum p), or 0 if the row admits no token. P is rounded to bf16 for the P.V product;
  *   partial softmax states merge in fp32 (tolerance parity against a float64 reference).
  * q bf16 [H, S, D] (head / row strides in elements, rows contiguous); key/value bf16 [Hk, cap, D]
- * contiguous; xk/xv bf16 [Hk, S, D] (strides as given); mask int32 [S]; out bf16 [S, H, D].
+ * contiguous; xk/xv bf16 [Hk, S, D] (head / row strides as given, each); mask int32 [S]; out bf16
+ * [S, H, D].
  * D in {64, 128, 256}; 1 <= S <= 16; (H / Hk) * S <= 64. seqlen is read on the device.
  * chunks_hint: 0 plans the context split (chunks of >= 128 tokens per wave); n > 0 splits the context
  * into at most n chunks per kv head of >= 32 tokens per wave (as the reference's chunks_hint steers
  * its split). */
 int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
-                    const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, const uint16_t* xv,
-                    int64_t x_head_stride, int64_t x_row_stride, const int32_t* mask, uint16_t* out, int64_t H,
+                    const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, int64_t xk_head_stride,
+                    int64_t xk_row_stride, const uint16_t* xv, int64_t xv_head_stride, int64_t xv_row_stride,
+                    const int32_t* mask, uint16_t* out, int64_t H,
                     int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint, void* workspace,
                     size_t workspace_bytes, void* stream);
 
@@ -260,6 +262,17 @@ int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* ab, co
 int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64_t gate_row_stride, int64_t gate_head,
                        int64_t gate_head_stride, int64_t gate_offset, const uint16_t* sig_lut, const uint16_t* h,
                        int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
+
+/* RMSNorm of bf16 rows in the library's fixed order (out = bf16((x * r) * w), r = 1 / sqrt(mean(x^2) +
+ * eps)). Serves the bf16 MTP draft block (comfy_mono_decode_xpu/draft_head.py:179-232: its embed / hidden
+ * / input / post / final norms). x, out bf16 [rows, K], K % 8 == 0, 16-byte aligned. */
+int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* out, int64_t rows, int64_t K,
+                void* stream);
+
+/* out[i] = bf16(float(silu_lut[g[i]]) * float(u[i])) over n bf16 elements (the draft block's SwiGLU,
+ * comfy_mono_decode_xpu/draft_head.py:214-226; the same rule as mono_mlp's gate/up epilogue). */
+int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t* silu_lut, uint16_t* out, int64_t n,
+                 void* stream);
 
 #ifdef __cplusplus
 }
