@@ -31,7 +31,10 @@ constexpr int MAXS = 16;
 struct GdnArgs {
     const uint16_t* proj;   // [R, C]
     const uint16_t* z;      // [R, HV * 128]
-    const uint16_t* ab;     // [R, 2 HV]: a then b
+    const uint16_t* xn;     // [R, K]: the normalised layer input (a = xn . wa[h], b = xn . wb[h])
+    const uint16_t* wa;     // [HV, K]
+    const uint16_t* wb;     // [HV, K]
+    int K;
     const uint16_t* conv_w; // [C, 4]
     uint16_t* conv_state;   // [C, 3]
     uint16_t* pb;           // [2][slots][C]
@@ -53,61 +56,79 @@ __device__ __forceinline__ bool ctl_ok(const GdnArgs& a) {
     return p >= 0 && p <= 1 && pending >= 0 && pending <= a.slots;
 }
 
+// One thread per channel (it owns the channel's history); the work-group stages its 256 channels'
+// projection rows in LDS, so the ancestors of a tree row are LDS reads by index.
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= a.C || !ctl_ok(a)) return;
-    const int S = a.slots, pending = a.ctl[0], p = a.ctl[1];
-    const int* acc = a.ctl + 2;
-    const int* parent = a.ctl + 2 + S;
+    __shared__ int sctl[2 + 3 * MAXS];
+    __shared__ uint16_t prl[MAXS][256];
+    const int t = threadIdx.x;
+    const int c = blockIdx.x * 256 + t;
+    if (t < 2 + 3 * a.slots) sctl[t] = a.ctl[t];
+    const int R = a.R;
     const int64_t C = a.C;
-    uint16_t old[CW], hist[CW];
+    const bool cl = c < a.C;
+    // every load up front (clamped addresses, no branches): this step's projections of the channel,
+    // its history, the previous step's accepted rows, its weights
+    uint16_t pr[MAXS];
 #pragma unroll
-    for (int r = 0; r < CW; ++r) old[r] = a.conv_state[c * CW + r];
-    // the history shifted by the previous step's accepted rows
+    for (int r = 0; r < MAXS; ++r) pr[r] = a.proj[(r < R ? r : R - 1) * C + (cl ? c : 0)];
+#pragma unroll
+    for (int r = 0; r < MAXS; ++r) prl[r][t] = pr[r];
+    __syncthreads();
+    const int S = a.slots, pending = sctl[0], p = sctl[1];
+    if (!cl || !(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;
+    const int* acc = sctl + 2;
+    const int* parent = sctl + 2 + S;
+    uint16_t old[CW], prevacc[CW];
 #pragma unroll
     for (int r = 0; r < CW; ++r) {
-        const int j = pending + r;
-        if (j < CW) {
-            hist[r] = old[j < 0 ? 0 : (j > CW - 1 ? CW - 1 : j)];
-        } else {
-            int slot = acc[j - CW];
-            slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
-            hist[r] = a.pb[((1 - p) * S + slot) * C + c];
-        }
+        old[r] = a.conv_state[c * CW + r];
+        const int j = pending + r - CW;
+        int slot = acc[j < 0 ? 0 : j];
+        slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
+        prevacc[r] = a.pb[((1 - p) * S + slot) * C + c];
     }
-#pragma unroll
-    for (int r = 0; r < CW; ++r) a.conv_state[c * CW + r] = hist[r];
     float w[CW + 1];
 #pragma unroll
     for (int d = 0; d <= CW; ++d) w[d] = bf2f(a.conv_w[c * (CW + 1) + d]);
+    // the history shifted by the previous step's accepted rows
+    uint16_t hist[CW];
+#pragma unroll
+    for (int r = 0; r < CW; ++r) {
+        const int j = pending + r;
+        hist[r] = j == 0 ? old[0] : (j == 1 ? old[1] : (j == 2 ? old[2] : prevacc[r]));
+    }
+#pragma unroll
+    for (int r = 0; r < CW; ++r) a.conv_state[c * CW + r] = hist[r];
     for (int ts = 0; ts < S; ++ts) {
-        uint16_t out = 0, pr = 0;
-        if (ts < a.R) {
-            pr = a.proj[ts * C + c];
+        uint16_t out = 0;
+        if (ts < R) {
             int anc = ts, miss = 0;
             float sum = 0.f;
 #pragma unroll
             for (int d = 0; d <= CW; ++d) {
                 if (d > 0) {
                     anc = anc >= 0 ? parent[anc] : -1;
-                    anc = anc >= a.R ? -1 : anc;  // a parent is an earlier row of this step
+                    anc = anc >= R ? -1 : anc;  // a parent is an earlier row of this step
                     miss += anc < 0;
                 }
-                const float v = anc >= 0 ? bf2f(a.proj[anc * C + c]) : bf2f(hist[CW - miss]);
+                const int hm = CW - miss;
+                const uint16_t hv = hm == 0 ? hist[0] : (hm == 1 ? hist[1] : hist[2]);
+                const float v = anc >= 0 ? bf2f(prl[anc][t]) : bf2f(hv);
                 sum = fmaf(v, w[CW - d], sum);
             }
             const float y = bfround(sum);
             out = f2bf(__fdiv_rn(y, __fadd_rn(1.f, expf(-y))));
         }
         a.qb[(p * S + ts) * C + c] = out;
-        a.pb[(p * S + ts) * C + c] = pr;
+        a.pb[(p * S + ts) * C + c] = ts < R ? prl[ts][t] : uint16_t(0);
     }
 }
 
 __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
-    __shared__ float kvec[2 * MAXS][DH], qvec[MAXS][DH], vvec[2 * MAXS][DH], rawb[MAXS][DH];
+    __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH], vvec[2 * MAXS][DH], rawb[MAXS][DH];
     __shared__ float mbuf[2][RG][DH], rbuf[2][RG][DH];
-    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], csum[MAXS][2], rss[MAXS];
+    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], cab[MAXS][2], csum[MAXS][2], rss[MAXS];
     __shared__ int ectl[2 + 3 * MAXS];
     if (!ctl_ok(a)) return;
     const int t = threadIdx.x, h = blockIdx.x;
@@ -128,12 +149,74 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
     const int E = E0 + E1;
     auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
 
-    // this step's gates and sums (parity p)
+    // this step's a / b projections and q / k sums of squares, one wave per dot product: lane l sums
+    // its elements in order (a / b: the 8-element blocks l + 64 j; sums: elements l and l + 64), then a
+    // halving tree over the lanes (the library's fixed order)
+    const int lane = t & 63, wv = t >> 6;
+    // a / b: 2 R dot products of length K over the 8 waves, all of a wave's loads issued first
+    constexpr int ABJ = (2 * MAXS + GT / 64 - 1) / (GT / 64);  // jobs per wave, at most
+    for (int j0 = 0; j0 < ABJ; j0 += 2) {
+        uint4 xv[2][8], wvv[2][8];
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int job = wv + (GT / 64) * (j0 + jj);
+            const bool live = job < 2 * R;
+            const int kind = live ? job / R : 0, ts = live ? job % R : 0;
+            const uint16_t* w = (kind == 0 ? a.wa : a.wb) + int64_t(h) * a.K;
+            const uint16_t* x = a.xn + int64_t(ts) * a.K;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int b0 = lane + 64 * i;
+                const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
+                xv[jj][i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
+                wvv[jj][i] = *reinterpret_cast<const uint4*>(w + 8 * bc);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int job = wv + (GT / 64) * (j0 + jj);
+            float part = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (lane + 64 * i >= a.K / 8) continue;  // (a dead job's sum is discarded)
+                const uint32_t xw[4] = {xv[jj][i].x, xv[jj][i].y, xv[jj][i].z, xv[jj][i].w};
+                const uint32_t ww[4] = {wvv[jj][i].x, wvv[jj][i].y, wvv[jj][i].z, wvv[jj][i].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xe = __uint_as_float((e & 1) ? (xw[e >> 1] & 0xFFFF0000u) : (xw[e >> 1] << 16));
+                    const float we = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
+                    part = fmaf(xe, we, part);
+                }
+            }
+            for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
+            if (lane == 0 && job < 2 * R) cab[job % R][job / R] = bfround(part);  // a, b as bf16
+        }
+    }
+    // q / k sums of squares of this step's rows: 2 R jobs, one per wave pass, loads first
+    {
+        float v0[4], v1[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int job = wv + (GT / 64) * jj;
+            const bool live = job < 2 * R;
+            const uint16_t* src = a.qb + (p * S + (live ? job % R : 0)) * C + (live ? job / R : 0) * KD + kh * DH;
+            v0[jj] = bf2f(src[lane]);
+            v1[jj] = bf2f(src[lane + 64]);  // (a dead job's sum is discarded)
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int job = wv + (GT / 64) * jj;
+            float part = fmaf(v1[jj], v1[jj], __fmul_rn(v0[jj], v0[jj]));
+            for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
+            if (lane == 0 && job < 2 * R) csum[job % R][job / R] = part;
+        }
+    }
+    __syncthreads();
     if (t < S) {
         float decay = 0.f, beta = 0.f;
         if (t < R) {
-            const float av = __fadd_rn(bf2f(a.ab[t * 2 * HV + h]), a.dt_bias[h]);
-            const float bv = bf2f(a.ab[t * 2 * HV + HV + h]);
+            const float av = __fadd_rn(cab[t][0], a.dt_bias[h]);
+            const float bv = cab[t][1];
             const float sp = av > 20.f ? av : log1pf(expf(av));
             decay = expf(__fmul_rn(a.g_decay[h], sp));
             beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bv))));
@@ -144,17 +227,8 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
         cgate[t][1] = beta;
     } else if (t >= 64 && t < 64 + 2 * S) {
         const int which = (t - 64) / S, ts = (t - 64) % S;
-        float s2 = 0.f;
-        if (ts < R) {
-            const uint16_t* src = a.qb + (p * S + ts) * C + which * KD + kh * DH;
-            for (int d = 0; d < DH; ++d) {
-                const float v = bf2f(src[d]);
-                s2 = fmaf(v, v, s2);
-            }
-        }
         // the heads of one key head write identical values
-        a.sums[((p * S + ts) * HK + kh) * 2 + which] = s2;
-        csum[ts][which] = s2;
+        a.sums[((p * S + ts) * HK + kh) * 2 + which] = ts < R ? csum[ts][which] : 0.f;
     }
     __syncthreads();
     // the entries' inputs: k * ki, (q * scale) * qi, v, decay, beta
@@ -168,6 +242,7 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
             egate[e][1] = cgate[ts][1];
         }
     }
+#pragma unroll 8
     for (int i = t; i < E * DH; i += GT) {
         const int e = i / DH, d = i % DH, ts = slot_of(e);
         const bool verify = e >= E0;
@@ -193,36 +268,51 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
         const bool verify = e >= E0;
         const bool commit = !verify || (prog[e - E0] & 32);
         const float decay = egate[e][0], beta = egate[e][1];
-        const float* kk = kvec[e] + rg * RPG;
-        float mem = 0.f;
+        // this entry's k^ (and q^) rows of the thread's row group, as 16-byte LDS broadcasts issued together
+        float kr[RPG], qr[RPG];
+        const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * RPG);
+#pragma unroll
+        for (int j = 0; j < RPG / 4; ++j) {
+            const float4 v = k4[j];
+            kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
+        }
+        if (verify) {
+            const float4* q4 = reinterpret_cast<const float4*>(qvec[e - E0] + rg * RPG);
+#pragma unroll
+            for (int j = 0; j < RPG / 4; ++j) {
+                const float4 v = q4[j];
+                qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
+            }
+        }
+        // kv partial over the 32 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3))
+        float m4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
             for (int r = 0; r < RPG; ++r) {
                 st[r] = __fmul_rn(st[r], decay);
-                mem = fmaf(st[r], kk[r], mem);
+                m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) mem = fmaf(__fmul_rn(st[r], decay), kk[r], mem);
+            for (int r = 0; r < RPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
         }
-        mbuf[e & 1][rg][col] = mem;
+        mbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
         __syncthreads();  // the one barrier per entry (mbuf / rbuf alternate)
         const float kv = __fadd_rn(__fadd_rn(__fadd_rn(mbuf[e & 1][0][col], mbuf[e & 1][1][col]), mbuf[e & 1][2][col]),
                                    mbuf[e & 1][3][col]);
         const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
-        float res = 0.f;
-        const float* qq = verify ? qvec[e - E0] + rg * RPG : nullptr;
+        float r4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) {
-                st[r] = fmaf(kk[r], delta, st[r]);
-                if (verify) res = fmaf(st[r], qq[r], res);
-            }
+            for (int r = 0; r < RPG; ++r) st[r] = fmaf(kr[r], delta, st[r]);
+            if (verify)
+#pragma unroll
+                for (int r = 0; r < RPG; ++r) r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
         } else {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) res = fmaf(fmaf(kk[r], delta, __fmul_rn(st[r], decay)), qq[r], res);
+            for (int r = 0; r < RPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
         }
-        if (verify) rbuf[e & 1][rg][col] = res;
+        if (verify) rbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
         if (e == E0 - 1 && replayed)
 #pragma unroll
             for (int r = 0; r < RPG; ++r) rs[r * DH] = st[r];
@@ -243,7 +333,6 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
     for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
     __syncthreads();
     // gated RMSNorm: one wave per row: lane l sums columns l and l + 64, then a halving tree
-    const int lane = t & 63, wv = t >> 6;
     for (int ts = wv; ts < R; ts += GT / 64) {
         if (!((written >> ts) & 1)) continue;
         const float x0 = rawb[ts][lane], x1 = rawb[ts][lane + 64];
@@ -271,21 +360,27 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
 
 using namespace mdx;
 
-extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* ab, const uint16_t* conv_w,
+extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa,
+                            const uint16_t* wb, int64_t K, const uint16_t* conv_w,
                             uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
                             const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums,
                             const uint16_t* gnorm_w, float gnorm_eps, float qscale, uint16_t* core, int64_t rows,
                             int64_t HK, int64_t HV, int64_t slots, void* stream) {
-    MDX_CHECK(proj && z && ab && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
+    MDX_CHECK(proj && z && xn && wa && wb && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
                   rec_state && gates && sums && gnorm_w && core,
               "null pointer");
     MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
     MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
     MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV <= 1024, "heads");
+    MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
+              "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
     GdnArgs a{};
     a.proj = proj;
     a.z = z;
-    a.ab = ab;
+    a.xn = xn;
+    a.wa = wa;
+    a.wb = wb;
+    a.K = int(K);
     a.conv_w = conv_w;
     a.conv_state = conv_state;
     a.pb = proj_buf;

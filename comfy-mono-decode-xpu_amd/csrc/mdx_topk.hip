@@ -16,8 +16,8 @@
 //   3. the candidates are ranked by counting (position = number of larger candidates); the segment's
 //      top-k goes to the workspace as a descending, zero-padded list;
 //   4. the row's last work-group (device-scope counter, reset by that work-group) merges the nseg
-//      lists: an entry's final position is its own position plus, for every other list, the number of
-//      entries above it (binary search).
+//      lists in two counting stages: each wave keeps the top k of a quarter of the lists, then the 4 k
+//      survivors are ranked among themselves.
 // Ranks are never 0 (the radix key of a non-NaN value is nonzero, and a NaN's rank has a nonzero
 // gather word), so 0 marks an empty slot.
 #include <algorithm>
@@ -187,22 +187,29 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     for (int e = t; e < total; e += TK_T)
         cand[e] = __hip_atomic_load(rl + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    for (int e = t; e < total; e += TK_T) {
-        const uint64_t v = cand[e];
-        if (v == 0) continue;
-        const int mine = e / K;
-        int pos = e % K;
-        for (int w = 0; w < a.nseg && pos < K; ++w) {
-            if (w == mine) continue;
-            const uint64_t* l = cand + w * K;
-            int b0 = 0, b1 = K;  // first entry of list w not above v (lists descend, zero-padded)
-            while (b0 < b1) {
-                const int m = (b0 + b1) >> 1;
-                if (l[m] > v) b0 = m + 1;
-                else b1 = m;
-            }
-            pos += b0;
+    // two-stage merge by counting: wave w ranks the entries of its quarter of the lists among that
+    // quarter (all lanes read the same LDS word at a time: broadcasts, no dependent chains) and keeps
+    // its top K; then every thread ranks the 4 K survivors among themselves
+    uint64_t* wtop = cand + total;  // [4][K]
+    {
+        const int w = t >> 6, lane = t & 63;
+        const int l0 = w * a.nseg / 4, l1 = (w + 1) * a.nseg / 4;
+        const int e0 = l0 * K, e1 = l1 * K;
+        for (int j = lane; j < K; j += 64) wtop[w * K + j] = 0;
+        __builtin_amdgcn_wave_barrier();
+        for (int e = e0 + lane; e - lane < e1; e += 64) {
+            const uint64_t v = e < e1 ? cand[e] : 0;
+            int above = 0;
+            for (int f = e0; f < e1; ++f) above += cand[f] > v;
+            if (v != 0 && above < K) wtop[w * K + above] = v;
         }
+    }
+    __syncthreads();
+    for (int e = t; e < 4 * K; e += TK_T) {
+        const uint64_t v = wtop[e];
+        if (v == 0) continue;
+        int pos = 0;
+        for (int f = 0; f < 4 * K; ++f) pos += wtop[f] > v;
         if (pos < K) {
             const uint32_t idx = index_of<ORD>(v);
             a.indices[int64_t(row) * K + pos] = idx;
@@ -227,10 +234,11 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     if (t == 0) __hip_atomic_store(a.counter + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// segments: about 2 x 256 work-groups over all rows, at least 1024 elements each
-void plan(int64_t rows, int64_t n, int& nseg, int& seg) {
+// segments: about 2 x 256 work-groups over all rows, at least 1024 elements each, at most 640 / k
+void plan(int64_t rows, int64_t n, int64_t k, int& nseg, int& seg) {
     int64_t s = std::max<int64_t>(1, std::min<int64_t>(TK_MAXSEG, 512 / rows));
     s = std::min<int64_t>(s, std::max<int64_t>(1, n / 1024));
+    s = std::min<int64_t>(s, std::max<int64_t>(4, 640 / k));  // the merge ranks <= 160 entries per wave
     int64_t len = (n + s - 1) / s;
     len = (len + 63) / 64 * 64;
     nseg = int((n + len - 1) / len);
@@ -239,7 +247,7 @@ void plan(int64_t rows, int64_t n, int& nseg, int& seg) {
 
 size_t lds_bytes(int k, int nseg, int seg) {
     const size_t cand = size_t(k) * size_t((seg + TK_T - 1) / TK_T);
-    return (TK_T + std::max(cand, size_t(nseg) * k)) * sizeof(uint64_t);
+    return (TK_T + std::max(cand, size_t(nseg) * k + 4 * size_t(k))) * sizeof(uint64_t);
 }
 
 size_t workspace_bytes(int64_t rows) {
@@ -251,7 +259,7 @@ int launch(const void* x, bool f32, int ord, int64_t rows, int64_t n, int64_t k,
     MDX_CHECK(ws && aligned(ws, 256) && ws_bytes >= workspace_bytes(rows), "workspace: %zu bytes, 256-byte aligned",
               workspace_bytes(rows));
     int nseg, seg;
-    plan(rows, n, nseg, seg);
+    plan(rows, n, k, nseg, seg);
     TopkArgs a{};
     a.x = x;
     a.n = n;

@@ -399,12 +399,12 @@ def bf16_linear(x, w, tiled=True, residual=None, out=None):
     return out
 
 
-def gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
+def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
              sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None):
     """The Gated-DeltaNet core of csrc/mono_gdn.sycl:313-607 (layer_gdn phases P3-P5; layer_gdn_core's
     output): deferred conv, gates, sums, replay + verify delta rule, gated RMSNorm. Buffers are updated
     in place; returns core bf16 [R, HV * 128]."""
-    for t, n in ((proj, "proj"), (z, "z"), (ab, "ab"), (conv_w, "conv_w"), (conv_state, "conv_state"),
+    for t, n in ((proj, "proj"), (z, "z"), (xn, "xn"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"), (conv_state, "conv_state"),
                  (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf"), (gnorm_w, "gnorm_w")):
         _dev(t, n)
         _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
@@ -415,13 +415,16 @@ def gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g
     R, C = proj.shape[-2], proj.shape[-1]
     HV = rec_state.shape[-3]
     _check(rec_state.shape[-2:] == (128, 128) and C == 2 * hk * 128 + HV * 128, "GDN shapes")
-    _check(z.shape[-1] == HV * 128 and ab.shape[-1] == 2 * HV and conv_w.numel() == C * 4
+    _check(xn.numel() == R * xn.shape[-1] and wa.shape == (HV, xn.shape[-1]) and wb.shape == wa.shape,
+           "xn [R, K], wa / wb [HV, K]")
+    _check(z.shape[-1] == HV * 128 and conv_w.numel() == C * 4
            and conv_state.numel() == C * 3, "GDN operand shapes")
     _check(proj_buf.numel() == 2 * slots * C and qkv_buf.numel() == 2 * slots * C, "proj / qkv buffers [2, slots, C]")
     _check(gates_buf.numel() == 2 * slots * HV * 2 and sums_buf.numel() == 2 * slots * hk * 2, "gates / sums buffers")
     if core is None:
         core = torch.empty(R, HV * 128, dtype=torch.bfloat16, device=proj.device)
-    _lib.call("mdx_gdn_core", _lib.ptr(proj), _lib.ptr(z), _lib.ptr(ab), _lib.ptr(conv_w), _lib.ptr(conv_state),
+    _lib.call("mdx_gdn_core", _lib.ptr(proj), _lib.ptr(z), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), xn.shape[-1],
+              _lib.ptr(conv_w), _lib.ptr(conv_state),
               _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias), _lib.ptr(g_decay),
               _lib.ptr(rec_state), _lib.ptr(gates_buf), _lib.ptr(sums_buf), _lib.ptr(gnorm_w), float(gnorm_eps),
               float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(proj))
@@ -552,16 +555,6 @@ def layer_post_h16(x, y, gate, sig_lut, oq, os_, osc, ocb, norm_w, eps, hadamard
     return layer_post(x, y, gate, sig_lut, oq, os_, osc, ocb, norm_w, eps, full[1], *rest)
 
 
-def _wab(sc, wa, wb):
-    key = ("ab", wa.data_ptr(), wb.data_ptr(), wa._version, wb._version)
-    hit = sc["wab"].get(key)
-    if hit is None or hit[0] is not wa or hit[1] is not wb:
-        if len(sc["wab"]) > 128:
-            sc["wab"].clear()
-        hit = sc["wab"][key] = (wa, wb, torch.cat([wa, wb]).contiguous())
-    return hit[2]
-
-
 def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
               rec_state, gates_buf, sums_buf, gnorm_w, gnorm_eps, qscale, hk, norm_post, eps_post, silu_lut, nwg=0,
               stop=11, tiled=True):
@@ -579,12 +572,10 @@ def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj
     xn, q, s = _buf(sc["xn"], R, 4096), _buf(sc["q1"], R, 4096), sc["s"][:R]
     _lib.call("mdx_rms_rot_quant", _lib.ptr(x2), _lib.ptr(norm_in), float(eps_in), _lib.ptr(xn), _lib.ptr(hadamard), rot,
               _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(x))
-    ab = _buf(sc["ab"], R, 2 * HV)
-    bf16_linear(xn, _wab(sc, wa, wb), tiled=False, out=ab)
     proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
     stream_gemv(q, s, [QKV, Z], [proj, z])
     core = _buf(sc["core"], R, HV * 128)
-    gdn_core(proj, z, ab, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
+    gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
              sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=core)
     if stop >= 6:
         U.cb = D.cb = G.cb

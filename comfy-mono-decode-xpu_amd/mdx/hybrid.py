@@ -126,7 +126,8 @@ class HybridModel:
                          o=_gptq(H, qd, gen, dev), qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1))
             else:
                 L.update(qkv=_gptq(self.gdn_ch, H, gen, dev), z=_gptq(hv * 128, H, gen, dev), o=_gptq(H, hv * 128, gen, dev),
-                         wab=(torch.randn(2 * hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
+                         wa=(torch.randn(hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
+                         wb=(torch.randn(hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
                          conv_w=(torch.randn(self.gdn_ch, 4, generator=gen, device=dev) * 0.5).bfloat16(),
                          dt_bias=torch.rand(hv, generator=gen, device=dev) * 2 - 1,
                          g_decay=-torch.exp(torch.rand(hv, generator=gen, device=dev) * 1.5 - 1),
@@ -228,12 +229,10 @@ class HybridModel:
         _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn), None,
                   _lib.ROT_NONE, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
         hv = c.gdn_value_heads
-        ab = _C._buf(sc["ab"], R, 2 * hv)
-        _C.bf16_linear(xn, L["wab"], tiled=False, out=ab)
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
         _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
         core = _C._buf(sc["core"], R, hv * 128)
-        _C.gdn_core(proj, z, ab, L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
+        _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
                     G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6)
 

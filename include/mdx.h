@@ -236,19 +236,21 @@ int mdx_bf16_linear(const uint16_t* x, const uint16_t* w, int32_t layout, const 
  *   conv: per channel, the history (conv_state) shifted by the previous step's accepted rows (their
  *   projections from proj_buf[1 - parity]), then for each row ts the k=4 causal conv over its tree
  *   ancestors (ctl parents; history past the root): y = bf16(sum of fma(v, w)), out = bf16(y / (1 + e^-y));
- *   gates: decay = exp(g_decay * softplus(a + dt_bias)), beta = bf16(sigmoid(b));
+ *   gates: a = bf16(xn . wa[h]), b = bf16(xn . wb[h]) (fp32 dot in the library's fixed order),
+ *   decay = exp(g_decay * softplus(a + dt_bias)), beta = bf16(sigmoid(b));
  *   entries: the previous step's accepted slots (replayed, committed; the persistent state keeps these)
  *   then this step's program (prog & 15 = slot, prog & 32 = commit): S *= decay, kv = k^ S,
  *   delta = (v - kv) beta, S += k^ delta, out = q^ S, with k^ = k / max(|k|, 1e-12),
  *   q^ = (q qscale) / max(|q|, 1e-12); gated RMSNorm: core = bf16(bf16((raw w) / sqrt(mean(raw^2) + eps))
  *   * bf16(silu(z))).
- * proj bf16 [rows, C] (C = 2 HK 128 + HV 128: q | k | v); z bf16 [rows, HV 128]; ab bf16 [rows, 2 HV] (a
- * then b); conv_w bf16 [C, 4]; conv_state bf16 [C, 3]; proj_buf, qkv_buf bf16 [2, slots, C]; ctl int32
+ * proj bf16 [rows, C] (C = 2 HK 128 + HV 128: q | k | v); z bf16 [rows, HV 128]; xn bf16 [rows, K] (the
+ * normalised layer input), wa / wb bf16 [HV, K] (K % 512 == 0, K <= 4096); conv_w bf16 [C, 4]; conv_state bf16 [C, 3]; proj_buf, qkv_buf bf16 [2, slots, C]; ctl int32
  * [2 + 3 slots] = (pending, parity, accepted[slots], parents[slots], prog[slots]); rec_state f32
  * [HV, 128, 128]; gates f32 [2, slots, HV, 2]; sums f32 [2, slots, HK, 2]; gnorm_w bf16 [128]; core bf16
  * [rows, HV 128] (rows without a verify entry are 0). slots in {8, 16}. Tolerance parity (float64
  * bound); the control walk is exact. */
-int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* ab, const uint16_t* conv_w,
+int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
+                 int64_t K, const uint16_t* conv_w,
                  uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias,
                  const float* g_decay, float* rec_state, float* gates, float* sums, const uint16_t* gnorm_w,
                  float gnorm_eps, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,

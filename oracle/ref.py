@@ -595,6 +595,15 @@ def gdn_conv(state, proj, conv_w, ctl, R, slots, dtype=np.float64):
     return out
 
 
+def gdn_ab(xn_bits, wa_bits, wb_bits, dtype=np.float64):
+    """a = xn . wa^T, b = xn . wb^T (the in_proj_a / in_proj_b linears, csrc/mono_gdn.sycl:232-268):
+    float64 unrounded (the reference bound), or the float32 dot rounded to bf16 (the chain)."""
+    x = bf16_to_f32(xn_bits).astype(dtype)
+    a = x @ bf16_to_f32(wa_bits).astype(dtype).T
+    b = x @ bf16_to_f32(wb_bits).astype(dtype).T
+    return _rnd(a, dtype), _rnd(b, dtype)
+
+
 def gdn_gates(a, b, dt_bias, g_decay, dtype=np.float64):
     """decay = exp(g_decay * softplus(a + dt_bias)) (softplus(x) = x above 20), beta = bf16(sigmoid(b))
     (csrc/mono_gdn.sycl:441-450). a, b: [R, HV] bf16 values."""

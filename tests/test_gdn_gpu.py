@@ -39,6 +39,8 @@ def test_gdn_two_steps_match_f64(C, dev, slots, widths):
     dt_bias = rng.uniform(-1, 1, HV).astype(np.float32)
     g_decay = (-np.exp(rng.uniform(-1, 0.5, HV))).astype(np.float32)
     gnw = _bf(1 + rng.standard_normal(DH) * 0.1)
+    wa = _bf(rng.standard_normal((HV, 4096)) * 0.02)
+    wb = _bf(rng.standard_normal((HV, 4096)) * 0.02)
     eps, qscale = 1e-6, DH ** -0.5
     st64 = dict(conv_state=_bf(rng.standard_normal((NCH, 3))), pb=np.zeros((2, slots, NCH), np.float32),
                 qb=np.zeros((2, slots, NCH), np.float32),
@@ -58,12 +60,15 @@ def test_gdn_two_steps_match_f64(C, dev, slots, widths):
         ctl = [pending, p] + accepted + parents + prog
         proj = _bf(rng.standard_normal((R, NCH)))
         z = _bf(rng.standard_normal((R, HV * DH)))
-        ab = _bf(rng.standard_normal((R, 2 * HV)))
+        xn = _bf(rng.standard_normal((R, 4096)))
+        xb, wab, wbb = ref.f32_to_bf16(xn), ref.f32_to_bf16(wa), ref.f32_to_bf16(wb)
         args = (conv_w, dt_bias, g_decay, gnw, eps, qscale, np.array(ctl), R, HK, slots)
-        c64 = ref.gdn_step(st64, proj, z, ab[:, :HV], ab[:, HV:], *args[:6], args[6], R, HK, slots)
-        c32 = ref.gdn_step(st32, proj, z, ab[:, :HV], ab[:, HV:], *args[:6], args[6], R, HK, slots,
-                           dtype=np.float32)
-        core = C.gdn_core(_tensor(proj, dev), _tensor(z, dev), _tensor(ab, dev), _tensor(conv_w, dev),
+        a64, b64 = ref.gdn_ab(xb, wab, wbb)
+        a32, b32 = ref.gdn_ab(xb, wab, wbb, np.float32)
+        c64 = ref.gdn_step(st64, proj, z, a64, b64, *args[:6], args[6], R, HK, slots)
+        c32 = ref.gdn_step(st32, proj, z, a32, b32, *args[:6], args[6], R, HK, slots, dtype=np.float32)
+        core = C.gdn_core(_tensor(proj, dev), _tensor(z, dev), _tensor(xn, dev), _tensor(wa, dev), _tensor(wb, dev),
+                          _tensor(conv_w, dev),
                            d["conv_state"], d["pb"], d["qb"], torch.tensor(ctl, dtype=torch.int32, device=dev),
                            _tensor(dt_bias, dev, torch.float32), _tensor(g_decay, dev, torch.float32), d["rec"],
                            d["gates"], d["sums"], _tensor(gnw, dev), eps, qscale, HK)
@@ -93,7 +98,7 @@ def test_gdn_first_step_without_history_rows(C, dev):
     before = rec.clone()
     ctl = torch.tensor([0, 0] + [0] * 8 + [-1, 0, 1] + [-1] * 5 + [32, 33, 2] + [0] * 5, dtype=torch.int32, device=dev)
     bf = lambda *s: torch.randn(*s, device=dev).bfloat16()
-    C.gdn_core(bf(R, NCH), bf(R, HV * DH), bf(R, 2 * HV), bf(NCH, 4), bf(NCH, 3), torch.zeros(2, slots, NCH, dtype=torch.bfloat16,
+    C.gdn_core(bf(R, NCH), bf(R, HV * DH), bf(R, 4096), bf(HV, 4096), bf(HV, 4096), bf(NCH, 4), bf(NCH, 3), torch.zeros(2, slots, NCH, dtype=torch.bfloat16,
                 device=dev), torch.zeros(2, slots, NCH, dtype=torch.bfloat16, device=dev), ctl,
                 torch.zeros(HV, device=dev), -torch.ones(HV, device=dev), rec, torch.zeros(2, slots, HV, 2, device=dev),
                 torch.zeros(2, slots, HK, 2, device=dev), torch.ones(DH, device=dev).bfloat16(), 1e-6, DH ** -0.5, HK)

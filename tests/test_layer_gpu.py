@@ -104,17 +104,12 @@ def test_layer_gdn_matches_oracle(C, dev):
                 dst["qb"], torch.tensor(ctl, dtype=torch.int32, device=dev), T(dt_bias, torch.float32),
                 T(g_decay, torch.float32), dst["rec"], dst["gates"], dst["sums"], T(gnw), 1e-6, DH ** -0.5, HK,
                 npo.to(dev), 1e-6, lut.to(dev), 0, 11, True)
-    # pre part (exact) and the a / b linear (float64 bound)
+    # pre part (exact), then the GDN core (float64 bound)
     xn, (proj, z) = ref.layer_pre(bits(x), bits(nin), 1e-6, "h256", bits(h), dicts[:2])
-    sc = C._scratch(torch.device(dev))
-    ab = C._buf(sc["ab"], R, 2 * HV).float().cpu().numpy()
-    want_ab, scale = ref.bf16_linear_f64(xn, np.concatenate([bits(wa), bits(wb)]))
-    assert (np.abs(ab - want_ab) <= np.abs(want_ab) * 2 ** -8 + scale * 2 ** -16 + 1e-30).all()
-    # GDN core from the GPU's own a / b (float64 bound)
-    args64 = (ref.bf16_to_f32(proj), ref.bf16_to_f32(z), ab[:, :HV], ab[:, HV:], conv_w, dt_bias, g_decay, gnw, 1e-6,
-              DH ** -0.5, np.array(ctl), R, HK, slots)
-    c64 = ref.gdn_step(st, *args64)
-    c32 = ref.gdn_step(st32, *args64, dtype=np.float32)
+    rest = (conv_w, dt_bias, g_decay, gnw, 1e-6, DH ** -0.5, np.array(ctl), R, HK, slots)
+    c64 = ref.gdn_step(st, ref.bf16_to_f32(proj), ref.bf16_to_f32(z), *ref.gdn_ab(xn, bits(wa), bits(wb)), *rest)
+    c32 = ref.gdn_step(st32, ref.bf16_to_f32(proj), ref.bf16_to_f32(z), *ref.gdn_ab(xn, bits(wa), bits(wb), np.float32),
+                       *rest, dtype=np.float32)
     core = C.layer_gdn_core(xd, R).float().cpu().numpy()
     e_ref, err = np.abs(c32 - c64), np.abs(core - c64)
     assert err.max() <= 1.5 * e_ref.max() + 1e-3 and err.mean() <= 1.5 * e_ref.mean() + 1e-5
