@@ -4,13 +4,16 @@ Default workload: the fused W4A8 SwiGLU MLP block (hidden 4096, intermediate 122
 in front, GPTQ int4 weights in groups of 128 with fp16 scales ~U(0.005, 0.02), per-token int8
 activations), one decode row. A "step" is one MLP call. Weights live in a ring of distinct copies
 (> 2x the 256 MB Infinity Cache) so each call streams its weights from HBM; the ring is captured
-in one HIP graph and replayed.
+in one HIP graph and replayed. The default run then also decodes the full synthetic 32-layer hybrid
+stack (the metric's second half: tok/s, ms per step) and reports it under "decode".
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rows M] [--workload mlp|linear]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rows M]
+                    [--workload mlp|linear|lmhead|attn|stack|copy] [--ctx L] [--prompt P]
 
 Prints one JSON line: value = whole-job achieved HBM GB/s (algorithmic bytes / wall time), plus
-`roofline` for the dominant kernel (the gate/up GEMV launch, timed on its own graph of launches)
-and `cpu_baseline` (the CPU oracle of the same operator chain on a bounded sample).
+`roofline` for the dominant kernel (the gate/up GEMV launch, timed on its own graph of launches;
+`traffic` from the committed rocprofv3 PMC summary) and `cpu_baseline` (the CPU oracle of the same
+operator chain on a bounded sample).
 """
 from __future__ import annotations
 
@@ -25,6 +28,16 @@ sys.path.insert(0, os.path.join(ROOT, "comfy-mono-decode-xpu_amd"))
 
 PEAK_HBM_GBS = 8000.0
 METRIC = "W4A8 GEMV achieved HBM GB/s (% of peak); decode tok/s at 9B hybrid, 8-draft tree"
+
+
+def pmc_traffic(key):
+    """HBM bytes per launch of a workload's dominant kernel, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE scaled by the counters' readings for a 256 MiB copy), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)[key]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def gptq_weight(N, K, gen, dev, tiled=True):
@@ -158,7 +171,8 @@ def bench_mlp(args, dev):
                    "algorithmic_bytes_per_step": per, "frac_of_peak": round(per / t_call / 1e9 / PEAK_HBM_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel (gate/up pair, SiLU epilogue)",
                      "achieved": round(gu_b / t_gu / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_b / t_gu / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_b / t_gu / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": pmc_traffic("mlp_gateup_rows1") if M == 1 else None,
                      "algorithmic_bytes_per_launch": gu_b, "avg_launch_us": round(t_gu * 1e6, 3)},
     }
     if not args.no_cpu:
@@ -203,7 +217,7 @@ def bench_linear(args, dev):
                    "algorithmic_bytes_per_step": per},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel", "achieved": round(per / t / 1e9, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(per / t / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "avg_launch_us": round(t * 1e6, 3)},
+                     "traffic": pmc_traffic("linear_rows1") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3)},
     }
 
 
@@ -344,6 +358,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="mlp: skip the full-stack decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the multi-GPU sharding is a design "
@@ -356,6 +371,15 @@ def main():
     dev = torch.device("cuda", 0)
     res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
            "attn": bench_attn, "stack": bench_stack}[args.workload](args, dev)
+    if args.workload == "mlp" and not args.no_decode:
+        # the second half of the metric: decode tok/s of the full synthetic hybrid stack (1024-token
+        # prompt, 64 graph-replayed steps)
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup, sub.prompt = 64, 4, 1024
+        d = bench_stack(sub, dev)
+        res["decode"] = {"metric": "decode tok/s at 9B hybrid, 8-draft tree", "value": d["value"], "unit": "tok/s",
+                         "ms_per_step": d["config"]["ms_per_step"],
+                         "accepted_per_step": d["config"]["accepted_per_step"], "workload": d["config"]["workload"]}
     print(json.dumps(res), flush=True)
 
 
