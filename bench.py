@@ -134,7 +134,7 @@ def bench_mlp(args, dev):
     nw = (1 + 0.02 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
     lut = layout.silu_lut(dev)
     out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(_lib.lib().mdx_mono_mlp_workspace(M, H, I), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(_lib.lib().mdx_mono_mlp_workspace(M, H, I), dtype=torch.uint8, device=dev)
 
     def all_ring():
         for g_, u_, d_ in ring:

@@ -45,23 +45,52 @@ namespace {
 
 constexpr int WAVE = 64;
 constexpr int CHUNK_K = 128;
-constexpr int PREP_THREADS = 256;
 constexpr int MAX_PREP_K = 16384;
-constexpr int PREP_BLK = MAX_PREP_K / 8 / PREP_THREADS;  // 8-element blocks per thread at most
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// global-memory pointers as such (accesses through generic pointers are "flat" ones, which also
+// wait for outstanding LDS traffic)
+#define MDX_G __attribute__((address_space(1)))
 
 // streamed-once weights: a non-temporal 16-byte load (does not displace reused data in L2)
 __device__ __forceinline__ uint4 ldg_stream(const void* p) {
     const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint4 ldg_stream(const MDX_G uint8_t* p) {
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const MDX_G v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Device-coherent plain accesses for data handed between work-groups of one launch: relaxed
+// agent-scope atomics (they bypass the non-coherent cache state instead of writing back and
+// invalidating whole caches, which is what an agent-scope fence costs on a multi-XCD chip).
+template <typename T>
+__device__ __forceinline__ T ld_c(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_c(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Hand-off: once every thread's coherent stores / atomics have completed (vector memory counter at
+// zero), one thread bumps the counter.
+__device__ __forceinline__ uint32_t publish(uint32_t* ctr) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t old = 0;
+    if (threadIdx.x == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return old;
+}
 
 // =================================================================================================
-// Row prep: [RMSNorm] -> [rotation] -> absmax -> int8 quantisation. One work-group per row.
-// Thread t owns the 8-element blocks b = t + 256 j (elements 8 b .. 8 b + 7), held in registers.
+// Row prep: [sigmoid gate] -> [RMSNorm] -> [rotation] -> absmax -> int8 quantisation, one
+// work-group per row (layout below, at the kernel).
 // =================================================================================================
 struct PrepArgs {
     const uint16_t* x;     // bf16 [rows, K]
@@ -81,200 +110,215 @@ struct PrepArgs {
     int g_head = 0, g_hstride = 0, g_off = 0;
 };
 
-__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+__device__ __forceinline__ void unpack4(const uint2& v, float* f) {
+    f[0] = __uint_as_float(v.x << 16);
+    f[1] = __uint_as_float(v.x & 0xFFFF0000u);
+    f[2] = __uint_as_float(v.y << 16);
+    f[3] = __uint_as_float(v.y & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ uint2 pack4(const float* f) {
+    return make_uint2(uint32_t(f2bf(f[0])) | (uint32_t(f2bf(f[1])) << 16),
+                      uint32_t(f2bf(f[2])) | (uint32_t(f2bf(f[3])) << 16));
+}
+
+// the value `v` of lane Q of this lane's quad (DPP quad_perm broadcast, both halves of the double)
+template <int Q>
+__device__ __forceinline__ double quad_lane(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u)), Q * 0x55, 0xF, 0xF, false));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u >> 32)), Q * 0x55, 0xF, 0xF, false));
+    return __builtin_bit_cast(double, uint64_t(lo) | (uint64_t(hi) << 32));
+}
+
+// output j of the radix-4 butterfly: the H4 row j applied to (a0, a1, a2, a3) left to right,
+// ((a0 + a1) + a2) - a3, ((a0 + a1) - a2) + a3, ((a0 - a1) + a2) + a3, ((a1 - a0) + a2) + a3: row j has
+// its one minus sign at position 3 - j (a - b and -b + a are the same IEEE operation)
+__device__ __forceinline__ double h4_out(const double* a, int j) {
+    double b[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    for (int k = 0; k < 4; ++k) b[k] = (k == 3 - j) ? -a[k] : a[k];
+    return __dadd_rn(__dadd_rn(__dadd_rn(b[0], b[1]), b[2]), b[3]);
+}
+
+// fp64 fast Walsh-Hadamard transform of one 256-group held 4 elements per lane (lane l: elements
+// 4 l .. 4 l + 3): radix-4 stages along the base-4 digits of the element index (strides 1, 4, 16, 64).
+// Digit 0 is the lane's own slot, digit 1 the lane within its quad, digits 2 and 3 the quad within
+// the 16-lane row and the row; each lane computes its own output of every butterfly.
+__device__ __forceinline__ void fwht256_lane(double* d, int lane) {
+    double o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = h4_out(d, e);
+    const int j1 = lane & 3, j2 = (lane >> 2) & 3, j3 = lane >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const double a[4] = {quad_lane<0>(o[e]), quad_lane<1>(o[e]), quad_lane<2>(o[e]), quad_lane<3>(o[e])};
+        d[e] = h4_out(a, j1);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        double a[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a[k] = __shfl(d[e], (lane & ~12) | (k << 2), 64);
+        o[e] = h4_out(a, j2);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        double a[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a[k] = __shfl(o[e], (lane & 15) | (k << 4), 64);
+        d[e] = h4_out(a, j3);
     }
 }
 
-// Block sum of 256 per-thread partials in the canonical tree (p[t] + p[t + 128], + 64, ..., + 1)
-__device__ float tree256(float p, float* red) {
-    const int t = threadIdx.x;
-    red[t] = p;
-    __syncthreads();
-    if (t < 128) red[t] = __fadd_rn(red[t], red[t + 128]);
-    __syncthreads();
-    float v = 0.f;
-    if (t < 64) {
-        v = __fadd_rn(red[t], red[t + 64]);
-        for (int s = 32; s >= 1; s >>= 1) v = __fadd_rn(v, shfl_down(v, s));
-        if (t == 0) red[300] = v;
-    }
-    __syncthreads();
-    const float r = red[300];
-    __syncthreads();
-    return r;
-}
-
-__global__ __launch_bounds__(PREP_THREADS) void prep_rows_kernel(PrepArgs a) {
-    extern __shared__ float smem[];
-    float* red = smem;                                   // [320]
-    double* grp = reinterpret_cast<double*>(smem + 320);  // [4][256] fp64 butterflies
-    float* xr = reinterpret_cast<float*>(grp + 4 * 256);  // [K] (rotation only)
-    const int t = threadIdx.x;
-    const int row = blockIdx.x, K = a.K, nb = K / 8;
-    const uint16_t* x = a.x + int64_t(row) * K;
-    float v[PREP_BLK][8];
-    uint4 raw[PREP_BLK];
+// Row prep. One work-group per row, one wave per 256-element group (wave w takes groups w, w + W, ...,
+// W = min(16, K / 256)); lane l holds elements 4 l .. 4 l + 3 of each of its groups in registers.
+// Canonical RMSNorm sum: per group, lane partial ((sq0 + sq1) + sq2) + sq3 of its four squares, the
+// halving tree over the 64 lanes (l + 32, + 16, ..., + 1), then the group sums added in group order.
+// The work-group's waves (any count) share the row; gsum holds K / 256 floats, wmax one per wave.
+// COH: the q / scale outputs are read by other work-groups of the same launch (coherent stores).
+template <int GPW, bool COH = false>
+__device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float* gsum, float* wmax) {
+    const int W = blockDim.x / WAVE, w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int K = a.K, G = K / 256;
+    const uint16_t* x = a.x + int64_t(row) * K + 4 * lane;
+    float v[GPW][4];
+    uint2 raw[GPW], wraw[GPW], graw[GPW];
+    // all loads first (group index clamped: no branches around loads)
 #pragma unroll
-    for (int j = 0; j < PREP_BLK; ++j) {
-        const int b = t + PREP_THREADS * j;
-        if (b < nb) raw[j] = *reinterpret_cast<const uint4*>(x + 8 * b);
+    for (int gi = 0; gi < GPW; ++gi) {
+        const int g = min(w + W * gi, G - 1);
+        raw[gi] = *reinterpret_cast<const uint2*>(x + 256 * g);
+        if (a.nw) wraw[gi] = *reinterpret_cast<const uint2*>(a.nw + 256 * g + 4 * lane);
+        if (a.gate) {
+            const int i0 = 256 * g + 4 * lane;
+            graw[gi] = *reinterpret_cast<const uint2*>(a.gate + row * a.g_row + (i0 / a.g_head) * a.g_hstride + a.g_off +
+                                                       i0 % a.g_head);
+        }
     }
 #pragma unroll
-    for (int j = 0; j < PREP_BLK; ++j) {
-        const int b = t + PREP_THREADS * j;
-        if (b < nb) unpack8(raw[j], v[j]);
-    }
+    for (int gi = 0; gi < GPW; ++gi) unpack4(raw[gi], v[gi]);
     if (a.gate) {
 #pragma unroll
-        for (int j = 0; j < PREP_BLK; ++j) {
-            const int b = t + PREP_THREADS * j;
-            if (b < nb) {
-                const int i0 = 8 * b;
-                const uint16_t* gp = a.gate + row * a.g_row + (i0 / a.g_head) * a.g_hstride + a.g_off + i0 % a.g_head;
-                const uint4 gv = *reinterpret_cast<const uint4*>(gp);
-                const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+        for (int gi = 0; gi < GPW; ++gi) {
+            const uint16_t gb[4] = {uint16_t(graw[gi].x), uint16_t(graw[gi].x >> 16), uint16_t(graw[gi].y),
+                                    uint16_t(graw[gi].y >> 16)};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t gb = uint16_t(gw[e >> 1] >> (16 * (e & 1)));
-                    v[j][e] = bfround(__fmul_rn(v[j][e], bf2f(a.sig[gb])));
-                }
-            }
+            for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(v[gi][e], bf2f(a.sig[gb[e]])));
         }
     }
     if (a.nw) {
-        // canonical RMSNorm: thread t's partial sums its own elements in increasing order
-        float p = 0.f;
-        bool first = true;
 #pragma unroll
-        for (int j = 0; j < PREP_BLK; ++j) {
-            const int b = t + PREP_THREADS * j;
-            if (b < nb)
+        for (int gi = 0; gi < GPW; ++gi) {
+            float q = __fmul_rn(v[gi][0], v[gi][0]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float sq = __fmul_rn(v[j][e], v[j][e]);
-                    p = first ? sq : __fadd_rn(p, sq);
-                    first = false;
-                }
+            for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
+            for (int s = 32; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+            const int g = w + W * gi;
+            if (lane == 0 && g < G) gsum[g] = q;
         }
-        const float ss = tree256(p, red);
+        __syncthreads();
+        float ss = gsum[0];
+        for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, gsum[g]);
         const float mean = __fdiv_rn(ss, float(K));
         const float r = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(mean, a.eps)));
 #pragma unroll
-        for (int j = 0; j < PREP_BLK; ++j) {
-            const int b = t + PREP_THREADS * j;
-            if (b < nb) {
-                float w[8];
-                unpack8(*reinterpret_cast<const uint4*>(a.nw + 8 * b), w);
-                uint32_t o[4];
+        for (int gi = 0; gi < GPW; ++gi) {
+            float wv[4];
+            unpack4(wraw[gi], wv);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[j][e] = bfround(__fmul_rn(__fmul_rn(v[j][e], r), w[e]));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = uint32_t(f2bf(v[j][2 * e])) | (uint32_t(f2bf(v[j][2 * e + 1])) << 16);
-                if (a.xn_out) *reinterpret_cast<uint4*>(a.xn_out + int64_t(row) * K + 8 * b) = make_uint4(o[0], o[1], o[2], o[3]);
-            }
+            for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], r), wv[e]));
+            const int g = w + W * gi;
+            if (a.xn_out && g < G)
+                *reinterpret_cast<uint2*>(a.xn_out + int64_t(row) * K + 256 * g + 4 * lane) = pack4(v[gi]);
         }
     }
     if (!a.q) return;  // RMSNorm only (xn_out)
-    if (a.rot != MDX_ROT_NONE) {
+    if (a.rot == MDX_ROT_H256) {
+        // fp64 FWHT, then * 1/16, rounded once to fp32 and once to bf16
 #pragma unroll
-        for (int j = 0; j < PREP_BLK; ++j) {
-            const int b = t + PREP_THREADS * j;
-            if (b < nb)
+        for (int gi = 0; gi < GPW; ++gi) {
+            double d[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xr[8 * b + e] = v[j][e];
+            for (int e = 0; e < 4; ++e) d[e] = double(v[gi][e]);
+            fwht256_lane(d, lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[gi][e] = bfround(float(__dmul_rn(d[e], 0.0625)));
         }
-        __syncthreads();
-        const int groups = K / 256;
-        if (a.rot == MDX_ROT_H256) {
-            // fp64 fast Walsh-Hadamard transform per 256-group: radix-4 stages along the base-4
-            // digits (strides 1, 4, 16, 64), butterfly out_j = sum_k a_k H4[k][j] in a fixed order,
-            // then * 1/16, rounded once to fp32 and once to bf16.
-            const int wave = t / WAVE, lane = t % WAVE;
-            for (int g0 = 0; g0 < groups; g0 += 4) {
-                const int g = g0 + wave;
-                double* bb = grp + wave * 256;
-                if (g < groups)
-                    for (int i = lane; i < 256; i += WAVE) bb[i] = double(xr[g * 256 + i]);
-                __syncthreads();
-                for (int st = 1; st < 256; st *= 4) {
-                    if (g < groups) {
-                        const int base = (lane / st) * (4 * st) + lane % st;
-                        const double a0 = bb[base], a1 = bb[base + st], a2 = bb[base + 2 * st], a3 = bb[base + 3 * st];
-                        bb[base] = __dsub_rn(__dadd_rn(__dadd_rn(a0, a1), a2), a3);
-                        bb[base + st] = __dadd_rn(__dsub_rn(__dadd_rn(a0, a1), a2), a3);
-                        bb[base + 2 * st] = __dadd_rn(__dadd_rn(__dsub_rn(a0, a1), a2), a3);
-                        bb[base + 3 * st] = __dadd_rn(__dadd_rn(__dsub_rn(a1, a0), a2), a3);
-                    }
-                    __syncthreads();
+    } else if (a.rot == MDX_ROT_MATRIX) {
+        // generic bf16 [256, 256] matrix: out_j = fp64 sum over k (in order, from 0.0) of the exact
+        // products x_k * h[k][j], then fp32, then bf16
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            double acc[4] = {0.0, 0.0, 0.0, 0.0};
+            for (int k4 = 0; k4 < 64; ++k4) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[gi][e]), k4));
+                    float hv[4];
+                    unpack4(*reinterpret_cast<const uint2*>(a.h + (4 * k4 + e) * 256 + 4 * lane), hv);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] = __dadd_rn(acc[j], __dmul_rn(double(xk), double(hv[j])));
                 }
-                if (g < groups)
-                    for (int i = lane; i < 256; i += WAVE) xr[g * 256 + i] = bfround(float(__dmul_rn(bb[i], 0.0625)));
-                __syncthreads();
             }
-        } else {
-            // generic bf16 matrix: fp64 sum over k in order of exact products, then fp32, then bf16
-            for (int g = 0; g < groups; ++g) {
-                double acc = 0.0;
-                for (int k = 0; k < 256; ++k)
-                    acc = __dadd_rn(acc, __dmul_rn(double(xr[g * 256 + k]), double(bf2f(a.h[k * 256 + t]))));
-                __syncthreads();
-                xr[g * 256 + t] = bfround(float(acc));
-                __syncthreads();
-            }
-        }
 #pragma unroll
-        for (int j = 0; j < PREP_BLK; ++j) {
-            const int b = t + PREP_THREADS * j;
-            if (b < nb)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[j][e] = xr[8 * b + e];
+            for (int j = 0; j < 4; ++j) v[gi][j] = bfround(float(acc[j]));
         }
     }
     // absmax (exact, order-free), scale, quantise
     float m = 0.f;
 #pragma unroll
-    for (int j = 0; j < PREP_BLK; ++j) {
-        const int b = t + PREP_THREADS * j;
-        if (b < nb)
+    for (int gi = 0; gi < GPW; ++gi)
+        if (w + W * gi < G)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[j][e]));
-    }
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[gi][e]));
     m = wave_max(m);
-    if (t % WAVE == 0) red[256 + t / WAVE] = m;
+    if (lane == 0) wmax[w] = m;
     __syncthreads();
-    const float rm = fmaxf(fmaxf(red[256], red[257]), fmaxf(red[258], red[259]));
+    float rm = wmax[0];
+    for (int i = 1; i < W; ++i) rm = fmaxf(rm, wmax[i]);
     const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
-    if (t == 0) a.scale[row] = s;
+    if (threadIdx.x == 0) {
+        if (COH) st_c(reinterpret_cast<uint32_t*>(a.scale) + row, __float_as_uint(s));
+        else a.scale[row] = s;
+    }
     uint16_t sb = f2bf(s);
     if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
     const float sbf = bf2f(sb);
 #pragma unroll
-    for (int j = 0; j < PREP_BLK; ++j) {
-        const int b = t + PREP_THREADS * j;
-        if (b < nb) {
-            uint32_t o[2] = {0, 0};
+    for (int gi = 0; gi < GPW; ++gi) {
+        const int g = w + W * gi;
+        if (g < G) {
+            uint32_t o = 0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float d = bfround(__fdiv_rn(v[j][e], sbf));
+            for (int e = 0; e < 4; ++e) {
+                const float d = bfround(__fdiv_rn(v[gi][e], sbf));
                 const int qv = int(fminf(fmaxf(rintf(d), -128.f), 127.f));
-                o[e >> 2] |= (uint32_t(qv) & 0xFFu) << (8 * (e & 3));
+                o |= (uint32_t(qv) & 0xFFu) << (8 * e);
             }
-            *reinterpret_cast<uint2*>(a.q + int64_t(row) * K + 8 * b) = make_uint2(o[0], o[1]);
+            uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + int64_t(row) * K + 256 * g + 4 * lane);
+            if (COH) st_c(qp, o);
+            else *qp = o;
         }
     }
 }
 
-size_t prep_smem(int K, int rot) { return 320 * 4 + 4 * 256 * 8 + (rot != MDX_ROT_NONE ? size_t(K) * 4 : 0); }
+template <int GPW>
+__global__ __launch_bounds__(1024) void prep_rows_kernel(PrepArgs a) {
+    __shared__ float gsum[MAX_PREP_K / 256];
+    __shared__ float wmax[16];
+    prep_row<GPW>(a, blockIdx.x, gsum, wmax);
+}
 
 int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
-    const size_t smem = prep_smem(a.K, a.rot);
-    if (smem > 64 * 1024) allow_smem(reinterpret_cast<const void*>(&prep_rows_kernel), smem);
-    hipLaunchKernelGGL(prep_rows_kernel, dim3(unsigned(rows)), dim3(PREP_THREADS), smem, st, a);
+    const int G = a.K / 256, W = std::min(16, G), gpw = (G + W - 1) / W;
+    const dim3 grid{unsigned(rows)}, block{unsigned(W * WAVE)};
+    switch (gpw) {
+        case 1: hipLaunchKernelGGL(prep_rows_kernel<1>, grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL(prep_rows_kernel<2>, grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL(prep_rows_kernel<3>, grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL(prep_rows_kernel<4>, grid, block, 0, st, a); break;
+    }
     MDX_LAUNCHED();
     return MDX_OK;
 }
@@ -282,7 +326,7 @@ int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
 // =================================================================================================
 // GEMV engine
 // =================================================================================================
-enum Epi : int { EPI_STORE = 0, EPI_SILU = 1 };
+enum Epi : int { EPI_STORE = 0, EPI_SILU = 1, EPI_ACC = 2 };
 
 struct MatArg {
     const uint8_t* q;
@@ -304,13 +348,32 @@ struct GemvArgs {
     const float* xs;      // f32 [rows]
     int rows;
     int KS, TPW;          // K slices per tile, tiles per work-group
-    int xglobal;          // MFMA only: activation too large for LDS, A fragments read from global
     int force_exact;      // MDX_DECODE_EXACT: never take the integral form
     int epi;
     void* out[3];
     const void* res[3];
     int out_dt;
     const uint16_t* lut;  // EPI_SILU
+    // EPI_ACC (one matrix, TPW 1, each tile's K range split over `split` work units): the units add
+    // their int32 sums into acc [rows, N]; the tile's last unit (counter tcnt[tile]) applies the
+    // store epilogue and leaves acc and tcnt at zero again
+    int32_t* acc;
+    uint32_t* tcnt;
+    int split;
+    int coh;              // EPI_SILU outputs are read within the launch: coherent stores
+};
+
+// What a work unit waits for before it stages its activation, and where the activation comes from.
+// Data handed between work-groups of one launch is written with coherent (write-through) stores and
+// read with ordinary loads only after the hand-off: nothing reads those lines earlier in the launch,
+// and a kernel starts with no stale lines in the L2s, so the first read misses and fetches the data
+// (later readers on the same XCD hit the L2).
+struct UnitIn {
+    const uint32_t* wait;   // null, or wait until *wait >= wait_for (flags: coherent loads)
+    uint32_t wait_for;
+    uint32_t* err;          // set to 1 if a wait gives up
+    const uint16_t* hr;     // null: int8 rows a.xq with scales a.xs; else bf16 rows [rows, K] quantised
+    const uint32_t* amax;   //   here with the rows' absmax (fp32 bits) from amax
 };
 
 struct Lut {
@@ -374,27 +437,68 @@ __device__ __forceinline__ float rd_scale(const uint8_t* p) {
 // -------------------------------------------------------------------------------------------------
 // epilogue
 // -------------------------------------------------------------------------------------------------
+// Per-matrix fields for a run-time matrix index. The three values are loaded at fixed offsets and
+// passed through an empty asm before the select: otherwise the compiler folds the select of loads
+// into one load at a run-time offset, which needs an addressable copy of the whole argument struct
+// (scratch memory, a round trip before every use).
+template <typename T>
+__device__ __forceinline__ T opaque(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+template <typename T>
+__device__ __forceinline__ T pick3(int i, T v0, T v1, T v2) {
+    v0 = opaque(v0);
+    v1 = opaque(v1);
+    v2 = opaque(v2);
+    return i == 0 ? v0 : (i == 1 ? v1 : v2);
+}
+// a pointer into global memory again (the asm hid where it came from)
+template <typename T>
+__device__ __forceinline__ MDX_G T* as_global(T* p) {
+    return (MDX_G T*)p;
+}
+__device__ __forceinline__ int mat_n(const GemvArgs& a, int mi) { return pick3(mi, a.m[0].n, a.m[1].n, a.m[2].n); }
+__device__ __forceinline__ int mat_tiles(const GemvArgs& a, int mi) {
+    return pick3(mi, a.m[0].tiles, a.m[1].tiles, a.m[2].tiles);
+}
+__device__ __forceinline__ MDX_G void* mat_out(const GemvArgs& a, int mi) {
+    return as_global(pick3(mi, a.out[0], a.out[1], a.out[2]));
+}
+__device__ __forceinline__ const MDX_G void* mat_res(const GemvArgs& a, int mi) {
+    return as_global(pick3(mi, a.res[0], a.res[1], a.res[2]));
+}
+__device__ __forceinline__ const MDX_G uint8_t* mat_q(const GemvArgs& a, int mi) {
+    return as_global(pick3(mi, a.m[0].q, a.m[1].q, a.m[2].q));
+}
+__device__ __forceinline__ const MDX_G uint8_t* mat_s(const GemvArgs& a, int mi) {
+    return as_global(pick3(mi, a.m[0].s, a.m[1].s, a.m[2].s));
+}
+__device__ __forceinline__ const MDX_G float* mat_sch(const GemvArgs& a, int mi) {
+    return as_global(pick3(mi, a.m[0].sch, a.m[1].sch, a.m[2].sch));
+}
+
 __device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, int r, int32_t acc, float xs, float sc) {
-    const MatArg& m = a.m[mi];
     const float f = scaleback(acc, xs, sc);
-    const int o = r * m.n + n;
+    const int o = r * mat_n(a, mi) + n;
+    const MDX_G void* res = mat_res(a, mi);
+    MDX_G void* out = mat_out(a, mi);
     if (a.out_dt == MDX_DT_BF16) {
         uint16_t v = f2bf(f);
-        if (a.res[mi]) v = f2bf(__fadd_rn(bf2f(reinterpret_cast<const uint16_t*>(a.res[mi])[o]), bf2f(v)));
-        reinterpret_cast<uint16_t*>(a.out[mi])[o] = v;
+        if (res) v = f2bf(__fadd_rn(bf2f(static_cast<const MDX_G uint16_t*>(res)[o]), bf2f(v)));
+        static_cast<MDX_G uint16_t*>(out)[o] = v;
     } else {
         float v = f;
-        if (a.res[mi]) v = __fadd_rn(reinterpret_cast<const float*>(a.res[mi])[o], v);
-        reinterpret_cast<float*>(a.out[mi])[o] = v;
+        if (res) v = __fadd_rn(static_cast<const MDX_G float*>(res)[o], v);
+        static_cast<MDX_G float*>(out)[o] = v;
     }
 }
 
-__device__ __forceinline__ void store_silu(const GemvArgs& a, int n, int r, int32_t ag, int32_t au, float xs, float scg,
-                                           float scu) {
+__device__ __forceinline__ uint16_t silu_h(const GemvArgs& a, int32_t ag, int32_t au, float xs, float scg, float scu) {
     const uint16_t g = f2bf(scaleback(ag, xs, scg));
     const uint16_t u = f2bf(scaleback(au, xs, scu));
     const float act = bf2f(a.lut[g]);
-    reinterpret_cast<uint16_t*>(a.out[0])[r * a.m[0].n + n] = f2bf(__fmul_rn(act, bf2f(u)));
+    return f2bf(__fmul_rn(act, bf2f(u)));
 }
 
 // red layout: [TPW][KS][16 columns][rows] (VALU) or [TPW][KS][64 lanes][4] (MFMA); sums the slices
@@ -408,26 +512,73 @@ __device__ __forceinline__ int32_t reduced(const GemvArgs& a, const int32_t* red
     return int32_t(s);
 }
 
+// Thread 0 polls *p until it reaches `target` (sleeping between polls), then the work-group
+// continues; what it reads next must be read with coherent loads. The poll is bounded: after about
+// 2^22 polls (seconds) it sets *err and gives up, so a broken producer costs wrong results, never a
+// hung GPU.
+__device__ __forceinline__ void wait_count(const uint32_t* p, uint32_t target, uint32_t* err) {
+    if (threadIdx.x == 0) {
+        uint32_t n = 0;
+        while (ld_c(p) < target) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++n == (1u << 22)) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+}
+
 template <bool MFMA>
-__device__ void epilogue(const GemvArgs& a, const int32_t* red, const float* prml) {
-    const int wg = blockIdx.x;
+__device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, const float* prml, int* flag) {
     const int per = 16 * a.rows;
     const float* xsl = prml + a.TPW * 16;
     if (a.epi == EPI_SILU) {
-        for (int e = threadIdx.x; e < per; e += blockDim.x) {
-            const int r = e >> 4, c = e & 15;
-            const int n = wg * 16 + c;  // pair: work-group wg owns gate tile wg and up tile wg
-            store_silu(a, n, r, reduced<MFMA>(a, red, 0, r, c), reduced<MFMA>(a, red, 1, r, c), xsl[r], prml[c],
-                       prml[16 + c]);
+        // pair: work unit wg owns gate tile wg and up tile wg; a thread stores two adjacent columns
+        for (int e = threadIdx.x; e < per / 2; e += blockDim.x) {
+            const int r = e >> 3, c = 2 * (e & 7);
+            const uint32_t v = uint32_t(silu_h(a, reduced<MFMA>(a, red, 0, r, c), reduced<MFMA>(a, red, 1, r, c), xsl[r],
+                                               prml[c], prml[16 + c])) |
+                               (uint32_t(silu_h(a, reduced<MFMA>(a, red, 0, r, c + 1), reduced<MFMA>(a, red, 1, r, c + 1),
+                                                xsl[r], prml[c + 1], prml[16 + c + 1]))
+                                << 16);
+            uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + wg * 16 + c);
+            if (a.coh) st_c(o, v);
+            else *o = v;
         }
         return;
     }
-    for (int e = threadIdx.x; e < a.TPW * per; e += blockDim.x) {
-        const int ts = e / per, rem = e - ts * per, r = rem >> 4, c = rem & 15;
+    if (a.epi == EPI_ACC) {
+        const int N = a.m[0].n;
+        for (int e = threadIdx.x; e < per; e += blockDim.x) {
+            const int r = e >> 4, c = e & 15;
+            __hip_atomic_fetch_add(a.acc + r * N + wg * 16 + c, reduced<MFMA>(a, red, 0, r, c), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const uint32_t old = publish(a.tcnt + wg);
+        if (threadIdx.x == 0) *flag = old == uint32_t(a.split - 1);
+        __syncthreads();
+        if (!*flag) return;
+        for (int e = threadIdx.x; e < per; e += blockDim.x) {
+            const int r = e >> 4, c = e & 15;
+            int32_t* p = a.acc + r * N + wg * 16 + c;
+            const int32_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            store_out(a, 0, wg * 16 + c, r, v, xsl[r], prml[c]);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(a.tcnt + wg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    for (int ts = 0; ts < a.TPW; ++ts) {  // one tile slot at a time: the matrix choice stays uniform
         int tile;
         const int mi = which_mat(a, wg * a.TPW + ts, tile);
-        if (tile >= a.m[mi].tiles) continue;
-        store_out(a, mi, tile * 16 + c, r, reduced<MFMA>(a, red, ts, r, c), xsl[r], prml[ts * 16 + c]);
+        if (tile >= mat_tiles(a, mi)) continue;
+        for (int e = threadIdx.x; e < per; e += blockDim.x) {
+            const int r = e >> 4, c = e & 15;
+            store_out(a, mi, tile * 16 + c, r, reduced<MFMA>(a, red, ts, r, c), xsl[r], prml[ts * 16 + c]);
+        }
     }
 }
 
@@ -442,78 +593,99 @@ __device__ __forceinline__ void nat_order(uint32_t lo, uint32_t hi, uint32_t& n0
 
 #define MDX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-// Copy `bytes` (a multiple of 16) from global to LDS with direct-to-LDS loads: one wave instruction
-// moves 64 x 16 contiguous bytes, no registers involved. The caller waits and barriers.
-__device__ __forceinline__ void dma_to_lds(const uint8_t* src, uint8_t* dst, int bytes) {
-    const int lane = threadIdx.x % WAVE, nw = blockDim.x / WAVE, w = threadIdx.x / WAVE;
-    for (int off = w * 1024; off < bytes; off += nw * 1024) {
-        if (off + lane * 16 < bytes)
-            __builtin_amdgcn_global_load_lds(src + off + lane * 16, MDX_LDS(dst + off), 16, 0, 0);
+// Copy `rows` runs of `bytes` (a multiple of 16) spaced `stride` apart in global memory into one
+// packed LDS block (row r at dst + r * bytes), 16 bytes per lane with direct-to-LDS loads (the LDS
+// side of one wave instruction is 64 x 16 contiguous bytes). The caller waits and barriers.
+__device__ __forceinline__ void dma_rows_to_lds(const MDX_G uint8_t* src, int stride, int bytes, int rows, uint8_t* dst,
+                                                int nthr) {
+    const int lane = threadIdx.x % WAVE, nw = nthr / WAVE, w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const int per = bytes / 16, pieces = rows * per;
+    for (int i0 = w * WAVE; i0 < pieces; i0 += nw * WAVE) {
+        const int i = i0 + lane;
+        if (i < pieces) {
+            const int r = i / per;
+            __builtin_amdgcn_global_load_lds(src + size_t(r) * stride + (i - r * per) * 16, MDX_LDS(dst + i0 * 16), 16, 0, 0);
+        }
     }
 }
 
+// The scale bytes a unit stages per tile row: the groups [g0, g1) that its chunk range touches when
+// those are whole 16-byte runs of every row, else the whole row.
+__device__ __forceinline__ void unit_groups(int cu0, int ncu, int lgG, int ng, int esz, int& g0, int& g1) {
+    g0 = (cu0 * CHUNK_K) >> lgG;
+    g1 = ((cu0 + ncu) * CHUNK_K + (1 << lgG) - 1) >> lgG;
+    if ((ng * esz) % 16 || (g0 * esz) % 16 || ((g1 - g0) * esz) % 16) {
+        g0 = 0;
+        g1 = ng;
+    }
+}
+
+// One work unit of the GEMV engine: work unit `wg` (TPW tiles, KS waves per tile) over the chunk
+// range [cu0, cu0 + ncu) of K.
+//
+// Issue order matters more than anything else here. Vector memory results return in issue order
+// and the wait instruction counts outstanding operations, so: first the one-shot operands (the
+// activation rows and the scales, straight to LDS, and the channel scales), then the weight ring
+// (RING loads in flight per wave), and only then a wait that lets the ring stay in flight. The
+// main loop runs whole ring rounds without conditions around the loads (a load under a condition
+// is merged at the join and waited for at once, which leaves one load in flight per wave): a chunk
+// past the slice re-reads the slice's last chunk and adds nothing. Everything that selects a
+// matrix or a tile is wave-uniform (scalar registers).
 template <bool MFMA, int R, int SDT, int RING>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+__device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds,
+                                          const UnitIn& in, int* flag) {
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
     const int K = a.K;
     const int ng = K >> a.lgG;
-    const int per_tile = 16 * ng * ESZ;
-    // LDS: activation rows (natural order) | scale blocks [TPW][16][ng] | reduction | parameters
+    const int Kr = ncu * CHUNK_K;
+    const int nthr = a.TPW * a.KS * WAVE;
+    int g0, g1;
+    unit_groups(cu0, ncu, a.lgG, ng, ESZ, g0, g1);
+    const int seg = (g1 - g0) * ESZ;  // scale bytes per tile row in LDS
+    // LDS: activation rows of the K range | scales [TPW][16][seg] | reduction | parameters [64] |
+    // 8 x activation sums per 32-k run [rows][Kr / 32] (one-row path) | flag
     uint8_t* xl = lds;
-    uint8_t* sl = xl + ((a.rows * K + 1023) & ~1023);
-    int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * per_tile + 1023) & ~1023));
+    uint8_t* sl = xl + ((a.rows * Kr + 1023) & ~1023);
+    int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
     float* prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
+    int32_t* xsum8 = reinterpret_cast<int32_t*>(prml + 64);
+    int* mixed = reinterpret_cast<int*>(xsum8 + ncu * 16);
 
     const int t = threadIdx.x;
-    const int wave = t / WAVE, lane = t % WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(t / WAVE), lane = t % WAVE;
     const int ts = wave / a.KS, slice = wave - ts * a.KS;
     int tile;
-    const int mi = which_mat(a, blockIdx.x * a.TPW + ts, tile);
-    const MatArg& M = a.m[mi];
-    const bool live = tile < M.tiles;
+    const int mi = which_mat(a, wg * a.TPW + ts, tile);
+    const MDX_G uint8_t* mq = mat_q(a, mi);
+    const int mtiles = mat_tiles(a, mi);
+    const bool live = tile < mtiles;
     const int NC = K / CHUNK_K;
-    const int c0 = live ? slice * NC / a.KS : 0, c1 = live ? (slice + 1) * NC / a.KS : 0;
+    const int c0 = live ? cu0 + slice * ncu / a.KS : 0, c1 = live ? cu0 + (slice + 1) * ncu / a.KS : 0;
     const int nch = c1 - c0;
     const int c = lane & 15, kq = lane >> 4;
     const int klane = 32 * kq;
     const int lgG = a.lgG;
 
-    // weight ring first (registers): every slot issues one load; reads past the slice repeat its
-    // last chunk so the wait counts are static
-    const uint8_t* wp;
-    int wstride;
-    if (a.layout == MDX_LAYOUT_TILE) {
-        wp = M.q + (tile * NC + c0) * 1024 + lane * 16;
-        wstride = 1024;
-    } else {
-        wp = M.q + (tile * 16 + c) * (K / 2) + c0 * 64 + kq * 16;
-        wstride = 64;
-    }
-    const int last = nch > 0 ? nch - 1 : 0;
-    uint4 buf[RING];
-#pragma unroll
-    for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
-
-    // then the one-shot operands straight into LDS: activation rows, the tiles' scale blocks
-    dma_to_lds(reinterpret_cast<const uint8_t*>(a.xq), xl, a.rows * K);
+    // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
+    if (!in.wait) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
     for (int tsi = 0; tsi < a.TPW; ++tsi) {
         int tl;
-        const int mm = which_mat(a, blockIdx.x * a.TPW + tsi, tl);
-        const uint8_t* sb = mm == 0 ? a.m[0].s : (mm == 1 ? a.m[1].s : a.m[2].s);
-        const int tiles = mm == 0 ? a.m[0].tiles : (mm == 1 ? a.m[1].tiles : a.m[2].tiles);
-        if (tl < tiles) dma_to_lds(sb + tl * per_tile, sl + tsi * per_tile, per_tile);
+        const int mm = which_mat(a, wg * a.TPW + tsi, tl);
+        const MDX_G uint8_t* sb = mat_s(a, mm);
+        if (tl >= mat_tiles(a, mm)) continue;
+        const MDX_G uint8_t* tb = sb + size_t(tl) * 16 * ng * ESZ;
+        if (seg % 16) dma_rows_to_lds(tb, 0, 16 * seg, 1, sl + tsi * 16 * seg, nthr);  // whole block at once
+        else dma_rows_to_lds(tb + g0 * ESZ, ng * ESZ, seg, 16, sl + tsi * 16 * seg, nthr);
     }
+    // channel scales: slice 0 of each tile slot loads its own tile's (wave-uniform matrix choice)
     float prm = 0.f;
-    if (t < a.TPW * 16) {
-        int tl;
-        const int mm = which_mat(a, blockIdx.x * a.TPW + t / 16, tl);
-        const float* sc = mm == 0 ? a.m[0].sch : (mm == 1 ? a.m[1].sch : a.m[2].sch);
-        const int tiles = mm == 0 ? a.m[0].tiles : (mm == 1 ? a.m[1].tiles : a.m[2].tiles);
-        prm = sc[(tl < tiles ? tl : 0) * 16 + (t & 15)];
-    } else if (t < a.TPW * 16 + a.rows) {
-        prm = a.xs[t - a.TPW * 16];
+    if (slice == 0 && lane < 16) {
+        const MDX_G float* sc = mat_sch(a, mi);
+        prm = sc[(live ? tile : 0) * 16 + lane];
+    } else if (!in.wait && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) {
+        prm = a.xs[lane - 16];
     }
+
     float cb[16];
     bool cbdef = true;
 #pragma unroll
@@ -521,65 +693,158 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         cb[i] = a.cb ? a.cb[i] : float(i - 8);
         cbdef = cbdef && cb[i] == float(i - 8);
     }
+
+    // 2. the weight ring: every slot issues one load; reads past the slice repeat its last chunk
+    const MDX_G uint8_t* wp;
+    int wstride;
+    if (a.layout == MDX_LAYOUT_TILE) {
+        wp = mq + (tile * NC + c0) * 1024 + lane * 16;
+        wstride = 1024;
+    } else {
+        wp = mq + (tile * 16 + c) * (K / 2) + c0 * 64 + kq * 16;
+        wstride = 64;
+    }
+    const int last = nch > 0 ? nch - 1 : 0;
+    uint4 buf[RING];
+#pragma unroll
+    for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
     const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
-    if (t < a.TPW * 16 + a.rows) prml[t] = prm;
-    __syncthreads();
-    const uint8_t* scol = sl + (ts * 16 + c) * ng * ESZ;
+    if (t == 0) *mixed = 0;
+
+    // 3. an activation produced in this launch: wait for it, then stage the rows' K range
+    if (in.wait) {
+        wait_count(in.wait, in.wait_for, in.err);
+        if (in.hr) {
+            // bf16 rows quantised with the row scale max(absmax / 127, 1e-30) (the row prep's formula)
+            const int per_row = Kr / 4;
+            for (int i = t; i < a.rows * per_row; i += nthr) {
+                const int r = i / per_row, j = i - r * per_row;
+                const float rm = __uint_as_float(ld_c(in.amax + r));
+                const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
+                uint16_t sb = f2bf(s);
+                if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+                const float sbf = bf2f(sb);
+                float v[4];
+                unpack4(*reinterpret_cast<const uint2*>(in.hr + r * K + cu0 * CHUNK_K + 4 * j), v);
+                uint32_t o = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float d = bfround(__fdiv_rn(v[e], sbf));
+                    o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
+                }
+                *reinterpret_cast<uint32_t*>(xl + r * Kr + 4 * j) = o;
+                if (j == 0) prml[a.TPW * 16 + r] = s;
+            }
+        } else {
+            dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
+            if (t < a.rows) prml[a.TPW * 16 + t] = a.xs[t];
+        }
+    }
+    if (in.wait) {
+        __syncthreads();
+    } else {
+        // the one-shot loads (issued before the ring) are complete once at most RING loads remain
+        static_assert(RING <= 15, "vmcnt field");
+        __builtin_amdgcn_s_waitcnt(RING | (7 << 4) | (15 << 8));  // vmcnt(RING), expcnt / lgkmcnt not waited
+        __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
+        __builtin_amdgcn_s_barrier();
+    }
+    // One pass over the staged operands: (a) (one row) every 8-byte group of the activation row becomes
+    // [x0 x2 x4 x6 | x1 x3 x5 x7], so the low / high nibble words of a code dword meet their
+    // activations without byte shuffles (a dot product is the same sum in any common k order), and
+    // the 8 * sum(x) corrections of the integral form per 32-k run are computed once per unit (with
+    // more rows this pass would touch rows x K bytes per unit for K / KS of work per wave: the MFMA
+    // path shuffles and sums per chunk instead); (b) whether every staged scale is an integer in
+    // [-15, 15] (then the unit takes the integral form throughout; both forms give the same int32
+    // sums, so the choice is free).
+    if (!MFMA) {
+        // consecutive lanes take consecutive 16-byte pieces (no LDS bank conflicts); the two pieces of
+        // a 32-k run meet by a shuffle
+        const int pieces = Kr / 16;
+        for (int base = 0; base < a.rows * pieces; base += nthr) {
+            const int i = base + t;
+            const int r = i / pieces, pc = i - r * pieces;
+            int s = 0;
+            if (i < a.rows * pieces) {
+                uint4* px = reinterpret_cast<uint4*>(xl + r * Kr + pc * 16);
+                const uint4 v = *px;
+                s = sdot4(int(v.x), 0x01010101, s);
+                s = sdot4(int(v.y), 0x01010101, s);
+                s = sdot4(int(v.z), 0x01010101, s);
+                s = sdot4(int(v.w), 0x01010101, s);
+                *px = make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x06040200u), __builtin_amdgcn_perm(v.y, v.x, 0x07050301u),
+                                 __builtin_amdgcn_perm(v.w, v.z, 0x06040200u), __builtin_amdgcn_perm(v.w, v.z, 0x07050301u));
+            }
+            s += shfl_xor(s, 1);
+            if (i < a.rows * pieces && pc % 2 == 0) xsum8[r * (Kr / 32) + pc / 2] = 8 * s;
+        }
+    }
+    if (can_int) {
+        bool bad = false;
+        for (int j = t; j < a.TPW * 16 * (seg / ESZ); j += nthr) {
+            const float s = rd_scale<SDT>(sl + j * ESZ);
+            bad = bad || !(s == rintf(s) && fabsf(s) <= 15.f);
+        }
+        if (bad) *mixed = 1;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done (the ring stays in flight)
+    __builtin_amdgcn_s_barrier();
+    const bool integ = can_int && *mixed == 0;  // uniform over the unit
+    const uint8_t* scol = sl + (ts * 16 + c) * seg - g0 * ESZ;
 
     if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
         int32_t tot[4] = {0, 0, 0, 0};  // integral chunks: sum of s * (chunk dot - 8 sum x)
         const bool xlive = (lane & 15) < a.rows;
-        const uint8_t* xrow = xl + (xlive ? (lane & 15) : 0) * K + klane;
+        const uint8_t* xrow = xl + (xlive ? (lane & 15) : 0) * Kr + klane - cu0 * CHUNK_K;
         for (int i0 = 0; i0 < nch; i0 += RING) {
 #pragma unroll
             for (int p = 0; p < RING; ++p) {
+                // whole rounds: a chunk past the slice re-reads the last one and adds nothing
                 const int i = i0 + p;
-                if (i < nch) {
-                    const uint4 w = buf[p];
-                    buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
-                    const int ch = c0 + i;
-                    const int k0 = ch * CHUNK_K + klane;
-                    const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
-                    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                    const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
-                    const uint4 xa = x4[0], xb = x4[1];
-                    uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                    if (!xlive)
+                const bool valid = i < nch;
+                const uint4 w = buf[p];
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
+                const int ch = c0 + min(i, last);
+                const int k0 = ch * CHUNK_K + klane;
+                const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
+                const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+                const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
+                const uint4 xa = x4[0], xb = x4[1];
+                uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                if (!xlive || !valid)
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) xd[j] = 0;
-                    const bool integ = can_int && __all(s0 == rintf(s0) && fabsf(s0) <= 15.f);
-                    if (integ) {
-                        v4i dacc = {0, 0, 0, 0};
+                    for (int j = 0; j < 8; ++j) xd[j] = 0;
+                if (integ) {
+                    v4i dacc = {0, 0, 0, 0};
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            uint32_t n0, n1;
-                            nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, n0, n1);
-                            dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
-                                                                         long(uint64_t(n0) | (uint64_t(n1) << 32)), dacc, 0, 0, 0);
-                        }
-                        // 8 * sum of the chunk's activation per row: own 32 bytes, then the 4 quarters
-                        int xsum = 0;
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t n0, n1;
+                        nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, n0, n1);
+                        dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                     long(uint64_t(n0) | (uint64_t(n1) << 32)), dacc, 0, 0, 0);
+                    }
+                    // 8 * sum of the chunk's activation per row: own 32 bytes, then the 4 quarters
+                    int xsum = 0;
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) xsum = sdot4(int(xd[j]), 0x01010101, xsum);
-                        xsum += shfl_xor(xsum, 16);
-                        xsum += shfl_xor(xsum, 32);
-                        const int sv = int(s0);
+                    for (int j = 0; j < 8; ++j) xsum = sdot4(int(xd[j]), 0x01010101, xsum);
+                    xsum += shfl_xor(xsum, 16);
+                    xsum += shfl_xor(xsum, 32);
+                    const int sv = valid ? int(s0) : 0;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int corr = 8 * __shfl(xsum, kq * 4 + r, 64);
-                            tot[r] += __mul24(sv, dacc[r] - corr);
-                        }
-                    } else {
-                        uint32_t lo[4], hi[4];
-                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
+                    for (int r = 0; r < 4; ++r) {
+                        const int corr = 8 * __shfl(xsum, kq * 4 + r, 64);
+                        tot[r] += __mul24(sv, dacc[r] - corr);
+                    }
+                } else {
+                    uint32_t lo[4], hi[4];
+                    decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            uint32_t n0, n1;
-                            nat_order(lo[j], hi[j], n0, n1);
-                            accE = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
-                                                                         long(uint64_t(n0) | (uint64_t(n1) << 32)), accE, 0, 0, 0);
-                        }
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t n0, n1;
+                        nat_order(lo[j], hi[j], n0, n1);
+                        accE = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                     long(uint64_t(n0) | (uint64_t(n1) << 32)), accE, 0, 0, 0);
                     }
                 }
             }
@@ -595,40 +860,39 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int p = 0; p < RING; ++p) {
                 const int i = i0 + p;
-                if (i < nch) {
-                    const uint4 w = buf[p];
-                    buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
-                    const int ch = c0 + i;
-                    const int k0 = ch * CHUNK_K + klane;
-                    const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
-                    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                    uint32_t nat[8];
-                    const bool integ = can_int && __all(s0 == rintf(s0) && fabsf(s0) <= 15.f);
-                    if (integ) {
+                const bool valid = i < nch;
+                const uint4 w = buf[p];
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
+                const int ch = c0 + min(i, last);
+                const int k0 = ch * CHUNK_K + klane;
+                const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
+                const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+                uint32_t lo[4], hi[4];  // even-k and odd-k weights (raw nibbles in the integral form)
+                if (integ) {
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, nat[2 * j], nat[2 * j + 1]);
-                    } else {
-                        uint32_t lo[4], hi[4];
-                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], nat[2 * j], nat[2 * j + 1]);
+                    for (int j = 0; j < 4; ++j) {
+                        lo[j] = wd[j] & 0x0F0F0F0Fu;
+                        hi[j] = (wd[j] >> 4) & 0x0F0F0F0Fu;
                     }
-                    const int sv = integ ? int(s0) : 1;
+                } else {
+                    decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
+                }
+                const int sv = valid ? (integ ? int(s0) : 1) : 0;
+                const int sg = (ch - cu0) * 4 + kq;  // this lane's 32-k run within the unit
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        if (r < a.rows) {
-                            const uint4* x4 = reinterpret_cast<const uint4*>(xl + r * K + ch * CHUNK_K + klane);
-                            const uint4 xa = x4[0], xb = x4[1];
-                            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                            int d = 0, xsum = 0;
+                for (int r = 0; r < R; ++r) {
+                    if (r < a.rows) {
+                        const uint4* x4 = reinterpret_cast<const uint4*>(xl + r * Kr + sg * 32);
+                        const uint4 xa = x4[0], xb = x4[1];
+                        const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                        int d = 0;
 #pragma unroll
-                            for (int j = 0; j < 8; ++j) d = sdot4(int(nat[j]), int(xv[j]), d);
-                            if (integ) {
-#pragma unroll
-                                for (int j = 0; j < 8; ++j) xsum = sdot4(int(xv[j]), 0x01010101, xsum);
-                            }
-                            tot[r] += __mul24(sv, d - 8 * xsum);
+                        for (int j = 0; j < 4; ++j) {
+                            d = sdot4(int(lo[j]), int(xv[2 * j]), d);
+                            d = sdot4(int(hi[j]), int(xv[2 * j + 1]), d);
                         }
+                        const int xs8 = integ ? xsum8[r * (Kr / 32) + sg] : 0;
+                        tot[r] += __mul24(sv, d - xs8);
                     }
                 }
             }
@@ -646,16 +910,36 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
             for (int r = 0; r < R; ++r)
                 if (r < a.rows) red[((ts * a.KS + slice) * 16 + lane) * a.rows + r] = tot[r];
     }
+    // the epilogue's parameters (only the epilogue reads them; written this late, their loads need no
+    // wait that would also wait for the ring)
+    if (slice == 0 && lane < 16) prml[ts * 16 + lane] = prm;
+    else if (!in.wait && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
     __syncthreads();
-    epilogue<MFMA>(a, red, prml);
+    epilogue<MFMA>(a, wg, red, prml, flag);
 }
 
-size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) {
-    const size_t per_tile = size_t(16) * (a.K >> a.lgG) * esz;
-    size_t s = ((size_t(a.rows) * a.K + 1023) & ~size_t(1023)) + ((a.TPW * per_tile + 1023) & ~size_t(1023));
-    s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
-    return s + 64 * 4;
+template <bool MFMA, int R, int SDT, int RING>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int flag;
+    gemv_unit<MFMA, R, SDT, RING>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
 }
+
+// LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
+size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
+    const int ng = a.K >> a.lgG;
+    int g0 = (cu0 * CHUNK_K) >> a.lgG, g1 = ((cu0 + ncu) * CHUNK_K + (1 << a.lgG) - 1) >> a.lgG;
+    if ((ng * esz) % 16 || (g0 * esz) % 16 || ((g1 - g0) * esz) % 16) {
+        g0 = 0;
+        g1 = ng;
+    }
+    const size_t seg = size_t(g1 - g0) * esz;
+    size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
+    s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
+    return s + 64 * 4 + size_t(ncu) * 16 * 4 + 16;  // parameters, activation sums, flag
+}
+
+size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mfma, esz, 0, a.K / CHUNK_K); }
 
 int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1); }
 
@@ -709,24 +993,9 @@ int check_w4(const mdx_w4* w, const char* what) {
 }
 
 // one GEMV launch over up to three matrices sharing K (or a gate/up pair)
-int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
-             void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st) {
-    MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
-    // the activation rows live in LDS: above 128 KiB, run the rows in two halves
-    if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
-        const int ra = 8, rb = rows - 8;
-        int rc = run_gemv(ws, nm, pair, xq, xs, ra, epi, outs, res, out_dt, lut, st);
-        if (rc) return rc;
-        const int esz = out_dt == MDX_DT_F32 ? 4 : 2;
-        void* o2[3];
-        const void* r2[3];
-        for (int i = 0; i < nm; ++i) {
-            o2[i] = static_cast<uint8_t*>(outs[i]) + size_t(ra) * ws[pair ? 0 : i]->n * esz;
-            r2[i] = res && res[i] ? static_cast<const uint8_t*>(res[i]) + size_t(ra) * ws[i]->n * esz : nullptr;
-        }
-        if (pair) o2[1] = o2[0];
-        return run_gemv(ws, nm, pair, xq + size_t(ra) * ws[0]->k, xs + ra, rb, epi, o2, r2, out_dt, lut, st);
-    }
+// Validate a GEMV's operands and fill its arguments (geometry left to the caller); total = tiles.
+int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
+               void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, GemvArgs& a, int& total) {
     MDX_CHECK(aligned(xq, 16), "x must be 16-byte aligned");
     const mdx_w4& w0 = *ws[0];
     for (int i = 0; i < nm; ++i) {
@@ -736,12 +1005,13 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
                       ws[i]->layout == w0.layout && ws[i]->decode == w0.decode,
                   "fused matrices must share K, group size, scale dtype, layout and decode mode");
         MDX_CHECK(ws[i]->codebook == w0.codebook, "fused matrices must share one codebook");
+        MDX_CHECK(aligned(ws[i]->s_rel, 16), "s_rel must be 16-byte aligned");
     }
     if (pair) MDX_CHECK(nm == 2 && ws[0]->n == ws[1]->n, "gate/up must have the same N");
-    GemvArgs a{};
+    a = GemvArgs{};
     a.nm = nm;
     a.pair = pair ? 1 : 0;
-    int total = 0;
+    total = 0;
     for (int i = 0; i < 3; ++i) {
         const mdx_w4& w = *ws[i < nm ? i : 0];
         a.m[i] = MatArg{reinterpret_cast<const uint8_t*>(w.q), reinterpret_cast<const uint8_t*>(w.s_rel), w.s_channel,
@@ -760,6 +1030,32 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     a.epi = epi;
     a.out_dt = out_dt;
     a.lut = lut;
+    a.force_exact = w0.decode == MDX_DECODE_EXACT;
+    return MDX_OK;
+}
+
+int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
+             void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st) {
+    MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
+    // the activation rows live in LDS: above 128 KiB, run the rows in two halves
+    if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
+        const int ra = 8, rb = rows - 8;
+        int rc = run_gemv(ws, nm, pair, xq, xs, ra, epi, outs, res, out_dt, lut, st);
+        if (rc) return rc;
+        const int esz = out_dt == MDX_DT_F32 ? 4 : 2;
+        void* o2[3];
+        const void* r2[3];
+        for (int i = 0; i < nm; ++i) {
+            o2[i] = static_cast<uint8_t*>(outs[i]) + size_t(ra) * ws[pair ? 0 : i]->n * esz;
+            r2[i] = res && res[i] ? static_cast<const uint8_t*>(res[i]) + size_t(ra) * ws[i]->n * esz : nullptr;
+        }
+        if (pair) o2[1] = o2[0];
+        return run_gemv(ws, nm, pair, xq + size_t(ra) * ws[0]->k, xs + ra, rb, epi, o2, r2, out_dt, lut, st);
+    }
+    GemvArgs a;
+    int total = 0;
+    int rc = setup_gemv(ws, nm, pair, xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
+    if (rc) return rc;
     const bool mfma = rows >= MFMA_MIN_ROWS;
     // geometry: TPW tiles per work-group, KS K-slices per tile (at most 16 waves per work-group):
     // the smallest split that puts >= 3072 waves on the chip (12 per CU), measured best on MI355X
@@ -779,22 +1075,153 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
         const int ks = atoi(env);
         if (ks >= 1 && ks <= maxks && NC % ks == 0) a.KS = ks;
     }
-    a.xglobal = 0;
-    const int esz = esz_of(w0.s_dtype);
-    MDX_CHECK((16 * (a.K >> a.lgG) * esz) % 16 == 0, "a tile's scale block must be a multiple of 16 bytes");
-    for (int i = 0; i < nm; ++i) MDX_CHECK(aligned(ws[i]->s_rel, 16), "s_rel must be 16-byte aligned");
+    const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
-    a.force_exact = w0.decode == MDX_DECODE_EXACT;
-    return launch_gemv_d<4>(a, w0.s_dtype, mfma, wgs, st);
+    return launch_gemv_d<4>(a, ws[0]->s_dtype, mfma, wgs, st);
+}
+
+// =================================================================================================
+// The fused MLP in one launch: a chain of work units, one per work-group, in work-group order.
+//   units [0, rows)              row prep of x (RMSNorm, rotation, int8) -> q1, s1
+//   next N1 / 16 units           gate/up tile pairs (SiLU epilogue -> h); the last of the 16 units of
+//                                a 256-column group rotates that group of every row -> hr, row absmax
+//   next (N2 / 16) x split       down: tile x K part; quantises its K part of hr, int32 partial sums
+//                                added into acc, the tile's last part stores out (+ residual); the
+//                                last tile to complete re-zeroes the control words
+// A unit only waits for units with smaller work-group ids. Work-groups are dispatched in id order,
+// so every unit a waiting unit depends on is running or done and waits for nothing later: no
+// dependence on how many work-groups fit on the chip. (The waits are bounded all the same.)
+// Hand-offs use coherent loads / stores and one counter bump per unit: no cache-wide fences and
+// no per-launch ticket counter (device atomics on one address serialise at ~11 ns each).
+// =================================================================================================
+enum : int { SY_PREP = 0, SY_GROUPS = 1, SY_TILES = 2, SY_ERR = 4, SY_HDR = 8 };
+// "x is quantised" and "h is rotated" are each broadcast to FLAG_N words FLAG_STRIDE words apart
+// (different memory channels), unit u polling word u % FLAG_N: a thousand work-groups polling one
+// word would queue on one channel and stall every weight stream that crosses it.
+constexpr int FLAG_N = 64, FLAG_STRIDE = 64;
+constexpr int CH_WAVES = 4;      // waves per work unit
+constexpr int CH_MAX_G1 = 64;    // 256-column groups of h at most (N1 <= 16384)
+constexpr int CH_MAX_K1 = 256 * CH_WAVES * 4;  // the row prep's reach with 4 waves x 4 groups
+
+struct MlpChain {
+    PrepArgs prep;        // x rows -> gu.xq / gu.xs
+    uint32_t* flags;      // [2][FLAG_N][FLAG_STRIDE]: x ready, h ready
+    GemvArgs gu, dn;      // gate/up pair (EPI_SILU into hb), down (EPI_ACC over K parts)
+    const uint16_t* hb;   // h [rows, N1]
+    uint16_t* hr;         // rotated h [rows, N1] (hb itself without rotation)
+    uint32_t* amax;       // [16] row absmax of hr, fp32 bits
+    uint32_t* sync;       // [SY_HDR + G1] control words, zero between launches
+    int rows, rot, n_prep, n_gu, n_dn, G1, dn_cu;
+};
+
+template <bool MFMA, int R, int SDT, int RING>
+__global__ __launch_bounds__(CH_WAVES * WAVE) void mlp_chain_kernel(MlpChain c) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float gsum[CH_MAX_K1 / 256];
+    __shared__ float wmax[CH_WAVES];
+    __shared__ int flag;
+    const int t = threadIdx.x;
+    const int u = blockIdx.x;
+    if (u < c.n_prep) {
+        prep_row<4, true>(c.prep, u, gsum, wmax);
+        const uint32_t old = publish(c.sync + SY_PREP);
+        if (t == 0) flag = old == uint32_t(c.n_prep - 1);
+        __syncthreads();
+        if (flag && t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 1u);
+    } else if (u < c.n_prep + c.n_gu) {
+        const int v = u - c.n_prep;
+        gemv_unit<MFMA, R, SDT, RING>(
+            c.gu, v, 0, c.gu.K / CHUNK_K, lds,
+            UnitIn{c.flags + (u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, nullptr, nullptr}, &flag);
+        const int g = v >> 4;
+        const uint32_t old = publish(c.sync + SY_HDR + g);
+        if (t == 0) flag = old == 15u;
+        __syncthreads();
+        if (flag) {
+            // group g of h is complete: rotate it (one wave per row), row absmax by atomic max of the
+            // non-negative fp32 bits (the same maximum as fmaxf over the waves of a row prep)
+            const int w = t / WAVE, lane = t % WAVE, N1 = c.gu.m[0].n;
+            for (int r = w; r < c.rows; r += CH_WAVES) {
+                float x[4];
+                unpack4(*reinterpret_cast<const uint2*>(c.hb + r * N1 + 256 * g + 4 * lane), x);
+                if (c.rot == MDX_ROT_H256) {
+                    double d[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d[e] = double(x[e]);
+                    fwht256_lane(d, lane);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = bfround(float(__dmul_rn(d[e], 0.0625)));
+                    const uint2 o = pack4(x);
+                    st_c(reinterpret_cast<uint64_t*>(c.hr + r * N1 + 256 * g + 4 * lane),
+                         uint64_t(o.x) | (uint64_t(o.y) << 32));
+                }
+                float m = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(x[e]));
+                m = wave_max(m);
+                if (lane == 0)
+                    __hip_atomic_fetch_max(c.amax + r, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (t == 0) st_c(c.sync + SY_HDR + g, 0u);
+            const uint32_t og = publish(c.sync + SY_GROUPS);
+            if (t == 0) flag = og == uint32_t(c.G1 - 1);
+            __syncthreads();
+            if (flag && t < FLAG_N) st_c(c.flags + (FLAG_N + t) * FLAG_STRIDE, 1u);
+        }
+    } else {
+        const int v = u - c.n_prep - c.n_gu;
+        const int tile = v / c.dn.split, part = v - tile * c.dn.split;
+        gemv_unit<MFMA, R, SDT, RING>(
+            c.dn, tile, part * c.dn_cu, c.dn_cu, lds,
+            UnitIn{c.flags + (FLAG_N + u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, c.hr, c.amax}, &flag);
+        // flag: this unit completed its tile. When every tile is complete, every unit of the launch
+        // is past its waits: the control words go back to zero for the next launch.
+        if (!flag) return;
+        __syncthreads();
+        if (t == 0)
+            flag = __hip_atomic_fetch_add(c.sync + SY_TILES, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   uint32_t(c.n_dn / c.dn.split - 1);
+        __syncthreads();
+        if (flag) {
+            if (t < 2 * FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 0u);
+            if (t < 16) st_c(c.amax + t, 0u);
+            if (t == 0) {
+                st_c(c.sync + SY_PREP, 0u);
+                st_c(c.sync + SY_GROUPS, 0u);
+                st_c(c.sync + SY_TILES, 0u);
+            }
+        }
+    }
+}
+
+template <bool MFMA, int R, int SDT>
+int launch_chain_t(const MlpChain& c, size_t smem, hipStream_t st) {
+    const void* fn = reinterpret_cast<const void*>(&mlp_chain_kernel<MFMA, R, SDT, 4>);
+    if (smem > 64 * 1024) allow_smem(fn, smem);
+    hipLaunchKernelGGL((mlp_chain_kernel<MFMA, R, SDT, 4>), dim3(unsigned(c.n_prep + c.n_gu + c.n_dn)),
+                       dim3(CH_WAVES * WAVE), smem, st, c);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
+int launch_chain(const MlpChain& c, int sdt, bool mfma, size_t smem, hipStream_t st) {
+    if (sdt == MDX_DT_F32) return mfma ? launch_chain_t<true, 4, MDX_DT_F32>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_F32>(c, smem, st);
+    if (sdt == MDX_DT_F16) return mfma ? launch_chain_t<true, 4, MDX_DT_F16>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_F16>(c, smem, st);
+    return mfma ? launch_chain_t<true, 4, MDX_DT_FP8E4M3>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_FP8E4M3>(c, smem, st);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-int prep_checks(int64_t rows, int64_t K, int32_t rot, const void* h) {
+int prep_checks(int64_t rows, int64_t K, int32_t rot, const void* h, const void* x = nullptr, const void* q = nullptr,
+                const void* nw = nullptr, const void* xn = nullptr) {
     MDX_CHECK(rows >= 0, "rows must be >= 0");
+    MDX_CHECK(aligned(x, 8) && aligned(nw, 8) && aligned(xn, 8) && aligned(q, 4),
+              "rows must be 8-byte aligned (int8 rows 4-byte aligned)");
     MDX_CHECK(K > 0 && K % 256 == 0 && K <= MAX_PREP_K, "K must be a multiple of 256 and <= 16384 (got %lld)",
               (long long)K);
     MDX_CHECK(rot == MDX_ROT_NONE || rot == MDX_ROT_H256 || (rot == MDX_ROT_MATRIX && h), "rotation");
+    MDX_CHECK(rot != MDX_ROT_MATRIX || aligned(h, 8), "rotation matrix must be 8-byte aligned");
+    MDX_CHECK(rows <= 65535, "rows must be <= 65535");
     return MDX_OK;
 }
 
@@ -817,7 +1244,7 @@ extern "C" int mdx_w4a8_decode_linear(const int8_t* x, const float* x_scale, con
 extern "C" int mdx_rot_quant(const uint16_t* x, const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows,
                              int64_t K, void* stream) {
     MDX_CHECK(x && q && scale, "null pointer");
-    int rc = prep_checks(rows, K, rot, h);
+    int rc = prep_checks(rows, K, rot, h, x, q);
     if (rc) return rc;
     if (rows == 0) return MDX_OK;
     PrepArgs a{x, nullptr, 0.f, nullptr, h, rot, q, scale, int(K)};
@@ -828,7 +1255,7 @@ extern "C" int mdx_rms_rot_quant(const uint16_t* x, const uint16_t* norm_w, floa
                                  const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K,
                                  void* stream) {
     MDX_CHECK(x && q && scale && norm_w, "null pointer");
-    int rc = prep_checks(rows, K, rot, h);
+    int rc = prep_checks(rows, K, rot, h, x, q, norm_w, xn_out);
     if (rc) return rc;
     if (rows == 0) return MDX_OK;
     PrepArgs a{x, norm_w, eps, xn_out, h, rot, q, scale, int(K)};
@@ -840,7 +1267,7 @@ extern "C" int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64
                                   const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K,
                                   void* stream) {
     MDX_CHECK(y && gate && sig_lut && q && scale, "null pointer");
-    int rc = prep_checks(rows, K, rot, h);
+    int rc = prep_checks(rows, K, rot, h, y, q);
     if (rc) return rc;
     MDX_CHECK(gate_head >= 8 && gate_head % 8 == 0 && K % gate_head == 0 && gate_head_stride % 8 == 0 &&
                   gate_offset % 8 == 0 && gate_row_stride % 8 == 0 && aligned(gate, 16),
@@ -859,8 +1286,8 @@ extern "C" int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64
 extern "C" int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* out, int64_t rows, int64_t K,
                            void* stream) {
     MDX_CHECK(x && norm_w && out, "null pointer");
-    MDX_CHECK(rows >= 0 && rows <= 65535 && K % 8 == 0 && K >= 8 && K <= 8 * PREP_THREADS * PREP_BLK,
-              "rows / K (K % 8 == 0, K <= %d)", 8 * PREP_THREADS * PREP_BLK);
+    MDX_CHECK(rows >= 0 && rows <= 65535 && K % 256 == 0 && K >= 256 && K <= MAX_PREP_K,
+              "rows / K (K % 256 == 0, K <= %d)", MAX_PREP_K);
     MDX_CHECK(aligned(x, 16) && aligned(norm_w, 16) && aligned(out, 16), "16-byte aligned rows");
     if (rows == 0) return MDX_OK;
     PrepArgs a{x, norm_w, eps, out, nullptr, MDX_ROT_NONE, nullptr, nullptr, int(K)};
@@ -884,9 +1311,127 @@ extern "C" int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t
     return MDX_OK;
 }
 
-extern "C" size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1) {
-    return align256(size_t(rows) * K1) + align256(size_t(rows) * N1) + align256(64 * 4) + align256(size_t(rows) * N1 * 2);
+namespace mdx {
+namespace {
+
+// Workspace of mdx_mono_mlp. First the zero-state part, at the same offsets whatever the shapes (a
+// call with fewer rows must not find its control words or accumulators inside the data of an
+// earlier call with more rows): control words [SY_HDR + CH_MAX_G1] | amax [16] | tile counters
+// [CH_MAX_K1 / 16] in a 4 KiB header, the broadcast flags [2][FLAG_N][FLAG_STRIDE], then
+// acc [16, CH_MAX_K1] int32. It must be zero before the
+// first call and every call leaves it zero (each call re-zeroes exactly what it used). Then,
+// 256-byte aligned, the data: q1 [rows, K1] | q2 [rows, N1] | scales [64] f32 | h [rows, N1] bf16 |
+// rotated h [rows, N1] bf16.
+constexpr size_t MLP_HDR = 4096;
+constexpr size_t MLP_FLAGS = size_t(2) * FLAG_N * FLAG_STRIDE * 4;
+static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header");
+
+struct MlpWs {
+    uint32_t* flags;
+    uint32_t* sync;
+    uint32_t* amax;
+    uint32_t* tcnt;
+    int32_t* acc;
+    int8_t* q1;
+    int8_t* q2;
+    float* s;
+    uint16_t* hb;
+    uint16_t* hr;
+    size_t bytes;
+};
+
+MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
+    MlpWs w{};
+    uint8_t* p = static_cast<uint8_t*>(base);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* q = p ? p + off : nullptr;
+        off += align256(bytes);
+        return q;
+    };
+    uint32_t* hdr = reinterpret_cast<uint32_t*>(take(MLP_HDR));
+    w.sync = hdr;
+    w.amax = hdr ? hdr + SY_HDR + CH_MAX_G1 : nullptr;
+    w.tcnt = hdr ? hdr + SY_HDR + CH_MAX_G1 + 16 : nullptr;
+    w.flags = reinterpret_cast<uint32_t*>(take(MLP_FLAGS));
+    w.acc = reinterpret_cast<int32_t*>(take(size_t(16) * CH_MAX_K1 * 4));
+    w.q1 = reinterpret_cast<int8_t*>(take(size_t(rows) * K1));
+    w.q2 = reinterpret_cast<int8_t*>(take(size_t(rows) * N1));
+    w.s = reinterpret_cast<float*>(take(64 * 4));
+    w.hb = reinterpret_cast<uint16_t*>(take(size_t(rows) * N1 * 2));
+    w.hr = reinterpret_cast<uint16_t*>(take(size_t(rows) * N1 * 2));
+    w.bytes = off;
+    return w;
 }
+
+// The one-launch chain, when the shapes fit it; returns -1 (nothing launched) when they do not.
+int mono_mlp_chain(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
+                   const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
+                   const uint16_t* residual, uint16_t* out, int rows, const MlpWs& w, hipStream_t st) {
+    const int64_t K1 = gate->k, N1 = gate->n;
+    if (rot == MDX_ROT_MATRIX || K1 > CH_MAX_K1 || N1 % 256 || N1 / 256 > CH_MAX_G1) return -1;
+    // opt-in (MDX_MLP_CHAIN=1): on MI355X the in-launch hand-offs (row prep of x, then the rotation
+    // of h) cost more than the two launch boundaries they remove (see the design notes)
+    const char* env = getenv("MDX_MLP_CHAIN");
+    if (!env || atoi(env) == 0) return -1;
+    MlpChain c{};
+    c.prep = PrepArgs{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
+    int total = 0, rc;
+    const mdx_w4* gu[2] = {gate, up};
+    void* o1[2] = {w.hb, w.hb};
+    if ((rc = setup_gemv(gu, 2, true, w.q1, w.s, rows, EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, c.gu, total)))
+        return rc;
+    const mdx_w4* dn[1] = {down};
+    void* o2[1] = {out};
+    const void* r2[1] = {residual};
+    if ((rc = setup_gemv(dn, 1, false, w.q2, w.s + 32, rows, EPI_ACC, o2, r2, MDX_DT_BF16, nullptr, c.dn, total)))
+        return rc;
+    MDX_CHECK(gate->s_dtype == down->s_dtype, "gate/up and down must share the scale dtype");
+    // gate/up: one tile pair per unit, 2 K slices; down: one tile per unit over a K part, 4 slices,
+    // the smallest number of parts that puts >= 3072 waves on the chip
+    c.gu.TPW = 2;
+    c.gu.KS = 2;
+    c.gu.coh = 1;
+    c.dn.TPW = 1;
+    c.dn.KS = 4;
+    const int NC2 = int(N1 / CHUNK_K), tiles2 = int(K1 / 16);
+    int split = 1;
+    for (int d = 1; d <= 16 && NC2 / d >= CH_WAVES; ++d) {
+        if (NC2 % d) continue;
+        split = d;
+        if (int64_t(tiles2) * d * CH_WAVES >= 3072) break;
+    }
+    c.dn.split = split;
+    c.dn.acc = w.acc;
+    c.dn.tcnt = w.tcnt;
+    c.dn_cu = NC2 / split;
+    c.hb = w.hb;
+    c.hr = rot == MDX_ROT_NONE ? w.hb : w.hr;
+    c.amax = w.amax;
+    c.sync = w.sync;
+    c.flags = w.flags;
+    c.rows = rows;
+    c.rot = rot;
+    c.n_prep = rows;
+    c.n_gu = int(N1 / 16);
+    c.n_dn = tiles2 * split;
+    c.G1 = int(N1 / 256);
+    const bool mfma = rows >= MFMA_MIN_ROWS;
+    const int esz = esz_of(gate->s_dtype);
+    size_t smem = std::max(gemv_smem(c.gu, mfma, esz), gemv_smem(c.dn, mfma, esz, 0, c.dn_cu));
+    smem = std::max(smem, gemv_smem(c.dn, mfma, esz, (split - 1) * c.dn_cu, c.dn_cu));
+    if (smem > 160 * 1024) return -1;
+    return launch_chain(c, gate->s_dtype, mfma, smem, st);
+}
+
+}  // namespace
+}  // namespace mdx
+
+extern "C" size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1) {
+    return mdx::mlp_ws(nullptr, rows, K1, N1).bytes;
+}
+
+extern "C" size_t mdx_mono_mlp_error_offset(void) { return 4 * mdx::SY_ERR; }
 
 extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
                             const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
@@ -895,32 +1440,29 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     MDX_CHECK(xn && silu_lut && gate && up && down && out && workspace, "null pointer");
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16");
     const int64_t K1 = gate->k, N1 = gate->n;
-    MDX_CHECK(up->n == N1 && up->k == K1 && down->k == N1, "gate/up [N1, K1], down [N2, N1] shapes");
-    int rc = prep_checks(rows, K1, rot, h);
+    MDX_CHECK(up->n == N1 && up->k == K1 && down->k == N1 && down->n == K1, "gate/up [N1, K1], down [K1, N1] shapes");
+    int rc = prep_checks(rows, K1, rot, h, xn, nullptr, norm_w);
     if (rc) return rc;
     if ((rc = prep_checks(rows, N1, rot, h))) return rc;
     MDX_CHECK(workspace_bytes >= mdx_mono_mlp_workspace(rows, K1, N1), "workspace too small");
     MDX_CHECK(aligned(workspace, 256), "workspace must be 256-byte aligned");
+    MDX_CHECK(aligned(out, 4) && aligned(residual, 4), "out / residual must be 4-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    uint8_t* p = static_cast<uint8_t*>(workspace);
-    int8_t* q1 = reinterpret_cast<int8_t*>(p);
-    p += align256(size_t(rows) * K1);
-    int8_t* q2 = reinterpret_cast<int8_t*>(p);
-    p += align256(size_t(rows) * N1);
-    float* s = reinterpret_cast<float*>(p);
-    p += align256(64 * 4);
-    uint16_t* hb = reinterpret_cast<uint16_t*>(p);
-    PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, q1, s, int(K1)};
+    const MlpWs w = mlp_ws(workspace, rows, K1, N1);
+    rc = mono_mlp_chain(xn, norm_w, eps, h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
+    if (rc >= 0) return rc;
+    // four launches: prep, gate/up, prep of h, down
+    PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
     if ((rc = launch_prep(pa, rows, st))) return rc;
     const mdx_w4* gu[2] = {gate, up};
-    void* o1[2] = {hb, hb};
-    if ((rc = run_gemv(gu, 2, true, q1, s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st))) return rc;
-    PrepArgs pb{hb, nullptr, 0.f, nullptr, h, rot, q2, s + 32, int(N1)};
+    void* o1[2] = {w.hb, w.hb};
+    if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st))) return rc;
+    PrepArgs pb{w.hb, nullptr, 0.f, nullptr, h, rot, w.q2, w.s + 32, int(N1)};
     if ((rc = launch_prep(pb, rows, st))) return rc;
     const mdx_w4* dn[1] = {down};
     void* o2[1] = {out};
     const void* r2[1] = {residual};
-    return run_gemv(dn, 1, false, q2, s + 32, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st);
+    return run_gemv(dn, 1, false, w.q2, w.s + 32, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st);
 }
 
 extern "C" int mdx_stream_gemv(const int8_t* x, const float* x_scale, const mdx_w4* const* mats, int32_t nmats,

@@ -89,6 +89,26 @@ def quant_rows(x):
     return q, scale
 
 
+_MLP_WS = {}
+
+
+def _mlp_workspace(dev):
+    """The per-device mono_mlp workspace (zero-filled once; every call leaves its control words and
+    accumulators zero), sized for 16 rows, hidden 4096, intermediate 16384."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _MLP_WS.get(key)
+    if ws is None:
+        ws = _MLP_WS[key] = torch.zeros(_lib.lib().mdx_mono_mlp_workspace(16, 4096, 16384), dtype=torch.uint8,
+                                        device=dev)
+    return ws
+
+
+def mlp_error(dev):
+    """1 if an in-kernel wait of a mono_mlp call on this device's workspace gave up (else 0)."""
+    off = _lib.lib().mdx_mono_mlp_error_offset()
+    return int(_mlp_workspace(dev)[off:off + 4].view(torch.int32).item())
+
+
 def mono_mlp_w4(xn, rot, h, silu_lut, gate: W4, up: W4, down: W4, norm_w=None, eps=1e-6, out=None, ws=None,
                 residual=None):
     """mono_mlp on prepared W4 handles (the library's own callers); norm_w: RMSNorm the input first;
@@ -99,7 +119,8 @@ def mono_mlp_w4(xn, rot, h, silu_lut, gate: W4, up: W4, down: W4, norm_w=None, e
         out = torch.empty(rows, down.n, dtype=torch.bfloat16, device=xn.device)
     ws_bytes = _lib.lib().mdx_mono_mlp_workspace(rows, K1, gate.n)
     if ws is None:
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=xn.device)
+        ws = _mlp_workspace(xn.device)
+    _check(ws.numel() >= ws_bytes, "mono_mlp workspace too small")
     _lib.call("mdx_mono_mlp", _lib.ptr(xn), _lib.ptr(norm_w), float(eps), _lib.ptr(h), rot, _lib.ptr(silu_lut),
               gate.struct(), up.struct(), down.struct(), _lib.ptr(residual), _lib.ptr(out), rows, _lib.ptr(ws),
               ws.numel(), _lib.stream_of(xn))
@@ -448,7 +469,7 @@ def _scratch(dev):
             q1=torch.empty(16, 16384, dtype=torch.int8, device=dev), s=torch.empty(64, dtype=torch.float32, device=dev),
             xn=torch.empty(16, 4096, **bf), x1=torch.empty(16, 4096, **bf), proj=torch.empty(16, 16384, **bf),
             z=torch.empty(16, 8192, **bf), ab=torch.empty(16, 256, **bf), core=torch.empty(16, 8192, **bf),
-            mlp_ws=torch.empty(_lib.lib().mdx_mono_mlp_workspace(16, 4096, 16384), dtype=torch.uint8, device=dev),
+            mlp_ws=_mlp_workspace(dev),
             wab={})
     return sc
 

@@ -38,6 +38,7 @@ SIGNATURES = {
     "mdx_w4a8_decode_linear": (ctypes.c_int, [c_void_p, c_void_p, W4P, c_void_p, c_void_p, c_int32, c_int64, c_void_p]),
     "mdx_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_mono_mlp_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "mdx_mono_mlp_error_offset": (c_size_t, []),
     "mdx_mono_mlp": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int32, c_void_p, W4P, W4P, W4P,
                                     c_void_p, c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "mdx_gate_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,

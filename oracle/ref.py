@@ -207,35 +207,26 @@ def rot_quant(x_bits, rot="h256", h=None):
 
 
 def rmsnorm_factor(xf, eps):
-    """r = 1 / sqrt(ss / K + eps) for float32 rows [rows, K]. ss: 256 partials, partial t sums
-    the squares of its elements in increasing order, its elements being the 8-element blocks
-    b = t + 256 j (elements 8 b .. 8 b + 7); then the halving tree p[t] + p[t + 128], + 64, .., + 1
-    (all float32). This is the library's canonical order."""
+    """r = 1 / sqrt(ss / K + eps) for float32 rows [rows, K] (K a multiple of 256), all float32.
+    ss in the library's canonical order: the row is cut into 256-element groups and each group
+    into 64 runs of 4 elements (run l: elements 4 l .. 4 l + 3); a run's partial is
+    ((sq0 + sq1) + sq2) + sq3, a group's sum is the halving tree over its 64 run partials
+    (p[l] + p[l + 32], then + 16, ..., + 1), and ss adds the group sums in group order."""
     xf = np.asarray(xf, dtype=np.float32)
     rows, K = xf.shape
-    sq = (xf * xf).astype(np.float32)
-    nb = K // 8
-    blk = sq.reshape(rows, nb, 8)
-    p = None
-    for j in range(-(-nb // 256)):
-        part = blk[:, 256 * j:256 * (j + 1), :]
-        if part.shape[1] < 256:  # threads without a block in this round keep their partial
-            pad = np.zeros((rows, 256 - part.shape[1], 8), np.float32)
-            part = np.concatenate([part, pad], axis=1)
-            valid = np.arange(256) < blk.shape[1] - 256 * j
-        else:
-            valid = np.ones(256, bool)
-        for e in range(8):
-            term = part[:, :, e]
-            if p is None:
-                p = np.where(valid[None, :], term, np.float32(0)).astype(np.float32)
-            else:
-                p = np.where(valid[None, :], (p + term).astype(np.float32), p)
-    n = 256
+    assert K % 256 == 0
+    sq = (xf * xf).astype(np.float32).reshape(rows, K // 256, 64, 4)
+    p = sq[..., 0]
+    for e in range(1, 4):
+        p = (p + sq[..., e]).astype(np.float32)
+    n = 64
     while n > 1:
         n //= 2
-        p = (p[:, :n] + p[:, n:2 * n]).astype(np.float32)
-    ss = p[:, 0]
+        p = (p[..., :n] + p[..., n:2 * n]).astype(np.float32)
+    gs = p[..., 0]
+    ss = gs[:, 0]
+    for g in range(1, K // 256):
+        ss = (ss + gs[:, g]).astype(np.float32)
     mean = (ss / np.float32(K)).astype(np.float32)
     return (np.float32(1.0) / np.sqrt((mean + np.float32(eps)).astype(np.float32))).astype(np.float32)
 

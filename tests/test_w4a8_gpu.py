@@ -204,3 +204,72 @@ def test_mlp_with_norm_matches_oracle(C, dev):
         xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
         want = ref.mono_mlp(xn, "none", None, bits(lut), *d)
         assert_bits_equal(bits(out), want, f"M={M}")
+
+
+def _mlp_handles(g, dev, fmt="gptq"):
+    from mdx import _lib, layout
+    ws, _ = _mlp_weights(g, fmt, dev, True)
+    cb = ws[0][3]
+    cbt = None if cb is None else cb.to(dev)
+    handles = [layout.W4(layout.tile_major_codes(q).to(dev), s.to(dev), c.to(dev), cbt, _lib.LAYOUT_TILE)
+               for q, s, c, _, _ in ws]
+    return ws, handles
+
+
+@pytest.mark.parametrize("rot", ["none", "h256"])
+def test_mlp_one_launch_equals_four_launches(C, dev, rot, monkeypatch):
+    """The one-launch MLP (ticket-ordered units, K-split down with int32 atomics) against the
+    four-launch form and the oracle, with a residual, for every row count class."""
+    from mdx import _lib, layout
+    g = torch.Generator().manual_seed(41)
+    ws, handles = _mlp_handles(g, dev)
+    lut = layout.silu_lut(dev)
+    nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    code = _lib.ROT_H256 if rot == "h256" else _lib.ROT_NONE
+    h = layout.regular_hadamard(dev) if rot == "h256" else None
+    d = _oracle_dicts(ws)
+    for M in (1, 2, 5, 8, 16):
+        print(f"case mlp-chain rot={rot} M={M}", flush=True)
+        x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        outs = []
+        for chain in ("1", "0"):  # one launch, four launches
+            monkeypatch.setenv("MDX_MLP_CHAIN", chain)
+            outs.append(C.mono_mlp_w4(x.to(dev), code, h, lut, *handles, norm_w=nw.to(dev), eps=1e-6,
+                                      residual=res.to(dev)))
+        torch.cuda.synchronize()
+        assert C.mlp_error(dev) == 0
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={M}"
+        xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
+        want = ref.add_bf16(bits(res), ref.mono_mlp(xn, rot, None if h is None else bits(h.cpu()), bits(lut.cpu()), *d))
+        assert_bits_equal(bits(outs[0]), want, f"M={M}")
+
+
+def test_mlp_one_launch_graph_replays(C, dev, monkeypatch):
+    """Captured once, replayed with new inputs between eager calls: every replay equals the eager
+    result (the control words and accumulators are back at zero after every launch)."""
+    from mdx import _lib, layout
+    monkeypatch.setenv("MDX_MLP_CHAIN", "1")
+    g = torch.Generator().manual_seed(43)
+    _, handles = _mlp_handles(g, dev)
+    lut = layout.silu_lut(dev)
+    hd = layout.regular_hadamard(dev)
+    nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    for M in (1, 8):
+        print(f"case mlp-chain graph M={M}", flush=True)
+        x = torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev)
+        out = torch.empty(M, 4096, dtype=torch.bfloat16, device=dev)
+        C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
+        for rep in range(4):
+            x.copy_(torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev))
+            graph.replay()
+            torch.cuda.synchronize()
+            got = out.clone()
+            want = C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6)
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={M} replay {rep}"
+        assert C.mlp_error(dev) == 0
