@@ -26,7 +26,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BF_RING = 8;
+constexpr int BF_RING = 4;
 
 struct Bf16Args {
     const uint16_t* x;     // [rows, K]
@@ -60,24 +60,32 @@ __global__ __launch_bounds__(1024) void bf16_linear_kernel(Bf16Args a) {
         wp = a.w + int64_t((live ? tile : 0) * 16 + c) * a.K + c0 * 32 + 8 * g;
         wstride = 32;
     }
-    u32x4 ring[RING];
-#pragma unroll
-    for (int p = 0; p < RING; ++p) ring[p] = ldnt(wp + min(p, last) * wstride);
+    // weights and activation both travel in the ring (RING chunks ahead); whole ring rounds without
+    // conditions around the loads (a chunk past the slice re-reads the last one and adds nothing)
     const bool xlive = c < a.rows;
     const uint16_t* xp = a.x + (xlive ? c : 0) * a.K + c0 * 32 + 8 * g;
+    u32x4 ring[RING], xring[RING];
+#pragma unroll
+    for (int p = 0; p < RING; ++p) {
+        // the same issue order as the loop's refills (static wait counts hold for every round)
+        ring[p] = ldnt(wp + min(p, last) * wstride);
+        xring[p] = *reinterpret_cast<const u32x4*>(xp + min(p, last) * 32);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int i0 = 0; i0 < nch; i0 += RING) {
 #pragma unroll
         for (int p = 0; p < RING; ++p) {
+            // consume the slot, then refill it (the old and new values never live at once, so the ring
+            // keeps its registers across iterations instead of being copied at the loop end)
             const int i = i0 + p;
-            if (i < nch) {
-                const u32x4 wv = ring[p];
-                ring[p] = ldnt(wp + min(i + RING, last) * wstride);
-                u32x4 xv = *reinterpret_cast<const u32x4*>(xp + i * 32);
-                if (!xlive) xv = u32x4{0u, 0u, 0u, 0u};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv),
-                                                              __builtin_bit_cast(bf16x8, xv), acc, 0, 0, 0);
-            }
+            u32x4 xv = xring[p];
+            if (!xlive || i >= nch) xv = u32x4{0u, 0u, 0u, 0u};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ring[p]), __builtin_bit_cast(bf16x8, xv),
+                                                          acc, 0, 0, 0);
+            ring[p] = ldnt(wp + min(i + RING, last) * wstride);
+            xring[p] = *reinterpret_cast<const u32x4*>(xp + min(i + RING, last) * 32);
+            __builtin_amdgcn_sched_barrier(0);  // both refills stay here, RING chunks ahead of their use
         }
     }
     // D: lane holds outputs n = 16 tile + 4 g + i of row c

@@ -804,7 +804,6 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const int i = i0 + p;
                 const bool valid = i < nch;
                 const uint4 w = buf[p];
-                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                 const int ch = c0 + min(i, last);
                 const int k0 = ch * CHUNK_K + klane;
                 const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
@@ -847,6 +846,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                                                                      long(uint64_t(n0) | (uint64_t(n1) << 32)), accE, 0, 0, 0);
                     }
                 }
+                // refill the slot only now: its old and new contents never live at once, so the ring
+                // keeps its registers across rounds (no copies, and no wait, at the loop end)
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         int32_t* dst = red + ((ts * a.KS + slice) * 64 + lane) * 4;
@@ -862,7 +865,6 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const int i = i0 + p;
                 const bool valid = i < nch;
                 const uint4 w = buf[p];
-                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
                 const int ch = c0 + min(i, last);
                 const int k0 = ch * CHUNK_K + klane;
                 const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
@@ -895,6 +897,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                         tot[r] += __mul24(sv, d - xs8);
                     }
                 }
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);  // refill after use (see above)
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         // fold the four k quarters of each column (lanes c, c + 16, c + 32, c + 48)
