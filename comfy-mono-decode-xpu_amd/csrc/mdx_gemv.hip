@@ -643,13 +643,15 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     unit_groups(cu0, ncu, a.lgG, ng, ESZ, g0, g1);
     const int seg = (g1 - g0) * ESZ;  // scale bytes per tile row in LDS
     // LDS: activation rows of the K range | scales [TPW][16][seg] | reduction | parameters [64] |
-    // 8 x activation sums per 32-k run [rows][Kr / 32] (one-row path) | flag
+    // 8 x activation sums (one row: [rows][Kr / 32] per 32-k run; MFMA: [ncu][16] per chunk) | flag |
+    // 32 zero bytes (the activation of MFMA rows past the last)
     uint8_t* xl = lds;
     uint8_t* sl = xl + ((a.rows * Kr + 1023) & ~1023);
     int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
     float* prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
     int32_t* xsum8 = reinterpret_cast<int32_t*>(prml + 64);
     int* mixed = reinterpret_cast<int*>(xsum8 + ncu * 16);
+    uint8_t* zeros = reinterpret_cast<uint8_t*>(mixed + 4);
 
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t / WAVE), lane = t % WAVE;
@@ -710,6 +712,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
     const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
     if (t == 0) *mixed = 0;
+    if (t < 8) reinterpret_cast<uint32_t*>(zeros)[t] = 0u;
 
     // 3. an activation produced in this launch: wait for it, then stage the rows' K range
     if (in.wait) {
@@ -749,34 +752,30 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
         __builtin_amdgcn_s_barrier();
     }
-    // One pass over the staged operands: (a) (one row) every 8-byte group of the activation row becomes
-    // [x0 x2 x4 x6 | x1 x3 x5 x7], so the low / high nibble words of a code dword meet their
-    // activations without byte shuffles (a dot product is the same sum in any common k order), and
-    // the 8 * sum(x) corrections of the integral form per 32-k run are computed once per unit (with
-    // more rows this pass would touch rows x K bytes per unit for K / KS of work per wave: the MFMA
-    // path shuffles and sums per chunk instead); (b) whether every staged scale is an integer in
-    // [-15, 15] (then the unit takes the integral form throughout; both forms give the same int32
-    // sums, so the choice is free).
-    if (!MFMA) {
-        // consecutive lanes take consecutive 16-byte pieces (no LDS bank conflicts); the two pieces of
-        // a 32-k run meet by a shuffle
-        const int pieces = Kr / 16;
+    // One pass over the staged operands: (a) the 8 * sum(x) corrections of the integral form, once
+    // per unit (one row: per 32-k run, [rows][Kr / 32]; MFMA: per 128-k chunk, [ncu][16 rows]);
+    // (b) whether every staged scale is an integer in [-15, 15] (then the unit takes the integral
+    // form throughout; both forms give the same int32 sums, so the choice is free). Consecutive
+    // lanes read consecutive 16-byte pieces (no LDS bank conflicts); the pieces of one run (2, or 8
+    // for a chunk) meet by shuffles.
+    {
+        const int pieces = Kr / 16, run = MFMA ? 8 : 2;
         for (int base = 0; base < a.rows * pieces; base += nthr) {
             const int i = base + t;
             const int r = i / pieces, pc = i - r * pieces;
             int s = 0;
             if (i < a.rows * pieces) {
-                uint4* px = reinterpret_cast<uint4*>(xl + r * Kr + pc * 16);
-                const uint4 v = *px;
+                const uint4 v = *reinterpret_cast<const uint4*>(xl + r * Kr + pc * 16);
                 s = sdot4(int(v.x), 0x01010101, s);
                 s = sdot4(int(v.y), 0x01010101, s);
                 s = sdot4(int(v.z), 0x01010101, s);
                 s = sdot4(int(v.w), 0x01010101, s);
-                *px = make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x06040200u), __builtin_amdgcn_perm(v.y, v.x, 0x07050301u),
-                                 __builtin_amdgcn_perm(v.w, v.z, 0x06040200u), __builtin_amdgcn_perm(v.w, v.z, 0x07050301u));
             }
-            s += shfl_xor(s, 1);
-            if (i < a.rows * pieces && pc % 2 == 0) xsum8[r * (Kr / 32) + pc / 2] = 8 * s;
+            for (int d = 1; d < run; d <<= 1) s += shfl_xor(s, d);
+            if (i < a.rows * pieces && pc % run == 0) {
+                if (MFMA) xsum8[(pc / run) * 16 + r] = 8 * s;
+                else xsum8[r * (Kr / 32) + pc / run] = 8 * s;
+            }
         }
     }
     if (can_int) {
@@ -790,13 +789,18 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done (the ring stays in flight)
     __builtin_amdgcn_s_barrier();
     const bool integ = can_int && *mixed == 0;  // uniform over the unit
+    // the tile-major layout keeps k 0..3 of a code word in its low nibbles and k 4..7 in its high
+    // ones (natural activation order); the checkpoint layout interleaves them (even k low, odd k high)
+    const bool split = a.layout == MDX_LAYOUT_TILE;
     const uint8_t* scol = sl + (ts * 16 + c) * seg - g0 * ESZ;
 
     if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
         int32_t tot[4] = {0, 0, 0, 0};  // integral chunks: sum of s * (chunk dot - 8 sum x)
+        // rows past the last read 32 zero bytes at every chunk (stride 0)
         const bool xlive = (lane & 15) < a.rows;
-        const uint8_t* xrow = xl + (xlive ? (lane & 15) : 0) * Kr + klane - cu0 * CHUNK_K;
+        const uint8_t* xrow = xlive ? xl + (lane & 15) * Kr + klane - cu0 * CHUNK_K : zeros;
+        const int xstride = xlive ? CHUNK_K : 0;
         for (int i0 = 0; i0 < nch; i0 += RING) {
 #pragma unroll
             for (int p = 0; p < RING; ++p) {
@@ -808,40 +812,35 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const int k0 = ch * CHUNK_K + klane;
                 const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
                 const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
+                const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * xstride);
                 const uint4 xa = x4[0], xb = x4[1];
                 uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                if (!xlive || !valid)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) xd[j] = 0;
                 if (integ) {
                     v4i dacc = {0, 0, 0, 0};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        uint32_t n0, n1;
-                        nat_order(wd[j] & 0x0F0F0F0Fu, (wd[j] >> 4) & 0x0F0F0F0Fu, n0, n1);
+                        uint32_t n0 = wd[j] & 0x0F0F0F0Fu, n1 = (wd[j] >> 4) & 0x0F0F0F0Fu;
+                        if (!split) nat_order(n0, n1, n0, n1);
                         dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
                                                                      long(uint64_t(n0) | (uint64_t(n1) << 32)), dacc, 0, 0, 0);
                     }
-                    // 8 * sum of the chunk's activation per row: own 32 bytes, then the 4 quarters
-                    int xsum = 0;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) xsum = sdot4(int(xd[j]), 0x01010101, xsum);
-                    xsum += shfl_xor(xsum, 16);
-                    xsum += shfl_xor(xsum, 32);
+                    // D rows 4 kq + r: minus 8 * that row's chunk sum, times the chunk's scale (0 past the slice)
+                    const int4 corr = *reinterpret_cast<const int4*>(xsum8 + (ch - cu0) * 16 + 4 * kq);
                     const int sv = valid ? int(s0) : 0;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int corr = 8 * __shfl(xsum, kq * 4 + r, 64);
-                        tot[r] += __mul24(sv, dacc[r] - corr);
-                    }
+                    tot[0] += __mul24(sv, dacc[0] - corr.x);
+                    tot[1] += __mul24(sv, dacc[1] - corr.y);
+                    tot[2] += __mul24(sv, dacc[2] - corr.z);
+                    tot[3] += __mul24(sv, dacc[3] - corr.w);
                 } else {
+                    if (!valid)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) xd[j] = 0;
                     uint32_t lo[4], hi[4];
                     decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        uint32_t n0, n1;
-                        nat_order(lo[j], hi[j], n0, n1);
+                        uint32_t n0 = lo[j], n1 = hi[j];
+                        if (!split) nat_order(n0, n1, n0, n1);
                         accE = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
                                                                      long(uint64_t(n0) | (uint64_t(n1) << 32)), accE, 0, 0, 0);
                     }
@@ -869,7 +868,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const int k0 = ch * CHUNK_K + klane;
                 const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
                 const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                uint32_t lo[4], hi[4];  // even-k and odd-k weights (raw nibbles in the integral form)
+                uint32_t lo[4], hi[4];  // weights of k 8 j + [0, 4) and + [4, 8) (raw nibbles in the integral form)
                 if (integ) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -879,6 +878,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 } else {
                     decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
                 }
+                if (!split)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], lo[j], hi[j]);
                 const int sv = valid ? (integ ? int(s0) : 1) : 0;
                 const int sg = (ch - cu0) * 4 + kq;  // this lane's 32-k run within the unit
 #pragma unroll
@@ -940,7 +942,7 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     const size_t seg = size_t(g1 - g0) * esz;
     size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
-    return s + 64 * 4 + size_t(ncu) * 16 * 4 + 16;  // parameters, activation sums, flag
+    return s + 64 * 4 + size_t(ncu) * 16 * 4 + 16 + 32;  // parameters, activation sums, flag, zeros
 }
 
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mfma, esz, 0, a.K / CHUNK_K); }

@@ -18,20 +18,39 @@ from . import _lib
 _SDT = {torch.float32: _lib.DT_F32, torch.float16: _lib.DT_F16, torch.float8_e4m3fn: _lib.DT_FP8E4M3}
 
 
+def _split_nibbles(b: torch.Tensor) -> torch.Tensor:
+    """Every 4-byte word of 8 codes in the packed order (byte i: code 2i low, 2i + 1 high) -> the
+    split order: low nibbles of bytes 0..3 = codes 0..3, high nibbles = codes 4..7."""
+    u = b.contiguous().view(torch.uint8).reshape(-1, 4)
+    codes = torch.stack([u & 15, u >> 4], dim=-1).reshape(-1, 8)
+    return (codes[:, :4] | (codes[:, 4:] << 4)).reshape(b.shape).view(torch.int8)
+
+
+def _join_nibbles(b: torch.Tensor) -> torch.Tensor:
+    """Inverse of _split_nibbles."""
+    u = b.contiguous().view(torch.uint8).reshape(-1, 4)
+    codes = torch.cat([u & 15, u >> 4], dim=-1)  # codes 0..7
+    return (codes[:, 0::2] | (codes[:, 1::2] << 4)).reshape(b.shape).view(torch.int8)
+
+
 def tile_major_codes(packed: torch.Tensor) -> torch.Tensor:
     """[N, K/2] codes -> the tile-major copy [N/16][K/128][4][16][16 B], kept as [N, K/2].
 
     Chunk (tile, k0) of 16 columns x 128 k becomes one contiguous KiB whose 16-byte piece
-    (kq, c) is column c's codes of k0 + 32 kq + [0, 32): one coalesced load per wave."""
+    (kq, c) is column c's codes of k0 + 32 kq + [0, 32): one coalesced load per wave. Within each
+    4-byte word (8 consecutive k) the low nibbles hold k 0..3 and the high nibbles k 4..7, so a
+    word's two nibble masks line up with two natural-order activation words (no byte shuffles)."""
     n, kb = packed.shape
     assert n % 16 == 0 and kb % 64 == 0, "N % 16 and K % 128"
-    return packed.reshape(n // 16, 16, kb // 64, 4, 16).permute(0, 2, 3, 1, 4).contiguous().reshape(n, kb)
+    t = packed.reshape(n // 16, 16, kb // 64, 4, 16).permute(0, 2, 3, 1, 4).contiguous().reshape(n, kb)
+    return _split_nibbles(t)
 
 
 def row_major_codes(tiled: torch.Tensor) -> torch.Tensor:
     """Inverse of tile_major_codes."""
     n, kb = tiled.shape
-    return tiled.reshape(n // 16, kb // 64, 4, 16, 16).permute(0, 3, 1, 2, 4).contiguous().reshape(n, kb)
+    t = _join_nibbles(tiled)
+    return t.reshape(n // 16, kb // 64, 4, 16, 16).permute(0, 3, 1, 2, 4).contiguous().reshape(n, kb)
 
 
 def pack_codes(codes: torch.Tensor) -> torch.Tensor:

@@ -166,11 +166,18 @@ def test_tile_major_layout_invariants():
     t = layout.tile_major_codes(q)
     assert t.shape == q.shape
     assert torch.equal(layout.row_major_codes(t), q)
-    assert torch.equal(torch.sort(t.flatten()).values, torch.sort(q.flatten()).values)
-    # first KiB = tile 0, chunk 0: piece (kq, c) = column c's bytes [16 kq, 16 kq + 16)
-    first = t.flatten()[:1024].view(4, 16, 16)
+    codes = layout.unpack_codes(q)  # [64, 1024] in k order
+    # tile 1, chunk 2: piece (kq, c) holds column 16 + c's codes of k = 256 + 32 kq + [0, 32), each
+    # 4-byte word w (k = 8 w + [0, 8)) with k 0..3 in its low nibbles and k 4..7 in its high nibbles
+    nc = 1024 // 128
+    blk = t.flatten().view(torch.uint8)[(1 * nc + 2) * 1024:(1 * nc + 3) * 1024].view(4, 16, 4, 4).to(torch.int32)
     for kq in range(4):
-        assert torch.equal(first[kq], q[:16, 16 * kq:16 * kq + 16])
+        for c in range(16):
+            for w in range(4):
+                k = 256 + 32 * kq + 8 * w
+                want = codes[16 + c, k:k + 8]
+                got = torch.cat([blk[kq, c, w] & 15, blk[kq, c, w] >> 4])
+                assert torch.equal(got, want), (kq, c, w)
 
 
 def test_gptq_packer_error_bound():
