@@ -15,9 +15,10 @@
 // (q, k sum of squares); ctl int32 [2 + 3 slots] = pending, parity, accepted slots, parents, program.
 // Channels of proj / qb: q [0, KD), k [KD, 2 KD), v [2 KD, 2 KD + HV 128), KD = HK 128.
 //
-// Launches: gdn_conv_kernel (one thread per channel: owns its conv history), then gdn_head_kernel (one
-// work-group of 512 per value head: thread (row group rg, column col) holds state rows
-// 32 rg .. 32 rg + 31 of column col in registers).
+// Launches: gdn_conv_kernel (one thread per channel: owns its conv history; the q / k work-groups also
+// take their heads' sums of squares; extra work-groups, four per value head, compute the a / b
+// projections beside them), then gdn_head_kernel (one work-group of 512 per value head: thread
+// (row group rg, column col) holds state rows 32 rg .. 32 rg + 31 of column col in registers).
 #include <math.h>
 
 #include "mdx_common.hpp"
@@ -56,12 +57,60 @@ __device__ __forceinline__ bool ctl_ok(const GdnArgs& a) {
     return p >= 0 && p <= 1 && pending >= 0 && pending <= a.slots;
 }
 
+// a / b projections of this step's rows for head h: 2 R dot products of length K spread over the
+// four work-groups of the head (one job per wave and pass); lane l sums its elements in order (the
+// 8-element blocks l + 64 j), then a halving tree over the lanes. The bf16-rounded results go to
+// gates[p][row][h][0 / 1]; the head kernel turns them into (decay, beta) in place.
+__device__ void gdn_ab_part(const GdnArgs& a, int h, int quarter, int p) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int R = a.R, S = a.slots;
+    for (int job = quarter * 4 + wv; job < 2 * R; job += 16) {
+        const int kind = job / R, ts = job % R;
+        const uint16_t* w = (kind == 0 ? a.wa : a.wb) + int64_t(h) * a.K;
+        const uint16_t* x = a.xn + int64_t(ts) * a.K;
+        uint4 xv[8], wvv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int b0 = lane + 64 * i;
+            const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
+            xv[i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
+            wvv[i] = *reinterpret_cast<const uint4*>(w + 8 * bc);
+        }
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (lane + 64 * i >= a.K / 8) continue;
+            const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            const uint32_t ww[4] = {wvv[i].x, wvv[i].y, wvv[i].z, wvv[i].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xe = __uint_as_float((e & 1) ? (xw[e >> 1] & 0xFFFF0000u) : (xw[e >> 1] << 16));
+                const float we = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
+                part = fmaf(xe, we, part);
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
+        if (lane == 0) a.gates[((p * S + ts) * a.HV + h) * 2 + kind] = bfround(part);
+    }
+}
+
 // One thread per channel (it owns the channel's history); the work-group stages its 256 channels'
-// projection rows in LDS, so the ancestors of a tree row are LDS reads by index.
+// projection rows in LDS, so the ancestors of a tree row are LDS reads by index. A work-group of q or
+// k channels (two heads) also takes the sums of squares of its heads' conv outputs per row (lane l:
+// elements l and l + 64, then a halving tree) into sums[p][row][kh][q / k]. The work-groups after
+// the channels' compute the a / b projections (four per value head).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     __shared__ int sctl[2 + 3 * MAXS];
     __shared__ uint16_t prl[MAXS][256];
+    __shared__ float sq[MAXS][256];
     const int t = threadIdx.x;
+    const int nconv = (a.C + 255) / 256;
+    if (int(blockIdx.x) >= nconv) {
+        if (!ctl_ok(a)) return;
+        const int b = blockIdx.x - nconv;
+        gdn_ab_part(a, b / 4, b % 4, a.ctl[1]);
+        return;
+    }
     const int c = blockIdx.x * 256 + t;
     if (t < 2 + 3 * a.slots) sctl[t] = a.ctl[t];
     const int R = a.R;
@@ -76,7 +125,8 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     for (int r = 0; r < MAXS; ++r) prl[r][t] = pr[r];
     __syncthreads();
     const int S = a.slots, pending = sctl[0], p = sctl[1];
-    if (!cl || !(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;
+    if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // uniform
+    if (!cl) return;  // (only a last, partial work-group of v channels, which takes no sums)
     const int* acc = sctl + 2;
     const int* parent = sctl + 2 + S;
     uint16_t old[CW], prevacc[CW];
@@ -122,13 +172,28 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
         }
         a.qb[(p * S + ts) * C + c] = out;
         a.pb[(p * S + ts) * C + c] = ts < R ? prl[ts][t] : uint16_t(0);
+        if (ts < R) sq[ts][t] = bf2f(out);
+    }
+    // q / k heads of this work-group: sums of squares per row (the v channels have none)
+    const int KD = a.HK * DH;
+    if (int(blockIdx.x) * 256 >= 2 * KD) return;
+    __syncthreads();
+    const int lane = t & 63, wv = t >> 6;
+    if (wv & 1) return;  // wave 2 j owns head j of the work-group (its elements 0..63; 64..127 from wave 2 j + 1)
+    const int c0 = blockIdx.x * 256 + 128 * (wv >> 1);
+    const int which = c0 >= KD, kh = (c0 - which * KD) / DH;
+    for (int ts = 0; ts < R; ++ts) {
+        const float v0 = sq[ts][64 * wv + lane], v1 = sq[ts][64 * wv + 64 + lane];
+        float part = fmaf(v1, v1, __fmul_rn(v0, v0));
+        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
+        if (lane == 0) a.sums[((p * S + ts) * a.HK + kh) * 2 + which] = part;
     }
 }
 
 __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH], vvec[2 * MAXS][DH], rawb[MAXS][DH];
     __shared__ float mbuf[2][RG][DH], rbuf[2][RG][DH];
-    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], cab[MAXS][2], csum[MAXS][2], rss[MAXS];
+    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], csum[MAXS][2], rss[MAXS];
     __shared__ int ectl[2 + 3 * MAXS];
     if (!ctl_ok(a)) return;
     const int t = threadIdx.x, h = blockIdx.x;
@@ -149,88 +214,29 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
     const int E = E0 + E1;
     auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
 
-    // this step's a / b projections and q / k sums of squares, one wave per dot product: lane l sums
-    // its elements in order (a / b: the 8-element blocks l + 64 j; sums: elements l and l + 64), then a
-    // halving tree over the lanes (the library's fixed order)
     const int lane = t & 63, wv = t >> 6;
-    // a / b: 2 R dot products of length K over the 8 waves, all of a wave's loads issued first
-    constexpr int ABJ = (2 * MAXS + GT / 64 - 1) / (GT / 64);  // jobs per wave, at most
-    for (int j0 = 0; j0 < ABJ; j0 += 2) {
-        uint4 xv[2][8], wvv[2][8];
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            const int job = wv + (GT / 64) * (j0 + jj);
-            const bool live = job < 2 * R;
-            const int kind = live ? job / R : 0, ts = live ? job % R : 0;
-            const uint16_t* w = (kind == 0 ? a.wa : a.wb) + int64_t(h) * a.K;
-            const uint16_t* x = a.xn + int64_t(ts) * a.K;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int b0 = lane + 64 * i;
-                const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
-                xv[jj][i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
-                wvv[jj][i] = *reinterpret_cast<const uint4*>(w + 8 * bc);
-            }
-        }
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            const int job = wv + (GT / 64) * (j0 + jj);
-            float part = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                if (lane + 64 * i >= a.K / 8) continue;  // (a dead job's sum is discarded)
-                const uint32_t xw[4] = {xv[jj][i].x, xv[jj][i].y, xv[jj][i].z, xv[jj][i].w};
-                const uint32_t ww[4] = {wvv[jj][i].x, wvv[jj][i].y, wvv[jj][i].z, wvv[jj][i].w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float xe = __uint_as_float((e & 1) ? (xw[e >> 1] & 0xFFFF0000u) : (xw[e >> 1] << 16));
-                    const float we = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
-                    part = fmaf(xe, we, part);
-                }
-            }
-            for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
-            if (lane == 0 && job < 2 * R) cab[job % R][job / R] = bfround(part);  // a, b as bf16
-        }
-    }
-    // q / k sums of squares of this step's rows: 2 R jobs, one per wave pass, loads first
-    {
-        float v0[4], v1[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int job = wv + (GT / 64) * jj;
-            const bool live = job < 2 * R;
-            const uint16_t* src = a.qb + (p * S + (live ? job % R : 0)) * C + (live ? job / R : 0) * KD + kh * DH;
-            v0[jj] = bf2f(src[lane]);
-            v1[jj] = bf2f(src[lane + 64]);  // (a dead job's sum is discarded)
-        }
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int job = wv + (GT / 64) * jj;
-            float part = fmaf(v1[jj], v1[jj], __fmul_rn(v0[jj], v0[jj]));
-            for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
-            if (lane == 0 && job < 2 * R) csum[job % R][job / R] = part;
-        }
-    }
-    __syncthreads();
+    // this step's gates from the a / b projections the conv launch left in gates[p] (then (decay, beta)
+    // in their place, for this step's entries and the next step's replay); this step's q / k sums
     if (t < S) {
         float decay = 0.f, beta = 0.f;
         if (t < R) {
-            const float av = __fadd_rn(cab[t][0], a.dt_bias[h]);
-            const float bv = cab[t][1];
+            const float av = __fadd_rn(a.gates[((p * S + t) * HV + h) * 2], a.dt_bias[h]);
+            const float bv = a.gates[((p * S + t) * HV + h) * 2 + 1];
             const float sp = av > 20.f ? av : log1pf(expf(av));
             decay = expf(__fmul_rn(a.g_decay[h], sp));
             beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bv))));
         }
-        a.gates[((p * S + t) * HV + h) * 2] = decay;
-        a.gates[((p * S + t) * HV + h) * 2 + 1] = beta;
         cgate[t][0] = decay;
         cgate[t][1] = beta;
-    } else if (t >= 64 && t < 64 + 2 * S) {
-        const int which = (t - 64) / S, ts = (t - 64) % S;
-        // the heads of one key head write identical values
-        a.sums[((p * S + ts) * HK + kh) * 2 + which] = ts < R ? csum[ts][which] : 0.f;
+    } else if (t >= 64 && t < 64 + 2 * R) {
+        const int which = (t - 64) / R, ts = (t - 64) % R;
+        csum[ts][which] = a.sums[((p * S + ts) * HK + kh) * 2 + which];
     }
     __syncthreads();
+    if (t < S) {
+        a.gates[((p * S + t) * HV + h) * 2] = cgate[t][0];
+        a.gates[((p * S + t) * HV + h) * 2 + 1] = cgate[t][1];
+    }
     // the entries' inputs: k * ki, (q * scale) * qi, v, decay, beta
     if (t < E) {
         const int e = t, ts = slot_of(e);
@@ -401,7 +407,7 @@ extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint1
     a.C = int(2 * HK * DH + HV * DH);
     a.slots = int(slots);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + 4 * a.HV), dim3(256), 0, st, a);
     MDX_LAUNCHED();
     hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV), dim3(GT), 0, st, a);
     MDX_LAUNCHED();
