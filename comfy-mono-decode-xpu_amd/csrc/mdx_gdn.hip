@@ -16,9 +16,12 @@
 // Channels of proj / qb: q [0, KD), k [KD, 2 KD), v [2 KD, 2 KD + HV 128), KD = HK 128.
 //
 // Launches: gdn_conv_kernel (one thread per channel: owns its conv history; the q / k work-groups also
-// take their heads' sums of squares; extra work-groups, four per value head, compute the a / b
-// projections beside them), then gdn_head_kernel (one work-group of 512 per value head: thread
-// (row group rg, column col) holds state rows 32 rg .. 32 rg + 31 of column col in registers).
+// take their heads' sums of squares; extra work-groups, four per value head, compute the gates beside
+// them), then gdn_head_kernel (four work-groups of 256 per value head, 32 state columns each: thread
+// (row group rg, column col) holds state rows 16 rg .. 16 rg + 15 of its column in registers; raw bf16
+// outputs), then the gated RMSNorm per head in place (the row-prep kernel's head-norm mode, which the
+// decode stack instead fuses into the output projection's activation prep: mdx_gdn_core_raw +
+// mdx_gnorm_rot_quant).
 #include <math.h>
 
 #include "mdx_common.hpp"
@@ -26,12 +29,11 @@
 namespace mdx {
 namespace {
 
-constexpr int DH = 128, CW = 3, RG = 4, RPG = DH / RG, GT = RG * DH;
+constexpr int DH = 128, CW = 3;
 constexpr int MAXS = 16;
 
 struct GdnArgs {
     const uint16_t* proj;   // [R, C]
-    const uint16_t* z;      // [R, HV * 128]
     const uint16_t* xn;     // [R, K]: the normalised layer input (a = xn . wa[h], b = xn . wb[h])
     const uint16_t* wa;     // [HV, K]
     const uint16_t* wb;     // [HV, K]
@@ -46,8 +48,7 @@ struct GdnArgs {
     float* rec;             // [HV][128][128]
     float* gates;           // [2][slots][HV][2]
     float* sums;            // [2][slots][HK][2]
-    const uint16_t* gnorm_w;// [128]
-    float eps, qscale;
+    float qscale;
     uint16_t* core;         // [R, HV * 128]
     int R, HK, HV, C, slots;
 };
@@ -57,40 +58,57 @@ __device__ __forceinline__ bool ctl_ok(const GdnArgs& a) {
     return p >= 0 && p <= 1 && pending >= 0 && pending <= a.slots;
 }
 
-// a / b projections of this step's rows for head h: 2 R dot products of length K spread over the
-// four work-groups of the head (one job per wave and pass); lane l sums its elements in order (the
-// 8-element blocks l + 64 j), then a halving tree over the lanes. The bf16-rounded results go to
-// gates[p][row][h][0 / 1]; the head kernel turns them into (decay, beta) in place.
-__device__ void gdn_ab_part(const GdnArgs& a, int h, int quarter, int p) {
+// This step's gates of head h: one wave per row computes a = xn . wa[h] and b = xn . wb[h] (lane l
+// sums its elements in order, the 8-element blocks l + 64 j, then a halving tree over the lanes; both
+// rounded to bf16), then decay = exp(g_decay * softplus(a + dt_bias)) and beta = bf16(sigmoid(b)) into
+// gates[p][row][h]; rows R .. slots - 1 get zeros. The four work-groups of a head share its rows.
+__device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter, int p) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int R = a.R, S = a.slots;
-    for (int job = quarter * 4 + wv; job < 2 * R; job += 16) {
-        const int kind = job / R, ts = job % R;
-        const uint16_t* w = (kind == 0 ? a.wa : a.wb) + int64_t(h) * a.K;
-        const uint16_t* x = a.xn + int64_t(ts) * a.K;
-        uint4 xv[8], wvv[8];
+    for (int ts = quarter * 4 + wv; ts < S; ts += 16) {
+        float decay = 0.f, beta = 0.f;
+        if (ts < R) {
+            const uint16_t* x = a.xn + int64_t(ts) * a.K;
+            const uint16_t* wa = a.wa + int64_t(h) * a.K;
+            const uint16_t* wb = a.wb + int64_t(h) * a.K;
+            uint4 xv[8], av[8], bv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int b0 = lane + 64 * i;
-            const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
-            xv[i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
-            wvv[i] = *reinterpret_cast<const uint4*>(w + 8 * bc);
-        }
-        float part = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (lane + 64 * i >= a.K / 8) continue;
-            const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            const uint32_t ww[4] = {wvv[i].x, wvv[i].y, wvv[i].z, wvv[i].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float xe = __uint_as_float((e & 1) ? (xw[e >> 1] & 0xFFFF0000u) : (xw[e >> 1] << 16));
-                const float we = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
-                part = fmaf(xe, we, part);
+            for (int i = 0; i < 8; ++i) {
+                const int b0 = lane + 64 * i;
+                const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
+                xv[i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
+                av[i] = *reinterpret_cast<const uint4*>(wa + 8 * bc);
+                bv[i] = *reinterpret_cast<const uint4*>(wb + 8 * bc);
             }
+            float pa = 0.f, pb = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (lane + 64 * i >= a.K / 8) continue;
+                const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+                const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+                const uint32_t bw[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int sh = (e & 1) ? 0 : 16;
+                    const uint32_t m = (e & 1) ? 0xFFFF0000u : 0xFFFFFFFFu;
+                    const float xe = __uint_as_float((xw[e >> 1] << sh) & m);
+                    pa = fmaf(xe, __uint_as_float((aw[e >> 1] << sh) & m), pa);
+                    pb = fmaf(xe, __uint_as_float((bw[e >> 1] << sh) & m), pb);
+                }
+            }
+            for (int off = 32; off >= 1; off >>= 1) {
+                pa = __fadd_rn(pa, shfl_down(pa, off));
+                pb = __fadd_rn(pb, shfl_down(pb, off));
+            }
+            const float avv = __fadd_rn(bfround(pa), a.dt_bias[h]);
+            const float sp = avv > 20.f ? avv : log1pf(expf(avv));
+            decay = expf(__fmul_rn(a.g_decay[h], sp));
+            beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bfround(pb)))));
         }
-        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
-        if (lane == 0) a.gates[((p * S + ts) * a.HV + h) * 2 + kind] = bfround(part);
+        if (lane == 0) {
+            a.gates[((p * S + ts) * a.HV + h) * 2] = decay;
+            a.gates[((p * S + ts) * a.HV + h) * 2 + 1] = beta;
+        }
     }
 }
 
@@ -98,7 +116,7 @@ __device__ void gdn_ab_part(const GdnArgs& a, int h, int quarter, int p) {
 // projection rows in LDS, so the ancestors of a tree row are LDS reads by index. A work-group of q or
 // k channels (two heads) also takes the sums of squares of its heads' conv outputs per row (lane l:
 // elements l and l + 64, then a halving tree) into sums[p][row][kh][q / k]. The work-groups after
-// the channels' compute the a / b projections (four per value head).
+// the channels' compute this step's gates (four per value head).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     __shared__ int sctl[2 + 3 * MAXS];
     __shared__ uint16_t prl[MAXS][256];
@@ -108,7 +126,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     if (int(blockIdx.x) >= nconv) {
         if (!ctl_ok(a)) return;
         const int b = blockIdx.x - nconv;
-        gdn_ab_part(a, b / 4, b % 4, a.ctl[1]);
+        gdn_gates_part(a, b / 4, b % 4, a.ctl[1]);
         return;
     }
     const int c = blockIdx.x * 256 + t;
@@ -190,13 +208,20 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     }
 }
 
-__global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
-    __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH], vvec[2 * MAXS][DH], rawb[MAXS][DH];
-    __shared__ float mbuf[2][RG][DH], rbuf[2][RG][DH];
-    __shared__ float egate[2 * MAXS][2], cgate[MAXS][2], csum[MAXS][2], rss[MAXS];
+// The delta rule of value head h over the columns [32 cs, 32 cs + 32) of its state (four work-groups
+// per head: the columns are independent). Thread (row group rg, column col) holds state rows
+// 16 rg .. 16 rg + 15 of its column in registers. Outputs: the raw bf16 rows of the verify entries (the
+// gated RMSNorm, which needs the whole head, is applied by whoever reads them); rows of this step that
+// no verify entry writes are zeros.
+constexpr int NSPLIT = 4, SC = DH / NSPLIT, HRG = 8, HRPG = DH / HRG, HT = HRG * SC;
+
+__global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
+    __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
+    __shared__ float vvec[2 * MAXS][SC], mbuf[2][HRG][SC], rbuf[2][HRG][SC], rawc[MAXS][SC];
+    __shared__ float egate[2 * MAXS][2];
     __shared__ int ectl[2 + 3 * MAXS];
     if (!ctl_ok(a)) return;
-    const int t = threadIdx.x, h = blockIdx.x;
+    const int t = threadIdx.x, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
     const int kh = h / (HV / HK);
     const int64_t C = a.C;
@@ -213,152 +238,107 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
         while (E1 < R && prog[E1] >= 0 && (prog[E1] & 15) < R) ++E1;
     const int E = E0 + E1;
     auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
-
-    const int lane = t & 63, wv = t >> 6;
-    // this step's gates from the a / b projections the conv launch left in gates[p] (then (decay, beta)
-    // in their place, for this step's entries and the next step's replay); this step's q / k sums
-    if (t < S) {
-        float decay = 0.f, beta = 0.f;
-        if (t < R) {
-            const float av = __fadd_rn(a.gates[((p * S + t) * HV + h) * 2], a.dt_bias[h]);
-            const float bv = a.gates[((p * S + t) * HV + h) * 2 + 1];
-            const float sp = av > 20.f ? av : log1pf(expf(av));
-            decay = expf(__fmul_rn(a.g_decay[h], sp));
-            beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bv))));
-        }
-        cgate[t][0] = decay;
-        cgate[t][1] = beta;
-    } else if (t >= 64 && t < 64 + 2 * R) {
-        const int which = (t - 64) / R, ts = (t - 64) % R;
-        csum[ts][which] = a.sums[((p * S + ts) * HK + kh) * 2 + which];
-    }
-    __syncthreads();
-    if (t < S) {
-        a.gates[((p * S + t) * HV + h) * 2] = cgate[t][0];
-        a.gates[((p * S + t) * HV + h) * 2 + 1] = cgate[t][1];
-    }
-    // the entries' inputs: k * ki, (q * scale) * qi, v, decay, beta
+    // the entries' gates (this step's from the conv launch, the replay's from the previous step) and
+    // inputs: k * ki, (q * scale) * qi over the whole head, v over this work-group's columns
     if (t < E) {
-        const int e = t, ts = slot_of(e);
-        if (e < E0) {
-            egate[e][0] = a.gates[(((1 - p) * S + ts) * HV + h) * 2];
-            egate[e][1] = a.gates[(((1 - p) * S + ts) * HV + h) * 2 + 1];
-        } else {
-            egate[e][0] = cgate[ts][0];
-            egate[e][1] = cgate[ts][1];
-        }
+        const int e = t, ts = slot_of(e), par = e < E0 ? 1 - p : p;
+        egate[e][0] = a.gates[((par * S + ts) * HV + h) * 2];
+        egate[e][1] = a.gates[((par * S + ts) * HV + h) * 2 + 1];
     }
-#pragma unroll 8
-    for (int i = t; i < E * DH; i += GT) {
+    for (int i = t; i < E * DH; i += HT) {
         const int e = i / DH, d = i % DH, ts = slot_of(e);
         const bool verify = e >= E0;
         const int par = verify ? p : 1 - p;
         const uint16_t* src = a.qb + (par * S + ts) * C;
-        const float sk = verify ? csum[ts][1] : a.sums[((par * S + ts) * HK + kh) * 2 + 1];
-        const float ki = __fdiv_rn(1.f, fmaxf(sqrt_rn(sk), 1e-12f));
+        const float* sm = a.sums + ((par * S + ts) * HK + kh) * 2;
+        const float ki = __fdiv_rn(1.f, fmaxf(sqrt_rn(sm[1]), 1e-12f));
         kvec[e][d] = __fmul_rn(bf2f(src[KD + kh * DH + d]), ki);
-        vvec[e][d] = bf2f(src[2 * KD + h * DH + d]);
         if (verify) {
-            const float qi = __fdiv_rn(1.f, fmaxf(sqrt_rn(csum[ts][0]), 1e-12f));
+            const float qi = __fdiv_rn(1.f, fmaxf(sqrt_rn(sm[0]), 1e-12f));
             qvec[e - E0][d] = __fmul_rn(__fmul_rn(bf2f(src[kh * DH + d]), a.qscale), qi);
         }
+        if (d < SC) vvec[e][d] = bf2f(src[2 * KD + h * DH + cs * SC + d]);
     }
-    // the state: rows 32 rg + r of column col
-    const int col = t % DH, rg = t / DH;
-    float st[RPG];
-    float* rs = a.rec + (int64_t(h) * DH + rg * RPG) * DH + col;
+    const int col = t % SC, rg = t / SC;
+    float st[HRPG];
+    float* rs = a.rec + (int64_t(h) * DH + rg * HRPG) * DH + cs * SC + col;
 #pragma unroll
-    for (int r = 0; r < RPG; ++r) st[r] = rs[r * DH];
+    for (int r = 0; r < HRPG; ++r) st[r] = rs[r * DH];
     __syncthreads();
     for (int e = 0; e < E; ++e) {
         const bool verify = e >= E0;
         const bool commit = !verify || (prog[e - E0] & 32);
         const float decay = egate[e][0], beta = egate[e][1];
-        // this entry's k^ (and q^) rows of the thread's row group, as 16-byte LDS broadcasts issued together
-        float kr[RPG], qr[RPG];
-        const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * RPG);
+        float kr[HRPG], qr[HRPG];
+        const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * HRPG);
 #pragma unroll
-        for (int j = 0; j < RPG / 4; ++j) {
+        for (int j = 0; j < HRPG / 4; ++j) {
             const float4 v = k4[j];
             kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
         }
         if (verify) {
-            const float4* q4 = reinterpret_cast<const float4*>(qvec[e - E0] + rg * RPG);
+            const float4* q4 = reinterpret_cast<const float4*>(qvec[e - E0] + rg * HRPG);
 #pragma unroll
-            for (int j = 0; j < RPG / 4; ++j) {
+            for (int j = 0; j < HRPG / 4; ++j) {
                 const float4 v = q4[j];
                 qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
             }
         }
-        // kv partial over the 32 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3))
+        // kv partial over the 16 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3))
         float m4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) {
+            for (int r = 0; r < HRPG; ++r) {
                 st[r] = __fmul_rn(st[r], decay);
                 m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
             }
         } else {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
+            for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
         }
         mbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
         __syncthreads();  // the one barrier per entry (mbuf / rbuf alternate)
-        const float kv = __fadd_rn(__fadd_rn(__fadd_rn(mbuf[e & 1][0][col], mbuf[e & 1][1][col]), mbuf[e & 1][2][col]),
-                                   mbuf[e & 1][3][col]);
+        float kv = mbuf[e & 1][0][col];
+#pragma unroll
+        for (int g = 1; g < HRG; ++g) kv = __fadd_rn(kv, mbuf[e & 1][g][col]);
         const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
         float r4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) st[r] = fmaf(kr[r], delta, st[r]);
+            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, st[r]);
             if (verify)
 #pragma unroll
-                for (int r = 0; r < RPG; ++r) r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
+                for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
         } else {
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
+            for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
         }
         if (verify) rbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
         if (e == E0 - 1 && replayed)
 #pragma unroll
-            for (int r = 0; r < RPG; ++r) rs[r * DH] = st[r];
+            for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
         // the previous verify entry's output row (its partials are complete after this barrier)
         if (e > E0 && rg == 0) {
             const int pe = e - 1;
-            rawb[slot_of(pe)][col] = bfround(__fadd_rn(__fadd_rn(__fadd_rn(rbuf[pe & 1][0][col], rbuf[pe & 1][1][col]),
-                                                                 rbuf[pe & 1][2][col]), rbuf[pe & 1][3][col]));
+            float o = rbuf[pe & 1][0][col];
+#pragma unroll
+            for (int g = 1; g < HRG; ++g) o = __fadd_rn(o, rbuf[pe & 1][g][col]);
+            rawc[slot_of(pe)][col] = bfround(o);
         }
     }
     __syncthreads();
     if (E1 > 0 && rg == 0) {
         const int pe = E - 1;
-        rawb[slot_of(pe)][col] = bfround(__fadd_rn(__fadd_rn(__fadd_rn(rbuf[pe & 1][0][col], rbuf[pe & 1][1][col]),
-                                                             rbuf[pe & 1][2][col]), rbuf[pe & 1][3][col]));
+        float o = rbuf[pe & 1][0][col];
+#pragma unroll
+        for (int g = 1; g < HRG; ++g) o = __fadd_rn(o, rbuf[pe & 1][g][col]);
+        rawc[slot_of(pe)][col] = bfround(o);
     }
     unsigned written = 0;
     for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
     __syncthreads();
-    // gated RMSNorm: one wave per row: lane l sums columns l and l + 64, then a halving tree
-    for (int ts = wv; ts < R; ts += GT / 64) {
-        if (!((written >> ts) & 1)) continue;
-        const float x0 = rawb[ts][lane], x1 = rawb[ts][lane + 64];
-        float s2 = __fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1));
-        for (int off = 32; off >= 1; off >>= 1) s2 = __fadd_rn(s2, shfl_down(s2, off));
-        if (lane == 0) rss[ts] = s2;
-    }
-    __syncthreads();
-    const float gw = bf2f(a.gnorm_w[col]);
-    for (int ts = rg; ts < R; ts += RG) {
-        uint16_t outv = 0;
-        if ((written >> ts) & 1) {
-            const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(rss[ts], float(DH)), a.eps)));
-            const float normed = bfround(__fmul_rn(__fmul_rn(rawb[ts][col], gw), rsq));
-            const float zz = bf2f(a.z[ts * HV * DH + h * DH + col]);
-            const float gz = bfround(__fdiv_rn(zz, __fadd_rn(1.f, expf(-zz))));
-            outv = f2bf(__fmul_rn(normed, gz));
-        }
-        a.core[ts * HV * DH + h * DH + col] = outv;
-    }
+    for (int ts = rg; ts < R; ts += HRG)
+        a.core[ts * HV * DH + h * DH + cs * SC + col] = ((written >> ts) & 1) ? f2bf(rawc[ts][col]) : uint16_t(0);
 }
 
 }  // namespace
@@ -366,23 +346,22 @@ __global__ __launch_bounds__(GT) void gdn_head_kernel(GdnArgs a) {
 
 using namespace mdx;
 
-extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa,
-                            const uint16_t* wb, int64_t K, const uint16_t* conv_w,
-                            uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
-                            const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums,
-                            const uint16_t* gnorm_w, float gnorm_eps, float qscale, uint16_t* core, int64_t rows,
-                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
-    MDX_CHECK(proj && z && xn && wa && wb && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
-                  rec_state && gates && sums && gnorm_w && core,
+namespace {
+
+int gdn_run(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
+            const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
+            const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums, float qscale,
+            uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, hipStream_t st) {
+    MDX_CHECK(proj && xn && wa && wb && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
+                  rec_state && gates && sums && core,
               "null pointer");
     MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
     MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
-    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV <= 1024, "heads");
+    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV % 2 == 0 && HV <= 128, "heads (HV even, <= 128)");
     MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
               "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
     GdnArgs a{};
     a.proj = proj;
-    a.z = z;
     a.xn = xn;
     a.wa = wa;
     a.wb = wb;
@@ -397,8 +376,6 @@ extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint1
     a.rec = rec_state;
     a.gates = gates;
     a.sums = sums;
-    a.gnorm_w = gnorm_w;
-    a.eps = gnorm_eps;
     a.qscale = qscale;
     a.core = core;
     a.R = int(rows);
@@ -406,10 +383,35 @@ extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint1
     a.HV = int(HV);
     a.C = int(2 * HK * DH + HV * DH);
     a.slots = int(slots);
-    hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + 4 * a.HV), dim3(256), 0, st, a);
     MDX_LAUNCHED();
-    hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV), dim3(GT), 0, st, a);
+    hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV * NSPLIT), dim3(HT), 0, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
+}
+
+}  // namespace
+
+extern "C" int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
+                                int64_t K, const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf,
+                                uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias, const float* g_decay,
+                                float* rec_state, float* gates, float* sums, float qscale, uint16_t* core, int64_t rows,
+                                int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    return gdn_run(proj, xn, wa, wb, K, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates,
+                   sums, qscale, core, rows, HK, HV, slots, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa,
+                            const uint16_t* wb, int64_t K, const uint16_t* conv_w,
+                            uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
+                            const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums,
+                            const uint16_t* gnorm_w, float gnorm_eps, float qscale, uint16_t* core, int64_t rows,
+                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    MDX_CHECK(z && gnorm_w, "null pointer");
+    int rc = gdn_run(proj, xn, wa, wb, K, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates,
+                     sums, qscale, core, rows, HK, HV, slots, static_cast<hipStream_t>(stream));
+    if (rc) return rc;
+    // the gated RMSNorm of each head, in place
+    return mdx_gnorm_rot_quant(core, z, gnorm_w, gnorm_eps, core, nullptr, MDX_ROT_NONE, nullptr, nullptr, rows,
+                               HV * DH, stream);
 }

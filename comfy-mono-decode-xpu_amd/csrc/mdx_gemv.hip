@@ -108,6 +108,11 @@ struct PrepArgs {
     const uint16_t* sig = nullptr;
     int64_t g_row = 0;
     int g_head = 0, g_hstride = 0, g_off = 0;
+    // optional gated RMSNorm per 128-element head (the Gated-DeltaNet output): x <- bf16(bf16(x * hw *
+    // rsqrt(mean_head(x^2) + heps)) * bf16(silu(hz))), hw bf16 [128] shared by the heads, hz bf16 [rows, K]
+    const uint16_t* hw = nullptr;
+    const uint16_t* hz = nullptr;
+    float heps = 0.f;
 };
 
 __device__ __forceinline__ void unpack4(const uint2& v, float* f) {
@@ -195,7 +200,10 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             graw[gi] = *reinterpret_cast<const uint2*>(a.gate + row * a.g_row + (i0 / a.g_head) * a.g_hstride + a.g_off +
                                                        i0 % a.g_head);
         }
+        if (a.hw) graw[gi] = *reinterpret_cast<const uint2*>(a.hz + int64_t(row) * K + 256 * g + 4 * lane);
     }
+    uint2 hwraw = make_uint2(0u, 0u);
+    if (a.hw) hwraw = *reinterpret_cast<const uint2*>(a.hw + 4 * (lane & 31));
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) unpack4(raw[gi], v[gi]);
     if (a.gate) {
@@ -205,6 +213,29 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
                                     uint16_t(graw[gi].y >> 16)};
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(v[gi][e], bf2f(a.sig[gb[e]])));
+        }
+    }
+    if (a.hw) {
+        // lanes 0..31 hold head 2 g of group g, lanes 32..63 head 2 g + 1: lane partial ((sq0 + sq1) + sq2)
+        // + sq3, a halving tree within each half (l + 16, ..., + 1), read back from lane 0 / 32
+        float hwf[4];
+        unpack4(hwraw, hwf);
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            float q = __fmul_rn(v[gi][0], v[gi][0]);
+#pragma unroll
+            for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
+            for (int s = 16; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+            q = __shfl(q, lane & 32, 64);
+            const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(q, 128.f), a.heps)));
+            float zf[4];
+            unpack4(graw[gi], zf);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float normed = bfround(__fmul_rn(__fmul_rn(v[gi][e], hwf[e]), rsq));
+                const float gz = bfround(__fdiv_rn(zf[e], __fadd_rn(1.f, expf(-zf[e]))));
+                v[gi][e] = bfround(__fmul_rn(normed, gz));
+            }
         }
     }
     if (a.nw) {
@@ -228,9 +259,14 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             unpack4(wraw[gi], wv);
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], r), wv[e]));
+        }
+    }
+    if (a.xn_out) {
+        // the normalised row (may be x itself: every lane has read its elements above)
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
             const int g = w + W * gi;
-            if (a.xn_out && g < G)
-                *reinterpret_cast<uint2*>(a.xn_out + int64_t(row) * K + 256 * g + 4 * lane) = pack4(v[gi]);
+            if (g < G) *reinterpret_cast<uint2*>(a.xn_out + int64_t(row) * K + 256 * g + 4 * lane) = pack4(v[gi]);
         }
     }
     if (!a.q) return;  // RMSNorm only (xn_out)
@@ -1286,6 +1322,22 @@ extern "C" int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64
     a.g_head = int(gate_head);
     a.g_hstride = int(gate_head_stride);
     a.g_off = int(gate_offset);
+    return launch_prep(a, rows, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_gnorm_rot_quant(const uint16_t* y, const uint16_t* z, const uint16_t* gnorm_w, float eps,
+                                   uint16_t* y_out, const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows,
+                                   int64_t K, void* stream) {
+    MDX_CHECK(y && z && gnorm_w, "null pointer");
+    MDX_CHECK((q && scale) || (!q && !scale && y_out && rot == MDX_ROT_NONE), "q and scale, or y_out only");
+    int rc = prep_checks(rows, K, rot, h, y, q, nullptr, y_out);
+    if (rc) return rc;
+    MDX_CHECK(aligned(z, 8) && aligned(gnorm_w, 8), "8-byte aligned z / gnorm_w");
+    if (rows == 0) return MDX_OK;
+    PrepArgs a{y, nullptr, 0.f, y_out, h, rot, q, scale, int(K)};
+    a.hw = gnorm_w;
+    a.hz = z;
+    a.heps = eps;
     return launch_prep(a, rows, static_cast<hipStream_t>(stream));
 }
 

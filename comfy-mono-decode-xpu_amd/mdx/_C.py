@@ -421,10 +421,11 @@ def bf16_linear(x, w, tiled=True, residual=None, out=None):
 
 
 def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
-             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None):
+             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None, raw=False):
     """The Gated-DeltaNet core of csrc/mono_gdn.sycl:313-607 (layer_gdn phases P3-P5; layer_gdn_core's
     output): deferred conv, gates, sums, replay + verify delta rule, gated RMSNorm. Buffers are updated
-    in place; returns core bf16 [R, HV * 128]."""
+    in place; returns core bf16 [R, HV * 128]. raw=True leaves out the gated RMSNorm (core holds the
+    delta rule's bf16 outputs; gnorm_rot_quant applies it later)."""
     for t, n in ((proj, "proj"), (z, "z"), (xn, "xn"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"), (conv_state, "conv_state"),
                  (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf"), (gnorm_w, "gnorm_w")):
         _dev(t, n)
@@ -444,6 +445,12 @@ def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt
     _check(gates_buf.numel() == 2 * slots * HV * 2 and sums_buf.numel() == 2 * slots * hk * 2, "gates / sums buffers")
     if core is None:
         core = torch.empty(R, HV * 128, dtype=torch.bfloat16, device=proj.device)
+    if raw:
+        _lib.call("mdx_gdn_core_raw", _lib.ptr(proj), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), xn.shape[-1],
+                  _lib.ptr(conv_w), _lib.ptr(conv_state), _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl),
+                  _lib.ptr(dt_bias), _lib.ptr(g_decay), _lib.ptr(rec_state), _lib.ptr(gates_buf), _lib.ptr(sums_buf),
+                  float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(proj))
+        return core
     _lib.call("mdx_gdn_core", _lib.ptr(proj), _lib.ptr(z), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), xn.shape[-1],
               _lib.ptr(conv_w), _lib.ptr(conv_state),
               _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias), _lib.ptr(g_decay),
@@ -525,7 +532,7 @@ def layer_pre(x, norm_w, eps, hadamard, mats, nwg=0, tiled=True):
     return [xn] + outs
 
 
-def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop):
+def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop, gnorm=None):
     R = _rows_of(x)
     _check(stop >= 6, "only the full post block (stop >= 6) is supported")
     _check(y.dtype == torch.bfloat16 and y.is_contiguous() and y.numel() == R * 4096, "y bf16 [R, 4096]")
@@ -533,7 +540,13 @@ def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D
     x2 = x.view(R, 4096)
     rot = classify_rotation(hadamard)
     q, s = _buf(sc["q1"], R, 4096), sc["s"][:R]
-    if gate is not None:
+    if gnorm is not None:
+        # y holds the Gated-DeltaNet's raw outputs: the per-head gated RMSNorm (z, weight, eps), written
+        # back into y, then the rotation + quantisation
+        z, gw, geps = gnorm
+        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(y), _lib.ptr(z), _lib.ptr(gw), float(geps), _lib.ptr(y),
+                  _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(y))
+    elif gate is not None:
         gate_rot_quant(y.view(R, 4096), gate, sig_lut, hadamard, q, s)
     else:
         _lib.call("mdx_rot_quant", _lib.ptr(y), _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R, 4096,
@@ -596,11 +609,14 @@ def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj
     proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
     stream_gemv(q, s, [QKV, Z], [proj, z])
     core = _buf(sc["core"], R, HV * 128)
+    full = stop >= 6
     gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
-             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=core)
-    if stop >= 6:
+             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=core, raw=full)
+    if full:
+        # the gated RMSNorm runs inside the out_proj activation prep (core is normed in place there)
         U.cb = D.cb = G.cb
-        _layer_post(x, core, None, None, O, norm_post, eps_post, hadamard, silu_lut, G, U, D, 6)
+        _layer_post(x, core, None, None, O, norm_post, eps_post, hadamard, silu_lut, G, U, D, 6,
+                    gnorm=(z, gnorm_w, gnorm_eps))
     return x
 
 

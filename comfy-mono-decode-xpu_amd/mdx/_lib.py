@@ -76,6 +76,11 @@ SIGNATURES = {
                                     c_void_p, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float,
                                     ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_gdn_core_raw": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_gnorm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
+                                           ctypes.c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_rmsnorm": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_silu_mul": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
 }

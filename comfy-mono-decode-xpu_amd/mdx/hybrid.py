@@ -233,8 +233,9 @@ class HybridModel:
         _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
         core = _C._buf(sc["core"], R, hv * 128)
         _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
-                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core)
-        _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6)
+                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
+        _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6,
+                       gnorm=(z, L["gnorm"], c.eps))
 
     def verify_layers(self, x, R, mask, seq, pos, freqs):
         for i in range(self.cfg.layers):

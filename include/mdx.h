@@ -255,14 +255,32 @@ int mdx_bf16_linear(const uint16_t* x, const uint16_t* w, int32_t layout, const 
  * normalised layer input), wa / wb bf16 [HV, K] (K % 512 == 0, K <= 4096); conv_w bf16 [C, 4]; conv_state bf16 [C, 3]; proj_buf, qkv_buf bf16 [2, slots, C]; ctl int32
  * [2 + 3 slots] = (pending, parity, accepted[slots], parents[slots], prog[slots]); rec_state f32
  * [HV, 128, 128]; gates f32 [2, slots, HV, 2]; sums f32 [2, slots, HK, 2]; gnorm_w bf16 [128]; core bf16
- * [rows, HV 128] (rows without a verify entry are 0). slots in {8, 16}. Tolerance parity (float64
- * bound); the control walk is exact. */
+ * [rows, HV 128] (rows without a verify entry are 0). slots in {8, 16}, HV even and <= 128. Tolerance
+ * parity (float64 bound); the control walk is exact. */
 int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
                  int64_t K, const uint16_t* conv_w,
                  uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias,
                  const float* g_decay, float* rec_state, float* gates, float* sums, const uint16_t* gnorm_w,
                  float gnorm_eps, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
                  void* stream);
+
+/* mdx_gdn_core without its last phase: core holds the raw bf16 outputs q^ S of the verify entries (the
+ * gated RMSNorm left to mdx_gnorm_rot_quant, which the decode step fuses into the output projection's
+ * activation prep). No counterpart of its own in the reference: the first phases of the same
+ * layer_gdn (csrc/mono_gdn.sycl:313-571). */
+int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
+                     const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf,
+                     const int32_t* ctl, const float* dt_bias, const float* g_decay, float* rec_state, float* gates,
+                     float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
+                     void* stream);
+
+/* Gated RMSNorm per 128-element head, then the rotation + row quantisation of mdx_rot_quant:
+ * y' = bf16(bf16((y gnorm_w) / sqrt(mean_head(y^2) + eps)) * bf16(silu(z))). y_out (optional, may be y)
+ * receives y'; with q = scale = NULL and rot = MDX_ROT_NONE only y' is written. y, z, y_out bf16
+ * [rows, K], gnorm_w bf16 [128], K % 256 == 0. Replaces: the gated RMSNorm phase of _C.layer_gdn
+ * (csrc/mono_gdn.sycl:574-607) together with the out_proj activation prep that follows it. */
+int mdx_gnorm_rot_quant(const uint16_t* y, const uint16_t* z, const uint16_t* gnorm_w, float eps, uint16_t* y_out,
+                        const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
 
 /* Sigmoid-gated rotation + row quantisation: y' = bf16(y * sig_lut[gate]), then rot_quant(y').
  * Replaces: the first phase of _C.layer_post (csrc/mono_layer.sycl:243-256: the gated attention output,
