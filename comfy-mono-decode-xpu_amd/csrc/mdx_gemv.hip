@@ -35,7 +35,9 @@
 // Split-K partial sums of the waves of a work-group are int32 and are added through LDS:
 // integer addition is associative, so every split gives the same bits.
 #include <algorithm>
+#include <mutex>
 #include <stdio.h>
+#include <vector>
 #include <stdlib.h>
 
 #include "mdx_common.hpp"
@@ -572,39 +574,61 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
     const int per = 16 * a.rows;
     const float* xsl = prml + a.TPW * 16;
     if (a.epi == EPI_SILU) {
-        // pair: work unit wg owns gate tile wg and up tile wg; a thread stores two adjacent columns
-        for (int e = threadIdx.x; e < per / 2; e += blockDim.x) {
-            const int r = e >> 3, c = 2 * (e & 7);
-            const uint32_t v = uint32_t(silu_h(a, reduced<MFMA>(a, red, 0, r, c), reduced<MFMA>(a, red, 1, r, c), xsl[r],
-                                               prml[c], prml[16 + c])) |
-                               (uint32_t(silu_h(a, reduced<MFMA>(a, red, 0, r, c + 1), reduced<MFMA>(a, red, 1, r, c + 1),
-                                                xsl[r], prml[c + 1], prml[16 + c + 1]))
+        // pairs: tile slots 2 p / 2 p + 1 hold gate / up tile wg TPW / 2 + p; a thread stores two
+        // adjacent columns
+        const int np = a.TPW / 2, half = per / 2;
+        for (int e = threadIdx.x; e < np * half; e += blockDim.x) {
+            const int p = e / half, rem = e - p * half, r = rem >> 3, c = 2 * (rem & 7);
+            const int tile = wg * np + p;
+            if (tile >= a.m[0].tiles) continue;
+            const int sg = 2 * p, su = 2 * p + 1;
+            const uint32_t v = uint32_t(silu_h(a, reduced<MFMA>(a, red, sg, r, c), reduced<MFMA>(a, red, su, r, c), xsl[r],
+                                               prml[sg * 16 + c], prml[su * 16 + c])) |
+                               (uint32_t(silu_h(a, reduced<MFMA>(a, red, sg, r, c + 1), reduced<MFMA>(a, red, su, r, c + 1),
+                                                xsl[r], prml[sg * 16 + c + 1], prml[su * 16 + c + 1]))
                                 << 16);
-            uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + wg * 16 + c);
+            uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + tile * 16 + c);
             if (a.coh) st_c(o, v);
             else *o = v;
         }
         return;
     }
     if (a.epi == EPI_ACC) {
-        const int N = a.m[0].n;
-        for (int e = threadIdx.x; e < per; e += blockDim.x) {
-            const int r = e >> 4, c = e & 15;
-            __hip_atomic_fetch_add(a.acc + r * N + wg * 16 + c, reduced<MFMA>(a, red, 0, r, c), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        // the unit's TPW tiles (tile wg TPW + ts): int32 sums into acc, one hand-off, then each tile
+        // whose last part this was stores its outputs; *flag = the number of tiles completed here
+        const int N = a.m[0].n, tiles = a.m[0].tiles;
+        for (int e = threadIdx.x; e < a.TPW * per; e += blockDim.x) {
+            const int ts = e / per, rem = e - ts * per, r = rem >> 4, c = rem & 15;
+            const int tile = wg * a.TPW + ts;
+            if (tile < tiles)
+                __hip_atomic_fetch_add(a.acc + r * N + tile * 16 + c, reduced<MFMA>(a, red, ts, r, c), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         }
-        const uint32_t old = publish(a.tcnt + wg);
-        if (threadIdx.x == 0) *flag = old == uint32_t(a.split - 1);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (!*flag) return;
-        for (int e = threadIdx.x; e < per; e += blockDim.x) {
-            const int r = e >> 4, c = e & 15;
-            int32_t* p = a.acc + r * N + wg * 16 + c;
+        if (threadIdx.x == 0) *flag = 0;
+        __syncthreads();
+        const int my = wg * a.TPW + int(threadIdx.x);
+        if (int(threadIdx.x) < a.TPW && my < tiles &&
+            __hip_atomic_fetch_add(a.tcnt + my, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(a.split - 1)) {
+            atomicOr(flag, 1 << threadIdx.x);
+            __hip_atomic_store(a.tcnt + my, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        const int done = *flag;
+        for (int e = threadIdx.x; e < a.TPW * per; e += blockDim.x) {
+            const int ts = e / per, rem = e - ts * per, r = rem >> 4, c = rem & 15;
+            if (!((done >> ts) & 1)) continue;
+            const int tile = wg * a.TPW + ts;
+            int32_t* p = a.acc + r * N + tile * 16 + c;
             const int32_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            store_out(a, 0, wg * 16 + c, r, v, xsl[r], prml[c]);
+            store_out(a, 0, tile * 16 + c, r, v, xsl[r], prml[ts * 16 + c]);
         }
-        if (threadIdx.x == 0) __hip_atomic_store(a.tcnt + wg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (threadIdx.x == 0) *flag = __popc(done);
+        __syncthreads();
         return;
     }
     for (int ts = 0; ts < a.TPW; ++ts) {  // one tile slot at a time: the matrix choice stays uniform
@@ -621,6 +645,13 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
 // -------------------------------------------------------------------------------------------------
 // the kernel
 // -------------------------------------------------------------------------------------------------
+// 16 (c - 8) as int8 for the four low / high nibbles c of a code dword: c ^ 8 moved into the byte's
+// high half reads, as a signed byte, as 16 (c - 8) (c < 8: c + 8 - 16; c >= 8: c - 8), without a
+// borrow between bytes; products against these bytes are 16 times the integral form's
+// sum x (c - 8), exactly (an arithmetic shift by 4 recovers it)
+__device__ __forceinline__ uint32_t sx16_lo(uint32_t w) { return ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u; }
+__device__ __forceinline__ uint32_t sx16_hi(uint32_t w) { return (w & 0xF0F0F0F0u) ^ 0x80808080u; }
+
 // natural-order code bytes of a code dword: [c0 c1 c2 c3], [c4 c5 c6 c7] from its low / high nibbles
 __device__ __forceinline__ void nat_order(uint32_t lo, uint32_t hi, uint32_t& n0, uint32_t& n1) {
     n0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
@@ -667,9 +698,12 @@ __device__ __forceinline__ void unit_groups(int cu0, int ncu, int lgG, int ng, i
 // is merged at the join and waited for at once, which leaves one load in flight per wave): a chunk
 // past the slice re-reads the slice's last chunk and adds nothing. Everything that selects a
 // matrix or a tile is wave-uniform (scalar registers).
-template <bool MFMA, int R, int SDT, int RING>
+// PRE: the ring's first RING loads were issued by issue_ring (same unit) and arrive in `pre`.
+// EPI false: the unit ends after its reduction operands are in LDS; the caller runs the epilogue
+// (after a barrier) with the pointers of unit_lds.
+template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true>
 __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds,
-                                          const UnitIn& in, int* flag) {
+                                          const UnitIn& in, int* flag, const uint4* pre = nullptr) {
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
     const int K = a.K;
     const int ng = K >> a.lgG;
@@ -678,15 +712,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     int g0, g1;
     unit_groups(cu0, ncu, a.lgG, ng, ESZ, g0, g1);
     const int seg = (g1 - g0) * ESZ;  // scale bytes per tile row in LDS
-    // LDS: activation rows of the K range | scales [TPW][16][seg] | reduction | parameters [64] |
-    // 8 x activation sums (one row: [rows][Kr / 32] per 32-k run; MFMA: [ncu][16] per chunk) | flag |
-    // 32 zero bytes (the activation of MFMA rows past the last)
+    // LDS: activation rows of the K range | scales [TPW][16][seg] | reduction | parameters [128] |
+    // flag | 32 zero bytes (the activation of MFMA rows past the last)
     uint8_t* xl = lds;
     uint8_t* sl = xl + ((a.rows * Kr + 1023) & ~1023);
     int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
     float* prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
-    int32_t* xsum8 = reinterpret_cast<int32_t*>(prml + 64);
-    int* mixed = reinterpret_cast<int*>(xsum8 + ncu * 16);
+    int* mixed = reinterpret_cast<int*>(prml + 128);
     uint8_t* zeros = reinterpret_cast<uint8_t*>(mixed + 4);
 
     const int t = threadIdx.x;
@@ -732,20 +764,23 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         cbdef = cbdef && cb[i] == float(i - 8);
     }
 
-    // 2. the weight ring: every slot issues one load; reads past the slice repeat its last chunk
+    // 2. the weight ring: every slot issues one load; reads past the slice repeat its last chunk. A
+    // tile slot past the matrix's last tile (a work-group's share can end inside its tile slots)
+    // reads tile 0 and adds nothing: its addresses must stay inside the matrix all the same.
+    const int tl = live ? tile : 0;
     const MDX_G uint8_t* wp;
     int wstride;
     if (a.layout == MDX_LAYOUT_TILE) {
-        wp = mq + (tile * NC + c0) * 1024 + lane * 16;
+        wp = mq + (tl * NC + c0) * 1024 + lane * 16;
         wstride = 1024;
     } else {
-        wp = mq + (tile * 16 + c) * (K / 2) + c0 * 64 + kq * 16;
+        wp = mq + (tl * 16 + c) * (K / 2) + c0 * 64 + kq * 16;
         wstride = 64;
     }
     const int last = nch > 0 ? nch - 1 : 0;
     uint4 buf[RING];
 #pragma unroll
-    for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
+    for (int p = 0; p < RING; ++p) buf[p] = PRE ? pre[p] : ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
     const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
     if (t == 0) *mixed = 0;
     if (t < 8) reinterpret_cast<uint32_t*>(zeros)[t] = 0u;
@@ -754,25 +789,51 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     if (in.wait) {
         wait_count(in.wait, in.wait_for, in.err);
         if (in.hr) {
-            // bf16 rows quantised with the row scale max(absmax / 127, 1e-30) (the row prep's formula)
-            const int per_row = Kr / 4;
-            for (int i = t; i < a.rows * per_row; i += nthr) {
-                const int r = i / per_row, j = i - r * per_row;
-                const float rm = __uint_as_float(ld_c(in.amax + r));
-                const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
-                uint16_t sb = f2bf(s);
-                if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-                const float sbf = bf2f(sb);
-                float v[4];
-                unpack4(*reinterpret_cast<const uint2*>(in.hr + r * K + cu0 * CHUNK_K + 4 * j), v);
-                uint32_t o = 0;
+            // bf16 rows quantised with the row scale max(absmax / 127, 1e-30) (the row prep's formula).
+            // The rows' pieces (16 bytes, up to HB per thread) and the rows' absmax are loaded
+            // together (one memory round trip), then quantised: v / sb as fp32(fp64(v) * (1 /
+            // fp64(sb))). For a bf16 v and a bf16 sb the exact quotient either has at most 8
+            // significant bits or lies at least 2^-33 (relative) from every fp32 rounding boundary,
+            // far beyond the fp64 product's error, so the fp32 result is the correctly rounded
+            // quotient (apart from fp32 subnormal quotients, which quantise to 0 either way).
+            constexpr int HB = 8;
+            double* rcp = reinterpret_cast<double*>(prml + 96);  // [rows]
+            const int per_row = Kr / 8, total = a.rows * per_row;
+            for (int base = 0; base < total; base += HB * nthr) {
+                uint4 raw[HB];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float d = bfround(__fdiv_rn(v[e], sbf));
-                    o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
+                for (int k = 0; k < HB; ++k) {
+                    const int i = min(base + k * nthr + t, total - 1);
+                    const int r = i / per_row, j = i - r * per_row;
+                    raw[k] = *reinterpret_cast<const uint4*>(in.hr + r * K + cu0 * CHUNK_K + 8 * j);
                 }
-                *reinterpret_cast<uint32_t*>(xl + r * Kr + 4 * j) = o;
-                if (j == 0) prml[a.TPW * 16 + r] = s;
+                if (base == 0) {
+                    if (t < a.rows) {
+                        const float s = fmaxf(__fdiv_rn(__uint_as_float(ld_c(in.amax + t)), 127.0f), 1e-30f);
+                        uint16_t sb = f2bf(s);
+                        if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+                        prml[a.TPW * 16 + t] = s;
+                        rcp[t] = 1.0 / double(bf2f(sb));
+                    }
+                    __syncthreads();
+                }
+#pragma unroll
+                for (int k = 0; k < HB; ++k) {
+                    const int i = base + k * nthr + t;
+                    if (i < total) {
+                        const int r = i / per_row, j = i - r * per_row;
+                        const double rr = rcp[r];
+                        const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+                        uint32_t o[2] = {0u, 0u};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
+                            const float d = bfround(float(__dmul_rn(double(v), rr)));
+                            o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
+                        }
+                        *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
+                    }
+                }
             }
         } else {
             dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
@@ -788,32 +849,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
         __builtin_amdgcn_s_barrier();
     }
-    // One pass over the staged operands: (a) the 8 * sum(x) corrections of the integral form, once
-    // per unit (one row: per 32-k run, [rows][Kr / 32]; MFMA: per 128-k chunk, [ncu][16 rows]);
-    // (b) whether every staged scale is an integer in [-15, 15] (then the unit takes the integral
-    // form throughout; both forms give the same int32 sums, so the choice is free). Consecutive
-    // lanes read consecutive 16-byte pieces (no LDS bank conflicts); the pieces of one run (2, or 8
-    // for a chunk) meet by shuffles.
-    {
-        const int pieces = Kr / 16, run = MFMA ? 8 : 2;
-        for (int base = 0; base < a.rows * pieces; base += nthr) {
-            const int i = base + t;
-            const int r = i / pieces, pc = i - r * pieces;
-            int s = 0;
-            if (i < a.rows * pieces) {
-                const uint4 v = *reinterpret_cast<const uint4*>(xl + r * Kr + pc * 16);
-                s = sdot4(int(v.x), 0x01010101, s);
-                s = sdot4(int(v.y), 0x01010101, s);
-                s = sdot4(int(v.z), 0x01010101, s);
-                s = sdot4(int(v.w), 0x01010101, s);
-            }
-            for (int d = 1; d < run; d <<= 1) s += shfl_xor(s, d);
-            if (i < a.rows * pieces && pc % run == 0) {
-                if (MFMA) xsum8[(pc / run) * 16 + r] = 8 * s;
-                else xsum8[r * (Kr / 32) + pc / run] = 8 * s;
-            }
-        }
-    }
+    // Whether every staged scale is an integer in [-15, 15]: then the unit takes the integral form
+    // throughout (both forms give the same int32 sums, so the choice is free).
     if (can_int) {
         bool bad = false;
         for (int j = t; j < a.TPW * 16 * (seg / ESZ); j += nthr) {
@@ -855,18 +892,17 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                     v4i dacc = {0, 0, 0, 0};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        uint32_t n0 = wd[j] & 0x0F0F0F0Fu, n1 = (wd[j] >> 4) & 0x0F0F0F0Fu;
+                        uint32_t n0 = sx16_lo(wd[j]), n1 = sx16_hi(wd[j]);
                         if (!split) nat_order(n0, n1, n0, n1);
                         dacc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
                                                                      long(uint64_t(n0) | (uint64_t(n1) << 32)), dacc, 0, 0, 0);
                     }
-                    // D rows 4 kq + r: minus 8 * that row's chunk sum, times the chunk's scale (0 past the slice)
-                    const int4 corr = *reinterpret_cast<const int4*>(xsum8 + (ch - cu0) * 16 + 4 * kq);
+                    // D rows 4 kq + r: 16 * sum x (c - 8), exactly; times the chunk's scale (0 past the slice)
                     const int sv = valid ? int(s0) : 0;
-                    tot[0] += __mul24(sv, dacc[0] - corr.x);
-                    tot[1] += __mul24(sv, dacc[1] - corr.y);
-                    tot[2] += __mul24(sv, dacc[2] - corr.z);
-                    tot[3] += __mul24(sv, dacc[3] - corr.w);
+                    tot[0] += __mul24(sv, dacc[0] >> 4);
+                    tot[1] += __mul24(sv, dacc[1] >> 4);
+                    tot[2] += __mul24(sv, dacc[2] >> 4);
+                    tot[3] += __mul24(sv, dacc[3] >> 4);
                 } else {
                     if (!valid)
 #pragma unroll
@@ -904,12 +940,12 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const int k0 = ch * CHUNK_K + klane;
                 const float s0 = rd_scale<SDT>(scol + (k0 >> lgG) * ESZ);
                 const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-                uint32_t lo[4], hi[4];  // weights of k 8 j + [0, 4) and + [4, 8) (raw nibbles in the integral form)
+                uint32_t lo[4], hi[4];  // weights of k 8 j + [0, 4) and + [4, 8) (16 (c - 8) in the integral form)
                 if (integ) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        lo[j] = wd[j] & 0x0F0F0F0Fu;
-                        hi[j] = (wd[j] >> 4) & 0x0F0F0F0Fu;
+                        lo[j] = sx16_lo(wd[j]);
+                        hi[j] = sx16_hi(wd[j]);
                     }
                 } else {
                     decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
@@ -931,8 +967,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                             d = sdot4(int(lo[j]), int(xv[2 * j]), d);
                             d = sdot4(int(hi[j]), int(xv[2 * j + 1]), d);
                         }
-                        const int xs8 = integ ? xsum8[r * (Kr / 32) + sg] : 0;
-                        tot[r] += __mul24(sv, d - xs8);
+                        tot[r] += __mul24(sv, integ ? (d >> 4) : d);
                     }
                 }
                 buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);  // refill after use (see above)
@@ -956,8 +991,48 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // wait that would also wait for the ring)
     if (slice == 0 && lane < 16) prml[ts * 16 + lane] = prm;
     else if (!in.wait && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
+    if (!EPI) return;
     __syncthreads();
     epilogue<MFMA>(a, wg, red, prml, flag);
+}
+
+// The reduction block and parameters of a unit in LDS (gemv_unit's layout), for a caller-run epilogue.
+template <bool MFMA, int SDT>
+__device__ __forceinline__ void unit_lds(const GemvArgs& a, const int cu0, const int ncu, uint8_t* lds, int32_t*& red,
+                                         float*& prml) {
+    constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
+    int g0, g1;
+    unit_groups(cu0, ncu, a.lgG, a.K >> a.lgG, ESZ, g0, g1);
+    const int seg = (g1 - g0) * ESZ;
+    uint8_t* sl = lds + ((a.rows * ncu * CHUNK_K + 1023) & ~1023);
+    red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
+    prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
+}
+
+// The first RING weight loads of a single-matrix unit (tiles wg TPW + ts, chunks [cu0, cu0 + ncu)
+// over KS slices), issued ahead of the unit itself (gemv_unit with PRE).
+template <int RING>
+__device__ __forceinline__ void issue_ring(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint4* out) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int ts = wave / a.KS, slice = wave % a.KS;
+    const int K = a.K, NC = K / CHUNK_K;
+    const int mt = wg * a.TPW + ts;
+    const bool live = mt < a.m[0].tiles;
+    const int c0 = live ? cu0 + slice * ncu / a.KS : 0, c1 = live ? cu0 + (slice + 1) * ncu / a.KS : 0;
+    const int nch = c1 - c0, last = nch > 0 ? nch - 1 : 0;
+    const MDX_G uint8_t* mq = as_global(a.m[0].q);
+    const int tile = live ? mt : 0;
+    const MDX_G uint8_t* wp;
+    int wstride;
+    if (a.layout == MDX_LAYOUT_TILE) {
+        wp = mq + (tile * NC + c0) * 1024 + lane * 16;
+        wstride = 1024;
+    } else {
+        wp = mq + (tile * 16 + (lane & 15)) * (K / 2) + c0 * 64 + (lane >> 4) * 16;
+        wstride = 64;
+    }
+#pragma unroll
+    for (int p = 0; p < RING; ++p) out[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
 }
 
 template <bool MFMA, int R, int SDT, int RING>
@@ -978,7 +1053,7 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     const size_t seg = size_t(g1 - g0) * esz;
     size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
-    return s + 64 * 4 + size_t(ncu) * 16 * 4 + 16 + 32;  // parameters, activation sums, flag, zeros
+    return s + 128 * 4 + 16 + 32;  // parameters, flag, zeros
 }
 
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mfma, esz, 0, a.K / CHUNK_K); }
@@ -1100,82 +1175,91 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     if (rc) return rc;
     const bool mfma = rows >= MFMA_MIN_ROWS;
     // geometry: TPW tiles per work-group, KS K-slices per tile (at most 16 waves per work-group):
-    // the smallest split that puts >= 3072 waves on the chip (12 per CU), measured best on MI355X
-    // for the 8-52 MB matrices of this model (longer streams per wave beat more, shorter waves)
+    // the smallest split that puts >= 3072 waves on the chip (12 per CU), but no slice shorter than
+    // 4 chunks, measured best on MI355X for the 8-52 MB matrices of this model (longer streams per
+    // wave beat more, shorter waves: 4096 x 4096 takes 6.4 us at 8 slices against 7.6 at 12)
     a.TPW = pair ? 2 : 1;
     const int NC = a.K / CHUNK_K;
-    const int wgs = (total + a.TPW - 1) / a.TPW;
     const int maxks = 16 / a.TPW;
     a.KS = 1;
-    for (int d = 1; d <= maxks && d <= NC; ++d) {
+    for (int d = 1; d <= maxks && 4 * d <= NC; ++d) {
         if (NC % d) continue;
         a.KS = d;
         if (int64_t(total) * d >= 3072) break;
     }
-    // MDX_GEMV_KS overrides the split (tuning sweeps)
+    // MDX_GEMV_TPW / MDX_GEMV_KS override the geometry (tuning sweeps)
+    if (const char* env = getenv("MDX_GEMV_TPW")) {
+        const int tpw = atoi(env);
+        if (tpw >= 1 && tpw <= 6 && (!pair || tpw % 2 == 0)) a.TPW = tpw;  // the parameter block holds 6 tiles
+    }
     if (const char* env = getenv("MDX_GEMV_KS")) {
         const int ks = atoi(env);
-        if (ks >= 1 && ks <= maxks && NC % ks == 0) a.KS = ks;
+        if (ks >= 1 && ks * a.TPW <= 16 && NC % ks == 0) a.KS = ks;
     }
+    if (a.TPW * a.KS > 16) a.KS = 16 / a.TPW;
+    const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
     return launch_gemv_d<4>(a, ws[0]->s_dtype, mfma, wgs, st);
 }
 
 // =================================================================================================
-// The fused MLP in one launch: a chain of work units, one per work-group, in work-group order.
-//   units [0, rows)              row prep of x (RMSNorm, rotation, int8) -> q1, s1
-//   next N1 / 16 units           gate/up tile pairs (SiLU epilogue -> h); the last of the 16 units of
-//                                a 256-column group rotates that group of every row -> hr, row absmax
-//   next (N2 / 16) x split       down: tile x K part; quantises its K part of hr, int32 partial sums
-//                                added into acc, the tile's last part stores out (+ residual); the
-//                                last tile to complete re-zeroes the control words
-// A unit only waits for units with smaller work-group ids. Work-groups are dispatched in id order,
-// so every unit a waiting unit depends on is running or done and waits for nothing later: no
-// dependence on how many work-groups fit on the chip. (The waits are bounded all the same.)
+// The fused MLP after the row prep of x: gate/up, the rotation of h and down in one launch.
+// Work-group u runs
+//   1. gate/up tile pair u (SiLU epilogue -> h, coherent stores); the last of the 16 pairs of a
+//      256-column group rotates that group of every row -> hr and raises the rows' absmax;
+//   2. down unit u (four tiles, one per wave, over K part u % split): its whole weight share is
+//      requested right after the pair's stream (before the pair's epilogue), so the down weights
+//      arrive while the gate/up pairs finish; after "h is rotated" it quantises its K part of hr,
+//      adds its int32 sums into acc, and each tile's last part stores out (+ residual); the last
+//      tile re-zeroes the control words.
+// Every work-group waits for work of every other one, so the launch requires all of them resident
+// at once: the host launches it only when the occupancy query admits the whole grid, and each wait
+// is bounded (a broken hand-off costs wrong results and an error flag, never a hung GPU).
 // Hand-offs use coherent loads / stores and one counter bump per unit: no cache-wide fences and
 // no per-launch ticket counter (device atomics on one address serialise at ~11 ns each).
 // =================================================================================================
-enum : int { SY_PREP = 0, SY_GROUPS = 1, SY_TILES = 2, SY_ERR = 4, SY_HDR = 8 };
-// "x is quantised" and "h is rotated" are each broadcast to FLAG_N words FLAG_STRIDE words apart
-// (different memory channels), unit u polling word u % FLAG_N: a thousand work-groups polling one
-// word would queue on one channel and stall every weight stream that crosses it.
+enum : int { SY_GROUPS = 1, SY_TILES = 2, SY_ERR = 4, SY_HDR = 8 };
+// "h is rotated" is broadcast to FLAG_N words FLAG_STRIDE words apart (different memory channels),
+// unit u polling word u % FLAG_N: a thousand work-groups polling one word would queue on one
+// channel and stall every weight stream that crosses it.
 constexpr int FLAG_N = 64, FLAG_STRIDE = 64;
-constexpr int CH_WAVES = 4;      // waves per work unit
+constexpr int CH_WAVES = 4;      // waves per work-group
 constexpr int CH_MAX_G1 = 64;    // 256-column groups of h at most (N1 <= 16384)
-constexpr int CH_MAX_K1 = 256 * CH_WAVES * 4;  // the row prep's reach with 4 waves x 4 groups
+constexpr int CH_MAX_K1 = 4096;  // down outputs at most (the acc block)
+constexpr int DN_RING = 8;       // down weights requested ahead per wave: a unit's whole share (8 chunks)
 
-struct MlpChain {
-    PrepArgs prep;        // x rows -> gu.xq / gu.xs
-    uint32_t* flags;      // [2][FLAG_N][FLAG_STRIDE]: x ready, h ready
+struct MlpFused {
+    uint32_t* flags;      // [FLAG_N][FLAG_STRIDE]: h ready
     GemvArgs gu, dn;      // gate/up pair (EPI_SILU into hb), down (EPI_ACC over K parts)
     const uint16_t* hb;   // h [rows, N1]
     uint16_t* hr;         // rotated h [rows, N1] (hb itself without rotation)
     uint32_t* amax;       // [16] row absmax of hr, fp32 bits
     uint32_t* sync;       // [SY_HDR + G1] control words, zero between launches
-    int rows, rot, n_prep, n_gu, n_dn, G1, dn_cu;
+    int rows, rot, n_gu, n_dn, G1, dn_cu;
 };
 
-template <bool MFMA, int R, int SDT, int RING>
-__global__ __launch_bounds__(CH_WAVES * WAVE) void mlp_chain_kernel(MlpChain c) {
+template <bool MFMA, int R, int SDT>
+__global__ __launch_bounds__(CH_WAVES * WAVE) void mlp_fused_kernel(MlpFused c) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float gsum[CH_MAX_K1 / 256];
-    __shared__ float wmax[CH_WAVES];
     __shared__ int flag;
     const int t = threadIdx.x;
     const int u = blockIdx.x;
-    if (u < c.n_prep) {
-        prep_row<4, true>(c.prep, u, gsum, wmax);
-        const uint32_t old = publish(c.sync + SY_PREP);
-        if (t == 0) flag = old == uint32_t(c.n_prep - 1);
+    const int grp = u / c.dn.split, part = u - grp * c.dn.split;  // down: tiles 4 grp .. 4 grp + 3, K part
+    uint4 dring[DN_RING];
+    if (u < c.n_gu) {
+        // the gate/up pair's stream, then this work-group's down weights are requested (they arrive
+        // while the pair's epilogue, the rotation of h and the wait run), then the pair's epilogue
+        gemv_unit<MFMA, R, SDT, 4, false, false>(c.gu, u, 0, c.gu.K / CHUNK_K, lds, UnitIn{}, &flag);
+        if (u < c.n_dn) issue_ring<DN_RING>(c.dn, grp, part * c.dn_cu, c.dn_cu, dring);
         __syncthreads();
-        if (flag && t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 1u);
-    } else if (u < c.n_prep + c.n_gu) {
-        const int v = u - c.n_prep;
-        gemv_unit<MFMA, R, SDT, RING>(
-            c.gu, v, 0, c.gu.K / CHUNK_K, lds,
-            UnitIn{c.flags + (u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, nullptr, nullptr}, &flag);
-        const int g = v >> 4;
+        {
+            int32_t* red;
+            float* prml;
+            unit_lds<MFMA, SDT>(c.gu, 0, c.gu.K / CHUNK_K, lds, red, prml);
+            epilogue<MFMA>(c.gu, u, red, prml, &flag);
+        }
+        const int g = u >> 4;
         const uint32_t old = publish(c.sync + SY_HDR + g);
         if (t == 0) flag = old == 15u;
         __syncthreads();
@@ -1208,48 +1292,67 @@ __global__ __launch_bounds__(CH_WAVES * WAVE) void mlp_chain_kernel(MlpChain c) 
             const uint32_t og = publish(c.sync + SY_GROUPS);
             if (t == 0) flag = og == uint32_t(c.G1 - 1);
             __syncthreads();
-            if (flag && t < FLAG_N) st_c(c.flags + (FLAG_N + t) * FLAG_STRIDE, 1u);
+            if (flag && t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 1u);
         }
-    } else {
-        const int v = u - c.n_prep - c.n_gu;
-        const int tile = v / c.dn.split, part = v - tile * c.dn.split;
-        gemv_unit<MFMA, R, SDT, RING>(
-            c.dn, tile, part * c.dn_cu, c.dn_cu, lds,
-            UnitIn{c.flags + (FLAG_N + u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, c.hr, c.amax}, &flag);
-        // flag: this unit completed its tile. When every tile is complete, every unit of the launch
-        // is past its waits: the control words go back to zero for the next launch.
-        if (!flag) return;
-        __syncthreads();
-        if (t == 0)
-            flag = __hip_atomic_fetch_add(c.sync + SY_TILES, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   uint32_t(c.n_dn / c.dn.split - 1);
-        __syncthreads();
-        if (flag) {
-            if (t < 2 * FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 0u);
-            if (t < 16) st_c(c.amax + t, 0u);
-            if (t == 0) {
-                st_c(c.sync + SY_PREP, 0u);
-                st_c(c.sync + SY_GROUPS, 0u);
-                st_c(c.sync + SY_TILES, 0u);
-            }
+        __syncthreads();  // the down unit below reuses the LDS
+    }
+    if (u >= c.n_dn) return;
+    if (u >= c.n_gu) issue_ring<DN_RING>(c.dn, grp, part * c.dn_cu, c.dn_cu, dring);
+    gemv_unit<MFMA, R, SDT, DN_RING, true>(c.dn, grp, part * c.dn_cu, c.dn_cu, lds,
+                                           UnitIn{c.flags + (u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, c.hr, c.amax},
+                                           &flag, dring);
+    // flag: the number of tiles this unit completed. When every tile is complete, every unit of the
+    // launch is past its waits: the control words go back to zero for the next launch.
+    if (!flag) return;
+    __syncthreads();
+    if (t == 0)
+        flag = __hip_atomic_fetch_add(c.sync + SY_TILES, uint32_t(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+                   uint32_t(flag) == uint32_t(c.dn.m[0].tiles);
+    __syncthreads();
+    if (flag) {
+        if (t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 0u);
+        if (t < 16) st_c(c.amax + t, 0u);
+        if (t == 0) {
+            st_c(c.sync + SY_GROUPS, 0u);
+            st_c(c.sync + SY_TILES, 0u);
         }
     }
 }
 
 template <bool MFMA, int R, int SDT>
-int launch_chain_t(const MlpChain& c, size_t smem, hipStream_t st) {
-    const void* fn = reinterpret_cast<const void*>(&mlp_chain_kernel<MFMA, R, SDT, 4>);
-    if (smem > 64 * 1024) allow_smem(fn, smem);
-    hipLaunchKernelGGL((mlp_chain_kernel<MFMA, R, SDT, 4>), dim3(unsigned(c.n_prep + c.n_gu + c.n_dn)),
-                       dim3(CH_WAVES * WAVE), smem, st, c);
-    MDX_LAUNCHED();
-    return MDX_OK;
+const void* fused_fn() {
+    return reinterpret_cast<const void*>(&mlp_fused_kernel<MFMA, R, SDT>);
 }
 
-int launch_chain(const MlpChain& c, int sdt, bool mfma, size_t smem, hipStream_t st) {
-    if (sdt == MDX_DT_F32) return mfma ? launch_chain_t<true, 4, MDX_DT_F32>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_F32>(c, smem, st);
-    if (sdt == MDX_DT_F16) return mfma ? launch_chain_t<true, 4, MDX_DT_F16>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_F16>(c, smem, st);
-    return mfma ? launch_chain_t<true, 4, MDX_DT_FP8E4M3>(c, smem, st) : launch_chain_t<false, 1, MDX_DT_FP8E4M3>(c, smem, st);
+const void* fused_kernel(int sdt, bool mfma) {
+    if (sdt == MDX_DT_F32) return mfma ? fused_fn<true, 4, MDX_DT_F32>() : fused_fn<false, 1, MDX_DT_F32>();
+    if (sdt == MDX_DT_F16) return mfma ? fused_fn<true, 4, MDX_DT_F16>() : fused_fn<false, 1, MDX_DT_F16>();
+    return mfma ? fused_fn<true, 4, MDX_DT_FP8E4M3>() : fused_fn<false, 1, MDX_DT_FP8E4M3>();
+}
+
+// Whether `grid` work-groups of `fn` (CH_WAVES waves, `smem` bytes of LDS) are resident at once on
+// the current device: the occupancy query times the CU count (cached per kernel, LDS size, device).
+bool all_resident(const void* fn, size_t smem, int grid) {
+    struct Entry {
+        const void* fn;
+        size_t smem;
+        int dev, capacity;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : cache)
+        if (e.fn == fn && e.smem == smem && e.dev == dev) return grid <= e.capacity;
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, CH_WAVES * WAVE, smem) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    cache.push_back(Entry{fn, smem, dev, cus * per});
+    return grid <= cus * per;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -1375,13 +1478,13 @@ namespace {
 // Workspace of mdx_mono_mlp. First the zero-state part, at the same offsets whatever the shapes (a
 // call with fewer rows must not find its control words or accumulators inside the data of an
 // earlier call with more rows): control words [SY_HDR + CH_MAX_G1] | amax [16] | tile counters
-// [CH_MAX_K1 / 16] in a 4 KiB header, the broadcast flags [2][FLAG_N][FLAG_STRIDE], then
+// [CH_MAX_K1 / 16] in a 4 KiB header, the broadcast flags [FLAG_N][FLAG_STRIDE], then
 // acc [16, CH_MAX_K1] int32. It must be zero before the
 // first call and every call leaves it zero (each call re-zeroes exactly what it used). Then,
 // 256-byte aligned, the data: q1 [rows, K1] | q2 [rows, N1] | scales [64] f32 | h [rows, N1] bf16 |
 // rotated h [rows, N1] bf16.
 constexpr size_t MLP_HDR = 4096;
-constexpr size_t MLP_FLAGS = size_t(2) * FLAG_N * FLAG_STRIDE * 4;
+constexpr size_t MLP_FLAGS = size_t(FLAG_N) * FLAG_STRIDE * 4;
 static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header");
 
 struct MlpWs {
@@ -1422,18 +1525,20 @@ MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
     return w;
 }
 
-// The one-launch chain, when the shapes fit it; returns -1 (nothing launched) when they do not.
-int mono_mlp_chain(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
-                   const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
-                   const uint16_t* residual, uint16_t* out, int rows, const MlpWs& w, hipStream_t st) {
+// gate/up + rotation of h + down in one launch (after the row prep of x), when the shapes fit it and
+// the whole grid is resident at once; returns -1 (nothing launched) otherwise.
+int mono_mlp_fused(const uint16_t* h, int32_t rot, const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up,
+                   const mdx_w4* down, const uint16_t* residual, uint16_t* out, int rows, const MlpWs& w,
+                   hipStream_t st) {
     const int64_t K1 = gate->k, N1 = gate->n;
     if (rot == MDX_ROT_MATRIX || K1 > CH_MAX_K1 || N1 % 256 || N1 / 256 > CH_MAX_G1) return -1;
-    // opt-in (MDX_MLP_CHAIN=1): on MI355X the in-launch hand-offs (row prep of x, then the rotation
-    // of h) cost more than the two launch boundaries they remove (see the design notes)
-    const char* env = getenv("MDX_MLP_CHAIN");
+    // opt-in (MDX_MLP_FUSED=1): on MI355X the in-launch hand-off (every gate/up pair's h, then the
+    // rotation of h, then the down units' wait) costs more than the two launch boundaries it removes
+    // (measured 37.9 against 31.3 us per block at one row, 46.3 against 38.0 us at eight)
+    const char* env = getenv("MDX_MLP_FUSED");
     if (!env || atoi(env) == 0) return -1;
-    MlpChain c{};
-    c.prep = PrepArgs{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
+    if (gate->s_dtype != down->s_dtype) return -1;
+    MlpFused c{};
     int total = 0, rc;
     const mdx_w4* gu[2] = {gate, up};
     void* o1[2] = {w.hb, w.hb};
@@ -1444,21 +1549,21 @@ int mono_mlp_chain(const uint16_t* xn, const uint16_t* norm_w, float eps, const 
     const void* r2[1] = {residual};
     if ((rc = setup_gemv(dn, 1, false, w.q2, w.s + 32, rows, EPI_ACC, o2, r2, MDX_DT_BF16, nullptr, c.dn, total)))
         return rc;
-    MDX_CHECK(gate->s_dtype == down->s_dtype, "gate/up and down must share the scale dtype");
-    // gate/up: one tile pair per unit, 2 K slices; down: one tile per unit over a K part, 4 slices,
-    // the smallest number of parts that puts >= 3072 waves on the chip
+    // gate/up: one tile pair per work-group, 2 K slices; down: four tiles per work-group (one per
+    // wave) over a K part, with as many parts as make as many down units as gate/up units (every
+    // work-group runs one of each). Each down unit quantises its K part of h for every row, so
+    // four tiles per unit quarter that repeated work against one tile per unit.
     c.gu.TPW = 2;
     c.gu.KS = 2;
     c.gu.coh = 1;
-    c.dn.TPW = 1;
-    c.dn.KS = 4;
-    const int NC2 = int(N1 / CHUNK_K), tiles2 = int(K1 / 16);
-    int split = 1;
-    for (int d = 1; d <= 16 && NC2 / d >= CH_WAVES; ++d) {
-        if (NC2 % d) continue;
-        split = d;
-        if (int64_t(tiles2) * d * CH_WAVES >= 3072) break;
-    }
+    c.dn.TPW = CH_WAVES;
+    c.dn.KS = 1;
+    const int NC2 = int(N1 / CHUNK_K), groups2 = int((K1 / 16 + CH_WAVES - 1) / CH_WAVES);
+    c.n_gu = int(N1 / 16);
+    int split = 0;
+    for (int d = 1; d <= NC2 && groups2 * d <= c.n_gu; ++d)
+        if (NC2 % d == 0) split = d;
+    if (split == 0) return -1;
     c.dn.split = split;
     c.dn.acc = w.acc;
     c.dn.tcnt = w.tcnt;
@@ -1470,16 +1575,21 @@ int mono_mlp_chain(const uint16_t* xn, const uint16_t* norm_w, float eps, const 
     c.flags = w.flags;
     c.rows = rows;
     c.rot = rot;
-    c.n_prep = rows;
-    c.n_gu = int(N1 / 16);
-    c.n_dn = tiles2 * split;
+    c.n_dn = groups2 * split;
     c.G1 = int(N1 / 256);
     const bool mfma = rows >= MFMA_MIN_ROWS;
     const int esz = esz_of(gate->s_dtype);
     size_t smem = std::max(gemv_smem(c.gu, mfma, esz), gemv_smem(c.dn, mfma, esz, 0, c.dn_cu));
     smem = std::max(smem, gemv_smem(c.dn, mfma, esz, (split - 1) * c.dn_cu, c.dn_cu));
+    const int grid = std::max(c.n_gu, c.n_dn);
+    const void* fn = fused_kernel(gate->s_dtype, mfma);
     if (smem > 160 * 1024) return -1;
-    return launch_chain(c, gate->s_dtype, mfma, smem, st);
+    if (smem > 64 * 1024) allow_smem(fn, smem);
+    if (!all_resident(fn, smem, grid)) return -1;
+    void* args[] = {&c};
+    (void)hipLaunchKernel(fn, dim3(unsigned(grid)), dim3(CH_WAVES * WAVE), args, smem, st);
+    MDX_LAUNCHED();
+    return MDX_OK;
 }
 
 }  // namespace
@@ -1507,11 +1617,11 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     MDX_CHECK(aligned(out, 4) && aligned(residual, 4), "out / residual must be 4-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const MlpWs w = mlp_ws(workspace, rows, K1, N1);
-    rc = mono_mlp_chain(xn, norm_w, eps, h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
-    if (rc >= 0) return rc;
-    // four launches: prep, gate/up, prep of h, down
     PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
     if ((rc = launch_prep(pa, rows, st))) return rc;
+    rc = mono_mlp_fused(h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
+    if (rc >= 0) return rc;
+    // three more launches: gate/up, prep of h, down
     const mdx_w4* gu[2] = {gate, up};
     void* o1[2] = {w.hb, w.hb};
     if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st))) return rc;

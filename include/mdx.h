@@ -98,9 +98,10 @@ size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1);
  * csrc/mono_layer.sycl:303-313).
  * workspace: >= mdx_mono_mlp_workspace(rows, K1, N1) bytes, 256-byte aligned, ZERO-FILLED before its
  * first use (its control words and int32 accumulators; every call leaves them zero again). Calls that
- * share a workspace must be ordered (one stream). K1 <= 4096, N1 % 256 == 0 and rot != MATRIX run as
- * one launch (row prep, gate/up, rotation of h, K-split down in one ticket-ordered grid); other shapes
- * as four launches. */
+ * share a workspace must be ordered (one stream). Four launches: row prep of x, gate/up, row prep of h,
+ * down. With MDX_MLP_FUSED=1 in the environment (opt-in: slower on MI355X), shapes with K1 <= 4096,
+ * N1 % 256 == 0 and rot != MATRIX whose grid is resident at once run as two: the row prep, then
+ * gate/up + rotation of h + K-split down in one launch. */
 int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
                  const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
                  const uint16_t* residual, uint16_t* out, int64_t rows, void* workspace, size_t workspace_bytes,

@@ -83,6 +83,25 @@ def test_w4a8_residual_and_f32_out(C, dev, fmt):
         assert_bits_equal(bits(out32), oracle_linear(x, xs, w, None, "f32").view(np.uint32), "f32 out")
 
 
+@pytest.mark.parametrize("tpw,ks", [(3, 4), (5, 2), (6, 1)])
+def test_w4a8_geometry_with_idle_tile_slots(C, dev, tpw, ks, monkeypatch):
+    """Work-group geometries whose last work-group has tile slots past the matrix (256 tiles in
+    groups of 3, 5, 6): the idle slots read inside the matrix and add nothing; every output equals
+    the oracle's. (Regression: the idle slots once formed their weight addresses past the end.)"""
+    g = torch.Generator().manual_seed(29 + tpw)
+    N, K = 4096, 4096
+    w = random_w4(N, K, g, "gptq")
+    wd = [t.to(dev) if t is not None else None for t in w[:4]]
+    monkeypatch.setenv("MDX_GEMV_TPW", str(tpw))
+    monkeypatch.setenv("MDX_GEMV_KS", str(ks))
+    for M in (1, 8):
+        print(f"case idle slots tpw={tpw} ks={ks} M={M}", flush=True)
+        x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+        out = C.w4a8_decode_linear(x.to(dev), xs.to(dev), *wd, None, w[4], 2, 0, False)
+        assert_bits_equal(bits(out), oracle_linear(x, xs, w), f"tpw={tpw} ks={ks} M={M}")
+
+
 def test_w4a8_rejects_bad_contracts(C, dev):
     x = torch.zeros(1, 4096, dtype=torch.int8, device=dev)
     xs = torch.ones(1, device=dev)
@@ -217,9 +236,10 @@ def _mlp_handles(g, dev, fmt="gptq"):
 
 
 @pytest.mark.parametrize("rot", ["none", "h256"])
-def test_mlp_one_launch_equals_four_launches(C, dev, rot, monkeypatch):
-    """The one-launch MLP (ticket-ordered units, K-split down with int32 atomics) against the
-    four-launch form and the oracle, with a residual, for every row count class."""
+def test_mlp_fused_equals_four_launches(C, dev, rot, monkeypatch):
+    """The fused MLP (row prep, then gate/up + rotation of h + K-split down with int32 atomics in
+    one launch) against the four-launch form and the oracle, with a residual, for every row count
+    class (16 rows do not fit the fused launch's residency bound: both runs take four launches)."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(41)
     ws, handles = _mlp_handles(g, dev)
@@ -229,12 +249,12 @@ def test_mlp_one_launch_equals_four_launches(C, dev, rot, monkeypatch):
     h = layout.regular_hadamard(dev) if rot == "h256" else None
     d = _oracle_dicts(ws)
     for M in (1, 2, 5, 8, 16):
-        print(f"case mlp-chain rot={rot} M={M}", flush=True)
+        print(f"case mlp-fused rot={rot} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         outs = []
-        for chain in ("1", "0"):  # one launch, four launches
-            monkeypatch.setenv("MDX_MLP_CHAIN", chain)
+        for fused in ("1", "0"):  # two launches, four launches
+            monkeypatch.setenv("MDX_MLP_FUSED", fused)
             outs.append(C.mono_mlp_w4(x.to(dev), code, h, lut, *handles, norm_w=nw.to(dev), eps=1e-6,
                                       residual=res.to(dev)))
         torch.cuda.synchronize()
@@ -245,18 +265,19 @@ def test_mlp_one_launch_equals_four_launches(C, dev, rot, monkeypatch):
         assert_bits_equal(bits(outs[0]), want, f"M={M}")
 
 
-def test_mlp_one_launch_graph_replays(C, dev, monkeypatch):
-    """Captured once, replayed with new inputs between eager calls: every replay equals the eager
-    result (the control words and accumulators are back at zero after every launch)."""
+def test_mlp_fused_graph_replays(C, dev, monkeypatch):
+    """The fused MLP captured once, replayed with new inputs between eager four-launch calls: every
+    replay equals the eager result (the control words and accumulators are back at zero after
+    every launch)."""
     from mdx import _lib, layout
-    monkeypatch.setenv("MDX_MLP_CHAIN", "1")
+    monkeypatch.setenv("MDX_MLP_FUSED", "1")
     g = torch.Generator().manual_seed(43)
     _, handles = _mlp_handles(g, dev)
     lut = layout.silu_lut(dev)
     hd = layout.regular_hadamard(dev)
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
     for M in (1, 8):
-        print(f"case mlp-chain graph M={M}", flush=True)
+        print(f"case mlp-fused graph M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev)
         out = torch.empty(M, 4096, dtype=torch.bfloat16, device=dev)
         C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
@@ -269,7 +290,9 @@ def test_mlp_one_launch_graph_replays(C, dev, monkeypatch):
             graph.replay()
             torch.cuda.synchronize()
             got = out.clone()
+            monkeypatch.setenv("MDX_MLP_FUSED", "0")
             want = C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6)
+            monkeypatch.setenv("MDX_MLP_FUSED", "1")
             torch.cuda.synchronize()
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={M} replay {rep}"
         assert C.mlp_error(dev) == 0
