@@ -218,52 +218,97 @@ constexpr int NSPLIT = 4, SC = DH / NSPLIT, HRG = 8, HRPG = DH / HRG, HT = HRG *
 __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
     __shared__ float vvec[2 * MAXS][SC], mbuf[2][HRG][SC], rbuf[2][HRG][SC], rawc[MAXS][SC];
-    __shared__ float egate[2 * MAXS][2];
+    __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
     __shared__ int ectl[2 + 3 * MAXS];
     if (!ctl_ok(a)) return;
-    const int t = threadIdx.x, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
+    const int t = threadIdx.x, lane = t % 64, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
     const int kh = h / (HV / HK);
     const int64_t C = a.C;
-    if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
-    __syncthreads();
-    const int pending = ectl[0], p = ectl[1];
-    const int* acc = ectl + 2;
-    const int* prog = ectl + 2 + 2 * S;
-    int E0 = 0;
-    while (E0 < pending && acc[E0] >= 0 && acc[E0] < S) ++E0;
-    const bool replayed = E0 == pending;
-    int E1 = 0;
-    if (replayed)
-        while (E1 < R && prog[E1] >= 0 && (prog[E1] & 15) < R) ++E1;
-    const int E = E0 + E1;
-    auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
-    // the entries' gates (this step's from the conv launch, the replay's from the previous step) and
-    // inputs: k * ki, (q * scale) * qi over the whole head, v over this work-group's columns
-    if (t < E) {
-        const int e = t, ts = slot_of(e), par = e < E0 ? 1 - p : p;
-        egate[e][0] = a.gates[((par * S + ts) * HV + h) * 2];
-        egate[e][1] = a.gates[((par * S + ts) * HV + h) * 2 + 1];
-    }
-    for (int i = t; i < E * DH; i += HT) {
-        const int e = i / DH, d = i % DH, ts = slot_of(e);
-        const bool verify = e >= E0;
-        const int par = verify ? p : 1 - p;
-        const uint16_t* src = a.qb + (par * S + ts) * C;
-        const float* sm = a.sums + ((par * S + ts) * HK + kh) * 2;
-        const float ki = __fdiv_rn(1.f, fmaxf(sqrt_rn(sm[1]), 1e-12f));
-        kvec[e][d] = __fmul_rn(bf2f(src[KD + kh * DH + d]), ki);
-        if (verify) {
-            const float qi = __fdiv_rn(1.f, fmaxf(sqrt_rn(sm[0]), 1e-12f));
-            qvec[e - E0][d] = __fmul_rn(__fmul_rn(bf2f(src[kh * DH + d]), a.qscale), qi);
-        }
-        if (d < SC) vvec[e][d] = bf2f(src[2 * KD + h * DH + cs * SC + d]);
-    }
+    // the state of this work-group's columns first (it does not depend on the control words)
     const int col = t % SC, rg = t / SC;
     float st[HRPG];
     float* rs = a.rec + (int64_t(h) * DH + rg * HRPG) * DH + cs * SC + col;
 #pragma unroll
     for (int r = 0; r < HRPG; ++r) st[r] = rs[r * DH];
+    if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
+    __syncthreads();
+    const int pending = ectl[0], p = ectl[1];
+    const int* acc = ectl + 2;
+    const int* prog = ectl + 2 + 2 * S;
+    // the entries: the leading valid accepted slots (replayed when all `pending` are valid), then the
+    // leading program entries with a valid row (each wave ballots the same counts)
+    const bool v0 = lane < pending && acc[lane < S ? lane : 0] >= 0 && acc[lane < S ? lane : 0] < S;
+    const int E0 = __builtin_ctzll(~__ballot(v0));
+    const bool replayed = E0 == pending;
+    const int pl = prog[lane < S ? lane : 0];
+    const bool v1 = replayed && lane < R && pl >= 0 && (pl & 15) < R;
+    const int E1 = replayed ? __builtin_ctzll(~__ballot(v1)) : 0;
+    const int E = E0 + E1;
+    auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
+    // raw inputs, every load issued before the first use: k (16 pieces of 8 per entry) and v (4 per
+    // entry) of every entry, q (16 per entry) of the verify entries; the entries' gates and norms
+    constexpr int KP = 2 * MAXS * 16 / HT, VP = 2 * MAXS * 4;
+    uint4 kraw[KP], qraw = make_uint4(0u, 0u, 0u, 0u), vraw = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < KP; ++j) kraw[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (E > 0) {  // (uniform) indices clamped into [0, E): every slot read is a validated one
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const int i = min(t + HT * j, E * 16 - 1), e = i / 16;
+        const int ts = slot_of(e), par = e < E0 ? 1 - p : p;
+        kraw[j] = *reinterpret_cast<const uint4*>(a.qb + (par * S + ts) * C + KD + kh * DH + (i % 16) * 8);
+    }
+    {
+        const int i = min(t, max(E1 * 16 - 1, 0)), e = E0 + i / 16;
+        qraw = *reinterpret_cast<const uint4*>(a.qb + (p * S + slot_of(min(e, E - 1))) * C + kh * DH + (i % 16) * 8);
+    }
+    if (t < VP) {
+        const int i = min(t, E * 4 - 1), e = i / 4;
+        const int ts = slot_of(e), par = e < E0 ? 1 - p : p;
+        vraw = *reinterpret_cast<const uint4*>(a.qb + (par * S + ts) * C + 2 * KD + h * DH + cs * SC + (i % 4) * 8);
+    }
+    }
+    if (t < E) {
+        const int e = t, ts = slot_of(e), par = e < E0 ? 1 - p : p;
+        const float* sm = a.sums + ((par * S + ts) * HK + kh) * 2;
+        const float* gt = a.gates + ((par * S + ts) * HV + h) * 2;
+        const float sq = sm[0], sk = sm[1];
+        egate[e][0] = gt[0];
+        egate[e][1] = gt[1];
+        egate[e][2] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sk), 1e-12f));
+        egate[e][3] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sq), 1e-12f));
+    }
+    __syncthreads();
+    // scaled into LDS: k * ki, (q * scale) * qi, v
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const int i = t + HT * j;
+        if (i < E * 16) {
+            const int e = i / 16, d0 = (i % 16) * 8;
+            const float ki = egate[e][2];
+            const uint32_t w[4] = {kraw[j].x, kraw[j].y, kraw[j].z, kraw[j].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                kvec[e][d0 + q] = __fmul_rn(__uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16)), ki);
+        }
+    }
+    if (t < E1 * 16) {
+        const int e = E0 + t / 16, d0 = (t % 16) * 8;
+        const float qi = egate[e][3];
+        const uint32_t w[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            qvec[e - E0][d0 + q] =
+                __fmul_rn(__fmul_rn(__uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16)), a.qscale), qi);
+    }
+    if (t < E * 4) {
+        const int e = t / 4, d0 = (t % 4) * 8;
+        const uint32_t w[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            vvec[e][d0 + q] = __uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16));
+    }
     __syncthreads();
     for (int e = 0; e < E; ++e) {
         const bool verify = e >= E0;
