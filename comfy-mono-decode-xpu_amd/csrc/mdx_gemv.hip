@@ -115,6 +115,9 @@ struct PrepArgs {
     const uint16_t* hw = nullptr;
     const uint16_t* hz = nullptr;
     float heps = 0.f;
+    // optional: work-group 0 also sets zero[0, zero_n) to 0 (slots a later launch accumulates into)
+    uint32_t* zero = nullptr;
+    int zero_n = 0;
 };
 
 __device__ __forceinline__ void unpack4(const uint2& v, float* f) {
@@ -346,6 +349,8 @@ __global__ __launch_bounds__(1024) void prep_rows_kernel(PrepArgs a) {
     __shared__ float gsum[MAX_PREP_K / 256];
     __shared__ float wmax[16];
     prep_row<GPW>(a, blockIdx.x, gsum, wmax);
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.zero_n; i += blockDim.x) a.zero[i] = 0u;
 }
 
 int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
@@ -399,7 +404,16 @@ struct GemvArgs {
     uint32_t* tcnt;
     int split;
     int coh;              // EPI_SILU outputs are read within the launch: coherent stores
+    // EPI_SILU with hmax_out: each work-group also raises the rows' |h| maxima in slot wg % HSLOTS of
+    // hmax_out [HSLOTS][16] (fp32 bits, atomic max; the slots start at zero)
+    uint32_t* hmax_out;
+    // HR units (gemv_kernel<.., HR>): the activation is hr (bf16 [rows, K]) quantised in the prologue
+    // with the row scale max(absmax / 127, 1e-30), absmax = the maximum over the HSLOTS slots of hmax
+    const uint16_t* hr;
+    const uint32_t* hmax;
 };
+
+constexpr int HSLOTS = 64;  // spread of the |h| maxima: same-address atomics serialise (~11 ns each)
 
 // What a work unit waits for before it stages its activation, and where the activation comes from.
 // Data handed between work-groups of one launch is written with coherent (write-through) stores and
@@ -590,6 +604,18 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
             uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + tile * 16 + c);
             if (a.coh) st_c(o, v);
             else *o = v;
+            if (a.hmax_out) {
+                // the row's |h| maximum over the 8 threads of this (pair, row) (NaN counts as 0, as in
+                // the row prep's fmaxf from 0), into this work-group's slot
+                float m = fmaxf(fabsf(bf2f(uint16_t(v))), fabsf(bf2f(uint16_t(v >> 16))));
+                m = fmaxf(m, __shfl_xor(m, 1, 8));
+                m = fmaxf(m, __shfl_xor(m, 2, 8));
+                m = fmaxf(m, __shfl_xor(m, 4, 8));
+                if ((rem & 7) == 0) {
+                    if (m != m) m = 0.f;
+                    atomicMax(a.hmax_out + (wg % HSLOTS) * 16 + r, __float_as_uint(m));
+                }
+            }
         }
         return;
     }
@@ -701,7 +727,8 @@ __device__ __forceinline__ void unit_groups(int cu0, int ncu, int lgG, int ng, i
 // PRE: the ring's first RING loads were issued by issue_ring (same unit) and arrive in `pre`.
 // EPI false: the unit ends after its reduction operands are in LDS; the caller runs the epilogue
 // (after a barrier) with the pointers of unit_lds.
-template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true>
+// HR: the activation is a.hr quantised in the prologue (a.hmax slots), not int8 rows a.xq.
+template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true, bool HR = false>
 __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds,
                                           const UnitIn& in, int* flag, const uint4* pre = nullptr) {
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
@@ -737,7 +764,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     const int lgG = a.lgG;
 
     // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
-    if (!in.wait) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
+    const bool own_x = !in.wait && !HR;  // int8 rows a.xq staged by this prologue
+    if (own_x) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
     for (int tsi = 0; tsi < a.TPW; ++tsi) {
         int tl;
         const int mm = which_mat(a, wg * a.TPW + tsi, tl);
@@ -752,8 +780,28 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     if (slice == 0 && lane < 16) {
         const MDX_G float* sc = mat_sch(a, mi);
         prm = sc[(live ? tile : 0) * 16 + lane];
-    } else if (!in.wait && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) {
+    } else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) {
         prm = a.xs[lane - 16];
+    }
+    // HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the rows' |h| maxima (lane l of
+    // wave w: slot l of rows w, w + waves, ...) are one-shot operands too
+    constexpr int HRP = HR ? 16 : 1;
+    uint4 hraw[HRP];
+    float hmx[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nwv = a.TPW * a.KS;
+    if (HR) {
+        const int total = a.rows * (Kr / 8), per_row = Kr / 8;
+#pragma unroll
+        for (int k = 0; k < HRP; ++k) {
+            const int i = k * nthr + t, r = i / per_row, j = i - r * per_row;
+            hraw[k] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = min(wave + nwv * i, a.rows - 1);
+            hmx[i] = __uint_as_float(a.hmax[lane * 16 + r]);
+        }
     }
 
     float cb[16];
@@ -848,6 +896,44 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_waitcnt(RING | (7 << 4) | (15 << 8));  // vmcnt(RING), expcnt / lgkmcnt not waited
         __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
         __builtin_amdgcn_s_barrier();
+    }
+    if (HR) {
+        // the rows' scales (the row prep's formula), then the rows quantised into LDS while the ring
+        // stays in flight: v / sb as fp32(fp64(v) * (1 / fp64(sb))), exact for bf16 v and sb (see the
+        // staging of a wait unit above)
+        double* rcp = reinterpret_cast<double*>(prml + 96);  // [rows]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = wave + nwv * i;
+            const float m = wave_max(hmx[i]);
+            if (lane == 0 && r < a.rows) {
+                const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
+                uint16_t sb = f2bf(s);
+                if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+                prml[a.TPW * 16 + r] = s;
+                rcp[r] = 1.0 / double(bf2f(sb));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        const int total = a.rows * (Kr / 8), per_row = Kr / 8;
+#pragma unroll
+        for (int k = 0; k < HRP; ++k) {
+            const int i = k * nthr + t;
+            if (i < total) {
+                const int r = i / per_row, j = i - r * per_row;
+                const double rr = rcp[r];
+                const uint32_t w[4] = {hraw[k].x, hraw[k].y, hraw[k].z, hraw[k].w};
+                uint32_t o[2] = {0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
+                    const float d = bfround(float(__dmul_rn(double(v), rr)));
+                    o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
+                }
+                *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
+            }
+        }
     }
     // Whether every staged scale is an integer in [-15, 15]: then the unit takes the integral form
     // throughout (both forms give the same int32 sums, so the choice is free).
@@ -990,7 +1076,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // the epilogue's parameters (only the epilogue reads them; written this late, their loads need no
     // wait that would also wait for the ring)
     if (slice == 0 && lane < 16) prml[ts * 16 + lane] = prm;
-    else if (!in.wait && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
+    else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
     if (!EPI) return;
     __syncthreads();
     epilogue<MFMA>(a, wg, red, prml, flag);
@@ -1035,11 +1121,12 @@ __device__ __forceinline__ void issue_ring(const GemvArgs& a, const int wg, cons
     for (int p = 0; p < RING; ++p) out[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
 }
 
-template <bool MFMA, int R, int SDT, int RING>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
+// HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per SIMD.
+template <bool MFMA, int R, int SDT, int RING, bool HR = false>
+__global__ __launch_bounds__(HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int flag;
-    gemv_unit<MFMA, R, SDT, RING>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
+    gemv_unit<MFMA, R, SDT, RING, false, true, HR>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
 }
 
 // LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
@@ -1060,15 +1147,20 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mf
 
 int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1); }
 
-template <bool MFMA, int R, int SDT, int RING>
-int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
+template <bool MFMA, int R, int SDT, int RING, bool HR>
+int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
     const size_t smem = gemv_smem(a, MFMA, esz_of(SDT));
-    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING>);
+    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING, HR>);
     if (smem > 64 * 1024) allow_smem(fn, smem);
     const int threads = a.TPW * a.KS * WAVE;
-    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
+    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING, HR>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
+}
+
+template <bool MFMA, int R, int SDT, int RING>
+int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
+    return a.hr ? launch_gemv_h<MFMA, R, SDT, RING, true>(a, wgs, st) : launch_gemv_h<MFMA, R, SDT, RING, false>(a, wgs, st);
 }
 
 template <int SDT, int RING>
@@ -1151,9 +1243,50 @@ int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, con
     return MDX_OK;
 }
 
+// The launch geometry: TPW tiles per work-group, KS K-slices per tile (at most 16 waves per
+// work-group): the smallest split that puts >= 3072 waves on the chip (12 per CU), but no slice
+// shorter than 4 chunks, measured best on MI355X for the 8-52 MB matrices of this model (longer
+// streams per wave beat more, shorter waves: 4096 x 4096 takes 6.4 us at 8 slices against 7.6 at 12).
+void gemv_geometry(int total, int K, bool pair, int& TPW, int& KS) {
+    TPW = pair ? 2 : 1;
+    const int NC = K / CHUNK_K;
+    const int maxks = 16 / TPW;
+    KS = 1;
+    for (int d = 1; d <= maxks && 4 * d <= NC; ++d) {
+        if (NC % d) continue;
+        KS = d;
+        if (int64_t(total) * d >= 3072) break;
+    }
+    // MDX_GEMV_TPW / MDX_GEMV_KS override the geometry (tuning sweeps)
+    if (const char* env = getenv("MDX_GEMV_TPW")) {
+        const int tpw = atoi(env);
+        if (tpw >= 1 && tpw <= 6 && (!pair || tpw % 2 == 0)) TPW = tpw;  // the parameter block holds 6 tiles
+    }
+    if (const char* env = getenv("MDX_GEMV_KS")) {
+        const int ks = atoi(env);
+        if (ks >= 1 && ks * TPW <= 16 && NC % ks == 0) KS = ks;
+    }
+    if (TPW * KS > 16) KS = 16 / TPW;
+}
+
+// Whether a one-matrix GEMV of `rows` rows over K quantises bf16 rows in its prologue (HR: at most
+// 16 pieces of 8 per thread, at most 12 waves per work-group). Every work-group reads and quantises
+// all of its rows, so this pays only for one or two rows: at 8 rows of 12288 the 256 work-groups
+// of a down GEMV would read 50 MB of h between them and lose more than the prep launch costs.
+bool gemv_hr_fits(const mdx_w4* w, int rows) {
+    int TPW, KS;
+    gemv_geometry(int(w->n / 16), int(w->k), false, TPW, KS);
+    return rows <= 2 && TPW * KS <= 12 && int64_t(rows) * (w->k / 8) <= int64_t(16) * TPW * KS * WAVE;
+}
+
+// hmax_out: EPI_SILU raises the rows' |h| slot maxima; hr / hmax: HR units (one matrix, rows <= 8,
+// gemv_hr_fits), xq / xs unused.
 int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
-             void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st) {
+             void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st,
+             uint32_t* hmax_out = nullptr, const uint16_t* hr = nullptr, const uint32_t* hmax = nullptr) {
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
+    MDX_CHECK(!hr || (nm == 1 && !pair && hmax && gemv_hr_fits(ws[0], rows)), "bf16-row GEMV geometry");
+    MDX_CHECK(!hmax_out || rows <= 8, "slot maxima rows");
     // the activation rows live in LDS: above 128 KiB, run the rows in two halves
     if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
         const int ra = 8, rb = rows - 8;
@@ -1171,32 +1304,13 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     }
     GemvArgs a;
     int total = 0;
-    int rc = setup_gemv(ws, nm, pair, xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
+    int rc = setup_gemv(ws, nm, pair, hr ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
     if (rc) return rc;
     const bool mfma = rows >= MFMA_MIN_ROWS;
-    // geometry: TPW tiles per work-group, KS K-slices per tile (at most 16 waves per work-group):
-    // the smallest split that puts >= 3072 waves on the chip (12 per CU), but no slice shorter than
-    // 4 chunks, measured best on MI355X for the 8-52 MB matrices of this model (longer streams per
-    // wave beat more, shorter waves: 4096 x 4096 takes 6.4 us at 8 slices against 7.6 at 12)
-    a.TPW = pair ? 2 : 1;
-    const int NC = a.K / CHUNK_K;
-    const int maxks = 16 / a.TPW;
-    a.KS = 1;
-    for (int d = 1; d <= maxks && 4 * d <= NC; ++d) {
-        if (NC % d) continue;
-        a.KS = d;
-        if (int64_t(total) * d >= 3072) break;
-    }
-    // MDX_GEMV_TPW / MDX_GEMV_KS override the geometry (tuning sweeps)
-    if (const char* env = getenv("MDX_GEMV_TPW")) {
-        const int tpw = atoi(env);
-        if (tpw >= 1 && tpw <= 6 && (!pair || tpw % 2 == 0)) a.TPW = tpw;  // the parameter block holds 6 tiles
-    }
-    if (const char* env = getenv("MDX_GEMV_KS")) {
-        const int ks = atoi(env);
-        if (ks >= 1 && ks * a.TPW <= 16 && NC % ks == 0) a.KS = ks;
-    }
-    if (a.TPW * a.KS > 16) a.KS = 16 / a.TPW;
+    gemv_geometry(total, a.K, pair, a.TPW, a.KS);
+    a.hmax_out = hmax_out;
+    a.hr = hr;
+    a.hmax = hmax;
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
@@ -1489,6 +1603,7 @@ static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header
 
 struct MlpWs {
     uint32_t* flags;
+    uint32_t* hmax;  // [HSLOTS][16] |h| slot maxima (the prep of x zeroes them)
     uint32_t* sync;
     uint32_t* amax;
     uint32_t* tcnt;
@@ -1515,6 +1630,7 @@ MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
     w.amax = hdr ? hdr + SY_HDR + CH_MAX_G1 : nullptr;
     w.tcnt = hdr ? hdr + SY_HDR + CH_MAX_G1 + 16 : nullptr;
     w.flags = reinterpret_cast<uint32_t*>(take(MLP_FLAGS));
+    w.hmax = reinterpret_cast<uint32_t*>(take(size_t(HSLOTS) * 16 * 4));
     w.acc = reinterpret_cast<int32_t*>(take(size_t(16) * CH_MAX_K1 * 4));
     w.q1 = reinterpret_cast<int8_t*>(take(size_t(rows) * K1));
     w.q2 = reinterpret_cast<int8_t*>(take(size_t(rows) * N1));
@@ -1617,19 +1733,33 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     MDX_CHECK(aligned(out, 4) && aligned(residual, 4), "out / residual must be 4-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const MlpWs w = mlp_ws(workspace, rows, K1, N1);
+    // Without a rotation, h needs no row prep launch: gate/up raises the rows' |h| slot maxima and
+    // the down GEMV quantises h in its prologue (the same scale and codes as the row prep), when
+    // its geometry holds the rows (MDX_MLP_HPREP=1 forces the prep launch).
+    const char* hp = getenv("MDX_MLP_HPREP");
+    const bool hr = rot == MDX_ROT_NONE && gemv_hr_fits(down, int(rows)) && !(hp && atoi(hp) != 0);
     PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
+    if (hr) {
+        pa.zero = w.hmax;
+        pa.zero_n = HSLOTS * 16;
+    }
     if ((rc = launch_prep(pa, rows, st))) return rc;
     rc = mono_mlp_fused(h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
     if (rc >= 0) return rc;
-    // three more launches: gate/up, prep of h, down
+    // gate/up, [prep of h], down
     const mdx_w4* gu[2] = {gate, up};
     void* o1[2] = {w.hb, w.hb};
-    if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st))) return rc;
-    PrepArgs pb{w.hb, nullptr, 0.f, nullptr, h, rot, w.q2, w.s + 32, int(N1)};
-    if ((rc = launch_prep(pb, rows, st))) return rc;
+    if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st,
+                       hr ? w.hmax : nullptr)))
+        return rc;
     const mdx_w4* dn[1] = {down};
     void* o2[1] = {out};
     const void* r2[1] = {residual};
+    if (hr)
+        return run_gemv(dn, 1, false, nullptr, nullptr, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st, nullptr,
+                        w.hb, w.hmax);
+    PrepArgs pb{w.hb, nullptr, 0.f, nullptr, h, rot, w.q2, w.s + 32, int(N1)};
+    if ((rc = launch_prep(pb, rows, st))) return rc;
     return run_gemv(dn, 1, false, w.q2, w.s + 32, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st);
 }
 
