@@ -115,9 +115,6 @@ struct PrepArgs {
     const uint16_t* hw = nullptr;
     const uint16_t* hz = nullptr;
     float heps = 0.f;
-    // optional: work-group 0 also sets zero[0, zero_n) to 0 (slots a later launch accumulates into)
-    uint32_t* zero = nullptr;
-    int zero_n = 0;
 };
 
 __device__ __forceinline__ void unpack4(const uint2& v, float* f) {
@@ -349,8 +346,6 @@ __global__ __launch_bounds__(1024) void prep_rows_kernel(PrepArgs a) {
     __shared__ float gsum[MAX_PREP_K / 256];
     __shared__ float wmax[16];
     prep_row<GPW>(a, blockIdx.x, gsum, wmax);
-    if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < a.zero_n; i += blockDim.x) a.zero[i] = 0u;
 }
 
 int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
@@ -404,16 +399,26 @@ struct GemvArgs {
     uint32_t* tcnt;
     int split;
     int coh;              // EPI_SILU outputs are read within the launch: coherent stores
-    // EPI_SILU with hmax_out: each work-group also raises the rows' |h| maxima in slot wg % HSLOTS of
-    // hmax_out [HSLOTS][16] (fp32 bits, atomic max; the slots start at zero)
+    // EPI_SILU with hmax_out (one gate/up pair per work-group): work-group wg also stores its rows'
+    // |h| maxima (fp32 bits) at hmax_out[wg * 16 + row]
     uint32_t* hmax_out;
-    // HR units (gemv_kernel<.., HR>): the activation is hr (bf16 [rows, K]) quantised in the prologue
-    // with the row scale max(absmax / 127, 1e-30), absmax = the maximum over the HSLOTS slots of hmax
+    // SRC_HR units: the activation is hr (bf16 [rows, K]) quantised in the prologue with the row
+    // scale max(absmax / 127, 1e-30), absmax = the maximum of hmax[w * 16 + row] over w < hmax_n
     const uint16_t* hr;
     const uint32_t* hmax;
+    int hmax_n;
+    // SRC_XP units (one row): the activation is the bf16 row xp_x, RMSNorm'd with xp_nw / xp_eps
+    // (xp_nw may be null) and quantised (no rotation) in the prologue: the row prep's arithmetic in
+    // its order
+    const uint16_t* xp_x;
+    const uint16_t* xp_nw;
+    float xp_eps;
 };
 
-constexpr int HSLOTS = 64;  // spread of the |h| maxima: same-address atomics serialise (~11 ns each)
+// Where a unit's activation comes from: int8 rows a.xq (DMA to LDS), bf16 rows quantised with
+// given maxima (SRC_HR), or one bf16 row prepared from scratch (SRC_XP).
+enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
+constexpr int XP_GPW = 4;  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
 
 // What a work unit waits for before it stages its activation, and where the activation comes from.
 // Data handed between work-groups of one launch is written with coherent (write-through) stores and
@@ -605,16 +610,13 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
             if (a.coh) st_c(o, v);
             else *o = v;
             if (a.hmax_out) {
-                // the row's |h| maximum over the 8 threads of this (pair, row) (NaN counts as 0, as in
-                // the row prep's fmaxf from 0), into this work-group's slot
+                // the row's |h| maximum over the 8 threads of this row (the work-group's one pair; NaN
+                // counts as 0, as in the row prep's fmaxf from 0), stored as this work-group's entry
                 float m = fmaxf(fabsf(bf2f(uint16_t(v))), fabsf(bf2f(uint16_t(v >> 16))));
                 m = fmaxf(m, __shfl_xor(m, 1, 8));
                 m = fmaxf(m, __shfl_xor(m, 2, 8));
                 m = fmaxf(m, __shfl_xor(m, 4, 8));
-                if ((rem & 7) == 0) {
-                    if (m != m) m = 0.f;
-                    atomicMax(a.hmax_out + (wg % HSLOTS) * 16 + r, __float_as_uint(m));
-                }
+                if ((rem & 7) == 0) a.hmax_out[wg * 16 + r] = __float_as_uint(m != m ? 0.f : m);
             }
         }
         return;
@@ -727,8 +729,8 @@ __device__ __forceinline__ void unit_groups(int cu0, int ncu, int lgG, int ng, i
 // PRE: the ring's first RING loads were issued by issue_ring (same unit) and arrive in `pre`.
 // EPI false: the unit ends after its reduction operands are in LDS; the caller runs the epilogue
 // (after a barrier) with the pointers of unit_lds.
-// HR: the activation is a.hr quantised in the prologue (a.hmax slots), not int8 rows a.xq.
-template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true, bool HR = false>
+// SRC: where the activation comes from (Src).
+template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true, int SRC = SRC_Q8>
 __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds,
                                           const UnitIn& in, int* flag, const uint4* pre = nullptr) {
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
@@ -764,7 +766,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     const int lgG = a.lgG;
 
     // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
-    const bool own_x = !in.wait && !HR;  // int8 rows a.xq staged by this prologue
+    constexpr bool HR = SRC == SRC_HR, XP = SRC == SRC_XP;
+    const bool own_x = !in.wait && SRC == SRC_Q8;  // int8 rows a.xq staged by this prologue
     if (own_x) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
     for (int tsi = 0; tsi < a.TPW; ++tsi) {
         int tl;
@@ -783,11 +786,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     } else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) {
         prm = a.xs[lane - 16];
     }
-    // HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the rows' |h| maxima (lane l of
-    // wave w: slot l of rows w, w + waves, ...) are one-shot operands too
+    // SRC_HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the maxima entries (thread t:
+    // entries t, t + threads, ... of both rows) are one-shot operands too; SRC_XP: the row's 4 elements
+    // per lane of groups wave, wave + waves, ... and their norm weights
     constexpr int HRP = HR ? 16 : 1;
     uint4 hraw[HRP];
-    float hmx[4] = {0.f, 0.f, 0.f, 0.f};
+    float hmx[2] = {0.f, 0.f};
+    uint2 xpx[XP ? XP_GPW : 1], xpw[XP ? XP_GPW : 1];
     const int nwv = a.TPW * a.KS;
     if (HR) {
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
@@ -797,10 +802,18 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             hraw[k] = make_uint4(0u, 0u, 0u, 0u);
             if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
         }
+        for (int w = t; w < a.hmax_n; w += nthr)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = min(wave + nwv * i, a.rows - 1);
-            hmx[i] = __uint_as_float(a.hmax[lane * 16 + r]);
+            for (int r = 0; r < 2; ++r)
+                if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[w * 16 + r]));
+    }
+    if (XP) {
+        const int G = K / 256;
+#pragma unroll
+        for (int gi = 0; gi < XP_GPW; ++gi) {
+            const int g = min(wave + nwv * gi, G - 1);
+            xpx[gi] = *reinterpret_cast<const uint2*>(a.xp_x + 256 * g + 4 * lane);
+            xpw[gi] = a.xp_nw ? *reinterpret_cast<const uint2*>(a.xp_nw + 256 * g + 4 * lane) : make_uint2(0u, 0u);
         }
     }
 
@@ -902,17 +915,22 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // stays in flight: v / sb as fp32(fp64(v) * (1 / fp64(sb))), exact for bf16 v and sb (see the
         // staging of a wait unit above)
         double* rcp = reinterpret_cast<double*>(prml + 96);  // [rows]
+        float* wm = reinterpret_cast<float*>(red);           // [2][16 waves] (the reduction block is free here)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = wave + nwv * i;
-            const float m = wave_max(hmx[i]);
-            if (lane == 0 && r < a.rows) {
-                const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
-                uint16_t sb = f2bf(s);
-                if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-                prml[a.TPW * 16 + r] = s;
-                rcp[r] = 1.0 / double(bf2f(sb));
-            }
+        for (int r = 0; r < 2; ++r) {
+            const float m = wave_max(hmx[r]);
+            if (lane == 0) wm[r * 16 + wave] = m;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (t < a.rows) {
+            float m = wm[t * 16];
+            for (int w = 1; w < nwv; ++w) m = fmaxf(m, wm[t * 16 + w]);
+            const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
+            uint16_t sb = f2bf(s);
+            if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+            prml[a.TPW * 16 + t] = s;
+            rcp[t] = 1.0 / double(bf2f(sb));
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
@@ -932,6 +950,68 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                     o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
                 }
                 *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
+            }
+        }
+    }
+    if (XP) {
+        // the row prep of one row (prep_row's arithmetic and order), the barriers without memory
+        // waits so that the ring stays in flight; the reduction block holds the group sums / maxima
+        const int G = K / 256;
+        float* gsum = reinterpret_cast<float*>(red);  // [G] group sums, then [waves] maxima
+        float v[XP_GPW][4];
+#pragma unroll
+        for (int gi = 0; gi < XP_GPW; ++gi) unpack4(xpx[gi], v[gi]);
+        if (a.xp_nw) {
+#pragma unroll
+            for (int gi = 0; gi < XP_GPW; ++gi) {
+                float q = __fmul_rn(v[gi][0], v[gi][0]);
+#pragma unroll
+                for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
+                for (int s = 32; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+                const int g = wave + nwv * gi;
+                if (lane == 0 && g < G) gsum[g] = q;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
+            float ss = gsum[0];
+            for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, gsum[g]);
+            const float rr = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, float(K)), a.xp_eps)));
+#pragma unroll
+            for (int gi = 0; gi < XP_GPW; ++gi) {
+                float wv[4];
+                unpack4(xpw[gi], wv);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], rr), wv[e]));
+            }
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < XP_GPW; ++gi)
+            if (wave + nwv * gi < G)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[gi][e]));
+        m = wave_max(m);
+        if (lane == 0) gsum[G + wave] = m;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        float rm = gsum[G];
+        for (int w = 1; w < nwv; ++w) rm = fmaxf(rm, gsum[G + w]);
+        const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
+        if (t == 0) prml[a.TPW * 16] = s;
+        uint16_t sb = f2bf(s);
+        if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+        const float sbf = bf2f(sb);
+#pragma unroll
+        for (int gi = 0; gi < XP_GPW; ++gi) {
+            const int g = wave + nwv * gi;
+            if (g < G) {
+                uint32_t o = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float d = bfround(__fdiv_rn(v[gi][e], sbf));
+                    o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
+                }
+                *reinterpret_cast<uint32_t*>(xl + 256 * g + 4 * lane) = o;
             }
         }
     }
@@ -1121,12 +1201,13 @@ __device__ __forceinline__ void issue_ring(const GemvArgs& a, const int wg, cons
     for (int p = 0; p < RING; ++p) out[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
 }
 
-// HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per SIMD.
-template <bool MFMA, int R, int SDT, int RING, bool HR = false>
-__global__ __launch_bounds__(HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
+// SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
+// SIMD.
+template <bool MFMA, int R, int SDT, int RING, int SRC = SRC_Q8>
+__global__ __launch_bounds__(SRC == SRC_HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int flag;
-    gemv_unit<MFMA, R, SDT, RING, false, true, HR>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
+    gemv_unit<MFMA, R, SDT, RING, false, true, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
 }
 
 // LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
@@ -1147,20 +1228,22 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mf
 
 int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1); }
 
-template <bool MFMA, int R, int SDT, int RING, bool HR>
+template <bool MFMA, int R, int SDT, int RING, int SRC>
 int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
     const size_t smem = gemv_smem(a, MFMA, esz_of(SDT));
-    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING, HR>);
+    const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING, SRC>);
     if (smem > 64 * 1024) allow_smem(fn, smem);
     const int threads = a.TPW * a.KS * WAVE;
-    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING, HR>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
+    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING, SRC>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
 
 template <bool MFMA, int R, int SDT, int RING>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
-    return a.hr ? launch_gemv_h<MFMA, R, SDT, RING, true>(a, wgs, st) : launch_gemv_h<MFMA, R, SDT, RING, false>(a, wgs, st);
+    if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR>(a, wgs, st);
+    if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP>(a, wgs, st);
+    return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8>(a, wgs, st);
 }
 
 template <int SDT, int RING>
@@ -1279,14 +1362,35 @@ bool gemv_hr_fits(const mdx_w4* w, int rows) {
     return rows <= 2 && TPW * KS <= 12 && int64_t(rows) * (w->k / 8) <= int64_t(16) * TPW * KS * WAVE;
 }
 
-// hmax_out: EPI_SILU raises the rows' |h| slot maxima; hr / hmax: HR units (one matrix, rows <= 8,
-// gemv_hr_fits), xq / xs unused.
+// Whether a GEMV of one row can run the row prep of its activation in its prologue (SRC_XP: K a
+// multiple of 256 with at most XP_GPW 256-groups per wave).
+bool gemv_xp_fits(const mdx_w4* const* ws, int nm, bool pair) {
+    int total = 0;
+    for (int i = 0; i < nm; ++i) total += int(ws[i]->n / 16);
+    int TPW, KS;
+    gemv_geometry(total, int(ws[0]->k), pair, TPW, KS);
+    return ws[0]->k % 256 == 0 && ws[0]->k / 256 <= int64_t(XP_GPW) * TPW * KS;
+}
+
+// Extra activation sources and outputs of one launch (all optional).
+struct GemvExtra {
+    uint32_t* hmax_out = nullptr;      // EPI_SILU pair: the work-groups' |h| maxima
+    const uint16_t* hr = nullptr;      // SRC_HR (gemv_hr_fits): bf16 rows with the maxima hmax[hmax_n]
+    const uint32_t* hmax = nullptr;
+    int hmax_n = 0;
+    const uint16_t* xp_x = nullptr;    // SRC_XP (gemv_xp_fits): one bf16 row and its prep (no rotation)
+    const uint16_t* xp_nw = nullptr;
+    float xp_eps = 0.f;
+};
+
 int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
              void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st,
-             uint32_t* hmax_out = nullptr, const uint16_t* hr = nullptr, const uint32_t* hmax = nullptr) {
+             const GemvExtra& ex = GemvExtra{}) {
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
-    MDX_CHECK(!hr || (nm == 1 && !pair && hmax && gemv_hr_fits(ws[0], rows)), "bf16-row GEMV geometry");
-    MDX_CHECK(!hmax_out || rows <= 8, "slot maxima rows");
+    MDX_CHECK(!ex.hr || (nm == 1 && !pair && ex.hmax && ex.hmax_n > 0 && gemv_hr_fits(ws[0], rows)),
+              "bf16-row GEMV geometry");
+    MDX_CHECK(!ex.hmax_out || (pair && rows <= 16), "|h| maxima need a gate/up pair");
+    MDX_CHECK(!ex.xp_x || (rows == 1 && gemv_xp_fits(ws, nm, pair)), "row-prep GEMV geometry");
     // the activation rows live in LDS: above 128 KiB, run the rows in two halves
     if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
         const int ra = 8, rb = rows - 8;
@@ -1304,13 +1408,18 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     }
     GemvArgs a;
     int total = 0;
-    int rc = setup_gemv(ws, nm, pair, hr ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
+    int rc = setup_gemv(ws, nm, pair, ex.hr || ex.xp_x ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
     if (rc) return rc;
     const bool mfma = rows >= MFMA_MIN_ROWS;
     gemv_geometry(total, a.K, pair, a.TPW, a.KS);
-    a.hmax_out = hmax_out;
-    a.hr = hr;
-    a.hmax = hmax;
+    MDX_CHECK(!ex.hmax_out || a.TPW == 2, "|h| maxima need one gate/up pair per work-group");
+    a.hmax_out = ex.hmax_out;
+    a.hr = ex.hr;
+    a.hmax = ex.hmax;
+    a.hmax_n = ex.hmax_n;
+    a.xp_x = ex.xp_x;
+    a.xp_nw = ex.xp_nw;
+    a.xp_eps = ex.xp_eps;
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
@@ -1603,7 +1712,7 @@ static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header
 
 struct MlpWs {
     uint32_t* flags;
-    uint32_t* hmax;  // [HSLOTS][16] |h| slot maxima (the prep of x zeroes them)
+    uint32_t* hmax;  // [N1 / 16][16] the gate/up work-groups' |h| maxima
     uint32_t* sync;
     uint32_t* amax;
     uint32_t* tcnt;
@@ -1630,7 +1739,7 @@ MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
     w.amax = hdr ? hdr + SY_HDR + CH_MAX_G1 : nullptr;
     w.tcnt = hdr ? hdr + SY_HDR + CH_MAX_G1 + 16 : nullptr;
     w.flags = reinterpret_cast<uint32_t*>(take(MLP_FLAGS));
-    w.hmax = reinterpret_cast<uint32_t*>(take(size_t(HSLOTS) * 16 * 4));
+    w.hmax = reinterpret_cast<uint32_t*>(take(size_t(N1 / 16) * 16 * 4));
     w.acc = reinterpret_cast<int32_t*>(take(size_t(16) * CH_MAX_K1 * 4));
     w.q1 = reinterpret_cast<int8_t*>(take(size_t(rows) * K1));
     w.q2 = reinterpret_cast<int8_t*>(take(size_t(rows) * N1));
@@ -1738,26 +1847,38 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     // its geometry holds the rows (MDX_MLP_HPREP=1 forces the prep launch).
     const char* hp = getenv("MDX_MLP_HPREP");
     const bool hr = rot == MDX_ROT_NONE && gemv_hr_fits(down, int(rows)) && !(hp && atoi(hp) != 0);
-    PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
-    if (hr) {
-        pa.zero = w.hmax;
-        pa.zero_n = HSLOTS * 16;
-    }
-    if ((rc = launch_prep(pa, rows, st))) return rc;
-    rc = mono_mlp_fused(h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
-    if (rc >= 0) return rc;
-    // gate/up, [prep of h], down
     const mdx_w4* gu[2] = {gate, up};
+    const char* fz = getenv("MDX_MLP_FUSED");
+    // one row: the gate/up GEMV prepares x itself (no row prep launch); MDX_MLP_HPREP=1 keeps both
+    // prep launches
+    const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && !(fz && atoi(fz) != 0);
+    if (!xp) {
+        PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
+        if ((rc = launch_prep(pa, rows, st))) return rc;
+        rc = mono_mlp_fused(h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
+        if (rc >= 0) return rc;
+    }
+    // gate/up, [prep of h], down
     void* o1[2] = {w.hb, w.hb};
-    if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st,
-                       hr ? w.hmax : nullptr)))
+    GemvExtra e1;
+    if (hr) e1.hmax_out = w.hmax;
+    if (xp) {
+        e1.xp_x = xn;
+        e1.xp_nw = norm_w;
+        e1.xp_eps = eps;
+    }
+    if ((rc = run_gemv(gu, 2, true, w.q1, w.s, int(rows), EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, st, e1)))
         return rc;
     const mdx_w4* dn[1] = {down};
     void* o2[1] = {out};
     const void* r2[1] = {residual};
-    if (hr)
-        return run_gemv(dn, 1, false, nullptr, nullptr, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st, nullptr,
-                        w.hb, w.hmax);
+    if (hr) {
+        GemvExtra e2;
+        e2.hr = w.hb;
+        e2.hmax = w.hmax;
+        e2.hmax_n = int(N1 / 16);
+        return run_gemv(dn, 1, false, nullptr, nullptr, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st, e2);
+    }
     PrepArgs pb{w.hb, nullptr, 0.f, nullptr, h, rot, w.q2, w.s + 32, int(N1)};
     if ((rc = launch_prep(pb, rows, st))) return rc;
     return run_gemv(dn, 1, false, w.q2, w.s + 32, int(rows), EPI_STORE, o2, r2, MDX_DT_BF16, nullptr, st);

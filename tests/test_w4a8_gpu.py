@@ -266,8 +266,9 @@ def test_mlp_fused_equals_four_launches(C, dev, rot, monkeypatch):
 
 
 def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
-    """Without a rotation the down GEMV quantises h itself from gate/up's |h| slot maxima: the same
-    outputs, bit for bit, as the row prep launch of h (MDX_MLP_HPREP=1), and as the oracle; with a
+    """Without a rotation, at one or two rows, the down GEMV quantises h itself from gate/up's |h|
+    maxima, and at one row the gate/up GEMV also prepares x itself (RMSNorm or none): the same
+    outputs, bit for bit, as the row prep launches (MDX_MLP_HPREP=1), and as the oracle; with a
     residual, one to eight rows, over calls that reuse the workspace."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(47)
@@ -275,20 +276,21 @@ def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
     lut = layout.silu_lut(dev)
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
     d = _oracle_dicts(ws)
-    for M in (1, 2, 5, 8, 3):
-        print(f"case mlp-hr M={M}", flush=True)
+    for M, norm in ((1, True), (1, False), (2, True), (5, True), (8, True), (3, True)):
+        print(f"case mlp-hr M={M} norm={norm}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        nwd = nw.to(dev) if norm else None
         outs = []
         for hp in ("0", "1"):
             monkeypatch.setenv("MDX_MLP_HPREP", hp)
-            outs.append(C.mono_mlp_w4(x.to(dev), _lib.ROT_NONE, None, lut, *handles, norm_w=nw.to(dev), eps=1e-6,
+            outs.append(C.mono_mlp_w4(x.to(dev), _lib.ROT_NONE, None, lut, *handles, norm_w=nwd, eps=1e-6,
                                       residual=res.to(dev)))
         torch.cuda.synchronize()
         assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={M}"
-        xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
+        xn = ref.rmsnorm(bits(x), bits(nw), 1e-6) if norm else bits(x)
         want = ref.add_bf16(bits(res), ref.mono_mlp(xn, "none", None, bits(lut.cpu()), *d))
-        assert_bits_equal(bits(outs[0]), want, f"M={M}")
+        assert_bits_equal(bits(outs[0]), want, f"M={M} norm={norm}")
 
 
 def test_mlp_fused_graph_replays(C, dev, monkeypatch):
