@@ -92,6 +92,37 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// the value of lane l + D (D < 16) of lane l's row of 16 (DPP row_shl); lanes whose partner lies past
+// the row read 0
+template <int D>
+__device__ __forceinline__ float row_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + D, 0xF, 0xF, false));
+}
+
+// The halving-tree sum of the wave's 64 values in lane 0 (lane l adds lane l + s for s = 32, 16, ...,
+// 1, each sum rounded): the strides below 16 by DPP, 32 and 16 by cross-row shuffles. Only lane 0's
+// result is the tree's.
+__device__ __forceinline__ float tree_sum64(float q) {
+    q = __fadd_rn(q, shfl_down(q, 32));
+    q = __fadd_rn(q, shfl_down(q, 16));
+    q = __fadd_rn(q, row_shl<8>(q));
+    q = __fadd_rn(q, row_shl<4>(q));
+    q = __fadd_rn(q, row_shl<2>(q));
+    q = __fadd_rn(q, row_shl<1>(q));
+    return q;
+}
+
+// The maximum of the wave's non-negative values, in every lane (lane 0's tree, broadcast).
+__device__ __forceinline__ float wave_max_nn(float v) {
+    v = fmaxf(v, shfl_down(v, 32));
+    v = fmaxf(v, shfl_down(v, 16));
+    v = fmaxf(v, row_shl<8>(v));
+    v = fmaxf(v, row_shl<4>(v));
+    v = fmaxf(v, row_shl<2>(v));
+    v = fmaxf(v, row_shl<1>(v));
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
 // fused_scaleback: (float(acc) * xs) * sc, each product rounded on its own
 __device__ __forceinline__ float scaleback(int32_t acc, float xs, float sc) {
     float f = float(acc);

@@ -227,7 +227,11 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             float q = __fmul_rn(v[gi][0], v[gi][0]);
 #pragma unroll
             for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-            for (int s = 16; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+            q = __fadd_rn(q, shfl_down(q, 16));
+            q = __fadd_rn(q, row_shl<8>(q));
+            q = __fadd_rn(q, row_shl<4>(q));
+            q = __fadd_rn(q, row_shl<2>(q));
+            q = __fadd_rn(q, row_shl<1>(q));
             q = __shfl(q, lane & 32, 64);
             const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(q, 128.f), a.heps)));
             float zf[4];
@@ -246,7 +250,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             float q = __fmul_rn(v[gi][0], v[gi][0]);
 #pragma unroll
             for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-            for (int s = 32; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+            q = tree_sum64(q);
             const int g = w + W * gi;
             if (lane == 0 && g < G) gsum[g] = q;
         }
@@ -310,7 +314,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
         if (w + W * gi < G)
 #pragma unroll
             for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[gi][e]));
-    m = wave_max(m);
+    m = wave_max_nn(m);
     if (lane == 0) wmax[w] = m;
     __syncthreads();
     float rm = wmax[0];
@@ -322,7 +326,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     }
     uint16_t sb = f2bf(s);
     if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-    const float sbf = bf2f(sb);
+    const double rr = 1.0 / double(bf2f(sb));  // v and sb are bf16: the exact fp64-reciprocal quotient
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
         const int g = w + W * gi;
@@ -330,7 +334,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             uint32_t o = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float d = bfround(__fdiv_rn(v[gi][e], sbf));
+                const float d = bfround(float(__dmul_rn(double(v[gi][e]), rr)));
                 const int qv = int(fminf(fmaxf(rintf(d), -128.f), 127.f));
                 o |= (uint32_t(qv) & 0xFFu) << (8 * e);
             }
@@ -815,6 +819,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             xpx[gi] = *reinterpret_cast<const uint2*>(a.xp_x + 256 * g + 4 * lane);
             xpw[gi] = a.xp_nw ? *reinterpret_cast<const uint2*>(a.xp_nw + 256 * g + 4 * lane) : make_uint2(0u, 0u);
         }
+        // the row before the weight ring: requested behind the ring, it would queue behind the
+        // whole chip's first round of weights; its prep then runs while that round streams in
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     }
 
     float cb[16];
@@ -918,7 +925,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         float* wm = reinterpret_cast<float*>(red);           // [2][16 waves] (the reduction block is free here)
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const float m = wave_max(hmx[r]);
+            const float m = wave_max_nn(hmx[r]);
             if (lane == 0) wm[r * 16 + wave] = m;
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -967,7 +974,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 float q = __fmul_rn(v[gi][0], v[gi][0]);
 #pragma unroll
                 for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-                for (int s = 32; s >= 1; s >>= 1) q = __fadd_rn(q, shfl_down(q, s));
+                q = tree_sum64(q);
                 const int g = wave + nwv * gi;
                 if (lane == 0 && g < G) gsum[g] = q;
             }
@@ -990,7 +997,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             if (wave + nwv * gi < G)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[gi][e]));
-        m = wave_max(m);
+        m = wave_max_nn(m);
         if (lane == 0) gsum[G + wave] = m;
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
@@ -1000,7 +1007,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         if (t == 0) prml[a.TPW * 16] = s;
         uint16_t sb = f2bf(s);
         if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-        const float sbf = bf2f(sb);
+        const double rr = 1.0 / double(bf2f(sb));  // bf16 v / bf16 sb: the exact fp64-reciprocal quotient
 #pragma unroll
         for (int gi = 0; gi < XP_GPW; ++gi) {
             const int g = wave + nwv * gi;
@@ -1008,7 +1015,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 uint32_t o = 0;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float d = bfround(__fdiv_rn(v[gi][e], sbf));
+                    const float d = bfround(float(__dmul_rn(double(v[gi][e]), rr)));
                     o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
                 }
                 *reinterpret_cast<uint32_t*>(xl + 256 * g + 4 * lane) = o;
