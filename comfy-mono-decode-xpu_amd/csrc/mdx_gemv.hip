@@ -6,30 +6,28 @@
 //   mono_mlp            csrc/mono_mlp.sycl:109-167
 //
 // Scales are always the row-major [N, K/G] array (both layouts); a work-group stages its tiles'
-// scale rows in LDS once. Weight stream. A wave owns one 16-column tile and a K slice. Its unit of work is a "chunk":
-// 16 columns x 128 k = 1 KiB of codes, fetched with ONE 16-byte load per lane (lane l: column
-// l % 16, quarter kq = l / 16 of the chunk, 32 consecutive k). In the tile-major layout the 64
-// lanes' 16-byte pieces are adjacent, so every chunk is one contiguous 1 KiB burst; in the
-// checkpoint (row-major) layout they are 16 pieces of 64 B. Lane l's dword j holds the codes of
-// k = chunk + 32 kq + 8 j + [0, 8): low nibbles are the even k, high nibbles the odd k. All
-// per-chunk address math is 32-bit pointer increments; group indices are shifts (G is a power
-// of two).
+// scale rows in LDS once. Weight stream: a wave owns one 16-column tile and a K slice; its unit of
+// work is a "chunk", 16 columns x 128 k = 1 KiB of codes, fetched with ONE 16-byte load per lane
+// (lane l: column l % 16, quarter kq = l / 16 of the chunk, 32 consecutive k). In the tile-major
+// layout the 64 lanes' pieces are adjacent, so every chunk is one contiguous 1 KiB burst, and each
+// code dword holds k 0..3 in its low nibbles and k 4..7 in its high ones (natural activation
+// order); in the checkpoint (row-major) layout the pieces are 16 runs of 64 B and a dword's low /
+// high nibbles are its even / odd k (two byte permutes put them in natural order). All per-chunk
+// address math is 32-bit pointer increments; group indices are shifts (G is a power of two).
 //
-// Activation. The int8 activation rows are staged in LDS with every 8-byte block de-interleaved
-// ([x0 x2 x4 x6 | x1 x3 x5 x7]) so the low / high nibble words of a code dword line up with two
-// activation words: no per-weight shuffles.
+// Activation. The int8 rows of the unit's K range are staged in LDS (natural order) by DMA, or
+// quantised there in the prologue from bf16 rows (Src).
 //
 // Decode. Per-weight form: a 16-entry int8 table per (lane, scale) is built with the reference
 // formula w8 = clamp(rint(cb[c] * s), +-127) (NaN -> 0), and codes are mapped through it with
-// v_perm_b32 byte selects. Integral form, chosen per chunk under MDX_DECODE_AUTO when the
-// codebook is c - 8 and every lane's scale of the chunk is an integer in [-15, 15] (a wave-uniform
-// choice): then w8 = (c - 8) * s exactly, so sum_k x * w8 = s * (sum_k x * c - 8 sum_k x): the
-// raw nibbles (0..15) feed the dot directly and 8 * sum_k x is precomputed per 32-k block of the
-// activation. Both forms give the same int32 accumulator (mod 2^32) as the reference, so they
-// can be mixed chunk by chunk.
+// v_perm_b32 byte selects. Integral form, taken by a unit under MDX_DECODE_AUTO when the codebook
+// is c - 8 and every staged scale is an integer in [-15, 15]: then w8 = (c - 8) * s exactly; the
+// codes become the int8 bytes 16 (c - 8), whose products give 16 sum_k x (c - 8) exactly, and an
+// arithmetic shift by 4 and the scale finish each group. Both forms give the same int32
+// accumulator (mod 2^32) as the reference.
 //
-// Products. Rows <= 2: v_dot4_i32_i8 on the VALU. Rows 3..16: v_mfma_i32_16x16x32_i8 with the
-// activation rows as A (rows past the last are zero) and the decoded tile as B; lane l's dword j
+// Products. One row: v_dot4_i32_i8 on the VALU. Rows 2..16: v_mfma_i32_16x16x32_i8 with the
+// activation rows as A (rows past the last read zeros) and the decoded tile as B; lane l's dword j
 // of codes is exactly its B fragment for the j-th MFMA of the chunk.
 //
 // Split-K partial sums of the waves of a work-group are int32 and are added through LDS:
