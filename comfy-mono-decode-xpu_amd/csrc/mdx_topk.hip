@@ -293,6 +293,38 @@ int launch(const void* x, bool f32, int ord, int64_t rows, int64_t n, int64_t k,
 
 using namespace mdx;
 
+namespace mdx {
+namespace {
+
+// Gumbel-max pick over each row's top k: score_j = vals[r, j] * (1 / temperature) + g_j, with
+// g_j = -log(-log(clamp(u[r, j], 1e-20, 1))), every operation an fp32 rounding as torch's elementwise
+// kernels round them (a tensor divided by a scalar is multiplied by the scalar's fp32 reciprocal);
+// the first maximal score wins, as torch.argmax picks; out[r] = idx[r, j*]. One wave per row (k <= 64).
+__global__ __launch_bounds__(64) void topk_sample_kernel(const float* vals, const int64_t* idx, const float* u, float temp,
+                                                         int64_t k, int64_t* out) {
+    const int r = blockIdx.x, j = threadIdx.x;
+    float sc = -INFINITY;
+    int at = 64;
+    if (j < k) {
+        const float uu = fminf(fmaxf(u[r * k + j], 1e-20f), 1.0f);
+        const float g = -logf(-logf(uu));
+        sc = __fadd_rn(__fmul_rn(vals[r * k + j], __fdiv_rn(1.f, temp)), g);
+        at = j;
+    }
+    // (max score, then the smaller position) over the wave; NaN scores lose to numbers
+    for (int d = 32; d >= 1; d >>= 1) {
+        const float os = __shfl_xor(sc, d, 64);
+        const int oa = __shfl_xor(at, d, 64);
+        const bool take = (os > sc) || (os == sc && oa < at) || (sc != sc && os == os);
+        sc = take ? os : sc;
+        at = take ? oa : at;
+    }
+    if (j == 0) out[r] = idx[r * k + (at < k ? at : 0)];
+}
+
+}  // namespace
+}  // namespace mdx
+
 extern "C" size_t mdx_topk_workspace(int64_t rows) { return workspace_bytes(std::max<int64_t>(rows, 1)); }
 
 extern "C" int mdx_fast_topk(const uint16_t* x, int64_t V, int64_t k, int32_t argmax_order, uint16_t* values,
@@ -322,4 +354,15 @@ extern "C" int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64
     MDX_CHECK(k >= 1 && k <= TK_MAXK && n >= 4096 && n < (int64_t(1) << 31), "1 <= k <= 64, 4096 <= N < 2^31");
     return launch(x, x_dtype == MDX_DT_F32, ORDER_F32, rows, n, k, false, values, indices, nullptr, workspace,
                   workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_topk_sample(const float* values, const int64_t* indices, const float* uniform, float temperature,
+                               int64_t rows, int64_t k, int64_t* out, void* stream) {
+    MDX_CHECK(values && indices && uniform && out, "null pointer");
+    MDX_CHECK(rows >= 1 && rows <= 65535 && k >= 1 && k <= 64, "1 <= rows, 1 <= k <= 64");
+    MDX_CHECK(temperature > 0.f, "temperature > 0");
+    hipLaunchKernelGGL(mdx::topk_sample_kernel, dim3(unsigned(rows)), dim3(64), 0, static_cast<hipStream_t>(stream),
+                       values, indices, uniform, temperature, k, out);
+    MDX_LAUNCHED();
+    return MDX_OK;
 }

@@ -355,6 +355,22 @@ def topk_rows(x, k):
     return [values, indices]
 
 
+def topk_sample(values, indices, uniform, temperature, out=None):
+    """Gumbel-max pick over the rows' top k (the decode loop's sampling, one launch): out[r] =
+    indices[r, argmax_j(values[r, j] / temperature - log(-log(clamp(uniform[r, j], 1e-20, 1))))]."""
+    _dev(values, "values")
+    R, k = values.shape
+    _check(values.dtype == torch.float32 and indices.dtype == torch.int64 and uniform.dtype == torch.float32
+           and values.is_contiguous() and indices.is_contiguous() and uniform.is_contiguous()
+           and indices.shape == values.shape and uniform.shape == values.shape, "values f32 / indices int64 / uniform f32 [R, k]")
+    if out is None:
+        out = torch.empty(R, dtype=torch.int64, device=values.device)
+    _check(out.dtype == torch.int64 and out.is_contiguous() and out.numel() == R, "out int64 [R]")
+    _lib.call("mdx_topk_sample", _lib.ptr(values), _lib.ptr(indices), _lib.ptr(uniform), float(temperature), R, k,
+              _lib.ptr(out), _lib.stream_of(values))
+    return out
+
+
 _ATTN_WS = {}
 
 

@@ -254,12 +254,15 @@ class HybridModel:
         cat = _C._buf(self.dcat, n, 2 * H)
         e = torch.index_select(self.embed, 0, tok.view(-1))
         ca = cat.view(n, 2, H)
-        ea, hb = torch.empty(n, H, dtype=torch.bfloat16, device=self.dev), torch.empty(n, H, dtype=torch.bfloat16,
-                                                                                        device=self.dev)
-        _C.rmsnorm(e, M["norm_e"], c.eps, out=ea)
-        _C.rmsnorm(h, M["norm_h"], c.eps, out=hb)
-        ca[:, 0].copy_(ea)
-        ca[:, 1].copy_(hb)
+        if n == 1:  # one row: the two halves of the concatenated row are contiguous outputs
+            _C.rmsnorm(e, M["norm_e"], c.eps, out=ca[0, 0].view(1, H))
+            _C.rmsnorm(h, M["norm_h"], c.eps, out=ca[0, 1].view(1, H))
+        else:
+            ea, hb = (torch.empty(n, H, dtype=torch.bfloat16, device=self.dev) for _ in range(2))
+            _C.rmsnorm(e, M["norm_e"], c.eps, out=ea)
+            _C.rmsnorm(h, M["norm_h"], c.eps, out=hb)
+            ca[:, 0].copy_(ea)
+            ca[:, 1].copy_(hb)
         x = _C._buf(self.dx, n, H)
         xn = _C._buf(self.dxn, n, H)
         _C.bf16_linear(cat, M["fc"], out=x)
@@ -282,9 +285,12 @@ class HybridModel:
         gu = _C._buf(self.dgu, n, 2 * c.inter)
         _C.bf16_linear(xn, M["gu"], out=gu)
         act = _C._buf(self.dact, n, c.inter)
-        g_, u_ = _C._buf(self.dg, n, c.inter), _C._buf(self.du, n, c.inter)
-        g_.copy_(gu[:, :c.inter])
-        u_.copy_(gu[:, c.inter:])
+        if n == 1:  # one row: the gate and up halves are contiguous as they lie
+            g_, u_ = gu[0, :c.inter], gu[0, c.inter:]
+        else:
+            g_, u_ = _C._buf(self.dg, n, c.inter), _C._buf(self.du, n, c.inter)
+            g_.copy_(gu[:, :c.inter])
+            u_.copy_(gu[:, c.inter:])
         _C.silu_mul(g_, u_, self.silu, out=act)
         _C.bf16_linear(act, M["d"], residual=x1, out=_C._buf(self.dh, n, H))
 
@@ -321,9 +327,7 @@ class HybridModel:
             self.toks.copy_(idx[:, :1].reshape(1, R))
         else:
             # Gumbel-max over the top-k: a sample of softmax(vals / T) restricted to the top k
-            g = -torch.log(-torch.log(torch.rand(R, c.top_k, device=self.dev).clamp_(1e-20, 1.0)))
-            pick = torch.argmax(vals / c.temperature + g, dim=1, keepdim=True)
-            self.toks.copy_(torch.gather(idx, 1, pick).view(1, R))
+            _C.topk_sample(vals, idx, torch.rand(R, c.top_k, device=self.dev), c.temperature, out=self.toks.view(R))
         _C.mtp_accept(self.st, self.toks, self.vtok, None, T["children"], R, T["depth"], self.x, self.nt,
                       self.hbuf.view(1, 1, -1), self.ctl, self.kv_ptrs, c.kv_heads, c.cap, c.head_dim, self.result)
 

@@ -204,6 +204,15 @@ int mdx_fast_pick(const uint16_t* x, int64_t V, int64_t k, uint16_t* values, int
 int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
                   int64_t* indices, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Gumbel-max sampling over each row's top k: out[r] = indices[r, j*], j* the first maximum over j of
+ * values[r, j] * (1 / temperature) - log(-log(clamp(uniform[r, j], 1e-20, 1))), in fp32 (each
+ * operation rounded as torch's elementwise kernels round it). values f32 / indices int64 / uniform f32
+ * [rows, k] (topk_rows' outputs and torch.rand), out int64 [rows], k <= 64. No counterpart in the
+ * reference's _C: the decode loop's sampling arithmetic over topk_rows (comfy_mono_decode_xpu/
+ * sampling.py, upstream torch ops), fused into one launch. */
+int mdx_topk_sample(const float* values, const int64_t* indices, const float* uniform, float temperature, int64_t rows,
+                    int64_t k, int64_t* out, void* stream);
+
 /* Bytes of device workspace mdx_attn_decode needs for H query heads, Hk kv heads, S rows, head_dim D
  * and cache capacity cap. Zero it once when allocated: every launch leaves its counters at zero. */
 size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint);

@@ -120,3 +120,25 @@ def test_topk_repeated_launches_reuse_workspace(C, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert np.array_equal(gi.cpu().numpy(), wi), rep
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_topk_sample_matches_torch_expression(C, dev, temperature):
+    """The fused Gumbel-max pick equals the decode loop's torch expression on the same uniforms
+    (fp32 roundings of the same operations; ties to the first position, as torch.argmax), with the
+    clamp's edges among the uniforms."""
+    g = torch.Generator(device=dev).manual_seed(int(temperature * 100))
+    for R, k in ((8, 20), (1, 1), (16, 64), (3, 7)):
+        print(f"case topk_sample R={R} k={k} T={temperature}", flush=True)
+        vals = (torch.randn(R, k, generator=g, device=dev) * 3).sort(dim=1, descending=True).values
+        vals[:, k // 2:] = vals[:, k // 2:].round()  # ties among the scores' first terms
+        idx = torch.randint(0, 151936, (R, k), generator=g, device=dev)
+        u = torch.rand(R, k, generator=g, device=dev)
+        u[0, 0] = 0.0
+        if k > 2:
+            u[0, 1], u[0, 2] = 1e-30, 0.99999994
+        got = C.topk_sample(vals, idx, u, temperature)
+        gum = -torch.log(-torch.log(u.clone().clamp_(1e-20, 1.0)))
+        pick = torch.argmax(vals / temperature + gum, dim=1, keepdim=True)
+        want = torch.gather(idx, 1, pick).view(R)
+        assert torch.equal(got, want), (got, want)

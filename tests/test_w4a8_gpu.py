@@ -179,7 +179,7 @@ def test_mono_mlp_matches_oracle(C, dev, fmt, tiled, rot):
     h = layout.regular_hadamard() if rot == "h256" else torch.eye(256).to(torch.bfloat16)
     lut = layout.silu_lut()
     d = _oracle_dicts(ws)
-    for M in (1, 3, 8, 16):
+    for M in (1, 2, 3, 8, 16):  # without rotation 1 and 2 rows take the in-prologue quantisations
         print(f"case mlp fmt={fmt} tiled={tiled} rot={rot} M={M}", flush=True)
         xn = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         out = C.mono_mlp(xn.to(dev), h.to(dev), lut.to(dev), *args, 0, 4, tiled)
