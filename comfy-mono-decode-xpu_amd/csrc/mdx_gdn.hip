@@ -209,15 +209,17 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
 }
 
 // The delta rule of value head h over the columns [32 cs, 32 cs + 32) of its state (four work-groups
-// per head: the columns are independent). Thread (row group rg, column col) holds state rows
-// 16 rg .. 16 rg + 15 of its column in registers. Outputs: the raw bf16 rows of the verify entries (the
-// gated RMSNorm, which needs the whole head, is applied by whoever reads them); rows of this step that
-// no verify entry writes are zeros.
+// per head: the columns are independent). Wave w owns columns 8 w .. 8 w + 7; lane l holds state rows
+// 16 rg .. 16 rg + 15 (rg = l / 8) of column 8 w + l % 8 in registers, so a column's 8 row groups are
+// 8 lanes of one wave: the k.S and q.S sums over the rows finish with three xor shuffles (strides 8,
+// 16, 32) and the waves run their entries without barriers. Outputs: the raw bf16 rows of the verify
+// entries (the gated RMSNorm, which needs the whole head, is applied by whoever reads them); rows of
+// this step that no verify entry writes are zeros.
 constexpr int NSPLIT = 4, SC = DH / NSPLIT, HRG = 8, HRPG = DH / HRG, HT = HRG * SC;
 
 __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
-    __shared__ float vvec[2 * MAXS][SC], mbuf[2][HRG][SC], rbuf[2][HRG][SC], rawc[MAXS][SC];
+    __shared__ float vvec[2 * MAXS][SC], rawc[MAXS][SC];
     __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
     __shared__ int ectl[2 + 3 * MAXS];
     if (!ctl_ok(a)) return;
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     const int kh = h / (HV / HK);
     const int64_t C = a.C;
     // the state of this work-group's columns first (it does not depend on the control words)
-    const int col = t % SC, rg = t / SC;
+    const int col = (t / 64) * 8 + (lane & 7), rg = lane >> 3;
     float st[HRPG];
     float* rs = a.rec + (int64_t(h) * DH + rg * HRPG) * DH + cs * SC + col;
 #pragma unroll
@@ -329,7 +331,8 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
                 qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
             }
         }
-        // kv partial over the 16 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3))
+        // k.S over the 16 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3)); then the
+        // column's 8 row groups by xor shuffles (every lane of the column ends with the same sum)
         float m4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
@@ -341,11 +344,10 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
 #pragma unroll
             for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
         }
-        mbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
-        __syncthreads();  // the one barrier per entry (mbuf / rbuf alternate)
-        float kv = mbuf[e & 1][0][col];
-#pragma unroll
-        for (int g = 1; g < HRG; ++g) kv = __fadd_rn(kv, mbuf[e & 1][g][col]);
+        float kv = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
+        kv = __fadd_rn(kv, shfl_xor(kv, 8));
+        kv = __fadd_rn(kv, shfl_xor(kv, 16));
+        kv = __fadd_rn(kv, shfl_xor(kv, 32));
         const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
         float r4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
@@ -358,32 +360,24 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
 #pragma unroll
             for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
         }
-        if (verify) rbuf[e & 1][rg][col] = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
+        if (verify) {
+            float o = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
+            o = __fadd_rn(o, shfl_xor(o, 8));
+            o = __fadd_rn(o, shfl_xor(o, 16));
+            o = __fadd_rn(o, shfl_xor(o, 32));
+            if (rg == 0) rawc[slot_of(e)][col] = bfround(o);
+        }
         if (e == E0 - 1 && replayed)
 #pragma unroll
             for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
-        // the previous verify entry's output row (its partials are complete after this barrier)
-        if (e > E0 && rg == 0) {
-            const int pe = e - 1;
-            float o = rbuf[pe & 1][0][col];
-#pragma unroll
-            for (int g = 1; g < HRG; ++g) o = __fadd_rn(o, rbuf[pe & 1][g][col]);
-            rawc[slot_of(pe)][col] = bfround(o);
-        }
     }
     __syncthreads();
-    if (E1 > 0 && rg == 0) {
-        const int pe = E - 1;
-        float o = rbuf[pe & 1][0][col];
-#pragma unroll
-        for (int g = 1; g < HRG; ++g) o = __fadd_rn(o, rbuf[pe & 1][g][col]);
-        rawc[slot_of(pe)][col] = bfround(o);
-    }
     unsigned written = 0;
     for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
-    __syncthreads();
-    for (int ts = rg; ts < R; ts += HRG)
-        a.core[ts * HV * DH + h * DH + cs * SC + col] = ((written >> ts) & 1) ? f2bf(rawc[ts][col]) : uint16_t(0);
+    for (int i = t; i < R * SC; i += HT) {
+        const int ts = i / SC, c = i % SC;
+        a.core[ts * HV * DH + h * DH + cs * SC + c] = ((written >> ts) & 1) ? f2bf(rawc[ts][c]) : uint16_t(0);
+    }
 }
 
 }  // namespace
