@@ -158,8 +158,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
                 z[tt][i] = ok ? st[tt][i] * a.zscale : -INFINITY;
                 mx = fmaxf(mx, z[tt][i]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_x32(max_x16(mx));
         const float mnew = fmaxf(m, mx);
         const float alpha = (m == -INFINITY) ? 0.f : exp2f(m - mnew);
         float p[2][4], ps = 0.f;
@@ -170,8 +169,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
                 p[tt][i] = z[tt][i] == -INFINITY ? 0.f : bfround(exp2f(z[tt][i] - mnew));
                 ps += p[tt][i];
             }
-        ps += __shfl_xor(ps, 16, 64);
-        ps += __shfl_xor(ps, 32, 64);
+        ps = sum_x32(sum_x16(ps));
         l = l * alpha + ps;
         m = mnew;
 #pragma unroll

@@ -87,6 +87,39 @@ __device__ __forceinline__ T shfl_down(T v, int d) { return __shfl_down(v, d, 64
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int d) { return __shfl_xor(v, d, 64); }
 
+// Cross-lane partners without the LDS crossbar (gfx950): v_permlane32_swap exchanges the wave's two
+// halves, v_permlane16_swap rows 0 <-> 1 and 2 <-> 3, DPP row_ror:8 the halves of each row. Given v
+// twice, a swap returns (own, partner) in the lower lanes and (partner, own) in the upper ones; a sum
+// or maximum of the two is the same value either way (a + b and b + a are the same float), so each of
+// these equals v op (the value of lane l ^ D) in every lane, bit for bit.
+__device__ __forceinline__ float sum_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x8(float v) {
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float max_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int isum_x32(int v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(uint32_t(v), uint32_t(v), false, false);
+    return int(r[0] + r[1]);
+}
+__device__ __forceinline__ int isum_x16(int v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(uint32_t(v), uint32_t(v), false, false);
+    return int(r[0] + r[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, shfl_xor(v, d));
     return v;
@@ -100,11 +133,11 @@ __device__ __forceinline__ float row_shl(float v) {
 }
 
 // The halving-tree sum of the wave's 64 values in lane 0 (lane l adds lane l + s for s = 32, 16, ...,
-// 1, each sum rounded): the strides below 16 by DPP, 32 and 16 by cross-row shuffles. Only lane 0's
-// result is the tree's.
+// 1, each sum rounded): the strides below 16 by DPP, 32 and 16 by lane swaps. Only lane 0's result is
+// the tree's.
 __device__ __forceinline__ float tree_sum64(float q) {
-    q = __fadd_rn(q, shfl_down(q, 32));
-    q = __fadd_rn(q, shfl_down(q, 16));
+    q = sum_x32(q);
+    q = sum_x16(q);
     q = __fadd_rn(q, row_shl<8>(q));
     q = __fadd_rn(q, row_shl<4>(q));
     q = __fadd_rn(q, row_shl<2>(q));
@@ -114,8 +147,8 @@ __device__ __forceinline__ float tree_sum64(float q) {
 
 // The maximum of the wave's non-negative values, in every lane (lane 0's tree, broadcast).
 __device__ __forceinline__ float wave_max_nn(float v) {
-    v = fmaxf(v, shfl_down(v, 32));
-    v = fmaxf(v, shfl_down(v, 16));
+    v = max_x32(v);
+    v = max_x16(v);
     v = fmaxf(v, row_shl<8>(v));
     v = fmaxf(v, row_shl<4>(v));
     v = fmaxf(v, row_shl<2>(v));

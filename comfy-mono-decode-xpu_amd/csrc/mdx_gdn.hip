@@ -96,10 +96,8 @@ __device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter, int p) {
                     pb = fmaf(xe, __uint_as_float((bw[e >> 1] << sh) & m), pb);
                 }
             }
-            for (int off = 32; off >= 1; off >>= 1) {
-                pa = __fadd_rn(pa, shfl_down(pa, off));
-                pb = __fadd_rn(pb, shfl_down(pb, off));
-            }
+            pa = tree_sum64(pa);  // (lane 0's values are the ones used)
+            pb = tree_sum64(pb);
             const float avv = __fadd_rn(bfround(pa), a.dt_bias[h]);
             const float sp = avv > 20.f ? avv : log1pf(expf(avv));
             decay = expf(__fmul_rn(a.g_decay[h], sp));
@@ -203,7 +201,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     for (int ts = 0; ts < R; ++ts) {
         const float v0 = sq[ts][64 * wv + lane], v1 = sq[ts][64 * wv + 64 + lane];
         float part = fmaf(v1, v1, __fmul_rn(v0, v0));
-        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
+        part = tree_sum64(part);
         if (lane == 0) a.sums[((p * S + ts) * a.HK + kh) * 2 + which] = part;
     }
 }
@@ -211,7 +209,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
 // The delta rule of value head h over the columns [32 cs, 32 cs + 32) of its state (four work-groups
 // per head: the columns are independent). Wave w owns columns 8 w .. 8 w + 7; lane l holds state rows
 // 16 rg .. 16 rg + 15 (rg = l / 8) of column 8 w + l % 8 in registers, so a column's 8 row groups are
-// 8 lanes of one wave: the k.S and q.S sums over the rows finish with three xor shuffles (strides 8,
+// 8 lanes of one wave: the k.S and q.S sums over the rows finish with three xor exchanges (strides 8,
 // 16, 32) and the waves run their entries without barriers. Outputs: the raw bf16 rows of the verify
 // entries (the gated RMSNorm, which needs the whole head, is applied by whoever reads them); rows of
 // this step that no verify entry writes are zeros.
@@ -332,7 +330,8 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             }
         }
         // k.S over the 16 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3)); then the
-        // column's 8 row groups by xor shuffles (every lane of the column ends with the same sum)
+        // column's 8 row groups by xor exchanges, DPP and lane swaps (every lane of the column ends with
+        // the same sum)
         float m4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
@@ -345,9 +344,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
         }
         float kv = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
-        kv = __fadd_rn(kv, shfl_xor(kv, 8));
-        kv = __fadd_rn(kv, shfl_xor(kv, 16));
-        kv = __fadd_rn(kv, shfl_xor(kv, 32));
+        kv = sum_x32(sum_x16(sum_x8(kv)));
         const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
         float r4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
@@ -362,9 +359,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
         }
         if (verify) {
             float o = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
-            o = __fadd_rn(o, shfl_xor(o, 8));
-            o = __fadd_rn(o, shfl_xor(o, 16));
-            o = __fadd_rn(o, shfl_xor(o, 32));
+            o = sum_x32(sum_x16(sum_x8(o)));
             if (rg == 0) rawc[slot_of(e)][col] = bfround(o);
         }
         if (e == E0 - 1 && replayed)

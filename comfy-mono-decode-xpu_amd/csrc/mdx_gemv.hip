@@ -225,12 +225,16 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             float q = __fmul_rn(v[gi][0], v[gi][0]);
 #pragma unroll
             for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-            q = __fadd_rn(q, shfl_down(q, 16));
+            q = sum_x16(q);
             q = __fadd_rn(q, row_shl<8>(q));
             q = __fadd_rn(q, row_shl<4>(q));
             q = __fadd_rn(q, row_shl<2>(q));
             q = __fadd_rn(q, row_shl<1>(q));
-            q = __shfl(q, lane & 32, 64);
+            {
+                const float q0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 0));
+                const float q32 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 32));
+                q = (lane & 32) ? q32 : q0;
+            }
             const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(q, 128.f), a.heps)));
             float zf[4];
             unpack4(graw[gi], zf);
@@ -789,12 +793,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         prm = a.xs[lane - 16];
     }
     // SRC_HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the maxima entries (thread t:
-    // entries t, t + threads, ... of both rows) are one-shot operands too; SRC_XP: the row's 4 elements
-    // per lane of groups wave, wave + waves, ... and their norm weights
+    // entries t, t + threads, ... of both rows) are one-shot operands too
     constexpr int HRP = HR ? 16 : 1;
     uint4 hraw[HRP];
     float hmx[2] = {0.f, 0.f};
-    uint2 xpx[XP ? XP_GPW : 1], xpw[XP ? XP_GPW : 1];
     const int nwv = a.TPW * a.KS;
     if (HR) {
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
@@ -809,17 +811,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             for (int r = 0; r < 2; ++r)
                 if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[w * 16 + r]));
     }
+    // SRC_XP: the bf16 row and its norm weights land in LDS by DMA with the other one-shot operands,
+    // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
+    // round of weights); the prep runs from LDS while that round streams in
+    uint8_t* xs_l = zeros + 32;  // SRC_XP: [K] bf16 row, then [K] bf16 norm weights
     if (XP) {
-        const int G = K / 256;
-#pragma unroll
-        for (int gi = 0; gi < XP_GPW; ++gi) {
-            const int g = min(wave + nwv * gi, G - 1);
-            xpx[gi] = *reinterpret_cast<const uint2*>(a.xp_x + 256 * g + 4 * lane);
-            xpw[gi] = a.xp_nw ? *reinterpret_cast<const uint2*>(a.xp_nw + 256 * g + 4 * lane) : make_uint2(0u, 0u);
-        }
-        // the row before the weight ring: requested behind the ring, it would queue behind the
-        // whole chip's first round of weights; its prep then runs while that round streams in
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
+        dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_x)), 0, 2 * K, 1, xs_l, nthr);
+        if (a.xp_nw) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_nw)), 0, 2 * K, 1, xs_l + 2 * K, nthr);
     }
 
     float cb[16];
@@ -910,8 +908,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __syncthreads();
     } else {
         // the one-shot loads (issued before the ring) are complete once at most RING loads remain
-        static_assert(RING <= 15, "vmcnt field");
-        __builtin_amdgcn_s_waitcnt(RING | (7 << 4) | (15 << 8));  // vmcnt(RING), expcnt / lgkmcnt not waited
+        static_assert(RING <= 63, "vmcnt field");  // vmcnt: bits 3:0 and 15:14
+        __builtin_amdgcn_s_waitcnt((RING & 15) | ((RING >> 4) << 14) | (7 << 4) | (15 << 8));  // vmcnt(RING) only
         __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
         __builtin_amdgcn_s_barrier();
     }
@@ -963,9 +961,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // waits so that the ring stays in flight; the reduction block holds the group sums / maxima
         const int G = K / 256;
         float* gsum = reinterpret_cast<float*>(red);  // [G] group sums, then [waves] maxima
+        // lane l of wave w: elements 4 l .. 4 l + 3 of the groups w, w + waves, ...
         float v[XP_GPW][4];
 #pragma unroll
-        for (int gi = 0; gi < XP_GPW; ++gi) unpack4(xpx[gi], v[gi]);
+        for (int gi = 0; gi < XP_GPW; ++gi)
+            unpack4(reinterpret_cast<const uint2*>(xs_l)[64 * min(wave + nwv * gi, G - 1) + lane], v[gi]);
         if (a.xp_nw) {
 #pragma unroll
             for (int gi = 0; gi < XP_GPW; ++gi) {
@@ -978,13 +978,15 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
-            float ss = gsum[0];
-            for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, gsum[g]);
+            // the group sums in group order (one LDS read per lane, then lane by lane)
+            const float gv = lane < G ? gsum[lane] : 0.f;
+            float ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gv)));
+            for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), g)));
             const float rr = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, float(K)), a.xp_eps)));
 #pragma unroll
             for (int gi = 0; gi < XP_GPW; ++gi) {
                 float wv[4];
-                unpack4(xpw[gi], wv);
+                unpack4(reinterpret_cast<const uint2*>(xs_l + 2 * K)[64 * min(wave + nwv * gi, G - 1) + lane], wv);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], rr), wv[e]));
             }
@@ -999,8 +1001,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         if (lane == 0) gsum[G + wave] = m;
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
-        float rm = gsum[G];
-        for (int w = 1; w < nwv; ++w) rm = fmaxf(rm, gsum[G + w]);
+        const float rm = wave_max_nn(lane < nwv ? gsum[G + lane] : 0.f);
         const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
         if (t == 0) prml[a.TPW * 16] = s;
         uint16_t sb = f2bf(s);
@@ -1148,10 +1149,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // fold the four k quarters of each column (lanes c, c + 16, c + 32, c + 48)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            int v = tot[r];
-            v += shfl_xor(v, 16);
-            v += shfl_xor(v, 32);
-            tot[r] = v;
+            tot[r] = isum_x32(isum_x16(tot[r]));
         }
         if (lane < 16)
 #pragma unroll
@@ -1226,7 +1224,8 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     const size_t seg = size_t(g1 - g0) * esz;
     size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
-    return s + 128 * 4 + 16 + 32;  // parameters, flag, zeros
+    s += 128 * 4 + 16 + 32;  // parameters, flag, zeros
+    return a.xp_x ? s + size_t(4) * a.K : s;  // SRC_XP: the bf16 row and its norm weights
 }
 
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mfma, esz, 0, a.K / CHUNK_K); }
@@ -1856,7 +1855,8 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     const char* fz = getenv("MDX_MLP_FUSED");
     // one row: the gate/up GEMV prepares x itself (no row prep launch); MDX_MLP_HPREP=1 keeps both
     // prep launches
-    const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && !(fz && atoi(fz) != 0);
+    const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && !(fz && atoi(fz) != 0) && aligned(xn, 16) &&
+                    (!norm_w || aligned(norm_w, 16));  // (the row and its weights are DMA'd in 16-byte pieces)
     if (!xp) {
         PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
         if ((rc = launch_prep(pa, rows, st))) return rc;

@@ -72,8 +72,7 @@ __global__ __launch_bounds__(WAVE) void rope_kv_kernel(RopeArgs a) {
 #pragma unroll
         for (int j = 0; j < MAX_D / WAVE; ++j)
             if (j < per) part = j == 0 ? __fmul_rn(x[0], x[0]) : __fadd_rn(part, __fmul_rn(x[j], x[j]));
-        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, shfl_down(part, off));
-        const float ss = __shfl(part, 0, WAVE);
+        const float ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tree_sum64(part))));
         const float r = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, float(D)), isq ? a.epsq : a.epsk)));
 #pragma unroll
         for (int j = 0; j < MAX_D / WAVE; ++j)
