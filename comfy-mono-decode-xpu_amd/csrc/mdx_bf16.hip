@@ -92,8 +92,17 @@ __global__ __launch_bounds__(1024) void bf16_linear_kernel(Bf16Args a) {
     *reinterpret_cast<f32x4*>(red + ((ts * a.KS + slice) * 64 + lane) * 4) = acc;
     __syncthreads();
     if (slice != 0 || !live || c >= a.rows) return;
+    // the slices' partials added in slice order; their reads four at a time (clamped, masked), so a
+    // round trip to LDS serves four slices
     f32x4 s = acc;
-    for (int k = 1; k < a.KS; ++k) s += *reinterpret_cast<const f32x4*>(red + ((ts * a.KS + k) * 64 + lane) * 4);
+    for (int k0 = 1; k0 < a.KS; k0 += 4) {
+        f32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = *reinterpret_cast<const f32x4*>(red + ((ts * a.KS + min(k0 + j, a.KS - 1)) * 64 + lane) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (k0 + j < a.KS) s += v[j];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t o = int64_t(c) * a.N + tile * 16 + 4 * g + i;

@@ -257,8 +257,10 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             if (lane == 0 && g < G) gsum[g] = q;
         }
         __syncthreads();
-        float ss = gsum[0];
-        for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, gsum[g]);
+        // the group sums in group order (G <= 64: one LDS read per lane, then lane by lane)
+        const float gv = lane < G ? gsum[lane] : 0.f;
+        float ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gv)));
+        for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), g)));
         const float mean = __fdiv_rn(ss, float(K));
         const float r = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(mean, a.eps)));
 #pragma unroll
@@ -319,8 +321,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     m = wave_max_nn(m);
     if (lane == 0) wmax[w] = m;
     __syncthreads();
-    float rm = wmax[0];
-    for (int i = 1; i < W; ++i) rm = fmaxf(rm, wmax[i]);
+    const float rm = wave_max_nn(lane < W ? wmax[lane] : 0.f);
     const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
     if (threadIdx.x == 0) {
         if (COH) st_c(reinterpret_cast<uint32_t*>(a.scale) + row, __float_as_uint(s));
@@ -567,10 +568,19 @@ __device__ __forceinline__ uint16_t silu_h(const GemvArgs& a, int32_t ag, int32_
 // red layout: [TPW][KS][16 columns][rows] (VALU) or [TPW][KS][64 lanes][4] (MFMA); sums the slices
 template <bool MFMA>
 __device__ __forceinline__ int32_t reduced(const GemvArgs& a, const int32_t* red, int ts, int r, int c) {
+    // the slices' partials four at a time (reads clamped to the last slice, masked; int32 sums are
+    // associative, so any order gives the same bits): one LDS round trip per four slices
     uint32_t s = 0;
-    for (int k = 0; k < a.KS; ++k) {
-        if (MFMA) s += uint32_t(red[((ts * a.KS + k) * 64 + (r >> 2) * 16 + c) * 4 + (r & 3)]);
-        else s += uint32_t(red[((ts * a.KS + k) * 16 + c) * a.rows + r]);
+    for (int k0 = 0; k0 < a.KS; k0 += 4) {
+        uint32_t v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = min(k0 + j, a.KS - 1);
+            v[j] = MFMA ? uint32_t(red[((ts * a.KS + k) * 64 + (r >> 2) * 16 + c) * 4 + (r & 3)])
+                        : uint32_t(red[((ts * a.KS + k) * 16 + c) * a.rows + r]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += k0 + j < a.KS ? v[j] : 0u;
     }
     return int32_t(s);
 }
@@ -917,8 +927,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // the rows' scales (the row prep's formula), then the rows quantised into LDS while the ring
         // stays in flight: v / sb as fp32(fp64(v) * (1 / fp64(sb))), exact for bf16 v and sb (see the
         // staging of a wait unit above)
-        double* rcp = reinterpret_cast<double*>(prml + 96);  // [rows]
-        float* wm = reinterpret_cast<float*>(red);           // [2][16 waves] (the reduction block is free here)
+        float* wm = reinterpret_cast<float*>(red);  // [2][16 waves] (the reduction block is free here)
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const float m = wave_max_nn(hmx[r]);
@@ -926,24 +935,25 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
-        if (t < a.rows) {
-            float m = wm[t * 16];
-            for (int w = 1; w < nwv; ++w) m = fmaxf(m, wm[t * 16 + w]);
+        // every wave takes the rows' maxima over the waves itself (no second hand-off); the first
+        // stores the scales for the epilogue
+        double rcp[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const float m = wave_max_nn(lane < nwv ? wm[r * 16 + lane] : 0.f);
             const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
             uint16_t sb = f2bf(s);
             if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-            prml[a.TPW * 16 + t] = s;
-            rcp[t] = 1.0 / double(bf2f(sb));
+            if (t == 0 && r < a.rows) prml[a.TPW * 16 + r] = s;
+            rcp[r] = 1.0 / double(bf2f(sb));
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_s_barrier();
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
 #pragma unroll
         for (int k = 0; k < HRP; ++k) {
             const int i = k * nthr + t;
             if (i < total) {
                 const int r = i / per_row, j = i - r * per_row;
-                const double rr = rcp[r];
+                const double rr = r ? rcp[1] : rcp[0];
                 const uint32_t w[4] = {hraw[k].x, hraw[k].y, hraw[k].z, hraw[k].w};
                 uint32_t o[2] = {0u, 0u};
 #pragma unroll
