@@ -18,6 +18,7 @@
 //   4. the row's last work-group (device-scope counter, reset by that work-group) merges the nseg
 //      lists in two counting stages: each wave keeps the top k of a quarter of the lists, then the 4 k
 //      survivors are ranked among themselves.
+// The counting loops read LDS eight words per round trip (indices clamped, masked).
 // Ranks are never 0 (the radix key of a non-NaN value is nonzero, and a NaN's rank has a nonzero
 // gather word), so 0 marks an empty slot.
 #include <algorithm>
@@ -31,6 +32,7 @@ constexpr int TK_T = 256;
 constexpr int TK_MAXK = 64;
 constexpr int TK_MAXR = 16;
 constexpr int TK_MAXSEG = 64;
+constexpr int TK_E = 24;  // elements per thread held in registers per pass (segments of 6144 in one pass)
 
 enum Order : int {
     ORDER_BF16 = 0,    // torch XPU topk of one bf16 row: bf16 radix key, gather 1024 x 4 loads x 8
@@ -67,15 +69,21 @@ __device__ __forceinline__ uint32_t key_argmax(uint16_t b) {
     return (b & 0x8000u) ? 0x7FFFu - (b & 0x7FFFu) : 0x8000u + b;
 }
 
-template <int ORD>
-__device__ __forceinline__ uint64_t rank_of(const void* row, uint32_t i, bool f32) {
-    if (ORD == ORDER_BF16)
-        return (uint64_t(key_bf16(static_cast<const uint16_t*>(row)[i])) << 32) |
-               (0xFFFFFFFFu - gather_pos<4, 8>(i));
-    if (ORD == ORDER_ARGMAX)
-        return (uint64_t(key_argmax(static_cast<const uint16_t*>(row)[i])) << 32) | (0xFFFFFFFFu - i);
-    const uint32_t u = f32 ? static_cast<const uint32_t*>(row)[i] : uint32_t(static_cast<const uint16_t*>(row)[i]) << 16;
-    return (uint64_t(key_f32(u)) << 32) | (0xFFFFFFFFu - gather_pos<8, 4>(i));
+// the element's bits: bf16 (ORDER_BF16 / ORDER_ARGMAX), fp32 bits (ORDER_F32; a bf16 row widened).
+// XF32 (fp32 rows) is a template parameter: a load chosen at run time would sit under a branch and be
+// waited for at its join.
+template <int ORD, bool XF32>
+__device__ __forceinline__ uint32_t raw_of(const void* row, uint32_t i) {
+    if (ORD == ORDER_F32 && XF32) return static_cast<const uint32_t*>(row)[i];
+    return static_cast<const uint16_t*>(row)[i];
+}
+
+// the rank of element i from its loaded bits (raw_of)
+template <int ORD, bool XF32 = false>
+__device__ __forceinline__ uint64_t rank_raw(uint32_t u, uint32_t i) {
+    if (ORD == ORDER_BF16) return (uint64_t(key_bf16(uint16_t(u))) << 32) | (0xFFFFFFFFu - gather_pos<4, 8>(i));
+    if (ORD == ORDER_ARGMAX) return (uint64_t(key_argmax(uint16_t(u))) << 32) | (0xFFFFFFFFu - i);
+    return (uint64_t(key_f32(XF32 ? u : u << 16)) << 32) | (0xFFFFFFFFu - gather_pos<8, 4>(i));
 }
 
 template <int ORD>
@@ -107,7 +115,21 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-template <int ORD>
+
+// the number of entries of buf[b0, b1) above v, eight reads per LDS round trip
+__device__ __forceinline__ int count_above(const uint64_t* buf, int b0, int b1, uint64_t v) {
+    int n = 0;
+    for (int f0 = b0; f0 < b1; f0 += 8) {
+        uint64_t c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = buf[min(f0 + j, b1 - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) n += (f0 + j < b1 && c[j] > v) ? 1 : 0;
+    }
+    return n;
+}
+
+template <int ORD, bool XF32>
 __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     extern __shared__ __align__(16) uint64_t sm[];
     uint64_t* tmax = sm;             // [256] thread maxima
@@ -124,14 +146,31 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     const int64_t end = int64_t(lo) + a.seg;
     const uint32_t hi = uint32_t(end < a.n ? end : a.n);
 
-    // 1. thread maxima (and the argmax rank for a pick)
+    // 1. thread maxima (and the argmax rank for a pick). The thread's elements lo + t + 256 j are read
+    // TK_E at a time into registers, every load of a pass issued before the first use (addresses
+    // clamped into the segment, no branches around the loads): one memory round trip per pass, where
+    // a load per iteration would wait for each element in turn. A segment of at most TK_E * 256
+    // elements takes one pass and stays in registers for step 3.
+    const int nb = (a.seg + TK_T - 1) / TK_T, npass = (nb + TK_E - 1) / TK_E;  // (uniform)
+    uint32_t rv[TK_E];
+    auto load_pass = [&](int p) {
+#pragma unroll
+        for (int j = 0; j < TK_E; ++j) rv[j] = raw_of<ORD, XF32>(xr, min(lo + t + uint32_t(TK_T * (p * TK_E + j)), hi - 1));
+    };
     uint64_t mx = 0, am = 0;
-    for (uint32_t i = lo + t; i < hi; i += TK_T) {
-        const uint64_t r = rank_of<ORD>(xr, i, f32);
-        mx = r > mx ? r : mx;
-        if (a.pick) {
-            const uint64_t q = rank_of<ORDER_ARGMAX>(xr, i, false);
-            am = q > am ? q : am;
+    for (int p = 0; p < npass; ++p) {
+        load_pass(p);
+#pragma unroll
+        for (int j = 0; j < TK_E; ++j) {
+            const uint32_t i = lo + t + uint32_t(TK_T * (p * TK_E + j));
+            if (p * TK_E + j < nb && i < hi) {
+                const uint64_t r = rank_raw<ORD, XF32>(rv[j], i);
+                mx = r > mx ? r : mx;
+                if (a.pick) {
+                    const uint64_t q = rank_raw<ORDER_ARGMAX>(rv[j], i);
+                    am = q > am ? q : am;
+                }
+            }
         }
     }
     tmax[t] = mx;
@@ -154,17 +193,23 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     const uint64_t theta = theta_s;
     // 3. candidates >= theta, ranked by counting
     if (mx >= theta)
-        for (uint32_t i = lo + t; i < hi; i += TK_T) {
-            const uint64_t r = rank_of<ORD>(xr, i, f32);
-            if (r >= theta) cand[atomicAdd(&ncand, 1u)] = r;
+        for (int p = 0; p < npass; ++p) {
+            if (npass > 1) load_pass(p);  // (one pass: the registers still hold it)
+#pragma unroll
+            for (int j = 0; j < TK_E; ++j) {
+                const uint32_t i = lo + t + uint32_t(TK_T * (p * TK_E + j));
+                if (p * TK_E + j < nb && i < hi) {
+                    const uint64_t r = rank_raw<ORD, XF32>(rv[j], i);
+                    if (r >= theta) cand[atomicAdd(&ncand, 1u)] = r;
+                }
+            }
         }
     __syncthreads();
     const int nc = int(ncand);
     uint64_t* mylist = a.lists + (int64_t(row) * a.nseg + sg) * K;
     for (int j = t; j < nc; j += TK_T) {
         const uint64_t v = cand[j];
-        int pos = 0;
-        for (int q = 0; q < nc; ++q) pos += cand[q] > v;
+        const int pos = count_above(cand, 0, nc, v);
         if (pos < K) mylist[pos] = v;
     }
     for (int j = nc + t; j < K; j += TK_T) mylist[j] = 0;
@@ -199,8 +244,7 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
         __builtin_amdgcn_wave_barrier();
         for (int e = e0 + lane; e - lane < e1; e += 64) {
             const uint64_t v = e < e1 ? cand[e] : 0;
-            int above = 0;
-            for (int f = e0; f < e1; ++f) above += cand[f] > v;
+            const int above = count_above(cand, e0, e1, v);
             if (v != 0 && above < K) wtop[w * K + above] = v;
         }
     }
@@ -208,8 +252,7 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     for (int e = t; e < 4 * K; e += TK_T) {
         const uint64_t v = wtop[e];
         if (v == 0) continue;
-        int pos = 0;
-        for (int f = 0; f < 4 * K; ++f) pos += wtop[f] > v;
+        const int pos = count_above(wtop, 0, 4 * K, v);
         if (pos < K) {
             const uint32_t idx = index_of<ORD>(v);
             a.indices[int64_t(row) * K + pos] = idx;
@@ -279,11 +322,13 @@ int launch(const void* x, bool f32, int ord, int64_t rows, int64_t n, int64_t k,
     MDX_CHECK(lds <= 64 * 1024, "top-k LDS plan %zu bytes exceeds 64 KiB", lds);
     const dim3 grid(unsigned(rows * nseg)), block(TK_T);
     if (ord == ORDER_BF16)
-        hipLaunchKernelGGL(topk_kernel<ORDER_BF16>, grid, block, lds, stream, a);
+        hipLaunchKernelGGL((topk_kernel<ORDER_BF16, false>), grid, block, lds, stream, a);
     else if (ord == ORDER_ARGMAX)
-        hipLaunchKernelGGL(topk_kernel<ORDER_ARGMAX>, grid, block, lds, stream, a);
+        hipLaunchKernelGGL((topk_kernel<ORDER_ARGMAX, false>), grid, block, lds, stream, a);
+    else if (f32)
+        hipLaunchKernelGGL((topk_kernel<ORDER_F32, true>), grid, block, lds, stream, a);
     else
-        hipLaunchKernelGGL(topk_kernel<ORDER_F32>, grid, block, lds, stream, a);
+        hipLaunchKernelGGL((topk_kernel<ORDER_F32, false>), grid, block, lds, stream, a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
