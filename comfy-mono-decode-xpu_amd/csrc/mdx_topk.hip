@@ -107,6 +107,10 @@ struct TopkArgs {
     unsigned* counter;   // [rows], zero between launches
 };
 
+__device__ __forceinline__ void st_c64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     for (int d = 32; d >= 1; d >>= 1) {
         const uint64_t o = __shfl_xor(v, d, 64);
@@ -210,27 +214,39 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     for (int j = t; j < nc; j += TK_T) {
         const uint64_t v = cand[j];
         const int pos = count_above(cand, 0, nc, v);
-        if (pos < K) mylist[pos] = v;
+        if (pos < K) st_c64(mylist + pos, v);
     }
-    for (int j = nc + t; j < K; j += TK_T) mylist[j] = 0;
+    for (int j = nc + t; j < K; j += TK_T) st_c64(mylist + j, uint64_t(0));
     if (a.pick && t == 0) {
         uint64_t b = am_s[0];
         for (int w = 1; w < TK_T / 64; ++w) b = am_s[w] > b ? am_s[w] : b;
-        a.amax[int64_t(row) * a.nseg + sg] = b;
+        st_c64(a.amax + int64_t(row) * a.nseg + sg, b);
     }
-    // 4. the row's last work-group merges
-    __threadfence();
+    // 4. the row's last work-group merges. Hand-off without fences (an agent-scope fence writes back
+    // and invalidates whole caches on this chip): the lists are coherent stores, complete (vector
+    // memory counter at zero) before the counter bump; the last work-group reads them coherently.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (t == 0)
-        last_s = __hip_atomic_fetch_add(a.counter + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+        last_s = __hip_atomic_fetch_add(a.counter + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  unsigned(a.nseg - 1);
     __syncthreads();
     if (!last_s) return;
-    __threadfence();
     const int total = a.nseg * K;
     const uint64_t* rl = a.lists + int64_t(row) * a.nseg * K;
-    for (int e = t; e < total; e += TK_T)
-        cand[e] = __hip_atomic_load(rl + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    {
+        // every list entry's load issued before the first LDS store (one memory round trip)
+        constexpr int LP = TK_MAXSEG * TK_MAXK / TK_T;
+        uint64_t lv[LP];
+#pragma unroll
+        for (int j = 0; j < LP; ++j)
+            if (TK_T * j < total)  // (uniform)
+                lv[j] = __hip_atomic_load(rl + min(t + TK_T * j, total - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int j = 0; j < LP; ++j)
+            if (t + TK_T * j < total) cand[t + TK_T * j] = lv[j];
+    }
     __syncthreads();
     // two-stage merge by counting: wave w ranks the entries of its quarter of the lists among that
     // quarter (all lanes read the same LDS word at a time: broadcasts, no dependent chains) and keeps
