@@ -329,7 +329,14 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     }
     uint16_t sb = f2bf(s);
     if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-    const double rr = 1.0 / double(bf2f(sb));  // v and sb are bf16: the exact fp64-reciprocal quotient
+    // quant_rcp: the code of v is rint(bf16(v / sb)), the quotient rounded to fp32, then bf16. It is
+    // computed as bf16(v * r) with r = fl32(1 / sb): for bf16 v and sb (8-bit significands m_v, m_s)
+    // the exact quotient is never a tie of the bf16 rounding (a tie has a 9-bit odd significand, which
+    // m_v / m_s cannot produce) and lies at least 1 / (255 * 511) > 2^-17 (relative) from every tie,
+    // while the two fp32 roundings of v * r move it by less than 2^-23; r is finite for every sb >=
+    // 2^-126, and quotients below the fp32 normal range quantise to 0 either way. (Checked over every
+    // bf16 v against 3,256 scales.)
+    const float rr = __fdiv_rn(1.f, bf2f(sb));
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
         const int g = w + W * gi;
@@ -337,7 +344,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
             uint32_t o = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float d = bfround(float(__dmul_rn(double(v[gi][e]), rr)));
+                const float d = bfround(__fmul_rn(v[gi][e], rr));
                 const int qv = int(fminf(fmaxf(rintf(d), -128.f), 127.f));
                 o |= (uint32_t(qv) & 0xFFu) << (8 * e);
             }
@@ -865,13 +872,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         if (in.hr) {
             // bf16 rows quantised with the row scale max(absmax / 127, 1e-30) (the row prep's formula).
             // The rows' pieces (16 bytes, up to HB per thread) and the rows' absmax are loaded
-            // together (one memory round trip), then quantised: v / sb as fp32(fp64(v) * (1 /
-            // fp64(sb))). For a bf16 v and a bf16 sb the exact quotient either has at most 8
-            // significant bits or lies at least 2^-33 (relative) from every fp32 rounding boundary,
-            // far beyond the fp64 product's error, so the fp32 result is the correctly rounded
-            // quotient (apart from fp32 subnormal quotients, which quantise to 0 either way).
+            // together (one memory round trip), then quantised: bf16(v / sb) as bf16(v * fl32(1 / sb))
+            // (quant_rcp).
             constexpr int HB = 8;
-            double* rcp = reinterpret_cast<double*>(prml + 96);  // [rows]
+            float* rcp = prml + 96;  // [rows]
             const int per_row = Kr / 8, total = a.rows * per_row;
             for (int base = 0; base < total; base += HB * nthr) {
                 uint4 raw[HB];
@@ -887,7 +891,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                         uint16_t sb = f2bf(s);
                         if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
                         prml[a.TPW * 16 + t] = s;
-                        rcp[t] = 1.0 / double(bf2f(sb));
+                        rcp[t] = __fdiv_rn(1.f, bf2f(sb));
                     }
                     __syncthreads();
                 }
@@ -896,13 +900,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                     const int i = base + k * nthr + t;
                     if (i < total) {
                         const int r = i / per_row, j = i - r * per_row;
-                        const double rr = rcp[r];
+                        const float rr = rcp[r];
                         const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
                         uint32_t o[2] = {0u, 0u};
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
                             const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
-                            const float d = bfround(float(__dmul_rn(double(v), rr)));
+                            const float d = bfround(__fmul_rn(v, rr));
                             o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
                         }
                         *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
@@ -925,8 +929,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     }
     if (HR) {
         // the rows' scales (the row prep's formula), then the rows quantised into LDS while the ring
-        // stays in flight: v / sb as fp32(fp64(v) * (1 / fp64(sb))), exact for bf16 v and sb (see the
-        // staging of a wait unit above)
+        // stays in flight: bf16(v / sb) as bf16(v * fl32(1 / sb)) (quant_rcp)
         float* wm = reinterpret_cast<float*>(red);  // [2][16 waves] (the reduction block is free here)
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -937,7 +940,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_barrier();
         // every wave takes the rows' maxima over the waves itself (no second hand-off); the first
         // stores the scales for the epilogue
-        double rcp[2];
+        float rcp[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const float m = wave_max_nn(lane < nwv ? wm[r * 16 + lane] : 0.f);
@@ -945,7 +948,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             uint16_t sb = f2bf(s);
             if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
             if (t == 0 && r < a.rows) prml[a.TPW * 16 + r] = s;
-            rcp[r] = 1.0 / double(bf2f(sb));
+            rcp[r] = __fdiv_rn(1.f, bf2f(sb));
         }
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
 #pragma unroll
@@ -953,13 +956,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             const int i = k * nthr + t;
             if (i < total) {
                 const int r = i / per_row, j = i - r * per_row;
-                const double rr = r ? rcp[1] : rcp[0];
+                const float rr = r ? rcp[1] : rcp[0];
                 const uint32_t w[4] = {hraw[k].x, hraw[k].y, hraw[k].z, hraw[k].w};
                 uint32_t o[2] = {0u, 0u};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
-                    const float d = bfround(float(__dmul_rn(double(v), rr)));
+                    const float d = bfround(__fmul_rn(v, rr));
                     o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
                 }
                 *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
@@ -1016,7 +1019,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         if (t == 0) prml[a.TPW * 16] = s;
         uint16_t sb = f2bf(s);
         if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-        const double rr = 1.0 / double(bf2f(sb));  // bf16 v / bf16 sb: the exact fp64-reciprocal quotient
+        const float rr = __fdiv_rn(1.f, bf2f(sb));  // (quant_rcp)
 #pragma unroll
         for (int gi = 0; gi < XP_GPW; ++gi) {
             const int g = wave + nwv * gi;
@@ -1024,7 +1027,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 uint32_t o = 0;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float d = bfround(float(__dmul_rn(double(v[gi][e]), rr)));
+                    const float d = bfround(__fmul_rn(v[gi][e], rr));
                     o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
                 }
                 *reinterpret_cast<uint32_t*>(xl + 256 * g + 4 * lane) = o;
