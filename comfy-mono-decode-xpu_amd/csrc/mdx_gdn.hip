@@ -17,8 +17,8 @@
 //
 // Launches: gdn_conv_kernel (one thread per channel: owns its conv history; the q / k work-groups also
 // take their heads' sums of squares; extra work-groups, four per value head, compute the gates beside
-// them), then gdn_head_kernel (four work-groups of 256 per value head, 32 state columns each: thread
-// (row group rg, column col) holds state rows 16 rg .. 16 rg + 15 of its column in registers; raw bf16
+// them), then gdn_head_kernel (eight work-groups of 256 per value head, 16 state columns each: thread
+// (row group rg, column col) holds state rows 8 rg .. 8 rg + 7 of its column in registers; raw bf16
 // outputs), then the gated RMSNorm per head in place (the row-prep kernel's head-norm mode, which the
 // decode stack instead fuses into the output projection's activation prep: mdx_gdn_core_raw +
 // mdx_gnorm_rot_quant).
@@ -206,14 +206,20 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     }
 }
 
-// The delta rule of value head h over the columns [32 cs, 32 cs + 32) of its state (four work-groups
-// per head: the columns are independent). Wave w owns columns 8 w .. 8 w + 7; lane l holds state rows
-// 16 rg .. 16 rg + 15 (rg = l / 8) of column 8 w + l % 8 in registers, so a column's 8 row groups are
-// 8 lanes of one wave: the k.S and q.S sums over the rows finish with three xor exchanges (strides 8,
-// 16, 32) and the waves run their entries without barriers. Outputs: the raw bf16 rows of the verify
+// The delta rule of value head h over the columns [16 cs, 16 cs + 16) of its state (eight work-groups
+// per head, one per CU: the columns are independent, and a thread's serial work per entry is 8 rows).
+// Wave w owns columns 4 w .. 4 w + 3; lane l holds state rows 8 rg .. 8 rg + 7 (rg = l / 4) of column
+// 4 w + l % 4 in registers, so a column's 16 row groups are 16 lanes of one wave: the k.S and q.S sums
+// over the rows finish with four exchanges inside the wave and the waves run their entries without
+// barriers. Outputs: the raw bf16 rows of the verify
 // entries (the gated RMSNorm, which needs the whole head, is applied by whoever reads them); rows of
 // this step that no verify entry writes are zeros.
-constexpr int NSPLIT = 4, SC = DH / NSPLIT, HRG = 8, HRPG = DH / HRG, HT = HRG * SC;
+constexpr int NSPLIT = 8, SC = DH / NSPLIT, HRG = 16, HRPG = DH / HRG, HT = HRG * SC, VPE = SC / 8;
+
+// v + (the value of lane l + 4 of lane l's row of 16, cyclically): DPP row_ror:4
+__device__ __forceinline__ float sum_r4(float v) {
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
+}
 
 __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     const int kh = h / (HV / HK);
     const int64_t C = a.C;
     // the state of this work-group's columns first (it does not depend on the control words)
-    const int col = (t / 64) * 8 + (lane & 7), rg = lane >> 3;
+    const int col = (t / 64) * 4 + (lane & 3), rg = lane >> 2;
     float st[HRPG];
     float* rs = a.rec + (int64_t(h) * DH + rg * HRPG) * DH + cs * SC + col;
 #pragma unroll
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
     // raw inputs, every load issued before the first use: k (16 pieces of 8 per entry) and v (4 per
     // entry) of every entry, q (16 per entry) of the verify entries; the entries' gates and norms
-    constexpr int KP = 2 * MAXS * 16 / HT, VP = 2 * MAXS * 4;
+    constexpr int KP = 2 * MAXS * 16 / HT, VP = 2 * MAXS * VPE;
     uint4 kraw[KP], qraw = make_uint4(0u, 0u, 0u, 0u), vraw = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int j = 0; j < KP; ++j) kraw[j] = make_uint4(0u, 0u, 0u, 0u);
@@ -264,9 +270,9 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
         qraw = *reinterpret_cast<const uint4*>(a.qb + (p * S + slot_of(min(e, E - 1))) * C + kh * DH + (i % 16) * 8);
     }
     if (t < VP) {
-        const int i = min(t, E * 4 - 1), e = i / 4;
+        const int i = min(t, E * VPE - 1), e = i / VPE;
         const int ts = slot_of(e), par = e < E0 ? 1 - p : p;
-        vraw = *reinterpret_cast<const uint4*>(a.qb + (par * S + ts) * C + 2 * KD + h * DH + cs * SC + (i % 4) * 8);
+        vraw = *reinterpret_cast<const uint4*>(a.qb + (par * S + ts) * C + 2 * KD + h * DH + cs * SC + (i % VPE) * 8);
     }
     }
     if (t < E) {
@@ -302,8 +308,8 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             qvec[e - E0][d0 + q] =
                 __fmul_rn(__fmul_rn(__uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16)), a.qscale), qi);
     }
-    if (t < E * 4) {
-        const int e = t / 4, d0 = (t % 4) * 8;
+    if (t < E * VPE) {
+        const int e = t / VPE, d0 = (t % VPE) * 8;
         const uint32_t w[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -329,9 +335,10 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
                 qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
             }
         }
-        // k.S over the 16 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3)); then the
-        // column's 8 row groups by xor exchanges, DPP and lane swaps (every lane of the column ends with
-        // the same sum)
+        // k.S over the thread's 8 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3));
+        // then the column's 16 row groups (lanes of one residue mod 4): row_ror 8 and 4 inside each row
+        // of 16 lanes, then the lane swaps across rows; each step adds values that already agree in
+        // pairs, so every lane of the column ends with the same sum
         float m4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
 #pragma unroll
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
         }
         float kv = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
-        kv = sum_x32(sum_x16(sum_x8(kv)));
+        kv = sum_x32(sum_x16(sum_r4(sum_x8(kv))));
         const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
         float r4[4] = {0.f, 0.f, 0.f, 0.f};
         if (commit) {
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
         }
         if (verify) {
             float o = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
-            o = sum_x32(sum_x16(sum_x8(o)));
+            o = sum_x32(sum_x16(sum_r4(sum_x8(o))));
             if (rg == 0) rawc[slot_of(e)][col] = bfround(o);
         }
         if (e == E0 - 1 && replayed)
