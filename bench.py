@@ -42,11 +42,11 @@ def pmc_traffic(key):
 
 def gptq_weight(N, K, gen, dev, tiled=True):
     import torch
-    from mdx import layout
+    from mdx import _lib, layout
     q = torch.randint(-8, 8, (N, K), generator=gen, device=dev, dtype=torch.int8)
     s = (torch.rand(N, K // 128, generator=gen, device=dev) * 0.015 + 0.005).half()
     packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=True)
-    w = layout.W4(packed, s_rel, sch, None)
+    w = layout.W4(packed, s_rel, sch, None, decode=_lib.DECODE_INTEGRAL)  # integral scales by construction
     return w.tiled() if tiled else w
 
 

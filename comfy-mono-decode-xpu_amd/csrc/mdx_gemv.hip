@@ -21,7 +21,8 @@
 // Decode. Per-weight form: a 16-entry int8 table per (lane, scale) is built with the reference
 // formula w8 = clamp(rint(cb[c] * s), +-127) (NaN -> 0), and codes are mapped through it with
 // v_perm_b32 byte selects. Integral form, taken by a unit under MDX_DECODE_AUTO when the codebook
-// is c - 8 and every staged scale is an integer in [-15, 15]: then w8 = (c - 8) * s exactly; the
+// is c - 8 and every staged scale is an integer in [-15, 15] (checked in the prologue), and under
+// MDX_DECODE_INTEGRAL (asserted by the caller, no check): then w8 = (c - 8) * s exactly; the
 // codes become the int8 bytes 16 (c - 8), whose products give 16 sum_k x (c - 8) exactly, and an
 // arithmetic shift by 4 and the scale finish each group. Both forms give the same int32
 // accumulator (mod 2^32) as the reference.
@@ -401,6 +402,7 @@ struct GemvArgs {
     int rows;
     int KS, TPW;          // K slices per tile, tiles per work-group
     int force_exact;      // MDX_DECODE_EXACT: never take the integral form
+    int assume_int;       // MDX_DECODE_INTEGRAL (every matrix): the integral form without the check
     int epi;
     void* out[3];
     const void* res[3];
@@ -1035,18 +1037,29 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         }
     }
     // Whether every staged scale is an integer in [-15, 15]: then the unit takes the integral form
-    // throughout (both forms give the same int32 sums, so the choice is free).
-    if (can_int) {
-        bool bad = false;
-        for (int j = t; j < a.TPW * 16 * (seg / ESZ); j += nthr) {
-            const float s = rd_scale<SDT>(sl + j * ESZ);
-            bad = bad || !(s == rintf(s) && fabsf(s) <= 15.f);
+    // throughout (both forms give the same int32 sums, so the choice is free). Under
+    // MDX_DECODE_INTEGRAL the caller asserts it: no check, and no barrier unless this prologue wrote
+    // the activation rows to LDS itself (SRC_HR, SRC_XP).
+    bool integ;
+    if (a.assume_int && can_int) {
+        if (HR || XP) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
         }
-        if (bad) *mixed = 1;
+        integ = true;
+    } else {
+        if (can_int) {
+            bool bad = false;
+            for (int j = t; j < a.TPW * 16 * (seg / ESZ); j += nthr) {
+                const float s = rd_scale<SDT>(sl + j * ESZ);
+                bad = bad || !(s == rintf(s) && fabsf(s) <= 15.f);
+            }
+            if (bad) *mixed = 1;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done (the ring stays in flight)
+        __builtin_amdgcn_s_barrier();
+        integ = can_int && *mixed == 0;  // uniform over the unit
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done (the ring stays in flight)
-    __builtin_amdgcn_s_barrier();
-    const bool integ = can_int && *mixed == 0;  // uniform over the unit
     // the tile-major layout keeps k 0..3 of a code word in its low nibbles and k 4..7 in its high
     // ones (natural activation order); the checkpoint layout interleaves them (even k low, odd k high)
     const bool split = a.layout == MDX_LAYOUT_TILE;
@@ -1295,7 +1308,8 @@ int check_w4(const mdx_w4* w, const char* what) {
     MDX_CHECK(w->s_dtype == MDX_DT_F32 || w->s_dtype == MDX_DT_F16 || w->s_dtype == MDX_DT_FP8E4M3,
               "%s: s_rel dtype must be f32, f16 or fp8 e4m3", what);
     MDX_CHECK(w->layout == MDX_LAYOUT_ROW || w->layout == MDX_LAYOUT_TILE, "%s: unknown layout", what);
-    MDX_CHECK(w->decode == MDX_DECODE_EXACT || w->decode == MDX_DECODE_AUTO, "%s: unknown decode mode", what);
+    MDX_CHECK(w->decode == MDX_DECODE_EXACT || w->decode == MDX_DECODE_AUTO || w->decode == MDX_DECODE_INTEGRAL,
+              "%s: unknown decode mode", what);
     MDX_CHECK(aligned(w->q, 16), "%s: codes must be 16-byte aligned", what);
     MDX_CHECK(w->n * w->k / 2 < (int64_t(1) << 31), "%s: weight larger than 2 GiB", what);
     return MDX_OK;
@@ -1340,6 +1354,8 @@ int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, con
     a.out_dt = out_dt;
     a.lut = lut;
     a.force_exact = w0.decode == MDX_DECODE_EXACT;
+    a.assume_int = 1;
+    for (int i = 0; i < nm; ++i) a.assume_int = a.assume_int && ws[i]->decode == MDX_DECODE_INTEGRAL;
     return MDX_OK;
 }
 

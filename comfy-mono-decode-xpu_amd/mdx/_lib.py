@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "libmdx.so")
 MDX_OK, MDX_EINVAL, MDX_EHIP = 0, 1, 2
 DT_F32, DT_F16, DT_FP8E4M3, DT_BF16 = 0, 1, 2, 3
 LAYOUT_ROW, LAYOUT_TILE = 0, 1
-DECODE_EXACT, DECODE_AUTO = 0, 1
+DECODE_EXACT, DECODE_AUTO, DECODE_INTEGRAL = 0, 1, 2
 ROT_NONE, ROT_H256, ROT_MATRIX = 0, 1, 2
 
 c_void_p, c_int32, c_int64, c_size_t = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t

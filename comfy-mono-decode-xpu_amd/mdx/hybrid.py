@@ -55,7 +55,7 @@ def _gptq(N, K, gen, dev):
     s = (torch.rand(N, K // 128, generator=gen, device=dev) * 0.015 + 0.005).half()
     packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=True)
     del q
-    return layout.W4(layout.tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE)
+    return layout.W4(layout.tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE, _lib.DECODE_INTEGRAL)
 
 
 def _norm(n, gen, dev, spread=0.02):

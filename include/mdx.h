@@ -40,6 +40,11 @@ extern "C" {
                               is an integer in [-15, 15], w8 = (code - 8) * s_rel exactly and the dot
                               is factorised per group; elsewhere the per-weight decode. The int32
                               accumulator is the same either way (mod 2^32). */
+#define MDX_DECODE_INTEGRAL 2 /* the caller asserts that the codebook is code - 8 (or NULL) and every
+                                 s_rel is an integer in [-15, 15] (the GPTQ packer's integral output):
+                                 the integral form throughout, without the per-launch check of the
+                                 staged scales. Scales outside the assertion give wrong sums, never a
+                                 fault. With group_size below 128 (MFMA rows) or 32, as AUTO. */
 
 /* rotation applied by rot_quant-style prologues */
 #define MDX_ROT_NONE 0    /* x_rot = x (the identity matrix) */

@@ -324,3 +324,33 @@ def test_mlp_fused_graph_replays(C, dev, monkeypatch):
             torch.cuda.synchronize()
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={M} replay {rep}"
         assert C.mlp_error(dev) == 0
+
+
+def test_integral_decode_mode_matches_oracle(C, dev):
+    """MDX_DECODE_INTEGRAL (the caller asserts integral scales; no per-launch check) gives the
+    oracle's bits, as MDX_DECODE_AUTO does: the MLP at 1, 2 and 8 rows (the row-prep, bf16-row and
+    int8-row sources) and a single linear at 1 and 8 rows."""
+    from mdx import _lib, layout
+    g = torch.Generator().manual_seed(61)
+    ws, _ = _mlp_weights(g, "gptq", dev, True)
+    handles = [layout.W4(layout.tile_major_codes(q).to(dev), s.to(dev), c.to(dev), None, _lib.LAYOUT_TILE,
+                         _lib.DECODE_INTEGRAL) for q, s, c, _, _ in ws]
+    lut = layout.silu_lut()
+    nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    d = _oracle_dicts(ws)
+    for M in (1, 2, 8):
+        print(f"case integral-mlp M={M}", flush=True)
+        x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        out = C.mono_mlp_w4(x.to(dev), _lib.ROT_NONE, None, lut.to(dev), *handles, norm_w=nw.to(dev), eps=1e-6)
+        want = ref.mono_mlp(ref.rmsnorm(bits(x), bits(nw), 1e-6), "none", None, bits(lut), *d)
+        assert_bits_equal(bits(out), want, f"M={M}")
+    w = random_w4(4096, 4096, g, "gptq")
+    h = layout.W4(layout.tile_major_codes(w[0]).to(dev), w[1].to(dev), w[2].to(dev), None, _lib.LAYOUT_TILE,
+                  _lib.DECODE_INTEGRAL)
+    for M in (1, 8):
+        print(f"case integral-linear M={M}", flush=True)
+        x = torch.randint(-127, 128, (M, 4096), generator=g, dtype=torch.int8)
+        xs = torch.rand(M, generator=g) * 0.01 + 1e-3
+        out = torch.empty(M, 4096, dtype=torch.bfloat16, device=dev)
+        C.stream_gemv(x.to(dev), xs.to(dev), [h], [out])
+        assert_bits_equal(bits(out), oracle_linear(x, xs, w), f"M={M}")
