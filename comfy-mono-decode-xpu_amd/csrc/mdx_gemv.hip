@@ -403,6 +403,7 @@ struct GemvArgs {
     int KS, TPW;          // K slices per tile, tiles per work-group
     int force_exact;      // MDX_DECODE_EXACT: never take the integral form
     int assume_int;       // MDX_DECODE_INTEGRAL (every matrix): the integral form without the check
+    int pwo;              // per-wave one-shots (one int8 row, G128, assume_int): no work-group barrier
     int epi;
     void* out[3];
     const void* res[3];
@@ -793,8 +794,28 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
     constexpr bool HR = SRC == SRC_HR, XP = SRC == SRC_XP;
     const bool own_x = !in.wait && SRC == SRC_Q8;  // int8 rows a.xq staged by this prologue
-    if (own_x) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
-    for (int tsi = 0; tsi < a.TPW; ++tsi) {
+    // Per-wave one-shots (a.pwo): each wave stages only what it reads, its slice's activation run
+    // (the TPW waves of a slice write the same bytes) and its tile's scales of its slice's groups
+    // into a region of its own, so no wave waits for another before its loop.
+    const bool pwo = a.pwo && SRC == SRC_Q8 && !MFMA && !in.wait;  // (uniform)
+    const int sbw = (ncu / a.KS) * ESZ;                               // pwo: scale bytes per tile row
+    uint8_t* swv = sl + wave * 16 * sbw;                              // pwo: [16][sbw]
+    if (pwo) {
+        const MDX_G uint8_t* xsrc = as_global(reinterpret_cast<const uint8_t*>(a.xq)) + c0 * CHUNK_K;
+        const int xp = nch * (CHUNK_K / 16);
+        for (int i0 = 0; i0 < xp; i0 += WAVE)
+            if (i0 + lane < xp)
+                __builtin_amdgcn_global_load_lds(xsrc + (i0 + lane) * 16, MDX_LDS(xl + (c0 - cu0) * CHUNK_K + i0 * 16), 16, 0, 0);
+        const int per = sbw / 16, sp = 16 * per;
+        const MDX_G uint8_t* ssrc = mat_s(a, mi) + size_t(live ? tile : 0) * 16 * ng * ESZ + c0 * ESZ;  // (G128: group = chunk)
+        for (int i0 = 0; i0 < sp; i0 += WAVE)
+            if (i0 + lane < sp) {
+                const int i = i0 + lane, r = i / per;
+                __builtin_amdgcn_global_load_lds(ssrc + size_t(r) * ng * ESZ + (i - r * per) * 16, MDX_LDS(swv + i0 * 16), 16, 0, 0);
+            }
+    }
+    if (own_x && !pwo) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
+    for (int tsi = 0; tsi < (pwo ? 0 : a.TPW); ++tsi) {
         int tl;
         const int mm = which_mat(a, wg * a.TPW + tsi, tl);
         const MDX_G uint8_t* sb = mat_s(a, mm);
@@ -922,6 +943,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     }
     if (in.wait) {
         __syncthreads();
+    } else if (pwo) {
+        // this wave's one-shots are complete once at most RING loads remain; no other wave's matter
+        __builtin_amdgcn_s_waitcnt((RING & 15) | ((RING >> 4) << 14) | (7 << 4) | (15 << 8));
     } else {
         // the one-shot loads (issued before the ring) are complete once at most RING loads remain
         static_assert(RING <= 63, "vmcnt field");  // vmcnt: bits 3:0 and 15:14
@@ -1041,7 +1065,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // MDX_DECODE_INTEGRAL the caller asserts it: no check, and no barrier unless this prologue wrote
     // the activation rows to LDS itself (SRC_HR, SRC_XP).
     bool integ;
-    if (a.assume_int && can_int) {
+    if (pwo) {
+        integ = true;  // (pwo implies assume_int with the default codebook and G128)
+    } else if (a.assume_int && can_int) {
         if (HR || XP) {
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
@@ -1063,7 +1089,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // the tile-major layout keeps k 0..3 of a code word in its low nibbles and k 4..7 in its high
     // ones (natural activation order); the checkpoint layout interleaves them (even k low, odd k high)
     const bool split = a.layout == MDX_LAYOUT_TILE;
-    const uint8_t* scol = sl + (ts * 16 + c) * seg - g0 * ESZ;
+    const uint8_t* scol = pwo ? swv + c * sbw - c0 * ESZ : sl + (ts * 16 + c) * seg - g0 * ESZ;
 
     if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
@@ -1354,6 +1380,7 @@ int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, con
     a.out_dt = out_dt;
     a.lut = lut;
     a.force_exact = w0.decode == MDX_DECODE_EXACT;
+    a.pwo = 0;
     a.assume_int = 1;
     for (int i = 0; i < nm; ++i) a.assume_int = a.assume_int && ws[i]->decode == MDX_DECODE_INTEGRAL;
     return MDX_OK;
@@ -1456,6 +1483,12 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
+    // per-wave one-shots: one int8 row, caller-asserted integral scales with the default codebook,
+    // G128, 16-byte runs of scales per slice and per row (MDX_GEMV_PWO=0 turns them off)
+    const char* pe = getenv("MDX_GEMV_PWO");
+    const int NCk = a.K / CHUNK_K;
+    a.pwo = !mfma && rows == 1 && a.assume_int && !a.cb && !ex.hr && !ex.xp_x && a.lgG == 7 &&
+            (NCk / a.KS) * esz % 16 == 0 && (a.K >> 7) * esz % 16 == 0 && aligned(xq, 16) && !(pe && atoi(pe) == 0);
     return launch_gemv_d<4>(a, ws[0]->s_dtype, mfma, wgs, st);
 }
 
