@@ -797,15 +797,17 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // Per-wave one-shots (a.pwo): each wave stages only what it reads, its slice's activation run
     // (the TPW waves of a slice write the same bytes) and its tile's scales of its slice's groups
     // into a region of its own, so no wave waits for another before its loop.
-    const bool pwo = a.pwo && SRC == SRC_Q8 && !MFMA && !in.wait;  // (uniform)
+    const bool pwo = a.pwo && !MFMA && !in.wait;  // (uniform)
     const int sbw = (ncu / a.KS) * ESZ;                               // pwo: scale bytes per tile row
     uint8_t* swv = sl + wave * 16 * sbw;                              // pwo: [16][sbw]
-    if (pwo) {
+    if (pwo && SRC == SRC_Q8) {
         const MDX_G uint8_t* xsrc = as_global(reinterpret_cast<const uint8_t*>(a.xq)) + c0 * CHUNK_K;
         const int xp = nch * (CHUNK_K / 16);
         for (int i0 = 0; i0 < xp; i0 += WAVE)
             if (i0 + lane < xp)
                 __builtin_amdgcn_global_load_lds(xsrc + (i0 + lane) * 16, MDX_LDS(xl + (c0 - cu0) * CHUNK_K + i0 * 16), 16, 0, 0);
+    }
+    if (pwo) {
         const int per = sbw / 16, sp = 16 * per;
         const MDX_G uint8_t* ssrc = mat_s(a, mi) + size_t(live ? tile : 0) * 16 * ng * ESZ + c0 * ESZ;  // (G128: group = chunk)
         for (int i0 = 0; i0 < sp; i0 += WAVE)
@@ -855,7 +857,21 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
     // round of weights); the prep runs from LDS while that round streams in
     uint8_t* xs_l = zeros + 32;  // SRC_XP: [K] bf16 row, then [K] bf16 norm weights
-    if (XP) {
+    if (XP && pwo) {
+        // per wave: the 256-groups its prep reads (group g: 512 bytes of the row, 512 of the weights)
+        const int G = K / 256, nw4 = a.TPW * a.KS;
+#pragma unroll
+        for (int gi = 0; gi < XP_GPW; ++gi) {
+            const int g = wave + nw4 * gi;
+            if (g < G && lane < 32) {
+                __builtin_amdgcn_global_load_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_x)) + 512 * g + lane * 16,
+                                                 MDX_LDS(xs_l + 512 * g), 16, 0, 0);
+                if (a.xp_nw)
+                    __builtin_amdgcn_global_load_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_nw)) + 512 * g + lane * 16,
+                                                     MDX_LDS(xs_l + 2 * K + 512 * g), 16, 0, 0);
+            }
+        }
+    } else if (XP) {
         dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_x)), 0, 2 * K, 1, xs_l, nthr);
         if (a.xp_nw) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_nw)), 0, 2 * K, 1, xs_l + 2 * K, nthr);
     }
@@ -1066,6 +1082,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // the activation rows to LDS itself (SRC_HR, SRC_XP).
     bool integ;
     if (pwo) {
+        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
+        }
         integ = true;  // (pwo implies assume_int with the default codebook and G128)
     } else if (a.assume_int && can_int) {
         if (HR || XP) {
@@ -1487,7 +1507,7 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     // G128, 16-byte runs of scales per slice and per row (MDX_GEMV_PWO=0 turns them off)
     const char* pe = getenv("MDX_GEMV_PWO");
     const int NCk = a.K / CHUNK_K;
-    a.pwo = !mfma && rows == 1 && a.assume_int && !a.cb && !ex.hr && !ex.xp_x && a.lgG == 7 &&
+    a.pwo = !mfma && rows == 1 && a.assume_int && !a.cb && a.lgG == 7 &&
             (NCk / a.KS) * esz % 16 == 0 && (a.K >> 7) * esz % 16 == 0 && aligned(xq, 16) && !(pe && atoi(pe) == 0);
     return launch_gemv_d<4>(a, ws[0]->s_dtype, mfma, wgs, st);
 }
