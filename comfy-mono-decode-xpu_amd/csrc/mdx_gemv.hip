@@ -420,7 +420,7 @@ struct GemvArgs {
     // |h| maxima (fp32 bits) at hmax_out[wg * 16 + row]
     uint32_t* hmax_out;
     // SRC_HR units: the activation is hr (bf16 [rows, K]) quantised in the prologue with the row
-    // scale max(absmax / 127, 1e-30), absmax = the maximum of hmax[w * 16 + row] over w < hmax_n
+    // scale max(absmax / 127, 1e-30), absmax = the maximum of hmax[row * hmax_n + w] over w < hmax_n
     const uint16_t* hr;
     const uint32_t* hmax;
     int hmax_n;
@@ -435,7 +435,8 @@ struct GemvArgs {
 // Where a unit's activation comes from: int8 rows a.xq (DMA to LDS), bf16 rows quantised with
 // given maxima (SRC_HR), or one bf16 row prepared from scratch (SRC_XP).
 enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
-constexpr int XP_GPW = 4;  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
+constexpr int XP_GPW = 4;
+constexpr int HMW = 16;  // SRC_HR: maxima per lane when every wave reads them all (<= 1024 work-groups)  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
 
 // What a work unit waits for before it stages its activation, and where the activation comes from.
 // Data handed between work-groups of one launch is written with coherent (write-through) stores and
@@ -642,7 +643,7 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
                 m = fmaxf(m, __shfl_xor(m, 1, 8));
                 m = fmaxf(m, __shfl_xor(m, 2, 8));
                 m = fmaxf(m, __shfl_xor(m, 4, 8));
-                if ((rem & 7) == 0) a.hmax_out[wg * 16 + r] = __float_as_uint(m != m ? 0.f : m);
+                if ((rem & 7) == 0) a.hmax_out[r * gridDim.x + wg] = __float_as_uint(m != m ? 0.f : m);
             }
         }
         return;
@@ -848,10 +849,25 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             hraw[k] = make_uint4(0u, 0u, 0u, 0u);
             if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
         }
-        for (int w = t; w < a.hmax_n; w += nthr)
+        if (a.hmax_n <= WAVE * HMW) {
+            // every wave reads all the maxima itself (HMW per lane, contiguous per row, issued at
+            // once): the rows' maxima need no exchange between the waves
+            float hv[2][HMW];
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[w * 16 + r]));
+            for (int j = 0; j < HMW; ++j)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+                    hv[r][j] = __uint_as_float(a.hmax[min(r, a.rows - 1) * a.hmax_n + min(lane + WAVE * j, a.hmax_n - 1)]);
+#pragma unroll
+            for (int j = 0; j < HMW; ++j)
+#pragma unroll
+                for (int r = 0; r < 2; ++r) hmx[r] = fmaxf(hmx[r], hv[r][j]);
+        } else {
+            for (int w = t; w < a.hmax_n; w += nthr)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+                    if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[r * a.hmax_n + w]));
+        }
     }
     // SRC_XP: the bf16 row and its norm weights land in LDS by DMA with the other one-shot operands,
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
@@ -973,19 +989,22 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // the rows' scales (the row prep's formula), then the rows quantised into LDS while the ring
         // stays in flight: bf16(v / sb) as bf16(v * fl32(1 / sb)) (quant_rcp)
         float* wm = reinterpret_cast<float*>(red);  // [2][16 waves] (the reduction block is free here)
+        const bool whole = a.hmax_n <= WAVE * HMW;  // (uniform) each wave holds every maximum
+        if (!whole) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const float m = wave_max_nn(hmx[r]);
-            if (lane == 0) wm[r * 16 + wave] = m;
+            for (int r = 0; r < 2; ++r) {
+                const float m = wave_max_nn(hmx[r]);
+                if (lane == 0) wm[r * 16 + wave] = m;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_s_barrier();
         // every wave takes the rows' maxima over the waves itself (no second hand-off); the first
         // stores the scales for the epilogue
         float rcp[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const float m = wave_max_nn(lane < nwv ? wm[r * 16 + lane] : 0.f);
+            const float m = whole ? wave_max_nn(hmx[r]) : wave_max_nn(lane < nwv ? wm[r * 16 + lane] : 0.f);
             const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
             uint16_t sb = f2bf(s);
             if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
@@ -1798,7 +1817,7 @@ static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header
 
 struct MlpWs {
     uint32_t* flags;
-    uint32_t* hmax;  // [N1 / 16][16] the gate/up work-groups' |h| maxima
+    uint32_t* hmax;  // [rows <= 2][N1 / 16] the gate/up work-groups' |h| maxima, row-major
     uint32_t* sync;
     uint32_t* amax;
     uint32_t* tcnt;
