@@ -250,25 +250,33 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
     const bool has = tree ? (a.mask != nullptr) : (cslot < active);
     float* rec = a.part + (int64_t(kh * a.RT + rt) * (a.C + 1) + cslot) * (32 + 16 * D);
     if (has) {
-        for (int e = threadIdx.x; e < 16 * D; e += 64 * AT_WAVES) {
-            const int row = e / D, d = e % D;
+        // the rows' maxima and the waves' weights once per row (threads 0..15), then each output
+        // element is four products; the same arithmetic, in the same order, as per element
+        __shared__ float fw[16][AT_WAVES];
+        if (threadIdx.x < 16) {
+            const int row = threadIdx.x;
             float M = -INFINITY;
 #pragma unroll
             for (int v = 0; v < AT_WAVES; ++v) M = fmaxf(M, reinterpret_cast<const float*>(smem + v * WREG)[row]);
-            float o = 0.f, s = 0.f;
+            float s = 0.f;
 #pragma unroll
             for (int v = 0; v < AT_WAVES; ++v) {
                 const float* wv = reinterpret_cast<const float*>(smem + v * WREG);
                 const float mv = wv[row];
                 const float f = mv == -INFINITY ? 0.f : exp2f(mv - M);
-                o += wv[32 + row * D + d] * f;
+                fw[row][v] = f;
                 s += wv[16 + row] * f;
             }
+            rec[row] = M;
+            rec[16 + row] = s;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < 16 * D; e += 64 * AT_WAVES) {
+            const int row = e / D, d = e % D;
+            float o = 0.f;
+#pragma unroll
+            for (int v = 0; v < AT_WAVES; ++v) o += reinterpret_cast<const float*>(smem + v * WREG)[32 + row * D + d] * fw[row][v];
             rec[32 + e] = o;
-            if (d == 0) {
-                rec[row] = M;
-                rec[16 + row] = s;
-            }
         }
     }
 }
