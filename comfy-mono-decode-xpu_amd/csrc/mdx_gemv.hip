@@ -6,7 +6,8 @@
 //   mono_mlp            csrc/mono_mlp.sycl:109-167
 //
 // Scales are always the row-major [N, K/G] array (both layouts); a work-group stages its tiles'
-// scale rows in LDS once. Weight stream: a wave owns one 16-column tile and a K slice; its unit of
+// scale rows in LDS once (at one row with caller-asserted integral G128 scales, each wave stages its
+// own tile's groups of its own slice, and its own activation run, and waits for no other wave). Weight stream: a wave owns one 16-column tile and a K slice; its unit of
 // work is a "chunk", 16 columns x 128 k = 1 KiB of codes, fetched with ONE 16-byte load per lane
 // (lane l: column l % 16, quarter kq = l / 16 of the chunk, 32 consecutive k). In the tile-major
 // layout the 64 lanes' pieces are adjacent, so every chunk is one contiguous 1 KiB burst, and each
