@@ -286,7 +286,6 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     __shared__ float wgt[72], lsum[72];
-    __shared__ float Ms;
     const int row = blockIdx.x % 16, rt = (blockIdx.x / 16) % a.RT, kh = blockIdx.x / (16 * a.RT);
     const int r = rt * 16 + row;
     if (r >= a.rows) return;
@@ -298,19 +297,27 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     const int np = active + (use_tree ? 1 : 0);
     const float* base = a.part + int64_t(kh * a.RT + rt) * (a.C + 1) * (32 + 16 * D);
     auto slot = [&](int i) { return i < active ? i : a.C; };
-    const int t = threadIdx.x;
-    for (int i = t; i < np; i += D) {
-        wgt[i] = base[slot(i) * (32 + 16 * D) + row];
-        lsum[i] = base[slot(i) * (32 + 16 * D) + 16 + row];
+    const int t = threadIdx.x, lane = t % 64;
+    // every wave takes the partials' maximum itself (lane i: partials i and i + 64, np <= 65), then
+    // the weights go to LDS (both waves write the same values): one barrier
+    const float m0 = lane < np ? base[slot(lane) * (32 + 16 * D) + row] : -INFINITY;
+    const float m1 = lane + 64 < np ? base[slot(lane + 64) * (32 + 16 * D) + row] : -INFINITY;
+    float M = fmaxf(m0, m1);
+    M = max_x32(max_x16(M));
+    M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x128, 0xF, 0xF, false)));  // row_ror:8
+    M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x124, 0xF, 0xF, false)));  // row_ror:4
+    M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x122, 0xF, 0xF, false)));  // row_ror:2
+    M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x121, 0xF, 0xF, false)));  // row_ror:1
+    if (t < 64 || D <= 64) {
+        if (lane < np) {
+            wgt[lane] = m0 == -INFINITY ? 0.f : exp2f(m0 - M);
+            lsum[lane] = base[slot(lane) * (32 + 16 * D) + 16 + row];
+        }
+        if (lane + 64 < np) {
+            wgt[lane + 64] = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
+            lsum[lane + 64] = base[slot(lane + 64) * (32 + 16 * D) + 16 + row];
+        }
     }
-    __syncthreads();
-    if (t == 0) {
-        float M = -INFINITY;
-        for (int i = 0; i < np; ++i) M = fmaxf(M, wgt[i]);
-        Ms = M;
-    }
-    __syncthreads();
-    for (int i = t; i < np; i += D) wgt[i] = wgt[i] == -INFINITY ? 0.f : exp2f(wgt[i] - Ms);
     __syncthreads();
     float o = 0.f, s = 0.f;
 #pragma unroll 8
