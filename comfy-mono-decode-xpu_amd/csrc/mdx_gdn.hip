@@ -117,6 +117,7 @@ __device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter, int p) {
 // the channels' compute this step's gates (four per value head).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     __shared__ int sctl[2 + 3 * MAXS];
+    __shared__ uint32_t anct[MAXS];
     __shared__ uint16_t prl[MAXS][256];
     __shared__ float sq[MAXS][256];
     const int t = threadIdx.x;
@@ -142,9 +143,25 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     __syncthreads();
     const int S = a.slots, pending = sctl[0], p = sctl[1];
     if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // uniform
-    if (!cl) return;  // (only a last, partial work-group of v channels, which takes no sums)
     const int* acc = sctl + 2;
     const int* parent = sctl + 2 + S;
+    // the ancestry of row t (the same for every channel), walked once: byte d - 1 says where the tap
+    // at distance d reads, an earlier row of this step (0 .. R - 1) or history entry 16 + (CW - the
+    // number of taps so far that fell before this step)
+    if (t < R) {
+        int anc = t, miss = 0;
+        uint32_t code = 0;
+#pragma unroll
+        for (int d = 1; d <= CW; ++d) {
+            anc = anc >= 0 ? parent[anc] : -1;
+            anc = anc >= R ? -1 : anc;  // a parent is an earlier row of this step
+            miss += anc < 0;
+            code |= uint32_t(anc >= 0 ? anc : 16 + CW - miss) << (8 * (d - 1));
+        }
+        anct[t] = code;
+    }
+    __syncthreads();
+    if (!cl) return;  // (only a last, partial work-group of v channels, which takes no sums)
     uint16_t old[CW], prevacc[CW];
 #pragma unroll
     for (int r = 0; r < CW; ++r) {
@@ -166,21 +183,18 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < CW; ++r) a.conv_state[c * CW + r] = hist[r];
-    for (int ts = 0; ts < S; ++ts) {
+#pragma unroll
+    for (int ts = 0; ts < MAXS; ++ts) {
+        if (ts >= S) break;
         uint16_t out = 0;
         if (ts < R) {
-            int anc = ts, miss = 0;
-            float sum = 0.f;
+            const uint32_t code = anct[ts];
+            float sum = fmaf(bf2f(prl[ts][t]), w[CW], 0.f);
 #pragma unroll
-            for (int d = 0; d <= CW; ++d) {
-                if (d > 0) {
-                    anc = anc >= 0 ? parent[anc] : -1;
-                    anc = anc >= R ? -1 : anc;  // a parent is an earlier row of this step
-                    miss += anc < 0;
-                }
-                const int hm = CW - miss;
-                const uint16_t hv = hm == 0 ? hist[0] : (hm == 1 ? hist[1] : hist[2]);
-                const float v = anc >= 0 ? bf2f(prl[anc][t]) : bf2f(hv);
+            for (int d = 1; d <= CW; ++d) {
+                const int src = (code >> (8 * (d - 1))) & 0xFF;
+                const uint16_t hv = src == 16 ? hist[0] : (src == 17 ? hist[1] : hist[2]);
+                const float v = src < 16 ? bf2f(prl[src][t]) : bf2f(hv);
                 sum = fmaf(v, w[CW - d], sum);
             }
             const float y = bfround(sum);
