@@ -53,18 +53,17 @@ struct GdnArgs {
     int R, HK, HV, C, slots;
 };
 
-__device__ __forceinline__ bool ctl_ok(const GdnArgs& a) {
-    const int pending = a.ctl[0], p = a.ctl[1];
-    return p >= 0 && p <= 1 && pending >= 0 && pending <= a.slots;
-}
 
 // This step's gates of head h: one wave per row computes a = xn . wa[h] and b = xn . wb[h] (lane l
 // sums its elements in order, the 8-element blocks l + 64 j, then a halving tree over the lanes; both
 // rounded to bf16), then decay = exp(g_decay * softplus(a + dt_bias)) and beta = bf16(sigmoid(b)) into
 // gates[p][row][h]; rows R .. slots - 1 get zeros. The four work-groups of a head share its rows.
-__device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter, int p) {
+__device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int R = a.R, S = a.slots;
+    // the control words are checked at the stores only, so that their load overlaps the others
+    const int pending = a.ctl[0], p = a.ctl[1];
+    const bool ok = p >= 0 && p <= 1 && pending >= 0 && pending <= S;
     for (int ts = quarter * 4 + wv; ts < S; ts += 16) {
         float decay = 0.f, beta = 0.f;
         if (ts < R) {
@@ -103,7 +102,7 @@ __device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter, int p) {
             decay = expf(__fmul_rn(a.g_decay[h], sp));
             beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bfround(pb)))));
         }
-        if (lane == 0) {
+        if (lane == 0 && ok) {
             a.gates[((p * S + ts) * a.HV + h) * 2] = decay;
             a.gates[((p * S + ts) * a.HV + h) * 2 + 1] = beta;
         }
@@ -123,9 +122,8 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     const int t = threadIdx.x;
     const int nconv = (a.C + 255) / 256;
     if (int(blockIdx.x) >= nconv) {
-        if (!ctl_ok(a)) return;
         const int b = blockIdx.x - nconv;
-        gdn_gates_part(a, b / 4, b % 4, a.ctl[1]);
+        gdn_gates_part(a, b / 4, b % 4);
         return;
     }
     const int c = blockIdx.x * 256 + t;
@@ -240,7 +238,6 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ float vvec[2 * MAXS][SC], rawc[MAXS][SC];
     __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
     __shared__ int ectl[2 + 3 * MAXS];
-    if (!ctl_ok(a)) return;
     const int t = threadIdx.x, lane = t % 64, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
     const int kh = h / (HV / HK);
@@ -254,6 +251,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
     __syncthreads();
     const int pending = ectl[0], p = ectl[1];
+    if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // (uniform) invalid control words
     const int* acc = ectl + 2;
     const int* prog = ectl + 2 + 2 * S;
     // the entries: the leading valid accepted slots (replayed when all `pending` are valid), then the
