@@ -361,9 +361,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="mlp: skip the full-stack decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "bench.py measures one GPU only: the path would shard the stack's "
-                                   "layers and the lm_head columns across GPUs, which is not implemented "
-                                   "or measured here", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "bench.py measures one GPU only: the 9B stack scales as one "
+                                   "data-parallel replica per GPU (about 5 GB each); tensor-parallel "
+                                   "sharding of the GEMVs, heads and lm_head is not implemented or "
+                                   "measured here", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
