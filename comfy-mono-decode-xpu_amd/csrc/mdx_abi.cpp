@@ -16,4 +16,4 @@ void set_error(const char* fmt, ...) {
 }  // namespace mdx
 
 extern "C" const char* mdx_last_error(void) { return mdx::g_err; }
-extern "C" int mdx_version(void) { return 1; }
+extern "C" int mdx_version(void) { return 2; }

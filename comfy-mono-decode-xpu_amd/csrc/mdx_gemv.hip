@@ -41,6 +41,7 @@
 #include <stdlib.h>
 
 #include "mdx_common.hpp"
+#include "mdx_row.hpp"
 
 namespace mdx {
 namespace {
@@ -117,67 +118,6 @@ struct PrepArgs {
     float heps = 0.f;
 };
 
-__device__ __forceinline__ void unpack4(const uint2& v, float* f) {
-    f[0] = __uint_as_float(v.x << 16);
-    f[1] = __uint_as_float(v.x & 0xFFFF0000u);
-    f[2] = __uint_as_float(v.y << 16);
-    f[3] = __uint_as_float(v.y & 0xFFFF0000u);
-}
-
-__device__ __forceinline__ uint2 pack4(const float* f) {
-    return make_uint2(uint32_t(f2bf(f[0])) | (uint32_t(f2bf(f[1])) << 16),
-                      uint32_t(f2bf(f[2])) | (uint32_t(f2bf(f[3])) << 16));
-}
-
-// the value `v` of lane Q of this lane's quad (DPP quad_perm broadcast, both halves of the double)
-template <int Q>
-__device__ __forceinline__ double quad_lane(double v) {
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u)), Q * 0x55, 0xF, 0xF, false));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(u >> 32)), Q * 0x55, 0xF, 0xF, false));
-    return __builtin_bit_cast(double, uint64_t(lo) | (uint64_t(hi) << 32));
-}
-
-// output j of the radix-4 butterfly: the H4 row j applied to (a0, a1, a2, a3) left to right,
-// ((a0 + a1) + a2) - a3, ((a0 + a1) - a2) + a3, ((a0 - a1) + a2) + a3, ((a1 - a0) + a2) + a3: row j has
-// its one minus sign at position 3 - j (a - b and -b + a are the same IEEE operation)
-__device__ __forceinline__ double h4_out(const double* a, int j) {
-    double b[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) b[k] = (k == 3 - j) ? -a[k] : a[k];
-    return __dadd_rn(__dadd_rn(__dadd_rn(b[0], b[1]), b[2]), b[3]);
-}
-
-// fp64 fast Walsh-Hadamard transform of one 256-group held 4 elements per lane (lane l: elements
-// 4 l .. 4 l + 3): radix-4 stages along the base-4 digits of the element index (strides 1, 4, 16, 64).
-// Digit 0 is the lane's own slot, digit 1 the lane within its quad, digits 2 and 3 the quad within
-// the 16-lane row and the row; each lane computes its own output of every butterfly.
-__device__ __forceinline__ void fwht256_lane(double* d, int lane) {
-    double o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = h4_out(d, e);
-    const int j1 = lane & 3, j2 = (lane >> 2) & 3, j3 = lane >> 4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const double a[4] = {quad_lane<0>(o[e]), quad_lane<1>(o[e]), quad_lane<2>(o[e]), quad_lane<3>(o[e])};
-        d[e] = h4_out(a, j1);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        double a[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) a[k] = __shfl(d[e], (lane & ~12) | (k << 2), 64);
-        o[e] = h4_out(a, j2);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        double a[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) a[k] = __shfl(o[e], (lane & 15) | (k << 4), 64);
-        d[e] = h4_out(a, j3);
-    }
-}
-
 // Row prep. One work-group per row, one wave per 256-element group (wave w takes groups w, w + W, ...,
 // W = min(16, K / 256)); lane l holds elements 4 l .. 4 l + 3 of each of its groups in registers.
 // Canonical RMSNorm sum: per group, lane partial ((sq0 + sq1) + sq2) + sq3 of its four squares, the
@@ -249,22 +189,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
         }
     }
     if (a.nw) {
-#pragma unroll
-        for (int gi = 0; gi < GPW; ++gi) {
-            float q = __fmul_rn(v[gi][0], v[gi][0]);
-#pragma unroll
-            for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-            q = tree_sum64(q);
-            const int g = w + W * gi;
-            if (lane == 0 && g < G) gsum[g] = q;
-        }
-        __syncthreads();
-        // the group sums in group order (G <= 64: one LDS read per lane, then lane by lane)
-        const float gv = lane < G ? gsum[lane] : 0.f;
-        float ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gv)));
-        for (int g = 1; g < G; ++g) ss = __fadd_rn(ss, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), g)));
-        const float mean = __fdiv_rn(ss, float(K));
-        const float r = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(mean, a.eps)));
+        const float r = row_rms_factor<GPW>(v, K, a.eps, gsum);
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
             float wv[4];

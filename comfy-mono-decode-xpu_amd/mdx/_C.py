@@ -660,3 +660,154 @@ def silu_mul(g, u, silu_lut, out=None):
         out = torch.empty_like(g)
     _lib.call("mdx_silu_mul", _lib.ptr(g), _lib.ptr(u), _lib.ptr(silu_lut), _lib.ptr(out), g.numel(), _lib.stream_of(g))
     return out
+
+
+# ---------------------------------------------------------------------------------------------------
+# fused draft-head ops (csrc/draft_fused.sycl, called from comfy_mono_decode_xpu/draft_head.py:179-211)
+# ---------------------------------------------------------------------------------------------------
+_LUTS = {}
+
+
+def _luts(dev):
+    """torch's sigmoid and SiLU of every bf16 value on this device (the draft ops' activations)."""
+    from . import layout
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    t = _LUTS.get(key)
+    if t is None:
+        t = _LUTS[key] = (layout.sigmoid_lut(dev), layout.silu_lut(dev))
+    return t
+
+
+def _present(t):
+    return t is not None and t.numel() > 0
+
+
+def _bf16c(t, what):
+    _dev(t, what)
+    _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{what}: contiguous bf16")
+
+
+_HROT = {}
+
+
+def _regular_h(hmat, what="hadamard"):
+    """True for the regular ConvRot H256 in fp32 [256, 256] (the only rotation the reference's draft ops
+    apply: csrc/draft_fused.sycl:46-73 runs the fixed transform whenever a matrix is passed)."""
+    from . import layout
+    _dev(hmat, what)
+    _check(hmat.dtype == torch.float32 and hmat.is_contiguous() and hmat.numel() == 65536, f"{what}: f32 [256, 256]")
+    key = (hmat.data_ptr(), hmat._version)
+    hit = _HROT.get(key)
+    if hit is None or hit[0] is not hmat:
+        ok = torch.equal(hmat.reshape(256, 256), layout.regular_hadamard(hmat.device, torch.float32))
+        if len(_HROT) >= 8:
+            _HROT.pop(next(iter(_HROT)))
+        hit = _HROT[key] = (hmat, ok)
+    _check(hit[1], f"{what}: only the regular ConvRot H256 (kron(H4, H4, H4, H4) / 16) is supported")
+    return True
+
+
+def draft_embed_norm_cat(token, q, s, hmat, emb, hidden, we, wh, eps_e, eps_h, out):
+    """Reference csrc/draft_fused.sycl:76-151: out = cat(RMSNorm_e(emb), RMSNorm_h(hidden)), the embedding
+    row gathered from an int8 ConvRot table (q [V, H] int8, s [V] f32, un-rotated by H256 when hmat is
+    given) at token, or given as the bf16 row emb (q empty). Rows: hidden [rows, H] (the reference: one)."""
+    _bf16c(hidden, "hidden")
+    _bf16c(we, "we")
+    _bf16c(wh, "wh")
+    H = we.numel()
+    _check(wh.numel() == H and H >= 256 and H % 256 == 0 and hidden.numel() % H == 0, "hidden size")
+    rows = hidden.numel() // H
+    _bf16c(out, "out")
+    _check(out.numel() == 2 * rows * H, "out bf16 [rows, 2 H]")
+    gather = _present(q)
+    if gather:
+        _dev(q, "q")
+        _check(q.dtype == torch.int8 and q.dim() == 2 and q.shape[1] == H and q.is_contiguous(), "q int8 [V, H]")
+        _check(s.dtype == torch.float32 and s.is_contiguous() and s.numel() == q.shape[0], "s float [V]")
+        _check(token.dtype == torch.int64 and token.is_contiguous() and token.numel() == rows, "token int64 [rows]")
+        unrot = _present(hmat) and _regular_h(hmat)
+        _lib.call("mdx_draft_embed_norm_cat", _lib.ptr(token), _lib.ptr(q), _lib.ptr(s), q.shape[0], int(unrot), None,
+                  _lib.ptr(hidden), _lib.ptr(we), _lib.ptr(wh), float(eps_e), float(eps_h), _lib.ptr(out), rows, H,
+                  _lib.stream_of(hidden))
+    else:
+        _bf16c(emb, "emb")
+        _check(emb.numel() == rows * H, "emb bf16 [rows, H]")
+        _lib.call("mdx_draft_embed_norm_cat", None, None, None, 0, 0, _lib.ptr(emb), _lib.ptr(hidden), _lib.ptr(we),
+                  _lib.ptr(wh), float(eps_e), float(eps_h), _lib.ptr(out), rows, H, _lib.stream_of(hidden))
+
+
+def draft_add_rmsnorm(x, h, w, eps, out):
+    """Reference csrc/draft_fused.sycl:153-184: x = bf16(x + h) in place (h empty: x unchanged), out =
+    RMSNorm(x). x / h / out [rows, H] bf16 (the reference: one row)."""
+    _bf16c(x, "x")
+    _bf16c(w, "w")
+    _bf16c(out, "out")
+    H = w.numel()
+    _check(H >= 256 and H % 256 == 0 and x.numel() % H == 0 and out.numel() == x.numel(), "bf16 [rows, H] rows")
+    if _present(h):
+        _bf16c(h, "h")
+        _check(h.numel() == x.numel(), "h bf16 like x")
+    _lib.call("mdx_draft_add_rmsnorm", _lib.ptr(x), _lib.ptr(h) if _present(h) else None, _lib.ptr(w), float(eps),
+              _lib.ptr(out), x.numel() // H, H, _lib.stream_of(x))
+
+
+def draft_sigmoid_mul(a, qg, head_dim, out):
+    """Reference csrc/draft_fused.sycl:186-203: out = bf16(a * bf16(sigmoid(gate))), the gate being the second
+    half of each 2 head_dim block of the q projection qg (contiguous, or rows [rows, >= 2 n] with a row
+    stride: the q part of a fused q|k|v projection)."""
+    _bf16c(a, "a")
+    _bf16c(out, "out")
+    _dev(qg, "qg")
+    _check(qg.dtype == torch.bfloat16 and qg.stride(-1) == 1, "q projection bf16")
+    D = int(head_dim)
+    if qg.is_contiguous():
+        rows, row_stride = 1, qg.numel()
+        n = a.numel()
+    else:
+        _check(qg.dim() == 2, "q projection: contiguous, or [rows, 2 n] rows")
+        rows, row_stride = qg.shape[0], qg.stride(0)
+        _check(a.numel() % rows == 0, "a [rows, n]")
+        n = a.numel() // rows
+        _check(qg.shape[1] >= 2 * n, "q projection [rows, 2 n]")
+    _check(D >= 1 and n % D == 0 and (qg.numel() >= 2 * n if rows == 1 else True) and out.numel() == a.numel(),
+           "q projection bf16 [heads x 2 head_dim]")
+    sig, _ = _luts(a.device)
+    _lib.call("mdx_draft_sigmoid_mul", _lib.ptr(a), _lib.ptr(qg), row_stride, D, _lib.ptr(sig), _lib.ptr(out), rows, n,
+              _lib.stream_of(a))
+
+
+def draft_silu_mul(gu, out):
+    """Reference csrc/draft_fused.sycl:205-218: out = bf16(bf16(silu(gate)) * up) over the concatenated
+    gate | up rows gu [rows, 2 I] (the reference: one row)."""
+    _bf16c(gu, "gu")
+    _bf16c(out, "out")
+    I = out.shape[-1]
+    _check(gu.numel() == 2 * out.numel() and out.numel() % I == 0, "gate | up bf16 [2I], out bf16 [I]")
+    rows = out.numel() // I
+    _, silu = _luts(gu.device)
+    _lib.call("mdx_draft_silu_mul", _lib.ptr(gu), 2 * I, _lib.ptr(silu), _lib.ptr(out), rows, I, _lib.stream_of(gu))
+
+
+def draft_norm_rot_quant(x, h, w, eps, hmat, xr, qx, sx):
+    """Reference csrc/draft_fused.sycl:220-287: x = bf16(x + h) in place (optional), xr = bf16(H256 rotation of
+    RMSNorm(x)), rowwise int8 quantisation of xr into qx / sx (scale = max(amax / 127, 1e-30), q = rint(xr /
+    bf16(scale))). An empty hmat (the reference requires one) leaves xr unrotated; empty qx / sx skip the
+    quantisation (a bf16 lm_head reads xr)."""
+    _bf16c(x, "x")
+    _bf16c(w, "w")
+    _bf16c(xr, "xr")
+    H = w.numel()
+    _check(H >= 256 and H % 256 == 0 and x.numel() % H == 0 and xr.numel() == x.numel(), "x / w / xr bf16 [rows, H]")
+    rows = x.numel() // H
+    rot = _lib.ROT_H256 if (_present(hmat) and _regular_h(hmat)) else _lib.ROT_NONE
+    if _present(h):
+        _bf16c(h, "h")
+        _check(h.numel() == x.numel(), "h bf16 like x")
+    quant = _present(qx)
+    if quant:
+        _dev(qx, "qx")
+        _check(qx.dtype == torch.int8 and qx.is_contiguous() and qx.numel() == x.numel(), "qx int8 [rows, H]")
+        _check(sx.dtype == torch.float32 and sx.is_contiguous() and sx.numel() == rows, "sx float [rows]")
+    _lib.call("mdx_draft_norm_rot_quant", _lib.ptr(x), _lib.ptr(h) if _present(h) else None, _lib.ptr(w), float(eps),
+              rot, _lib.ptr(xr), _lib.ptr(qx) if quant else None, _lib.ptr(sx) if quant else None, rows, H,
+              _lib.stream_of(x))

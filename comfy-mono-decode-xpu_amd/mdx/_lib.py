@@ -85,6 +85,16 @@ SIGNATURES = {
                                        c_void_p]),
     "mdx_rmsnorm": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_silu_mul": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "mdx_draft_embed_norm_cat": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,
+                                                c_void_p, c_void_p, ctypes.c_float, ctypes.c_float, c_void_p, c_int64,
+                                                c_int64, c_void_p]),
+    "mdx_draft_add_rmsnorm": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64,
+                                             c_void_p]),
+    "mdx_draft_sigmoid_mul": (ctypes.c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                             c_int64, c_void_p]),
+    "mdx_draft_silu_mul": (ctypes.c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "mdx_draft_norm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int32, c_void_p,
+                                                c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
 }
 
 _lib = None

@@ -307,8 +307,8 @@ int mdx_gate_rot_quant(const uint16_t* y, const uint16_t* gate, int64_t gate_row
                        int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
 
 /* RMSNorm of bf16 rows in the library's fixed order (out = bf16((x * r) * w), r = 1 / sqrt(mean(x^2) +
- * eps)). Serves the bf16 MTP draft block (comfy_mono_decode_xpu/draft_head.py:179-232: its embed / hidden
- * / input / post / final norms). x, out bf16 [rows, K], K % 8 == 0, 16-byte aligned. */
+ * eps)). Serves the bf16 lm_head input of the decode loop (the final norm, comfy_mono_decode_xpu/
+ * mtp_loop.py:221-225). x, out bf16 [rows, K], K % 256 == 0, K <= 16384, 16-byte aligned. */
 int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* out, int64_t rows, int64_t K,
                 void* stream);
 
@@ -316,6 +316,45 @@ int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* 
  * comfy_mono_decode_xpu/draft_head.py:214-226; the same rule as mono_mlp's gate/up epilogue). */
 int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t* silu_lut, uint16_t* out, int64_t n,
                  void* stream);
+
+/* ---- the fused draft-head row ops (comfy_mono_decode_xpu/draft_head.py:179-211) -------------------
+ * One work-group per row, rows of hidden size H (H % 256 == 0, H <= 16384). RMSNorm is the library's
+ * fixed order (as mdx_rmsnorm); rotations are the exact fp64 FWHT rounded once to fp32 and once to bf16;
+ * sigmoid / SiLU come from bf16 lookup tables of torch's own values. The reference computes these in
+ * fp32 without a fixed order (draft tokens are only proposals); its tolerance, 1e-2 relative, bounds
+ * the difference. Rows of one call are independent: the reference's single-row ops are rows == 1. */
+
+/* fc input of the MTP block: out[r] = [RMSNorm_e(e) | RMSNorm_h(hidden[r])] (bf16 [rows, 2 H]), with the
+ * embedding row e = bf16(unrotate(q[t] * s[t])), t = token[r] clamped into [0, V) (int8 [V, H] table,
+ * f32 scales [V]; unrotate: the group times H256, or none), or, with q == NULL, e = emb[r] (bf16 [rows, H]).
+ * Replaces: _C.draft_embed_norm_cat, csrc/draft_fused.sycl:76-151 (bindings.cpp:34-36). */
+int mdx_draft_embed_norm_cat(const int64_t* token, const int8_t* q, const float* s, int64_t V, int32_t unrotate,
+                             const uint16_t* emb, const uint16_t* hidden, const uint16_t* we, const uint16_t* wh,
+                             float eps_e, float eps_h, uint16_t* out, int64_t rows, int64_t H, void* stream);
+
+/* x = bf16(x + h) in place when h != NULL (else x is left alone), out = RMSNorm(x) (bf16 [rows, H]).
+ * Replaces: _C.draft_add_rmsnorm, csrc/draft_fused.sycl:153-184 (bindings.cpp:37). */
+int mdx_draft_add_rmsnorm(uint16_t* x, const uint16_t* h, const uint16_t* w, float eps, uint16_t* out, int64_t rows,
+                          int64_t H, void* stream);
+
+/* out[r, i] = bf16(a[r, i] * sig_lut[g]), g = qg[r * qg_row_stride + (i / head_dim) * 2 head_dim + head_dim +
+ * i % head_dim] (the gate half of each head of the gated q projection). a, out bf16 [rows, n].
+ * Replaces: _C.draft_sigmoid_mul, csrc/draft_fused.sycl:186-203 (bindings.cpp:38). */
+int mdx_draft_sigmoid_mul(const uint16_t* a, const uint16_t* qg, int64_t qg_row_stride, int64_t head_dim,
+                          const uint16_t* sig_lut, uint16_t* out, int64_t rows, int64_t n, void* stream);
+
+/* out[r, i] = bf16(silu_lut[g] * u), g = gu[r * gu_row_stride + i], u = gu[r * gu_row_stride + n + i] (the
+ * concatenated gate | up projection). Replaces: _C.draft_silu_mul, csrc/draft_fused.sycl:205-218
+ * (bindings.cpp:39). */
+int mdx_draft_silu_mul(const uint16_t* gu, int64_t gu_row_stride, const uint16_t* silu_lut, uint16_t* out,
+                       int64_t rows, int64_t n, void* stream);
+
+/* The draft's final norm and the lm_head's activation prep: x = bf16(x + h) in place (h optional),
+ * xr = bf16(rotate(RMSNorm(x))) (rot MDX_ROT_H256 or MDX_ROT_NONE); with qx / sx: scale = max(amax(xr) /
+ * 127, 1e-30) -> sx, qx = int8(clamp(rint(fl32(xr / bf16(scale))), -128, 127)).
+ * Replaces: _C.draft_norm_rot_quant, csrc/draft_fused.sycl:220-287 (bindings.cpp:40-41). */
+int mdx_draft_norm_rot_quant(uint16_t* x, const uint16_t* h, const uint16_t* w, float eps, int32_t rot, uint16_t* xr,
+                             int8_t* qx, float* sx, int64_t rows, int64_t H, void* stream);
 
 #ifdef __cplusplus
 }

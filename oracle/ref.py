@@ -181,7 +181,7 @@ def rotate_rows(xf, rot, h=None):
 
 def quantize_rows(xr):
     """scale = max(amax / 127, 1e-30) (f32), sb = bf16(scale) (0 -> 0x0080),
-    q = int8(clamp(rint(float(bf16(xr / sb))), -128, 127)) (csrc/act_prep.sycl:175-195)."""
+    q = int8(clamp(rint(float(bf16(xr / sb))), -128, 127)) (csrc/act_prep.sycl:70-91)."""
     xr = np.asarray(xr, dtype=np.float32)
     amax = np.fmax.reduce(np.abs(xr), axis=1, initial=np.float32(0)).astype(np.float32)
     scale = np.maximum((amax / np.float32(127.0)).astype(np.float32), np.float32(1e-30)).astype(np.float32)
@@ -563,7 +563,9 @@ def gdn_conv(state, proj, conv_w, ctl, R, slots, dtype=np.float64):
     hist = np.empty((C, GDN_CW), dtype=dtype)
     for r in range(GDN_CW):
         j = pending + r
-        hist[:, r] = old[:, j] if j < GDN_CW else prev[acc_slots[j - GDN_CW]]
+        # an accepted slot outside [0, slots) is clamped into the range (the reference reads it
+        # unchecked, mono_gdn.sycl:345-349; such a step replays nothing, see gdn_step)
+        hist[:, r] = old[:, j] if j < GDN_CW else prev[min(max(int(acc_slots[j - GDN_CW]), 0), slots - 1)]
     w = conv_w.astype(dtype)
     out = np.zeros((slots, C), dtype=dtype)
     for ts in range(R):
@@ -571,6 +573,7 @@ def gdn_conv(state, proj, conv_w, ctl, R, slots, dtype=np.float64):
         miss = [0]
         for d in range(1, GDN_CW + 1):
             a = parents[anc[-1]] if anc[-1] >= 0 else -1
+            a = -1 if a >= R else a  # a parent is an earlier row of this step
             anc.append(a)
             miss.append(miss[-1] + (a < 0))
         s = np.zeros(C, dtype=dtype)
@@ -603,6 +606,17 @@ def gdn_gates(a, b, dt_bias, g_decay, dtype=np.float64):
     decay = np.exp(g_decay.astype(dtype) * sp)
     beta = _rnd(1 / (1 + np.exp(-b.astype(dtype))), dtype)
     return decay, beta
+
+
+def gdn_delta(S, kn, v, decay, beta, dtype=np.float64):
+    """One entry of the gated delta rule on a value head's state S [d_k rows, d_v columns] (stored
+    as rec_state[(h * 128 + row) * 128 + col], csrc/mono_gdn.sycl:385,526-571): S <- S * decay,
+    kv[c] = sum_r S[r, c] kn[r], delta = (v - kv) * beta, S[r, c] <- S[r, c] + kn[r] delta[c].
+    Returns the updated state (the caller keeps it only for a committing entry)."""
+    Sd = S * dtype(decay)
+    kv = kn @ Sd
+    delta = (v - kv) * dtype(beta)
+    return Sd + np.outer(kn, delta)
 
 
 def gdn_step(state, proj, z, a, b, conv_w, dt_bias, g_decay, gnorm_w, eps, qscale, ctl, R, HK, slots,
@@ -659,18 +673,15 @@ def gdn_step(state, proj, z, a, b, conv_w, dt_bias, g_decay, gnorm_w, eps, qscal
             v = src[ts, 2 * KD + h * DH:2 * KD + (h + 1) * DH].astype(dtype)
             kn = k / max(np.sqrt(sq[1]), 1e-12)
             qn = (q * qscale) / max(np.sqrt(sq[0]), 1e-12)
-            Sd = S * dtype(dec)
-            kv = kn @ Sd                      # [col]
-            delta = (v - kv) * dtype(bet)
-            Su = Sd + np.outer(kn, delta)
+            Su = gdn_delta(S, kn, v, dec, bet, dtype)
             if verify:
                 raw[ts] = _rnd(qn @ Su, dtype)
             if commit:
                 S = Su
-            if e == E0 - 1:
+            # the persistent state keeps the replayed entries only, and only when every pending slot
+            # was valid (csrc/mono_gdn.sycl:568)
+            if e == E0 - 1 and replayed:
                 state["rec"][h] = S.astype(state["rec"].dtype)
-        if E0 == 0 and replayed:
-            pass
         for ts, rv in raw.items():
             ss = np.sum(rv.astype(dtype) ** 2)
             rsq = 1 / np.sqrt(ss / DH + eps)
@@ -744,3 +755,63 @@ def layer_post(x_bits, y_bits, gate_bits, sig_bits, o, norm_w_bits, eps, rot, h,
                                                                                       o["G"])), s, o["sch"])))
     mlp = mono_mlp(rmsnorm(x1, norm_w_bits, eps), rot, h, lut_bits, g, u, d)
     return add_bf16(x1, mlp), x1
+
+
+# ---------------------------------------------------------------------------------------------
+# fused draft-head ops (csrc/draft_fused.sycl:76-287; comfy_mono_decode_xpu/draft_head.py:179-211).
+# The reference computes them in fp32 without a fixed order; the library's fixed order is restated
+# (the rmsnorm above, the exact FWHT of rotate_rows), pinned to float64 within the reference's
+# tolerance (tests/test_draft_fused.py:10-12: 1e-2 relative L2).
+# ---------------------------------------------------------------------------------------------
+
+
+def draft_embed_norm_cat(hidden_bits, we_bits, wh_bits, eps_e, eps_h, emb_bits=None, q=None, s=None, token=None,
+                         unrotate=False):
+    """[RMSNorm_e(e) | RMSNorm_h(hidden)] per row, e = emb_bits, or the int8 table row q[t] * s[t]
+    (t = token clamped into [0, V)), un-rotated by H256 (exact sum, one rounding to fp32), then bf16
+    (csrc/draft_fused.sycl:113-149)."""
+    hidden_bits = np.asarray(hidden_bits, dtype=np.uint16).reshape(-1, np.asarray(we_bits).size)
+    if q is not None:
+        t = np.clip(np.asarray(token, dtype=np.int64).reshape(-1), 0, q.shape[0] - 1)
+        row = (np.asarray(q, dtype=np.float32)[t] * np.asarray(s, dtype=np.float32)[t][:, None]).astype(np.float32)
+        if unrotate:
+            g = row.reshape(row.shape[0], -1, 256).astype(np.float64)
+            row = (fwht256_f64(g) * 0.0625).astype(np.float32).reshape(row.shape)
+        emb_bits = f32_to_bf16(row)
+    emb_bits = np.asarray(emb_bits, dtype=np.uint16).reshape(hidden_bits.shape)
+    return np.concatenate([rmsnorm(emb_bits, we_bits, eps_e), rmsnorm(hidden_bits, wh_bits, eps_h)], axis=1)
+
+
+def draft_add_rmsnorm(x_bits, h_bits, w_bits, eps):
+    """(x', out): x' = bf16(x + h) (x when h is None), out = RMSNorm(x') (csrc/draft_fused.sycl:164-182)."""
+    x_bits = np.asarray(x_bits, dtype=np.uint16).reshape(-1, np.asarray(w_bits).size)
+    xn = x_bits if h_bits is None else add_bf16(x_bits, np.asarray(h_bits, dtype=np.uint16).reshape(x_bits.shape))
+    return xn, rmsnorm(xn, w_bits, eps)
+
+
+def draft_sigmoid_mul(a_bits, qg_bits, head_dim, sig_lut_bits):
+    """bf16(a * sig[gate]) with the gate the second half of each 2 head_dim block of the q projection row
+    (csrc/draft_fused.sycl:196-201). a [rows, n], qg [rows, >= 2 n]."""
+    a_bits = np.asarray(a_bits, dtype=np.uint16)
+    rows, n = a_bits.shape
+    qg = np.asarray(qg_bits, dtype=np.uint16)[:, :2 * n].reshape(rows, n // head_dim, 2, head_dim)
+    return gate_mul(a_bits, qg[:, :, 1].reshape(rows, n), sig_lut_bits)
+
+
+def draft_silu_mul(gu_bits, lut_bits):
+    """bf16(silu[g] * u) over gate | up rows gu [rows, 2 I] (csrc/draft_fused.sycl:211-216)."""
+    gu = np.asarray(gu_bits, dtype=np.uint16)
+    I = gu.shape[1] // 2
+    return silu_mul(bf16_to_f32(gu[:, :I]), bf16_to_f32(gu[:, I:]), lut_bits)
+
+
+def draft_norm_rot_quant(x_bits, h_bits, w_bits, eps, rot="h256"):
+    """(x', xr, q, scale): x' = bf16(x + h), xr = bf16(rotate(RMSNorm(x'))), scale = max(amax(xr) / 127,
+    1e-30), q = clamp(rint(fl32(xr / bf16(scale))), -128, 127) (csrc/draft_fused.sycl:245-286)."""
+    xn, n = draft_add_rmsnorm(x_bits, h_bits, w_bits, eps)
+    xr = rotate_rows(bf16_to_f32(n), rot)
+    amax = np.max(np.abs(xr), axis=1).astype(np.float32)
+    scale = np.maximum((amax / np.float32(127)).astype(np.float32), np.float32(1e-30)).astype(np.float32)
+    div = bfround(scale)
+    q = np.clip(np.rint((xr / div[:, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    return xn, f32_to_bf16(xr), q, scale

@@ -32,7 +32,7 @@ def _bound(got, want, chain, what):
     assert err.mean() <= 1.5 * e_ref.mean() + 1e-5, (what, err.mean(), e_ref.mean())
 
 
-@pytest.mark.parametrize("slots,widths", [(8, (4, 3)), (8, (1,) * 7), (16, (4, 3, 2, 2, 2)), (8, (1,))])
+@pytest.mark.parametrize("slots,widths", [(8, (4, 3)), (8, (1,) * 7), (16, (4, 3, 2, 2, 2)), (8, (1,)), (8, ())])
 def test_gdn_two_steps_match_f64(C, dev, slots, widths):
     rng = np.random.default_rng(40 + slots + len(widths))
     conv_w = _bf(rng.standard_normal((NCH, 4)) * 0.5)
@@ -57,6 +57,7 @@ def test_gdn_two_steps_match_f64(C, dev, slots, widths):
     pending = 0
     for step in range(2):
         p = step % 2
+        print(f"case gdn slots={slots} widths={widths} R={R} step={step}", flush=True)
         ctl = [pending, p] + accepted + parents + prog
         proj = _bf(rng.standard_normal((R, NCH)))
         z = _bf(rng.standard_normal((R, HV * DH)))
@@ -103,3 +104,39 @@ def test_gdn_first_step_without_history_rows(C, dev):
                 torch.zeros(HV, device=dev), -torch.ones(HV, device=dev), rec, torch.zeros(2, slots, HV, 2, device=dev),
                 torch.zeros(2, slots, HK, 2, device=dev), torch.ones(DH, device=dev).bfloat16(), 1e-6, DH ** -0.5, HK)
     assert torch.equal(rec, before)
+
+
+@pytest.mark.parametrize("bad", [-1, 8])
+def test_gdn_invalid_accepted_slot_replays_nothing(C, dev, bad):
+    """A pending list with an out-of-range slot: nothing is replayed or verified (the state and the
+    outputs stay as they are, csrc/mono_gdn.sycl:398-407,568); the conv history reads the slot clamped
+    into range, as the oracle does."""
+    print(f"case gdn invalid slot {bad}", flush=True)
+    rng = np.random.default_rng(60 + bad)
+    slots = 8
+    tree = ref.tree_from_spec(ref.spec_of_widths((4, 3)), slots)
+    R = 8
+    parents = tree[0][:R]
+    ctl = [3, 0] + [0, bad, 2] + [0] * (slots - 3) + parents + ref.verify_program(parents, R)
+    conv_w = _bf(rng.standard_normal((NCH, 4)) * 0.5)
+    st = dict(conv_state=_bf(rng.standard_normal((NCH, 3))), pb=_bf(rng.standard_normal((2, slots, NCH))),
+              qb=_bf(rng.standard_normal((2, slots, NCH))), rec=(rng.standard_normal((HV, DH, DH)) * 0.1).astype(np.float32),
+              gates=rng.uniform(0.1, 0.9, (2, slots, HV, 2)).astype(np.float32),
+              sums=rng.uniform(0.5, 2, (2, slots, HK, 2)).astype(np.float32))
+    d = {k: _tensor(v, dev, torch.bfloat16 if k in ("conv_state", "pb", "qb") else torch.float32) for k, v in st.items()}
+    rec0 = d["rec"].clone()
+    proj, z, xn = (_bf(rng.standard_normal(s_)) for s_ in ((R, NCH), (R, HV * DH), (R, 4096)))
+    wa, wb = (_bf(rng.standard_normal((HV, 4096)) * 0.02) for _ in range(2))
+    dt_bias = rng.uniform(-1, 1, HV).astype(np.float32)
+    g_decay = (-np.exp(rng.uniform(-1, 0.5, HV))).astype(np.float32)
+    gnw = _bf(1 + rng.standard_normal(DH) * 0.1)
+    core = C.gdn_core(_tensor(proj, dev), _tensor(z, dev), _tensor(xn, dev), _tensor(wa, dev), _tensor(wb, dev),
+                      _tensor(conv_w, dev), d["conv_state"], d["pb"], d["qb"], torch.tensor(ctl, dtype=torch.int32, device=dev),
+                      _tensor(dt_bias, dev, torch.float32), _tensor(g_decay, dev, torch.float32), d["rec"], d["gates"],
+                      d["sums"], _tensor(gnw, dev), 1e-6, DH ** -0.5, HK)
+    assert torch.equal(d["rec"], rec0)
+    assert not core.float().abs().sum().item()
+    want = ref.gdn_step(st, proj, z, *ref.gdn_ab(ref.f32_to_bf16(xn), ref.f32_to_bf16(wa), ref.f32_to_bf16(wb)), conv_w,
+                        dt_bias, g_decay, gnw, 1e-6, DH ** -0.5, np.array(ctl), R, HK, slots)
+    assert not want.any()
+    assert_bits_equal(bits(d["conv_state"]), ref.f32_to_bf16(st["conv_state"]), "conv history")

@@ -54,7 +54,7 @@ def test_layer_post_matches_oracle(C, dev, gated, compact):
     hd = h.to(dev)
     if compact:
         hd = torch.stack((hd[:16, :16], -hd[:16, :16])).contiguous()
-    for R in (1, 8):
+    for R in (1, 8, 16):
         print(f"case layer_post gated={gated} compact={compact} R={R}", flush=True)
         x = torch.randn(R, 4096, generator=g).bfloat16()
         y = torch.randn(R, 4096, generator=g).bfloat16()
@@ -70,9 +70,11 @@ def test_layer_post_matches_oracle(C, dev, gated, compact):
         assert_bits_equal(bits(xd), want, f"x R={R}")
 
 
-def test_layer_gdn_matches_oracle(C, dev):
+@pytest.mark.parametrize("widths", [(4, 3), ()])
+def test_layer_gdn_matches_oracle(C, dev, widths):
     from mdx import layout
-    g = torch.Generator().manual_seed(52)
+    print(f"case layer_gdn widths={widths}", flush=True)
+    g = torch.Generator().manual_seed(52 + len(widths))
     HK, HV, DH = 16, 32, 128
     NCH = 2 * HK * DH + HV * DH
     shapes = [(NCH, 4096), (4096, 4096), (4096, 4096), (12288, 4096), (12288, 4096), (4096, 12288)]
@@ -89,9 +91,10 @@ def test_layer_gdn_matches_oracle(C, dev):
     gnw = bfn(1 + rng.standard_normal(DH) * 0.1)
     nin = (1 + torch.randn(4096, generator=g) * 0.05).bfloat16()
     npo = (1 + torch.randn(4096, generator=g) * 0.05).bfloat16()
-    slots, R = 8, 8
-    parents = ref.tree_from_spec(ref.spec_of_widths((4, 3)), slots)[0][:R]
-    ctl = [0, 0] + [0] * slots + parents + ref.verify_program(parents, R)
+    slots, R = 8, 1 + sum(widths)
+    parents = ref.tree_from_spec(ref.spec_of_widths(widths), slots)[0][:R]
+    ctl = ([0, 0] + [0] * slots + parents + [-1] * (slots - R) + ref.verify_program(parents, R)
+           + [0] * (slots - R))
     st = dict(conv_state=bfn(rng.standard_normal((NCH, 3))), pb=np.zeros((2, slots, NCH), np.float32),
               qb=np.zeros((2, slots, NCH), np.float32), rec=(rng.standard_normal((HV, DH, DH)) * 0.1).astype(np.float32),
               gates=np.zeros((2, slots, HV, 2), np.float32), sums=np.zeros((2, slots, HK, 2), np.float32))
