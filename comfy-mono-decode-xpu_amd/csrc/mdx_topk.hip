@@ -23,6 +23,8 @@
 // gather word), so 0 marks an empty slot.
 #include <algorithm>
 
+#include <mutex>
+
 #include "mdx_common.hpp"
 
 namespace mdx {
@@ -415,6 +417,64 @@ extern "C" int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64
     MDX_CHECK(k >= 1 && k <= TK_MAXK && n >= 4096 && n < (int64_t(1) << 31), "1 <= k <= 64, 4096 <= N < 2^31");
     return launch(x, x_dtype == MDX_DT_F32, ORDER_F32, rows, n, k, false, values, indices, nullptr, workspace,
                   workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+// ---- the allocation-free entry point --------------------------------------------------------------
+// A file-scope device array stands in for the caller's workspace, sized for the largest call (16 rows):
+// 16 x 64 segments x (64 + 1) ranks x 8 B + 256 B of counters = 532,736 B per device, held until the
+// process ends. Host code never uses its name as an address: the per-device address comes from
+// hipGetSymbolAddress with that device current.
+namespace mdx {
+namespace {
+constexpr size_t TOPK_SCRATCH_BYTES = size_t(TK_MAXR) * TK_MAXSEG * (TK_MAXK + 1) * sizeof(uint64_t) + 256;
+constexpr int SCRATCH_MAX_DEVICES = 64;
+
+__global__ __launch_bounds__(64) void zero_words_kernel(unsigned* p) { p[threadIdx.x] = 0u; }
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+}  // namespace
+}  // namespace mdx
+
+static __device__ __align__(256) uint8_t scratch[mdx::TOPK_SCRATCH_BYTES];
+
+namespace mdx {
+namespace {
+// The current device's copy of `scratch`; at the first call on a device its counter words (the first
+// 256 bytes) are cleared by a fill kernel on `st` (a kernel, not a memset: it may be captured).
+int scratch_of_current_device(hipStream_t st, void** out) {
+    int dev = -1;
+    MDX_HIP(hipGetDevice(&dev));
+    MDX_CHECK(dev >= 0 && dev < SCRATCH_MAX_DEVICES, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        MDX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        MDX_CHECK(p != nullptr && aligned(p, 256), "scratch symbol address");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, st, static_cast<unsigned*>(p));
+        MDX_LAUNCHED();
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MDX_OK;
+}
+}  // namespace
+}  // namespace mdx
+
+extern "C" int mdx_topk_rows_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k,
+                                     float* values, int64_t* indices, void* stream) {
+    MDX_CHECK(x && values && indices, "null pointer");
+    MDX_CHECK(x_dtype == MDX_DT_F32 || x_dtype == MDX_DT_BF16, "x: fp32 or bf16");
+    MDX_CHECK(rows >= 1 && rows <= TK_MAXR,
+              "1 <= rows <= %d (the library's static top-k scratch holds %d rows; got %lld)", TK_MAXR, TK_MAXR,
+              (long long)rows);
+    MDX_CHECK(k >= 1 && k <= TK_MAXK && n >= 4096 && n < (int64_t(1) << 31), "1 <= k <= 64, 4096 <= N < 2^31");
+    MDX_CHECK(workspace_bytes(rows) <= TOPK_SCRATCH_BYTES, "scratch size");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    if (int rc = scratch_of_current_device(st, &ws)) return rc;
+    return launch(x, x_dtype == MDX_DT_F32, ORDER_F32, rows, n, k, false, values, indices, nullptr, ws,
+                  TOPK_SCRATCH_BYTES, st);
 }
 
 extern "C" int mdx_topk_sample(const float* values, const int64_t* indices, const float* uniform, float temperature,

@@ -81,6 +81,8 @@ SIGNATURES = {
                                         ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "mdx_gnorm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
                                            ctypes.c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "mdx_topk_rows_noalloc": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                             c_void_p]),
     "mdx_topk_sample": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int64, c_int64, c_void_p,
                                        c_void_p]),
     "mdx_rmsnorm": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64, c_void_p]),

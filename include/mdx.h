@@ -209,6 +209,17 @@ int mdx_fast_pick(const uint16_t* x, int64_t V, int64_t k, uint16_t* values, int
 int mdx_topk_rows(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
                   int64_t* indices, void* workspace, size_t workspace_bytes, void* stream);
 
+/* mdx_topk_rows without a workspace argument: its partial lists and counters live in a file-scope
+ * device array of the library (532,736 bytes per device, held until the process ends), so the call
+ * allocates nothing (no hipMalloc, hipFree or allocating library routine; the first call on a device
+ * takes the array's address and clears its counters with a fill kernel). rows <= 16 (larger counts are
+ * rejected). Every call on a device shares that device's array: calls that overlap on one device (two
+ * streams, two threads) race; calls on one stream are ordered and each leaves the counters at zero.
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
+ * serving loops and harnesses that forbid allocation). */
+int mdx_topk_rows_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t k, float* values,
+                          int64_t* indices, void* stream);
+
 /* Gumbel-max sampling over each row's top k: out[r] = indices[r, j*], j* the first maximum over j of
  * values[r, j] * (1 / temperature) - log(-log(clamp(uniform[r, j], 1e-20, 1))), in fp32 (each
  * operation rounded as torch's elementwise kernels round it). values f32 / indices int64 / uniform f32
