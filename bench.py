@@ -18,6 +18,7 @@ operator chain on a bounded sample).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -40,13 +41,27 @@ def pmc_traffic(key):
         return None
 
 
-def gptq_weight(N, K, gen, dev, tiled=True):
+def read_roof(key):
+    """The single-launch streaming-read roof (GB/s) at a launch size, from the committed summary of
+    `bench.py --workload read` (the best over the work-group counts tried), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "read_roof.json")) as f:
+            return json.load(f)["roof_gbs"][key]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def gptq_weight(N, K, gen, dev, tiled=True, integral=True):
+    """A random GPTQ int4 matrix (q ~ U{-8..7}, fp16 G128 scales ~ U(0.005, 0.02)) in the packed-W4
+    contract. integral=True: the group scales become 4-bit integer multiples of a channel scale (the
+    integral decode; up to smax / (30 s_g) relative scale error per group); False: the fp16 group
+    scales relative to the channel scale, decoded per weight by rint (the reference contract)."""
     import torch
     from mdx import _lib, layout
     q = torch.randint(-8, 8, (N, K), generator=gen, device=dev, dtype=torch.int8)
     s = (torch.rand(N, K // 128, generator=gen, device=dev) * 0.015 + 0.005).half()
-    packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=True)
-    w = layout.W4(packed, s_rel, sch, None, decode=_lib.DECODE_INTEGRAL)  # integral scales by construction
+    packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=integral)
+    w = layout.W4(packed, s_rel, sch, None, decode=_lib.DECODE_INTEGRAL if integral else _lib.DECODE_AUTO)
     return w.tiled() if tiled else w
 
 
@@ -66,28 +81,53 @@ def linear_bytes(rows, N=4096, K=4096):
     return N * K // 2 + N * K // 128 * 2 + N * 4 + rows * (K + 4) + rows * N * 2
 
 
-def graph_time(fn, replays, warmup):
-    """Capture fn() once in a HIP graph; seconds per replay over `replays` timed replays."""
+def ring_time(call, ring_n, steps, warmup):
+    """Seconds per call of exactly `steps` calls call(0), call(1), ... cycling through a ring of
+    `ring_n` weight copies: one captured graph of a whole ring replayed steps // ring_n times, then a
+    graph of the remaining steps % ring_n calls (HIP events on the capturing stream's order)."""
     import torch
+    full, rem = divmod(steps, ring_n)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fn()  # eager warm-up (workspace, LDS attributes)
+        for i in range(ring_n):
+            call(i)  # eager warm-up (workspaces, LDS attributes)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        fn()
-    for _ in range(max(warmup, 1)):
-        g.replay()
+    graphs = []
+    for n in (ring_n if full else 0, rem):
+        if n:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(n):
+                    call(i)
+            graphs.append((g, full if n == ring_n and full else 1))
+    for _ in range(max(1, -(-warmup // ring_n))):
+        graphs[0][0].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(replays):
-        g.replay()
+    for g, reps in graphs:
+        for _ in range(reps):
+            g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / replays
+    return e0.elapsed_time(e1) / 1e3 / steps
+
+
+def cpu_info():
+    """(model name, threads used by the CPU baseline): numpy's BLAS pool is pinned to the process's
+    affinity count for the timed leg."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, cpu_threads()
 
 
 def cpu_threads():
@@ -97,28 +137,36 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
-def cpu_baseline_mlp(ring0, rows, xb, nwb, lutb, budget_s=20.0):
+def cpu_baseline_mlp(ring0, rows, xb, nwb, lutb, budget_s=25.0):
     """The oracle's operator chain (RMSNorm, quantise, decode + int dot, SiLU, quantise, decode +
-    int dot) on the host, on one set of the same weights; median over a bounded number of calls."""
+    int dot) on the host, on one set of the same weights: 3 warm-up calls, then the median of >= 10
+    timed calls (fewer only if the budget runs out), with numpy's BLAS threads pinned to the
+    process's CPU affinity count."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
     sys.path.insert(0, ROOT)
     from oracle import ref
+    from mdx import layout
     d = []
     for w in ring0:
-        from mdx import layout
         q = layout.row_major_codes(w.q).cpu().numpy()
-        s = w.s.float().cpu().numpy()
-        d.append(dict(packed=q, s=s, sch=w.sc.cpu().numpy(), cb=None, G=128))
+        d.append(dict(packed=q, s=w.s.float().cpu().numpy(), sch=w.sc.cpu().numpy(), cb=None, G=128))
+    model, threads = cpu_info()
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 and (not times or time.perf_counter() + times[-1] < t_end):
-        for dd in d:
-            dd.pop("w8", None)  # the decode is part of every call of the chain
-        t0 = time.perf_counter()
-        xn = ref.rmsnorm(xb, nwb, 1e-6)
-        ref.mono_mlp(xn, "none", None, lutb, *d)
-        times.append(time.perf_counter() - t0)
-    return float(np.median(times)), len(times)
+    with threadpool_limits(limits=threads):
+        for i in range(13):
+            for dd in d:
+                dd.pop("w8", None)  # the decode is part of every call of the chain
+            t0 = time.perf_counter()
+            xn = ref.rmsnorm(xb, nwb, 1e-6)
+            ref.mono_mlp(xn, "none", None, lutb, *d)
+            dt = time.perf_counter() - t0
+            if i >= 3:
+                times.append(dt)
+            if time.perf_counter() + dt > t_end and len(times) >= 3:
+                break
+    return float(np.median(times)), len(times), model, threads
 
 
 def bench_mlp(args, dev):
@@ -136,35 +184,37 @@ def bench_mlp(args, dev):
     out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
     ws = torch.zeros(_lib.lib().mdx_mono_mlp_workspace(M, H, I), dtype=torch.uint8, device=dev)
 
-    def all_ring():
-        for g_, u_, d_ in ring:
+    def mlp(r):
+        def call(i):
+            g_, u_, d_ = r[i]
             _C.mono_mlp_w4(x, _lib.ROT_NONE, None, lut, g_, u_, d_, norm_w=nw, eps=1e-6, out=out, ws=ws)
+        return call
 
-    reps = max(1, args.steps // ring_n)
-    t_call = graph_time(all_ring, reps, args.warmup) / ring_n
+    t_call = ring_time(mlp(ring), ring_n, args.steps, args.warmup)
     # the dominant kernel alone: the gate/up GEMV launch over the same ring
     q1, s1 = _C.rms_rot_quant(x, nw, 1e-6)
     hbuf = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
 
-    def all_gateup():
-        for g_, u_, _ in ring:
-            _C.stream_gemv(q1, s1, [g_, u_], [hbuf], gate_up=True, silu_lut=lut)
+    def gateup(i):
+        g_, u_, _ = ring[i]
+        _C.stream_gemv(q1, s1, [g_, u_], [hbuf], gate_up=True, silu_lut=lut)
 
-    t_gu = graph_time(all_gateup, reps, args.warmup) / ring_n
+    t_gu = ring_time(gateup, ring_n, args.steps, args.warmup)
     gu_b = gateup_bytes(M)
     res = {
         "metric": METRIC,
         "value": round(per / t_call / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": reps * ring_n,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(t_call * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xint4->int32, bf16 out",
-        "data": "synthetic (seeded GPTQ int4 weights, fp16 G128 scales, N(0,1) activations)",
+        "data": "synthetic (seeded GPTQ int4 weights; fp16 G128 group scales ~U(0.005, 0.02) packed as 4-bit "
+                "integer multiples of a channel scale (integral decode); N(0,1) activations)",
         "config": {"workload": f"fused W4A8 SwiGLU MLP 4096->2x12288->4096, RMSNorm 1e-6, rows={M}, "
                                f"tile-major weights, {ring_n}-copy weight ring",
                    "rows": M, "hidden": H, "intermediate": I, "group_size": 128,
@@ -173,18 +223,28 @@ def bench_mlp(args, dev):
                      "achieved": round(gu_b / t_gu / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gu_b / t_gu / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": pmc_traffic("mlp_gateup_rows1") if M == 1 else None,
-                     "algorithmic_bytes_per_launch": gu_b, "avg_launch_us": round(t_gu * 1e6, 3)},
+                     "algorithmic_bytes_per_launch": gu_b, "avg_launch_us": round(t_gu * 1e6, 3),
+                     "single_launch_read_roof_gbs": read_roof("52MB")},
     }
+    # the same block with the fp16-faithful packer (group scales kept as fp16 ratios, per-weight rint decode)
+    del ring
+    torch.cuda.empty_cache()
+    ring_f = [(gptq_weight(I, H, gen, dev, integral=False), gptq_weight(I, H, gen, dev, integral=False),
+               gptq_weight(H, I, gen, dev, integral=False)) for _ in range(ring_n)]
+    t_f = ring_time(mlp(ring_f), ring_n, args.steps, args.warmup)
+    res["faithful_scales"] = {"value": round(per / t_f / 1e9, 2), "unit": "GB/s", "ms_per_step": round(t_f * 1e3, 5),
+                              "data": "fp16 G128 group scales kept as fp16 ratios to the channel scale (reference "
+                                      "contract), per-weight rint decode"}
     if not args.no_cpu:
-        from oracle import ref as _ref  # noqa: F401
         xb = x.view(torch.int16).cpu().numpy().view("uint16")
         nwb = nw.view(torch.int16).cpu().numpy().view("uint16")
         lutb = lut.view(torch.int16).cpu().numpy().view("uint16")
-        t_cpu, n = cpu_baseline_mlp(ring[0], M, xb, nwb, lutb)
-        res["cpu_baseline"] = {"value": round(per / t_cpu / 1e9, 4), "unit": "GB/s", "cores": cpu_threads(),
-                               "kind": "port", "ms_per_step": round(t_cpu * 1e3, 1),
-                               "sample": f"{n} MLP calls of the numpy oracle chain (decode + float64 int dot), "
-                                         f"same weights and rows"}
+        t_cpu, n, model, threads = cpu_baseline_mlp(ring_f[0], M, xb, nwb, lutb)
+        res["cpu_baseline"] = {"value": round(per / t_cpu / 1e9, 4), "unit": "GB/s", "cores": threads,
+                               "kind": "port", "ms_per_step": round(t_cpu * 1e3, 1), "cpu_model": model,
+                               "sample": f"median of {n} MLP calls (after 3 warm-up calls) of the numpy oracle chain "
+                                         f"(decode + float64 int dot), one weight set, same rows; BLAS threads "
+                                         f"pinned to {threads}"}
     return res
 
 
@@ -202,22 +262,19 @@ def bench_linear(args, dev):
     s = s.view(-1)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
-    def all_ring():
-        for w in ring:
-            _C.stream_gemv(q, s, [w], [out])
-
-    reps = max(1, args.steps // ring_n)
-    t = graph_time(all_ring, reps, args.warmup) / ring_n
+    t = ring_time(lambda i: _C.stream_gemv(q, s, [ring[i]], [out]), ring_n, args.steps, args.warmup)
     return {
-        "metric": METRIC, "value": round(per / t / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": reps * ring_n,
+        "metric": METRIC, "value": round(per / t / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8xint4->int32, bf16 out",
-        "data": "synthetic (seeded GPTQ int4 weights, fp16 G128 scales)",
+        "data": "synthetic (seeded GPTQ int4 weights; fp16 G128 scales packed as 4-bit integer multiples of a "
+                "channel scale)",
         "config": {"workload": f"single W4A8 linear M={M} K=N=4096 G128, {ring_n}-copy weight ring", "rows": M,
                    "algorithmic_bytes_per_step": per},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel", "achieved": round(per / t / 1e9, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(per / t / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": pmc_traffic("linear_rows1") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3)},
+                     "traffic": pmc_traffic("linear_rows1") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3),
+                     "single_launch_read_roof_gbs": read_roof("8.7MB")},
     }
 
 
@@ -245,10 +302,10 @@ def bench_lmhead(args, dev):
     w = layout.tile_major_bf16((torch.randn(V, H, generator=gen, device=dev) * 0.02).bfloat16())
     x = torch.randn(M, H, generator=gen, device=dev).bfloat16()
     out = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
-    reps = max(1, args.steps // 10)
-    t = graph_time(lambda: _C.bf16_linear(x, w, tiled=True, out=out), reps, args.warmup)
+    steps = max(1, args.steps // 10)  # (about 0.2 ms per call)
+    t = ring_time(lambda i: _C.bf16_linear(x, w, tiled=True, out=out), 1, steps, args.warmup)
     gbs = per / t / 1e9
-    return _line(args, round(gbs, 2), "GB/s", t, reps, "bf16 x bf16 -> fp32 acc, bf16 out",
+    return _line(args, round(gbs, 2), "GB/s", t, steps, "bf16 x bf16 -> fp32 acc, bf16 out",
                  "synthetic (seeded N(0, 0.02) weights, N(0,1) rows)",
                  {"workload": f"bf16 lm_head 151936x4096, rows={M}, tile-major", "rows": M,
                   "algorithmic_bytes_per_step": per},
@@ -280,14 +337,10 @@ def bench_attn(args, dev):
     mask = torch.tensor(m, dtype=torch.int32, device=dev)
     sl = torch.tensor([L], dtype=torch.int32, device=dev)
 
-    def all_ring():
-        for k, v in caches:
-            _C.attn_dpas(q, k, v, sl, xk, xv, mask, 0)
-
-    reps = max(1, args.steps // ring_n)
-    t = graph_time(all_ring, reps, args.warmup) / ring_n
+    t = ring_time(lambda i: _C.attn_dpas(q, caches[i][0], caches[i][1], sl, xk, xv, mask, 0), ring_n, args.steps,
+                  args.warmup)
     gbs = per / t / 1e9
-    return _line(args, round(gbs, 2), "GB/s", t, reps * ring_n, "bf16 x bf16 -> fp32 (MFMA), bf16 out",
+    return _line(args, round(gbs, 2), "GB/s", t, args.steps, "bf16 x bf16 -> fp32 (MFMA), bf16 out",
                  "synthetic (seeded N(0,1) KV cache and rows)",
                  {"workload": f"tree-verify decode attention, 32q/8kv heads, head_dim 128, 16 rows, ctx={L}, "
                               f"{ring_n}-copy KV ring", "ctx": L, "rows": S, "algorithmic_bytes_per_step": per},
@@ -296,15 +349,19 @@ def bench_attn(args, dev):
                   "avg_launch_us": round(t * 1e6, 3)})
 
 
-def bench_stack(args, dev):
+def bench_stack(args, dev, tokens=0):
     """The full synthetic 32-layer hybrid stack (3 GDN : 1 attention, hidden 4096, MLP 12288, W4A8
     GPTQ G128), 1-layer bf16 MTP draft block, bf16 lm_head over 151936, tree_spec (4, 3) (8 rows, 2
     drafts per step), top-k 20 sampling; a seeded random prompt is prefilled (not timed), then each
-    decode step is one replayed HIP graph. value = accepted tokens per second."""
+    decode step is one replayed HIP graph. value = accepted tokens per second. tokens > 0: decode
+    until that many tokens are committed (chunks of 64 steps, each timed by events, the committed
+    count read between chunks); else exactly `steps` steps."""
     import torch
     from mdx import hybrid
     steps, warm = args.steps, max(args.warmup, 2)
-    cap = args.prompt + 8 * (steps + warm + 4) + 64
+    per = 3  # at most len(widths) + 1 tokens committed per step
+    budget = tokens + 64 if tokens else steps
+    cap = args.prompt + per * (budget + warm + 4) + 64
     cfg = hybrid.HybridConfig(cap=cap)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
@@ -316,21 +373,197 @@ def bench_stack(args, dev):
     setup = time.perf_counter() - t0
     st0 = int(m.st[0].item())
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    m.replay(steps)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / 1e3
-    tokens = int(m.st[0].item()) - st0
-    per_step = t / steps
-    return _line(args, round(tokens / t, 2), "tok/s", per_step, steps, "W4A8 int8 x int4 -> int32; bf16 draft, lm_head",
+    t, done, got = 0.0, 0, 0
+    while True:
+        n = min(64, steps - done) if not tokens else 64
+        if n <= 0 or (tokens and got >= tokens):
+            break
+        torch.cuda.synchronize()
+        e0.record()
+        m.replay(n)
+        e1.record()
+        torch.cuda.synchronize()
+        t += e0.elapsed_time(e1) / 1e3
+        done += n
+        got = int(m.st[0].item()) - st0
+    per_step = t / done
+    what = f"{got} tokens decoded" if tokens else f"{done} decode steps"
+    return _line(args, round(got / t, 2), "tok/s", per_step, done, "W4A8 int8 x int4 -> int32; bf16 draft, lm_head",
                  "synthetic (random-init weights, seeded random prompt)",
                  {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936, "
-                              f"MTP draft, tree (4, 3), top-k 20, prompt {args.prompt}, {steps} decode steps",
-                  "prompt": args.prompt, "steps": steps, "tokens": tokens,
-                  "accepted_per_step": round(tokens / steps, 3), "ms_per_step": round(per_step * 1e3, 4),
+                              f"MTP draft, tree (4, 3), top-k 20, prompt {args.prompt}, {what}",
+                  "prompt": args.prompt, "steps": done, "tokens": got,
+                  "accepted_per_step": round(got / done, 3), "ms_per_step": round(per_step * 1e3, 4),
                   "setup_s": round(setup, 1)})
+
+
+def w4_bytes(w):
+    return w.q.numel() + w.s.numel() * w.s.element_size() + w.sc.numel() * 4
+
+
+def bench_attn_layer(args, dev):
+    """One full-attention decoder layer's mixer for 16 tree-verify rows: RMSNorm + int8 quantisation,
+    W4A8 q/k/v (one launch), Q/K RMSNorm + RoPE (theta 1e7, 64 rotary dims) + the KV cache write, GQA
+    tree-verify attention over `--ctx` cached tokens (32 q / 8 kv heads, head_dim 128), quantisation of
+    its output, W4A8 o_proj with the residual. Weights and KV caches cycle through a ring > 2x the
+    Infinity Cache."""
+    import torch
+    from mdx import _C, _lib, hybrid
+    gen = torch.Generator(device=dev).manual_seed(3)
+    H, Hk, D, S, L, Hd = 32, 8, 128, 16, args.ctx, 4096
+    cap = L + S
+    cfg = hybrid.HybridConfig(cap=cap + 8)
+    ftab = hybrid.rope_table(cfg, dev)
+    parents = [-1, 0, 1, 2, 3, 4, 5, 6, 0, 8, 1, 10, 2, 12, 3, 14]
+    depth, m = [], []
+    for r, p_ in enumerate(parents):
+        depth.append(depth[p_] + 1 if p_ >= 0 else 0)
+        m.append((m[p_] if p_ >= 0 else 0) | (1 << r))
+    mask = torch.tensor(m, dtype=torch.int32, device=dev)
+    pos = torch.arange(L, L + S, dtype=torch.int64, device=dev)
+    freqs = torch.index_select(ftab, 0, torch.tensor(depth, device=dev) + L).contiguous()
+    seq = torch.tensor([L], dtype=torch.int32, device=dev)
+    def layer_w():
+        return dict(q=gptq_weight(H * D, Hd, gen, dev), k=gptq_weight(Hk * D, Hd, gen, dev),
+                    v=gptq_weight(Hk * D, Hd, gen, dev), o=gptq_weight(Hd, H * D, gen, dev),
+                    key=torch.randn(1, Hk, cap, D, generator=gen, device=dev).bfloat16(),
+                    value=torch.randn(1, Hk, cap, D, generator=gen, device=dev).bfloat16())
+    first = layer_w()
+    per_w = sum(w4_bytes(first[k]) for k in "qkvo")
+    per = per_w + 2 * Hk * L * D * 2 + 2 * Hk * S * D * 2 + 2 * S * Hd * 2 + Hd * 2
+    ring_n = _ring_count(per_w + 2 * Hk * cap * D * 2)
+    ring = [first] + [layer_w() for _ in range(ring_n - 1)]
+    x = torch.randn(S, Hd, generator=gen, device=dev).bfloat16()
+    nw = (1 + 0.02 * torch.randn(Hd, generator=gen, device=dev)).bfloat16()
+    qn = (1 + 0.1 * torch.randn(D, generator=gen, device=dev)).bfloat16()
+    kn = (1 + 0.1 * torch.randn(D, generator=gen, device=dev)).bfloat16()
+    xo = torch.empty_like(x)
+    xn = torch.empty_like(x)
+    qkv = [torch.empty(S, n, dtype=torch.bfloat16, device=dev) for n in (H * D, Hk * D, Hk * D)]
+    qh = torch.empty(1, H, S, D, dtype=torch.bfloat16, device=dev)
+    kh = torch.empty(1, Hk, S, D, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=dev)
+    q2 = torch.empty(S, H * D, dtype=torch.int8, device=dev)
+    s2 = torch.empty(S, dtype=torch.float32, device=dev)
+
+    def call(i):
+        w = ring[i]
+        q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
+        _C.stream_gemv(q1, s1, [w["q"], w["k"], w["v"]], qkv)
+        vv = qkv[2].view(1, S, Hk, D)
+        _C.qk_norm_rope_kv(qkv[0].view(1, S, H, D), qkv[1].view(1, S, Hk, D), vv, qn, kn, freqs, w["key"], w["value"],
+                           pos, 1e-6, 1e-6, 64, outs=(qh, kh))
+        _C.attn_dpas(qh, w["key"], w["value"], seq, kh, vv.transpose(1, 2), mask, 0, out=y)
+        _lib.call("mdx_rot_quant", _lib.ptr(y), None, _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), S, H * D,
+                  _lib.stream_of(y))
+        _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
+
+    t = ring_time(call, ring_n, args.steps, args.warmup)
+    gbs = per / t / 1e9
+    return _line(args, round(gbs, 2), "GB/s", t, args.steps, "W4A8 int8 x int4 -> int32; bf16 attention (MFMA)",
+                 "synthetic (seeded GPTQ int4 weights, integral 4-bit group scales; N(0,1) KV cache and rows)",
+                 {"workload": f"full-attention layer mixer, 16 tree rows, 32q/8kv heads, head_dim 128, ctx={L}, "
+                              f"{ring_n}-copy weight + KV ring", "ctx": L, "rows": S,
+                  "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                  "launches_per_step": 7})
+
+
+def bench_gdn_layer(args, dev):
+    """One Gated-DeltaNet layer's mixer for `--rows` chain rows (1 or 8): RMSNorm + int8 quantisation,
+    W4A8 qkv | z (one launch), the causal conv (kernel 4) + gates + L2 norms and the delta-rule update of
+    the fp32 128x128 state of each of 32 value heads (every row committed), the gated RMSNorm +
+    quantisation, W4A8 out_proj with the residual. Weights and states cycle through a ring > 2x the
+    Infinity Cache."""
+    import torch
+    from mdx import _C, _lib
+    gen = torch.Generator(device=dev).manual_seed(4)
+    M, Hd, HK, HV, DH, S = args.rows, 4096, 16, 32, 128, 8
+    if not 1 <= M <= S:
+        raise SystemExit("gdn_layer: --rows must be 1..8")
+    C = 2 * HK * DH + HV * DH
+    bf = dict(dtype=torch.bfloat16, device=dev)
+
+    def layer_w():
+        return dict(qkv=gptq_weight(C, Hd, gen, dev), z=gptq_weight(HV * DH, Hd, gen, dev), o=gptq_weight(Hd, HV * DH, gen, dev),
+                    wa=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
+                    wb=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
+                    conv_w=(torch.randn(C, 4, generator=gen, device=dev) * 0.5).bfloat16(),
+                    conv=torch.randn(C, 3, generator=gen, device=dev).bfloat16(),
+                    pb=torch.zeros(2, S, C, **bf), qb=torch.zeros(2, S, C, **bf),
+                    rec=torch.randn(HV, DH, DH, generator=gen, device=dev) * 0.1,
+                    gates=torch.zeros(2, S, HV, 2, device=dev), sums=torch.zeros(2, S, HK, 2, device=dev))
+    first = layer_w()
+    per_w = sum(w4_bytes(first[k]) for k in ("qkv", "z", "o"))
+    per = (per_w + 2 * HV * Hd * 2 + C * 4 * 2 + 2 * C * 3 * 2 + 2 * HV * DH * DH * 4 + 2 * M * Hd * 2 + Hd * 2 + DH * 2)
+    ring_n = _ring_count(per)
+    ring = [first] + [layer_w() for _ in range(ring_n - 1)]
+    dt_bias = torch.rand(HV, generator=gen, device=dev) * 2 - 1
+    g_decay = -torch.exp(torch.rand(HV, generator=gen, device=dev) * 1.5 - 1)
+    gnw = (1 + 0.1 * torch.randn(DH, generator=gen, device=dev)).bfloat16()
+    nw = (1 + 0.02 * torch.randn(Hd, generator=gen, device=dev)).bfloat16()
+    x = torch.randn(M, Hd, generator=gen, device=dev).bfloat16()
+    xo, xn = torch.empty_like(x), torch.empty_like(x)
+    proj = torch.empty(M, C, **bf)
+    z = torch.empty(M, HV * DH, **bf)
+    core = torch.empty(M, HV * DH, **bf)
+    q2 = torch.empty(M, HV * DH, dtype=torch.int8, device=dev)
+    s2 = torch.empty(M, dtype=torch.float32, device=dev)
+    # nothing pending; a chain of M verify rows, each committed (program bit 5)
+    ctl = torch.tensor([0, 0] + [0] * S + [r - 1 for r in range(M)] + [-1] * (S - M) + [r | 32 for r in range(M)]
+                       + [0] * (S - M), dtype=torch.int32, device=dev)
+
+    def call(i):
+        w = ring[i]
+        q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
+        _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
+        _C.gdn_core(proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay,
+                    w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True)
+        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnw), 1e-6, _lib.ptr(core), None,
+                  _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), M, HV * DH, _lib.stream_of(core))
+        _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
+
+    t = ring_time(call, ring_n, args.steps, args.warmup)
+    gbs = per / t / 1e9
+    return _line(args, round(gbs, 2), "GB/s", t, args.steps, "W4A8 int8 x int4 -> int32; fp32 recurrent state",
+                 "synthetic (seeded GPTQ int4 weights, integral 4-bit group scales; state N(0, 0.1))",
+                 {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
+                              f"{ring_n}-copy weight + state ring", "rows": M,
+                  "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                  "launches_per_step": 6})
+
+
+def bench_read(args, dev):
+    """Single-launch read roofs: one streaming read (the GEMV's load pattern, libmdx's calibration
+    kernel) per launch at the decode path's matrix sizes, over a ring of buffers > 2x the Infinity
+    Cache, for several work-group counts. The best per size is the roof a one-launch GEMV of that size
+    can reach."""
+    import torch
+    from mdx import _lib
+    sizes = {"8.7MB": 8679424, "26MB": 25990144, "52MB": 52031488, "78MB": 77996032}
+    buf_bytes = max(sizes.values())
+    ring_n = -(-2 * 256 * 2 ** 20 // min(sizes.values())) + 1
+    bufs = [torch.ones(buf_bytes // 4, dtype=torch.int32, device=dev) for _ in range(min(ring_n, 16))]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {}
+    for key, nbytes in sizes.items():
+        nbytes = nbytes // 1024 * 1024
+        # distinct regions (buffer, offset) of this size, enough to exceed 2x the cache
+        regions = [b.data_ptr() + off for off in range(0, buf_bytes - nbytes + 1, nbytes) for b in bufs]
+        rn = min(len(regions), max(2, -(-2 * 256 * 2 ** 20 // nbytes) + 1))
+        best = None
+        for wgs in (256, 512, 768, 1024, 2048):
+            t = ring_time(lambda i: _lib.call("mdx_stream_read", ctypes.c_void_p(regions[i]), nbytes, wgs,
+                                              _lib.ptr(sink), _lib.stream_of(sink)), rn, args.steps, args.warmup)
+            gbs = nbytes / t / 1e9
+            out[f"{key}_wg{wgs}"] = {"us": round(t * 1e6, 3), "gbs": round(gbs, 1)}
+            best = gbs if best is None else max(best, gbs)
+        out[key] = round(best, 1)
+    roof = {k: v for k, v in out.items() if "_wg" not in k}
+    return {"metric": "single-launch streaming read GB/s", "value": roof["52MB"], "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": "read roof per launch size (calibration)", "roof_gbs": roof},
+            "detail": {k: v for k, v in out.items() if "_wg" in k}}
 
 
 def bench_copy(args, dev):
@@ -340,10 +573,10 @@ def bench_copy(args, dev):
     n = 256 * 2 ** 20
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    reps = max(1, args.steps // 100)
-    t = graph_time(lambda: dst.copy_(src), reps, args.warmup)
+    steps = max(1, args.steps // 100)
+    t = ring_time(lambda i: dst.copy_(src), 1, steps, args.warmup)
     return {"metric": "device copy GB/s (read + write)", "value": round(2 * n / t / 1e9, 2), "unit": "GB/s",
-            "n_gpus": 1, "steps": reps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5),
+            "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
             "config": {"workload": "copy of 256 MiB (traffic calibration)", "bytes_read": n, "bytes_written": n}}
 
@@ -354,7 +587,9 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1)
-    ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn", "stack"], default="mlp")
+    ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn", "stack", "read", "attn_layer",
+                                           "gdn_layer"], default="mlp")
+    ap.add_argument("--tokens", type=int, default=0, help="stack: decode until this many tokens are committed")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -371,14 +606,18 @@ def main():
         print(json.dumps({"error": "no ROCm device"}))
         sys.exit(1)
     dev = torch.device("cuda", 0)
-    res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
-           "attn": bench_attn, "stack": bench_stack}[args.workload](args, dev)
+    if args.workload == "stack":
+        res = bench_stack(args, dev, tokens=args.tokens)
+    else:
+        res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
+               "attn": bench_attn, "read": bench_read, "attn_layer": bench_attn_layer,
+               "gdn_layer": bench_gdn_layer}[args.workload](args, dev)
     if args.workload == "mlp" and not args.no_decode:
         # the second half of the metric: decode tok/s of the full synthetic hybrid stack (1024-token
-        # prompt, 64 graph-replayed steps)
+        # prompt, 512 tokens decoded by graph-replayed steps)
         sub = argparse.Namespace(**vars(args))
-        sub.steps, sub.warmup, sub.prompt = 64, 4, 1024
-        d = bench_stack(sub, dev)
+        sub.steps, sub.warmup, sub.prompt = 0, 4, 1024
+        d = bench_stack(sub, dev, tokens=512)
         res["decode"] = {"metric": "decode tok/s at 9B hybrid, 8-draft tree", "value": d["value"], "unit": "tok/s",
                          "ms_per_step": d["config"]["ms_per_step"],
                          "accepted_per_step": d["config"]["accepted_per_step"], "workload": d["config"]["workload"]}

@@ -52,10 +52,14 @@ __global__ __launch_bounds__(WAVE) void rope_kv_kernel(RopeArgs a) {
     const int s = blockIdx.x / H, h = blockIdx.x % H;
     const int D = a.D, per = D / WAVE;
     const int64_t p = a.pos[s];
+    // a position outside the cache writes nothing (the callers bound their positions on the host;
+    // this keeps a bad position from writing past the cache)
+    const bool in_cache = p >= 0 && p < a.cap;
     if (h >= a.Hq + a.Hk) {  // v: cache write only
         const int hv = h - a.Hq - a.Hk;
-        for (int d = lane; d < D; d += WAVE)
-            a.value[(int64_t(hv) * a.cap + p) * D + d] = a.v[s * a.vs + hv * a.vh + d];
+        if (in_cache)
+            for (int d = lane; d < D; d += WAVE)
+                a.value[(int64_t(hv) * a.cap + p) * D + d] = a.v[s * a.vs + hv * a.vh + d];
         return;
     }
     const bool isq = h < a.Hq;
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(WAVE) void rope_kv_kernel(RopeArgs a) {
         }
         const uint16_t ob = f2bf(o);
         dst[d] = ob;
-        if (!isq) a.key[(int64_t(hh) * a.cap + p) * D + d] = ob;
+        if (!isq && in_cache) a.key[(int64_t(hh) * a.cap + p) * D + d] = ob;
     }
 }
 

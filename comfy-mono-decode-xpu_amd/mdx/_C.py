@@ -372,14 +372,19 @@ def topk_sample(values, indices, uniform, temperature, out=None):
 
 
 _ATTN_WS = {}
+_ATTN_WS_RETIRED = []
 
 
 def _attn_ws(dev, nbytes):
     """Per-device attention workspace, grown on demand (zeroed when allocated; launches keep their
-    counters at zero). Growing happens outside graph capture: warm up once per shape before capturing."""
+    counters at zero). Growing happens outside graph capture: warm up once per shape before capturing.
+    A workspace that is outgrown stays allocated for the life of the process: a graph captured
+    earlier still holds its address."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _ATTN_WS.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _ATTN_WS_RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _ATTN_WS[key] = ws
     return ws

@@ -97,6 +97,7 @@ SIGNATURES = {
     "mdx_draft_silu_mul": (ctypes.c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_draft_norm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int32, c_void_p,
                                                 c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "mdx_stream_read": (ctypes.c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
 }
 
 _lib = None

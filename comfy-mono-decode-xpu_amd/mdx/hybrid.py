@@ -201,6 +201,20 @@ class HybridModel:
         self.dlogits = torch.zeros(1, c.vocab, **bf)
         self.empty_mask = torch.empty(0, dtype=torch.int32, device=dev)
         self.graphs = {}
+        # host-side upper bound of the committed position st[0]: every KV write of a step lands at
+        # most R - 1 past it, and each step commits at most len(widths) + 1 tokens
+        self.pos_bound = None
+
+    def _reserve(self, steps):
+        """Raise before launching `steps` decode steps whose KV writes could pass the cache capacity."""
+        if self.pos_bound is None:
+            raise RuntimeError("prefill() first")
+        per = len(self.cfg.widths) + 1
+        need = self.pos_bound + steps * per + self.R
+        if need > self.cfg.cap:
+            raise RuntimeError(f"{steps} more decode steps may write KV position {need - 1}, past the cache capacity "
+                               f"{self.cfg.cap}")
+        self.pos_bound += steps * per
 
     # ---- the pieces of a step ------------------------------------------------------------------
     def _attn_layer(self, i, x, R, mask, seq, pos, freqs):
@@ -305,7 +319,10 @@ class HybridModel:
         return _C.fast_topk(self.dlogits, width, False)[1]
 
     def step(self, parity):
-        """One decode step on the device (drafts, verify, sampling, accept)."""
+        """One decode step on the device (drafts, verify, sampling, accept). An eager step checks the
+        KV capacity itself; a captured one is checked when its graph is replayed."""
+        if not torch.cuda.is_current_stream_capturing():
+            self._reserve(1)
         c, T = self.cfg, self.tree
         R = self.R
         # drafts: depth k proposes the children of chain node k
@@ -340,6 +357,9 @@ class HybridModel:
         S = c.slots
         dev = self.dev
         prompt = prompt.to(dev)
+        if prompt.numel() < 2 or prompt.numel() + self.R > c.cap:
+            raise RuntimeError(f"prompt of {prompt.numel()} tokens: needs 2 <= tokens and tokens + {self.R} tree rows "
+                               f"<= the cache capacity {c.cap}")
         body = prompt[:-1]
         n0, parity = 0, 0
         while n0 < body.numel():
@@ -369,6 +389,7 @@ class HybridModel:
             n0 += n
         self.nt.fill_(int(prompt[-1].item()))
         self.parity = parity
+        self.pos_bound = body.numel()
 
     # ---- graphs ----------------------------------------------------------------------------------
     def capture(self):
@@ -386,6 +407,7 @@ class HybridModel:
             self.graphs[p] = g
 
     def replay(self, steps):
+        self._reserve(steps)
         for _ in range(steps):
             self.graphs[self.parity].replay()
             self.parity ^= 1

@@ -367,6 +367,13 @@ int mdx_draft_silu_mul(const uint16_t* gu, int64_t gu_row_stride, const uint16_t
 int mdx_draft_norm_rot_quant(uint16_t* x, const uint16_t* h, const uint16_t* w, float eps, int32_t rot, uint16_t* xr,
                              int8_t* qx, float* sx, int64_t rows, int64_t H, void* stream);
 
+/* Calibration: one streaming read of `bytes` (a multiple of 1024) from `src` with the W4A8 GEMV's load
+ * pattern (1 KiB per wave instruction, four loads in flight per wave), over `work_groups` work-groups
+ * of 256 threads; `sink` (4 bytes) is written only if the data hashes to a marker value. It has no
+ * counterpart in the reference: it measures the read roof a single launch of a given size reaches,
+ * beside the 8 TB/s spec figure. */
+int mdx_stream_read(const void* src, int64_t bytes, int32_t work_groups, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
