@@ -35,7 +35,6 @@
 // Split-K partial sums of the waves of a work-group are int32 and are added through LDS:
 // integer addition is associative, so every split gives the same bits.
 #include <algorithm>
-#include <mutex>
 #include <stdio.h>
 #include <vector>
 #include <stdlib.h>
@@ -66,29 +65,6 @@ __device__ __forceinline__ uint4 ldg_stream(const void* p) {
 __device__ __forceinline__ uint4 ldg_stream(const MDX_G uint8_t* p) {
     const v4u v = __builtin_nontemporal_load(reinterpret_cast<const MDX_G v4u*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// Device-coherent plain accesses for data handed between work-groups of one launch: relaxed
-// agent-scope atomics (they bypass the non-coherent cache state instead of writing back and
-// invalidating whole caches, which is what an agent-scope fence costs on a multi-XCD chip).
-template <typename T>
-__device__ __forceinline__ T ld_c(const T* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ void st_c(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Hand-off: once every thread's coherent stores / atomics have completed (vector memory counter at
-// zero), one thread bumps the counter.
-__device__ __forceinline__ uint32_t publish(uint32_t* ctr) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t old = 0;
-    if (threadIdx.x == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return old;
 }
 
 // =================================================================================================
@@ -123,8 +99,7 @@ struct PrepArgs {
 // Canonical RMSNorm sum: per group, lane partial ((sq0 + sq1) + sq2) + sq3 of its four squares, the
 // halving tree over the 64 lanes (l + 32, + 16, ..., + 1), then the group sums added in group order.
 // The work-group's waves (any count) share the row; gsum holds K / 256 floats, wmax one per wave.
-// COH: the q / scale outputs are read by other work-groups of the same launch (coherent stores).
-template <int GPW, bool COH = false>
+template <int GPW>
 __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float* gsum, float* wmax) {
     const int W = blockDim.x / WAVE, w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int K = a.K, G = K / 256;
@@ -250,10 +225,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     __syncthreads();
     const float rm = wave_max_nn(lane < W ? wmax[lane] : 0.f);
     const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
-    if (threadIdx.x == 0) {
-        if (COH) st_c(reinterpret_cast<uint32_t*>(a.scale) + row, __float_as_uint(s));
-        else a.scale[row] = s;
-    }
+    if (threadIdx.x == 0) a.scale[row] = s;
     uint16_t sb = f2bf(s);
     if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
     // quant_rcp: the code of v is rint(bf16(v / sb)), the quotient rounded to fp32, then bf16. It is
@@ -276,8 +248,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
                 o |= (uint32_t(qv) & 0xFFu) << (8 * e);
             }
             uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + int64_t(row) * K + 256 * g + 4 * lane);
-            if (COH) st_c(qp, o);
-            else *qp = o;
+            *qp = o;
         }
     }
 }
@@ -305,7 +276,7 @@ int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
 // =================================================================================================
 // GEMV engine
 // =================================================================================================
-enum Epi : int { EPI_STORE = 0, EPI_SILU = 1, EPI_ACC = 2 };
+enum Epi : int { EPI_STORE = 0, EPI_SILU = 1 };
 
 struct MatArg {
     const uint8_t* q;
@@ -335,13 +306,6 @@ struct GemvArgs {
     const void* res[3];
     int out_dt;
     const uint16_t* lut;  // EPI_SILU
-    // EPI_ACC (one matrix, TPW 1, each tile's K range split over `split` work units): the units add
-    // their int32 sums into acc [rows, N]; the tile's last unit (counter tcnt[tile]) applies the
-    // store epilogue and leaves acc and tcnt at zero again
-    int32_t* acc;
-    uint32_t* tcnt;
-    int split;
-    int coh;              // EPI_SILU outputs are read within the launch: coherent stores
     // EPI_SILU with hmax_out (one gate/up pair per work-group): work-group wg also stores its rows'
     // |h| maxima (fp32 bits) at hmax_out[wg * 16 + row]
     uint32_t* hmax_out;
@@ -363,19 +327,6 @@ struct GemvArgs {
 enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
 constexpr int XP_GPW = 4;
 constexpr int HMW = 16;  // SRC_HR: maxima per lane when every wave reads them all (<= 1024 work-groups)  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
-
-// What a work unit waits for before it stages its activation, and where the activation comes from.
-// Data handed between work-groups of one launch is written with coherent (write-through) stores and
-// read with ordinary loads only after the hand-off: nothing reads those lines earlier in the launch,
-// and a kernel starts with no stale lines in the L2s, so the first read misses and fetches the data
-// (later readers on the same XCD hit the L2).
-struct UnitIn {
-    const uint32_t* wait;   // null, or wait until *wait >= wait_for (flags: coherent loads)
-    uint32_t wait_for;
-    uint32_t* err;          // set to 1 if a wait gives up
-    const uint16_t* hr;     // null: int8 rows a.xq with scales a.xs; else bf16 rows [rows, K] quantised
-    const uint32_t* amax;   //   here with the rows' absmax (fp32 bits) from amax
-};
 
 struct Lut {
     uint32_t w[4];
@@ -522,27 +473,8 @@ __device__ __forceinline__ int32_t reduced(const GemvArgs& a, const int32_t* red
     return int32_t(s);
 }
 
-// Thread 0 polls *p until it reaches `target` (sleeping between polls), then the work-group
-// continues; what it reads next must be read with coherent loads. The poll is bounded: after about
-// 2^22 polls (seconds) it sets *err and gives up, so a broken producer costs wrong results, never a
-// hung GPU.
-__device__ __forceinline__ void wait_count(const uint32_t* p, uint32_t target, uint32_t* err) {
-    if (threadIdx.x == 0) {
-        uint32_t n = 0;
-        while (ld_c(p) < target) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++n == (1u << 22)) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-}
-
 template <bool MFMA>
-__device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, const float* prml, int* flag) {
+__device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, const float* prml) {
     const int per = 16 * a.rows;
     const float* xsl = prml + a.TPW * 16;
     if (a.epi == EPI_SILU) {
@@ -560,8 +492,7 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
                                                 xsl[r], prml[sg * 16 + c + 1], prml[su * 16 + c + 1]))
                                 << 16);
             uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + tile * 16 + c);
-            if (a.coh) st_c(o, v);
-            else *o = v;
+            *o = v;
             if (a.hmax_out) {
                 // the row's |h| maximum over the 8 threads of this row (the work-group's one pair; NaN
                 // counts as 0, as in the row prep's fmaxf from 0), stored as this work-group's entry
@@ -572,44 +503,6 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
                 if ((rem & 7) == 0) a.hmax_out[r * gridDim.x + wg] = __float_as_uint(m != m ? 0.f : m);
             }
         }
-        return;
-    }
-    if (a.epi == EPI_ACC) {
-        // the unit's TPW tiles (tile wg TPW + ts): int32 sums into acc, one hand-off, then each tile
-        // whose last part this was stores its outputs; *flag = the number of tiles completed here
-        const int N = a.m[0].n, tiles = a.m[0].tiles;
-        for (int e = threadIdx.x; e < a.TPW * per; e += blockDim.x) {
-            const int ts = e / per, rem = e - ts * per, r = rem >> 4, c = rem & 15;
-            const int tile = wg * a.TPW + ts;
-            if (tile < tiles)
-                __hip_atomic_fetch_add(a.acc + r * N + tile * 16 + c, reduced<MFMA>(a, red, ts, r, c), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0) *flag = 0;
-        __syncthreads();
-        const int my = wg * a.TPW + int(threadIdx.x);
-        if (int(threadIdx.x) < a.TPW && my < tiles &&
-            __hip_atomic_fetch_add(a.tcnt + my, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(a.split - 1)) {
-            atomicOr(flag, 1 << threadIdx.x);
-            __hip_atomic_store(a.tcnt + my, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        const int done = *flag;
-        for (int e = threadIdx.x; e < a.TPW * per; e += blockDim.x) {
-            const int ts = e / per, rem = e - ts * per, r = rem >> 4, c = rem & 15;
-            if (!((done >> ts) & 1)) continue;
-            const int tile = wg * a.TPW + ts;
-            int32_t* p = a.acc + r * N + tile * 16 + c;
-            const int32_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            store_out(a, 0, tile * 16 + c, r, v, xsl[r], prml[ts * 16 + c]);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) *flag = __popc(done);
-        __syncthreads();
         return;
     }
     for (int ts = 0; ts < a.TPW; ++ts) {  // one tile slot at a time: the matrix choice stays uniform
@@ -679,13 +572,9 @@ __device__ __forceinline__ void unit_groups(int cu0, int ncu, int lgG, int ng, i
 // is merged at the join and waited for at once, which leaves one load in flight per wave): a chunk
 // past the slice re-reads the slice's last chunk and adds nothing. Everything that selects a
 // matrix or a tile is wave-uniform (scalar registers).
-// PRE: the ring's first RING loads were issued by issue_ring (same unit) and arrive in `pre`.
-// EPI false: the unit ends after its reduction operands are in LDS; the caller runs the epilogue
-// (after a barrier) with the pointers of unit_lds.
 // SRC: where the activation comes from (Src).
-template <bool MFMA, int R, int SDT, int RING, bool PRE = false, bool EPI = true, int SRC = SRC_Q8>
-__device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds,
-                                          const UnitIn& in, int* flag, const uint4* pre = nullptr) {
+template <bool MFMA, int R, int SDT, int RING, int SRC = SRC_Q8>
+__device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint8_t* lds) {
     constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
     const int K = a.K;
     const int ng = K >> a.lgG;
@@ -720,11 +609,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 
     // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
     constexpr bool HR = SRC == SRC_HR, XP = SRC == SRC_XP;
-    const bool own_x = !in.wait && SRC == SRC_Q8;  // int8 rows a.xq staged by this prologue
+    const bool own_x = SRC == SRC_Q8;  // int8 rows a.xq staged by this prologue
     // Per-wave one-shots (a.pwo): each wave stages only what it reads, its slice's activation run
     // (the TPW waves of a slice write the same bytes) and its tile's scales of its slice's groups
     // into a region of its own, so no wave waits for another before its loop.
-    const bool pwo = a.pwo && !MFMA && !in.wait;  // (uniform)
+    const bool pwo = a.pwo && !MFMA;  // (uniform)
     const int sbw = (ncu / a.KS) * ESZ;                               // pwo: scale bytes per tile row
     uint8_t* swv = sl + wave * 16 * sbw;                              // pwo: [16][sbw]
     if (pwo && SRC == SRC_Q8) {
@@ -842,66 +731,12 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     const int last = nch > 0 ? nch - 1 : 0;
     uint4 buf[RING];
 #pragma unroll
-    for (int p = 0; p < RING; ++p) buf[p] = PRE ? pre[p] : ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
+    for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
     const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
     if (t == 0) *mixed = 0;
     if (t < 8) reinterpret_cast<uint32_t*>(zeros)[t] = 0u;
 
-    // 3. an activation produced in this launch: wait for it, then stage the rows' K range
-    if (in.wait) {
-        wait_count(in.wait, in.wait_for, in.err);
-        if (in.hr) {
-            // bf16 rows quantised with the row scale max(absmax / 127, 1e-30) (the row prep's formula).
-            // The rows' pieces (16 bytes, up to HB per thread) and the rows' absmax are loaded
-            // together (one memory round trip), then quantised: bf16(v / sb) as bf16(v * fl32(1 / sb))
-            // (quant_rcp).
-            constexpr int HB = 8;
-            float* rcp = prml + 96;  // [rows]
-            const int per_row = Kr / 8, total = a.rows * per_row;
-            for (int base = 0; base < total; base += HB * nthr) {
-                uint4 raw[HB];
-#pragma unroll
-                for (int k = 0; k < HB; ++k) {
-                    const int i = min(base + k * nthr + t, total - 1);
-                    const int r = i / per_row, j = i - r * per_row;
-                    raw[k] = *reinterpret_cast<const uint4*>(in.hr + r * K + cu0 * CHUNK_K + 8 * j);
-                }
-                if (base == 0) {
-                    if (t < a.rows) {
-                        const float s = fmaxf(__fdiv_rn(__uint_as_float(ld_c(in.amax + t)), 127.0f), 1e-30f);
-                        uint16_t sb = f2bf(s);
-                        if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
-                        prml[a.TPW * 16 + t] = s;
-                        rcp[t] = __fdiv_rn(1.f, bf2f(sb));
-                    }
-                    __syncthreads();
-                }
-#pragma unroll
-                for (int k = 0; k < HB; ++k) {
-                    const int i = base + k * nthr + t;
-                    if (i < total) {
-                        const int r = i / per_row, j = i - r * per_row;
-                        const float rr = rcp[r];
-                        const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-                        uint32_t o[2] = {0u, 0u};
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
-                            const float d = bfround(__fmul_rn(v, rr));
-                            o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
-                        }
-                        *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
-                    }
-                }
-            }
-        } else {
-            dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xq)) + cu0 * CHUNK_K, K, Kr, a.rows, xl, nthr);
-            if (t < a.rows) prml[a.TPW * 16 + t] = a.xs[t];
-        }
-    }
-    if (in.wait) {
-        __syncthreads();
-    } else if (pwo) {
+    if (pwo) {
         // this wave's one-shots are complete once at most RING loads remain; no other wave's matter
         __builtin_amdgcn_s_waitcnt((RING & 15) | ((RING >> 4) << 14) | (7 << 4) | (15 << 8));
     } else {
@@ -1177,48 +1012,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // wait that would also wait for the ring)
     if (slice == 0 && lane < 16) prml[ts * 16 + lane] = prm;
     else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
-    if (!EPI) return;
     __syncthreads();
-    epilogue<MFMA>(a, wg, red, prml, flag);
-}
-
-// The reduction block and parameters of a unit in LDS (gemv_unit's layout), for a caller-run epilogue.
-template <bool MFMA, int SDT>
-__device__ __forceinline__ void unit_lds(const GemvArgs& a, const int cu0, const int ncu, uint8_t* lds, int32_t*& red,
-                                         float*& prml) {
-    constexpr int ESZ = SDT == MDX_DT_F32 ? 4 : (SDT == MDX_DT_F16 ? 2 : 1);
-    int g0, g1;
-    unit_groups(cu0, ncu, a.lgG, a.K >> a.lgG, ESZ, g0, g1);
-    const int seg = (g1 - g0) * ESZ;
-    uint8_t* sl = lds + ((a.rows * ncu * CHUNK_K + 1023) & ~1023);
-    red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
-    prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
-}
-
-// The first RING weight loads of a single-matrix unit (tiles wg TPW + ts, chunks [cu0, cu0 + ncu)
-// over KS slices), issued ahead of the unit itself (gemv_unit with PRE).
-template <int RING>
-__device__ __forceinline__ void issue_ring(const GemvArgs& a, const int wg, const int cu0, const int ncu, uint4* out) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
-    const int ts = wave / a.KS, slice = wave % a.KS;
-    const int K = a.K, NC = K / CHUNK_K;
-    const int mt = wg * a.TPW + ts;
-    const bool live = mt < a.m[0].tiles;
-    const int c0 = live ? cu0 + slice * ncu / a.KS : 0, c1 = live ? cu0 + (slice + 1) * ncu / a.KS : 0;
-    const int nch = c1 - c0, last = nch > 0 ? nch - 1 : 0;
-    const MDX_G uint8_t* mq = as_global(a.m[0].q);
-    const int tile = live ? mt : 0;
-    const MDX_G uint8_t* wp;
-    int wstride;
-    if (a.layout == MDX_LAYOUT_TILE) {
-        wp = mq + (tile * NC + c0) * 1024 + lane * 16;
-        wstride = 1024;
-    } else {
-        wp = mq + (tile * 16 + (lane & 15)) * (K / 2) + c0 * 64 + (lane >> 4) * 16;
-        wstride = 64;
-    }
-#pragma unroll
-    for (int p = 0; p < RING; ++p) out[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
+    epilogue<MFMA>(a, wg, red, prml);
 }
 
 // SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
@@ -1226,8 +1021,7 @@ __device__ __forceinline__ void issue_ring(const GemvArgs& a, const int wg, cons
 template <bool MFMA, int R, int SDT, int RING, int SRC = SRC_Q8>
 __global__ __launch_bounds__(SRC == SRC_HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ int flag;
-    gemv_unit<MFMA, R, SDT, RING, false, true, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds, UnitIn{}, &flag);
+    gemv_unit<MFMA, R, SDT, RING, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds);
 }
 
 // LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
@@ -1457,158 +1251,6 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     return launch_gemv_d<4>(a, ws[0]->s_dtype, mfma, wgs, st);
 }
 
-// =================================================================================================
-// The fused MLP after the row prep of x: gate/up, the rotation of h and down in one launch.
-// Work-group u runs
-//   1. gate/up tile pair u (SiLU epilogue -> h, coherent stores); the last of the 16 pairs of a
-//      256-column group rotates that group of every row -> hr and raises the rows' absmax;
-//   2. down unit u (four tiles, one per wave, over K part u % split): its whole weight share is
-//      requested right after the pair's stream (before the pair's epilogue), so the down weights
-//      arrive while the gate/up pairs finish; after "h is rotated" it quantises its K part of hr,
-//      adds its int32 sums into acc, and each tile's last part stores out (+ residual); the last
-//      tile re-zeroes the control words.
-// Every work-group waits for work of every other one, so the launch requires all of them resident
-// at once: the host launches it only when the occupancy query admits the whole grid, and each wait
-// is bounded (a broken hand-off costs wrong results and an error flag, never a hung GPU).
-// Hand-offs use coherent loads / stores and one counter bump per unit: no cache-wide fences and
-// no per-launch ticket counter (device atomics on one address serialise at ~11 ns each).
-// =================================================================================================
-enum : int { SY_GROUPS = 1, SY_TILES = 2, SY_ERR = 4, SY_HDR = 8 };
-// "h is rotated" is broadcast to FLAG_N words FLAG_STRIDE words apart (different memory channels),
-// unit u polling word u % FLAG_N: a thousand work-groups polling one word would queue on one
-// channel and stall every weight stream that crosses it.
-constexpr int FLAG_N = 64, FLAG_STRIDE = 64;
-constexpr int CH_WAVES = 4;      // waves per work-group
-constexpr int CH_MAX_G1 = 64;    // 256-column groups of h at most (N1 <= 16384)
-constexpr int CH_MAX_K1 = 4096;  // down outputs at most (the acc block)
-constexpr int DN_RING = 8;       // down weights requested ahead per wave: a unit's whole share (8 chunks)
-
-struct MlpFused {
-    uint32_t* flags;      // [FLAG_N][FLAG_STRIDE]: h ready
-    GemvArgs gu, dn;      // gate/up pair (EPI_SILU into hb), down (EPI_ACC over K parts)
-    const uint16_t* hb;   // h [rows, N1]
-    uint16_t* hr;         // rotated h [rows, N1] (hb itself without rotation)
-    uint32_t* amax;       // [16] row absmax of hr, fp32 bits
-    uint32_t* sync;       // [SY_HDR + G1] control words, zero between launches
-    int rows, rot, n_gu, n_dn, G1, dn_cu;
-};
-
-template <bool MFMA, int R, int SDT>
-__global__ __launch_bounds__(CH_WAVES * WAVE) void mlp_fused_kernel(MlpFused c) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ int flag;
-    const int t = threadIdx.x;
-    const int u = blockIdx.x;
-    const int grp = u / c.dn.split, part = u - grp * c.dn.split;  // down: tiles 4 grp .. 4 grp + 3, K part
-    uint4 dring[DN_RING];
-    if (u < c.n_gu) {
-        // the gate/up pair's stream, then this work-group's down weights are requested (they arrive
-        // while the pair's epilogue, the rotation of h and the wait run), then the pair's epilogue
-        gemv_unit<MFMA, R, SDT, 4, false, false>(c.gu, u, 0, c.gu.K / CHUNK_K, lds, UnitIn{}, &flag);
-        if (u < c.n_dn) issue_ring<DN_RING>(c.dn, grp, part * c.dn_cu, c.dn_cu, dring);
-        __syncthreads();
-        {
-            int32_t* red;
-            float* prml;
-            unit_lds<MFMA, SDT>(c.gu, 0, c.gu.K / CHUNK_K, lds, red, prml);
-            epilogue<MFMA>(c.gu, u, red, prml, &flag);
-        }
-        const int g = u >> 4;
-        const uint32_t old = publish(c.sync + SY_HDR + g);
-        if (t == 0) flag = old == 15u;
-        __syncthreads();
-        if (flag) {
-            // group g of h is complete: rotate it (one wave per row), row absmax by atomic max of the
-            // non-negative fp32 bits (the same maximum as fmaxf over the waves of a row prep)
-            const int w = t / WAVE, lane = t % WAVE, N1 = c.gu.m[0].n;
-            for (int r = w; r < c.rows; r += CH_WAVES) {
-                float x[4];
-                unpack4(*reinterpret_cast<const uint2*>(c.hb + r * N1 + 256 * g + 4 * lane), x);
-                if (c.rot == MDX_ROT_H256) {
-                    double d[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) d[e] = double(x[e]);
-                    fwht256_lane(d, lane);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] = bfround(float(__dmul_rn(d[e], 0.0625)));
-                    const uint2 o = pack4(x);
-                    st_c(reinterpret_cast<uint64_t*>(c.hr + r * N1 + 256 * g + 4 * lane),
-                         uint64_t(o.x) | (uint64_t(o.y) << 32));
-                }
-                float m = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(x[e]));
-                m = wave_max(m);
-                if (lane == 0)
-                    __hip_atomic_fetch_max(c.amax + r, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            if (t == 0) st_c(c.sync + SY_HDR + g, 0u);
-            const uint32_t og = publish(c.sync + SY_GROUPS);
-            if (t == 0) flag = og == uint32_t(c.G1 - 1);
-            __syncthreads();
-            if (flag && t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 1u);
-        }
-        __syncthreads();  // the down unit below reuses the LDS
-    }
-    if (u >= c.n_dn) return;
-    if (u >= c.n_gu) issue_ring<DN_RING>(c.dn, grp, part * c.dn_cu, c.dn_cu, dring);
-    gemv_unit<MFMA, R, SDT, DN_RING, true>(c.dn, grp, part * c.dn_cu, c.dn_cu, lds,
-                                           UnitIn{c.flags + (u % FLAG_N) * FLAG_STRIDE, 1u, c.sync + SY_ERR, c.hr, c.amax},
-                                           &flag, dring);
-    // flag: the number of tiles this unit completed. When every tile is complete, every unit of the
-    // launch is past its waits: the control words go back to zero for the next launch.
-    if (!flag) return;
-    __syncthreads();
-    if (t == 0)
-        flag = __hip_atomic_fetch_add(c.sync + SY_TILES, uint32_t(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
-                   uint32_t(flag) == uint32_t(c.dn.m[0].tiles);
-    __syncthreads();
-    if (flag) {
-        if (t < FLAG_N) st_c(c.flags + t * FLAG_STRIDE, 0u);
-        if (t < 16) st_c(c.amax + t, 0u);
-        if (t == 0) {
-            st_c(c.sync + SY_GROUPS, 0u);
-            st_c(c.sync + SY_TILES, 0u);
-        }
-    }
-}
-
-template <bool MFMA, int R, int SDT>
-const void* fused_fn() {
-    return reinterpret_cast<const void*>(&mlp_fused_kernel<MFMA, R, SDT>);
-}
-
-const void* fused_kernel(int sdt, bool mfma) {
-    if (sdt == MDX_DT_F32) return mfma ? fused_fn<true, 4, MDX_DT_F32>() : fused_fn<false, 1, MDX_DT_F32>();
-    if (sdt == MDX_DT_F16) return mfma ? fused_fn<true, 4, MDX_DT_F16>() : fused_fn<false, 1, MDX_DT_F16>();
-    return mfma ? fused_fn<true, 4, MDX_DT_FP8E4M3>() : fused_fn<false, 1, MDX_DT_FP8E4M3>();
-}
-
-// Whether `grid` work-groups of `fn` (CH_WAVES waves, `smem` bytes of LDS) are resident at once on
-// the current device: the occupancy query times the CU count (cached per kernel, LDS size, device).
-bool all_resident(const void* fn, size_t smem, int grid) {
-    struct Entry {
-        const void* fn;
-        size_t smem;
-        int dev, capacity;
-    };
-    static std::mutex mu;
-    static std::vector<Entry> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Entry& e : cache)
-        if (e.fn == fn && e.smem == smem && e.dev == dev) return grid <= e.capacity;
-    int cus = 0, per = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, CH_WAVES * WAVE, smem) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    cache.push_back(Entry{fn, smem, dev, cus * per});
-    return grid <= cus * per;
-}
-
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int prep_checks(int64_t rows, int64_t K, int32_t rot, const void* h, const void* x = nullptr, const void* q = nullptr,
@@ -1729,25 +1371,15 @@ extern "C" int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t
 namespace mdx {
 namespace {
 
-// Workspace of mdx_mono_mlp. First the zero-state part, at the same offsets whatever the shapes (a
-// call with fewer rows must not find its control words or accumulators inside the data of an
-// earlier call with more rows): control words [SY_HDR + CH_MAX_G1] | amax [16] | tile counters
-// [CH_MAX_K1 / 16] in a 4 KiB header, the broadcast flags [FLAG_N][FLAG_STRIDE], then
-// acc [16, CH_MAX_K1] int32. It must be zero before the
-// first call and every call leaves it zero (each call re-zeroes exactly what it used). Then,
-// 256-byte aligned, the data: q1 [rows, K1] | q2 [rows, N1] | scales [64] f32 | h [rows, N1] bf16 |
-// rotated h [rows, N1] bf16.
+// Workspace of mdx_mono_mlp (256-byte aligned pieces): a 4 KiB header whose word MLP_ERR is the error
+// word (no launch of this library waits on another work-group, so it stays zero), then the gate/up
+// work-groups' |h| maxima [16][N1 / 16] (fp32 bits, row-major), q1 [rows, K1] int8 | q2 [rows, N1]
+// int8 | scales [64] f32 | h [rows, N1] bf16 | rotated h [rows, N1] bf16.
 constexpr size_t MLP_HDR = 4096;
-constexpr size_t MLP_FLAGS = size_t(FLAG_N) * FLAG_STRIDE * 4;
-static_assert((SY_HDR + CH_MAX_G1 + 16 + CH_MAX_K1 / 16) * 4 <= MLP_HDR, "header");
+constexpr size_t MLP_ERR = 4;
 
 struct MlpWs {
-    uint32_t* flags;
-    uint32_t* hmax;  // [rows <= 2][N1 / 16] the gate/up work-groups' |h| maxima, row-major
-    uint32_t* sync;
-    uint32_t* amax;
-    uint32_t* tcnt;
-    int32_t* acc;
+    uint32_t* hmax;  // [rows][N1 / 16] the gate/up work-groups' |h| maxima, row-major
     int8_t* q1;
     int8_t* q2;
     float* s;
@@ -1765,13 +1397,8 @@ MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
         off += align256(bytes);
         return q;
     };
-    uint32_t* hdr = reinterpret_cast<uint32_t*>(take(MLP_HDR));
-    w.sync = hdr;
-    w.amax = hdr ? hdr + SY_HDR + CH_MAX_G1 : nullptr;
-    w.tcnt = hdr ? hdr + SY_HDR + CH_MAX_G1 + 16 : nullptr;
-    w.flags = reinterpret_cast<uint32_t*>(take(MLP_FLAGS));
+    take(MLP_HDR);
     w.hmax = reinterpret_cast<uint32_t*>(take(size_t(N1 / 16) * 16 * 4));
-    w.acc = reinterpret_cast<int32_t*>(take(size_t(16) * CH_MAX_K1 * 4));
     w.q1 = reinterpret_cast<int8_t*>(take(size_t(rows) * K1));
     w.q2 = reinterpret_cast<int8_t*>(take(size_t(rows) * N1));
     w.s = reinterpret_cast<float*>(take(64 * 4));
@@ -1781,73 +1408,6 @@ MlpWs mlp_ws(void* base, int64_t rows, int64_t K1, int64_t N1) {
     return w;
 }
 
-// gate/up + rotation of h + down in one launch (after the row prep of x), when the shapes fit it and
-// the whole grid is resident at once; returns -1 (nothing launched) otherwise.
-int mono_mlp_fused(const uint16_t* h, int32_t rot, const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up,
-                   const mdx_w4* down, const uint16_t* residual, uint16_t* out, int rows, const MlpWs& w,
-                   hipStream_t st) {
-    const int64_t K1 = gate->k, N1 = gate->n;
-    if (rot == MDX_ROT_MATRIX || K1 > CH_MAX_K1 || N1 % 256 || N1 / 256 > CH_MAX_G1) return -1;
-    // opt-in (MDX_MLP_FUSED=1): on MI355X the in-launch hand-off (every gate/up pair's h, then the
-    // rotation of h, then the down units' wait) costs more than the two launch boundaries it removes
-    // (measured 37.9 against 31.3 us per block at one row, 46.3 against 38.0 us at eight)
-    const char* env = getenv("MDX_MLP_FUSED");
-    if (!env || atoi(env) == 0) return -1;
-    if (gate->s_dtype != down->s_dtype) return -1;
-    MlpFused c{};
-    int total = 0, rc;
-    const mdx_w4* gu[2] = {gate, up};
-    void* o1[2] = {w.hb, w.hb};
-    if ((rc = setup_gemv(gu, 2, true, w.q1, w.s, rows, EPI_SILU, o1, nullptr, MDX_DT_BF16, silu_lut, c.gu, total)))
-        return rc;
-    const mdx_w4* dn[1] = {down};
-    void* o2[1] = {out};
-    const void* r2[1] = {residual};
-    if ((rc = setup_gemv(dn, 1, false, w.q2, w.s + 32, rows, EPI_ACC, o2, r2, MDX_DT_BF16, nullptr, c.dn, total)))
-        return rc;
-    // gate/up: one tile pair per work-group, 2 K slices; down: four tiles per work-group (one per
-    // wave) over a K part, with as many parts as make as many down units as gate/up units (every
-    // work-group runs one of each). Each down unit quantises its K part of h for every row, so
-    // four tiles per unit quarter that repeated work against one tile per unit.
-    c.gu.TPW = 2;
-    c.gu.KS = 2;
-    c.gu.coh = 1;
-    c.dn.TPW = CH_WAVES;
-    c.dn.KS = 1;
-    const int NC2 = int(N1 / CHUNK_K), groups2 = int((K1 / 16 + CH_WAVES - 1) / CH_WAVES);
-    c.n_gu = int(N1 / 16);
-    int split = 0;
-    for (int d = 1; d <= NC2 && groups2 * d <= c.n_gu; ++d)
-        if (NC2 % d == 0) split = d;
-    if (split == 0) return -1;
-    c.dn.split = split;
-    c.dn.acc = w.acc;
-    c.dn.tcnt = w.tcnt;
-    c.dn_cu = NC2 / split;
-    c.hb = w.hb;
-    c.hr = rot == MDX_ROT_NONE ? w.hb : w.hr;
-    c.amax = w.amax;
-    c.sync = w.sync;
-    c.flags = w.flags;
-    c.rows = rows;
-    c.rot = rot;
-    c.n_dn = groups2 * split;
-    c.G1 = int(N1 / 256);
-    const bool mfma = rows >= MFMA_MIN_ROWS;
-    const int esz = esz_of(gate->s_dtype);
-    size_t smem = std::max(gemv_smem(c.gu, mfma, esz), gemv_smem(c.dn, mfma, esz, 0, c.dn_cu));
-    smem = std::max(smem, gemv_smem(c.dn, mfma, esz, (split - 1) * c.dn_cu, c.dn_cu));
-    const int grid = std::max(c.n_gu, c.n_dn);
-    const void* fn = fused_kernel(gate->s_dtype, mfma);
-    if (smem > 160 * 1024) return -1;
-    if (smem > 64 * 1024) allow_smem(fn, smem);
-    if (!all_resident(fn, smem, grid)) return -1;
-    void* args[] = {&c};
-    (void)hipLaunchKernel(fn, dim3(unsigned(grid)), dim3(CH_WAVES * WAVE), args, smem, st);
-    MDX_LAUNCHED();
-    return MDX_OK;
-}
-
 }  // namespace
 }  // namespace mdx
 
@@ -1855,7 +1415,7 @@ extern "C" size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1) {
     return mdx::mlp_ws(nullptr, rows, K1, N1).bytes;
 }
 
-extern "C" size_t mdx_mono_mlp_error_offset(void) { return 4 * mdx::SY_ERR; }
+extern "C" size_t mdx_mono_mlp_error_offset(void) { return 4 * mdx::MLP_ERR; }
 
 extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
                             const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
@@ -1879,16 +1439,13 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     const char* hp = getenv("MDX_MLP_HPREP");
     const bool hr = rot == MDX_ROT_NONE && gemv_hr_fits(down, int(rows)) && !(hp && atoi(hp) != 0);
     const mdx_w4* gu[2] = {gate, up};
-    const char* fz = getenv("MDX_MLP_FUSED");
     // one row: the gate/up GEMV prepares x itself (no row prep launch); MDX_MLP_HPREP=1 keeps both
     // prep launches
-    const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && !(fz && atoi(fz) != 0) && aligned(xn, 16) &&
+    const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && aligned(xn, 16) &&
                     (!norm_w || aligned(norm_w, 16));  // (the row and its weights are DMA'd in 16-byte pieces)
     if (!xp) {
         PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
         if ((rc = launch_prep(pa, rows, st))) return rc;
-        rc = mono_mlp_fused(h, rot, silu_lut, gate, up, down, residual, out, int(rows), w, st);
-        if (rc >= 0) return rc;
     }
     // gate/up, [prep of h], down
     void* o1[2] = {w.hb, w.hb};

@@ -236,10 +236,9 @@ def _mlp_handles(g, dev, fmt="gptq"):
 
 
 @pytest.mark.parametrize("rot", ["none", "h256"])
-def test_mlp_fused_equals_four_launches(C, dev, rot, monkeypatch):
-    """The fused MLP (row prep, then gate/up + rotation of h + K-split down with int32 atomics in
-    one launch) against the four-launch form and the oracle, with a residual, for every row count
-    class (16 rows do not fit the fused launch's residency bound: both runs take four launches)."""
+def test_mlp_with_residual_matches_oracle(C, dev, rot):
+    """The MLP block with RMSNorm in front and a residual, for every row count class (one row, two,
+    up to eight, sixteen), with and without the rotation of h, against the oracle bit for bit."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(41)
     ws, handles = _mlp_handles(g, dev)
@@ -249,20 +248,13 @@ def test_mlp_fused_equals_four_launches(C, dev, rot, monkeypatch):
     h = layout.regular_hadamard(dev) if rot == "h256" else None
     d = _oracle_dicts(ws)
     for M in (1, 2, 5, 8, 16):
-        print(f"case mlp-fused rot={rot} M={M}", flush=True)
+        print(f"case mlp-residual rot={rot} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
-        outs = []
-        for fused in ("1", "0"):  # two launches, four launches
-            monkeypatch.setenv("MDX_MLP_FUSED", fused)
-            outs.append(C.mono_mlp_w4(x.to(dev), code, h, lut, *handles, norm_w=nw.to(dev), eps=1e-6,
-                                      residual=res.to(dev)))
-        torch.cuda.synchronize()
-        assert C.mlp_error(dev) == 0
-        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={M}"
+        out = C.mono_mlp_w4(x.to(dev), code, h, lut, *handles, norm_w=nw.to(dev), eps=1e-6, residual=res.to(dev))
         xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
         want = ref.add_bf16(bits(res), ref.mono_mlp(xn, rot, None if h is None else bits(h.cpu()), bits(lut.cpu()), *d))
-        assert_bits_equal(bits(outs[0]), want, f"M={M}")
+        assert_bits_equal(bits(out), want, f"M={M}")
 
 
 def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
@@ -293,37 +285,34 @@ def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
         assert_bits_equal(bits(outs[0]), want, f"M={M} norm={norm}")
 
 
-def test_mlp_fused_graph_replays(C, dev, monkeypatch):
-    """The fused MLP captured once, replayed with new inputs between eager four-launch calls: every
-    replay equals the eager result (the control words and accumulators are back at zero after
-    every launch)."""
+@pytest.mark.parametrize("rot", ["none", "h256"])
+def test_mlp_graph_replays(C, dev, rot):
+    """The MLP block captured once, replayed with new inputs between eager calls of the same block:
+    every replay equals the eager result (no launch keeps state between calls)."""
     from mdx import _lib, layout
-    monkeypatch.setenv("MDX_MLP_FUSED", "1")
     g = torch.Generator().manual_seed(43)
     _, handles = _mlp_handles(g, dev)
     lut = layout.silu_lut(dev)
-    hd = layout.regular_hadamard(dev)
+    code = _lib.ROT_H256 if rot == "h256" else _lib.ROT_NONE
+    hd = layout.regular_hadamard(dev) if rot == "h256" else None
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
-    for M in (1, 8):
-        print(f"case mlp-fused graph M={M}", flush=True)
+    for M in (1, 2, 8):
+        print(f"case mlp graph rot={rot} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev)
         out = torch.empty(M, 4096, dtype=torch.bfloat16, device=dev)
-        C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
+        C.mono_mlp_w4(x, code, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
+            C.mono_mlp_w4(x, code, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
         for rep in range(4):
             x.copy_(torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev))
             graph.replay()
             torch.cuda.synchronize()
             got = out.clone()
-            monkeypatch.setenv("MDX_MLP_FUSED", "0")
-            want = C.mono_mlp_w4(x, _lib.ROT_H256, hd, lut, *handles, norm_w=nw, eps=1e-6)
-            monkeypatch.setenv("MDX_MLP_FUSED", "1")
+            want = C.mono_mlp_w4(x, code, hd, lut, *handles, norm_w=nw, eps=1e-6)
             torch.cuda.synchronize()
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={M} replay {rep}"
-        assert C.mlp_error(dev) == 0
 
 
 def test_integral_decode_mode_matches_oracle(C, dev):
