@@ -349,7 +349,7 @@ def bench_attn(args, dev):
                   "avg_launch_us": round(t * 1e6, 3)})
 
 
-def bench_stack(args, dev, tokens=0):
+def bench_stack(args, dev, tokens=0, two_stage=False):
     """The full synthetic 32-layer hybrid stack (3 GDN : 1 attention, hidden 4096, MLP 12288, W4A8
     GPTQ G128), 1-layer bf16 MTP draft block, bf16 lm_head over 151936, tree_spec (4, 3) (8 rows, 2
     drafts per step), top-k 20 sampling; a seeded random prompt is prefilled (not timed), then each
@@ -362,7 +362,7 @@ def bench_stack(args, dev, tokens=0):
     per = 3  # at most len(widths) + 1 tokens committed per step
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
-    cfg = hybrid.HybridConfig(cap=cap)
+    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -391,7 +391,8 @@ def bench_stack(args, dev, tokens=0):
     return _line(args, round(got / t, 2), "tok/s", per_step, done, "W4A8 int8 x int4 -> int32; bf16 draft, lm_head",
                  "synthetic (random-init weights, seeded random prompt)",
                  {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936, "
-                              f"MTP draft, tree (4, 3), top-k 20, prompt {args.prompt}, {what}",
+                              f"MTP draft{' (two-stage head)' if two_stage else ''}, tree (4, 3), top-k 20, "
+                              f"prompt {args.prompt}, {what}",
                   "prompt": args.prompt, "steps": done, "tokens": got,
                   "accepted_per_step": round(got / done, 3), "ms_per_step": round(per_step * 1e3, 4),
                   "setup_s": round(setup, 1)})
@@ -590,6 +591,8 @@ def main():
     ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn", "stack", "read", "attn_layer",
                                            "gdn_layer"], default="mlp")
     ap.add_argument("--tokens", type=int, default=0, help="stack: decode until this many tokens are committed")
+    ap.add_argument("--two-stage", action="store_true", help="stack: drafts score the vocabulary with an int4 copy "
+                                                               "of the lm_head and recompute their candidates exactly")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -607,7 +610,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     if args.workload == "stack":
-        res = bench_stack(args, dev, tokens=args.tokens)
+        res = bench_stack(args, dev, tokens=args.tokens, two_stage=args.two_stage)
     else:
         res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
                "attn": bench_attn, "read": bench_read, "attn_layer": bench_attn_layer,
@@ -621,6 +624,11 @@ def main():
         res["decode"] = {"metric": "decode tok/s at 9B hybrid, 8-draft tree", "value": d["value"], "unit": "tok/s",
                          "ms_per_step": d["config"]["ms_per_step"],
                          "accepted_per_step": d["config"]["accepted_per_step"], "workload": d["config"]["workload"]}
+        # the same decode with the two-stage draft head (int4 scores + exact recompute of the candidates)
+        d2 = bench_stack(sub, dev, tokens=512, two_stage=True)
+        res["decode_two_stage_drafts"] = {"value": d2["value"], "unit": "tok/s", "ms_per_step": d2["config"]["ms_per_step"],
+                                          "accepted_per_step": d2["config"]["accepted_per_step"],
+                                          "workload": d2["config"]["workload"]}
     print(json.dumps(res), flush=True)
 
 

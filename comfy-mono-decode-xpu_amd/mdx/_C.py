@@ -816,3 +816,82 @@ def draft_norm_rot_quant(x, h, w, eps, hmat, xr, qx, sx):
     _lib.call("mdx_draft_norm_rot_quant", _lib.ptr(x), _lib.ptr(h) if _present(h) else None, _lib.ptr(w), float(eps),
               rot, _lib.ptr(xr), _lib.ptr(qx) if quant else None, _lib.ptr(sx) if quant else None, rows, H,
               _lib.stream_of(x))
+
+
+# ---------------------------------------------------------------------------------------------------
+# two-stage draft lm_head (csrc/draft_lmhead.sycl, comfy_mono_decode_xpu/draft_lmhead.py)
+# ---------------------------------------------------------------------------------------------------
+_PICK_WS = {}
+
+
+def _pick_ws(dev):
+    """The per-device draft-pick workspace (zeroed once; every call leaves its counter at zero)."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _PICK_WS.get(key)
+    if ws is None:
+        ws = _PICK_WS[key] = torch.zeros(_lib.lib().mdx_draft_pick_workspace(), dtype=torch.uint8, device=dev)
+    return ws
+
+
+def _pick_outputs(top, ranks_row, token, vtok, children, calls, nout):
+    for t, n in ((token, "token"), (vtok, "vtok")):
+        _dev(t, n)
+        _check(t.dtype == torch.int64 and t.is_contiguous(), f"{n}: contiguous int64")
+    _check(token.numel() == 1, "token: one int64")
+    for t, n in ((top, "top"), (ranks_row, "ranks row")):
+        if _present(t):
+            _check(t.dtype == torch.int64 and t.is_contiguous() and t.numel() >= nout, f"{n}: int64 [>= nout]")
+    ch = [int(c) for c in children]
+    _check(1 <= len(ch) <= 8 and len(ch) <= nout, "children: 1..min(8, nout) rows")
+    _check(all(0 <= c < vtok.numel() for c in ch), "child row")
+    if calls is not None:
+        _check(calls.dtype == torch.int64 and calls.numel() >= 1, "calls counter int64")
+    return (ctypes.c_int64 * len(ch))(*ch), len(ch)
+
+
+def draft_pick(approx, qx, sx, w, sw, nout, argmax_first, top, ranks_row, token, vtok, children, calls):
+    """Reference csrc/draft_lmhead.sycl:82-291: from approximate scores approx bf16 [N], the exact int8 logits
+    of candidates (the 32 best scores of each of 32 segments), their top-nout in torch topk order and the
+    argmax; writes top / ranks_row[:nout] (either may be empty), token, vtok[children] and calls += 1. An
+    empty w: the scores are the logits (qx, sx, sw ignored)."""
+    _dev(approx, "approx")
+    _check(approx.dtype == torch.bfloat16 and approx.is_contiguous(), "approx: bf16 row")
+    N = approx.numel()
+    exact = w.numel() == 0
+    K = 0
+    if not exact:
+        _check(w.dtype == torch.int8 and w.is_contiguous() and w.dim() == 2 and w.shape[0] == N, "w: int8 [N, K]")
+        K = w.shape[1]
+        _check(qx.dtype == torch.int8 and qx.is_contiguous() and qx.numel() == K, "qx: int8 [K]")
+        _check(sx.dtype == torch.float32 and sx.numel() == 1, "sx: one float")
+        _check(sw.dtype == torch.float32 and sw.is_contiguous() and sw.numel() == N, "sw: float [N]")
+    _check(1 <= int(nout) <= 8, "1 <= nout <= 8")
+    ch, nch = _pick_outputs(top, ranks_row, token, vtok, children, calls, int(nout))
+    ws = _pick_ws(approx.device)
+    _lib.call("mdx_draft_pick", _lib.ptr(approx), N, None if exact else _lib.ptr(qx), None if exact else _lib.ptr(sx),
+              None if exact else _lib.ptr(w), None if exact else _lib.ptr(sw), K, int(nout), int(bool(argmax_first)),
+              _lib.ptr(top) if _present(top) else None, _lib.ptr(ranks_row) if _present(ranks_row) else None,
+              _lib.ptr(token), _lib.ptr(vtok), vtok.numel(), ch, nch, _lib.ptr(calls), _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(approx))
+
+
+def draft_pick_bf16(approx, x, w, nout, argmax_first, top, top_values, token, vtok, children, calls=None, tiled=True):
+    """The draft pick of a bf16 lm_head (this library's own): as draft_pick, with the candidates' exact logits
+    those bf16_linear(x, w) gives (recomputed with its MFMA chain), 16 candidates per segment; top_values
+    (bf16, may be None) receives the top-nout logits. Equals bf16_linear + fast_topk whenever their top-nout
+    lies within the candidates."""
+    _dev(approx, "approx")
+    _check(approx.dtype == torch.bfloat16 and approx.is_contiguous(), "approx: bf16 row")
+    N = approx.numel()
+    _check(w.dtype == torch.bfloat16 and w.is_contiguous() and w.dim() == 2 and w.shape[0] == N, "w: bf16 [N, K]")
+    K = w.shape[1]
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.numel() == K, "x: bf16 [K]")
+    _check(1 <= int(nout) <= 8, "1 <= nout <= 8")
+    if top_values is not None:
+        _check(top_values.dtype == torch.bfloat16 and top_values.numel() >= nout, "top values bf16 [>= nout]")
+    ch, nch = _pick_outputs(top, None, token, vtok, children, calls, int(nout))
+    ws = _pick_ws(approx.device)
+    _lib.call("mdx_draft_pick_bf16", _lib.ptr(approx), _lib.ptr(x), _lib.ptr(w), _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW,
+              N, K, int(nout), int(bool(argmax_first)), _lib.ptr(top) if _present(top) else None,
+              _lib.ptr(top_values), _lib.ptr(token), _lib.ptr(vtok), vtok.numel(), ch, nch, _lib.ptr(calls), _lib.ptr(ws),
+              ws.numel(), _lib.stream_of(approx))

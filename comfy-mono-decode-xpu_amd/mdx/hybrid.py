@@ -43,6 +43,7 @@ class HybridConfig:
     top_k: int = 20
     temperature: float = 1.0
     greedy: bool = False          # take the top-1 instead of sampling
+    two_stage: bool = False       # drafts: int4 scores + the draft pick instead of the full bf16 lm_head
     eps: float = 1e-6
     cap: int = 2048
 
@@ -83,11 +84,13 @@ def tree_tensors(widths, slots, dev):
     chain_nodes = [0]
     while children[chain_nodes[-1]]:
         chain_nodes.append(children[chain_nodes[-1]][0])
-    fill = [torch.tensor(children[chain_nodes[k]], dtype=torch.int64, device=dev) for k in range(len(widths))]
+    fill_rows = [list(children[chain_nodes[k]]) for k in range(len(widths))]
+    fill = [torch.tensor(r, dtype=torch.int64, device=dev) for r in fill_rows]
     tree_ctl = torch.tensor(parents[:R] + [-1] * (slots - R) + prog + [0] * (slots - R), dtype=torch.int32, device=dev)
     return dict(R=R, depth=chain, parents=parents[:R], prog=prog,
                 mask=torch.tensor(mask, dtype=torch.int32, device=dev), children=ch.reshape(-1).to(dev),
-                tree_pos=torch.tensor(depth[:R], dtype=torch.int64, device=dev), tree_ctl=tree_ctl, fill=fill)
+                tree_pos=torch.tensor(depth[:R], dtype=torch.int64, device=dev), tree_ctl=tree_ctl, fill=fill,
+                fill_rows=fill_rows)
 
 
 def rope_table(cfg, dev):
@@ -111,7 +114,11 @@ class HybridModel:
         hk, hv = c.gdn_key_heads, c.gdn_value_heads
         self.gdn_ch = 2 * hk * 128 + hv * 128
         self.embed = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.5).bfloat16()
-        self.lm_head = _bf16w(c.vocab, H, gen, dev, 0.02)
+        head = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.02).bfloat16()
+        self.lm_head = layout.tile_major_bf16(head)
+        # the draft head's first stage: an int4 copy of the lm_head scored by the W4A8 GEMV
+        self.lm4 = layout.int4_scoring_copy(head)
+        del head
         self.final_norm = _norm(H, gen, dev)
         self.h256 = layout.regular_hadamard(dev)
         self.silu = layout.silu_lut(dev)
@@ -199,6 +206,8 @@ class HybridModel:
         self.dg = torch.zeros(S, c.inter, **bf)
         self.du = torch.zeros(S, c.inter, **bf)
         self.dlogits = torch.zeros(1, c.vocab, **bf)
+        self.dtop = torch.zeros(len(c.widths), 8, **i64)
+        self.dtok = torch.zeros(len(c.widths), 1, **i64)
         self.empty_mask = torch.empty(0, dtype=torch.int32, device=dev)
         self.graphs = {}
         # host-side upper bound of the committed position st[0]: every KV write of a step lands at
@@ -310,13 +319,24 @@ class HybridModel:
 
     def draft(self, k, tok, h, width):
         """Draft depth k: the MTP block on the chain token `tok` [1] and hidden row `h` [1, H] at the
-        device positions of mtp_prep_draft, then the final norm, the lm_head and the top-`width`."""
-        c = self.cfg
+        device positions of mtp_prep_draft, then the final norm, the lm_head and the top-`width`, written
+        to the tree rows of depth k + 1 (chain child first). Returns the chain token [1].
+        two_stage: the lm_head's int4 copy scores the vocabulary and the draft pick recomputes the exact
+        bf16 logits of its candidates (the same result whenever the exact top-width is among them)."""
+        c, T = self.cfg, self.tree
         _C.mtp_prep_draft(self.st, k, self.ftab.view(1, 1, c.cap, c.rotary // 2, 2, 2), self.dfreqs, self.mpos, self.mseq)
         self.mtp_block(1, tok, h, self.dfreqs.view(1, c.rotary // 2, 2, 2), self.mpos[:1], self.mseq, None)
         xf = _C.rmsnorm(self.dh[:1], self.mtp["norm_f"], c.eps)
+        if c.two_stage:
+            q, s = _C.quant_rows(xf)
+            _C.stream_gemv(q, s.view(-1), [self.lm4], [self.dlogits])
+            _C.draft_pick_bf16(self.dlogits.view(-1), xf.view(-1), self.lm_head, width, False, self.dtop[k], None,
+                               self.dtok[k], self.vtok.view(-1), T["fill_rows"][k])
+            return self.dtok[k]
         _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
-        return _C.fast_topk(self.dlogits, width, False)[1]
+        top = _C.fast_topk(self.dlogits, width, False)[1]
+        self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
+        return top.view(-1)[:1]
 
     def step(self, parity):
         """One decode step on the device (drafts, verify, sampling, accept). An eager step checks the
@@ -329,9 +349,7 @@ class HybridModel:
         tok, h = self.nt.view(-1), self.hbuf
         self.vtok[0, 0:1].copy_(self.nt.view(-1))
         for k, w in enumerate(c.widths):
-            top = self.draft(k, tok, h, w)
-            self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
-            tok, h = top.view(-1)[:1], self.dh[:1]
+            tok, h = self.draft(k, tok, h, w), self.dh[:1]
         # verify
         _C.mtp_prep_verify(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0)
         torch.index_select(self.ftab, 0, self.vpos.view(-1), out=self.vfreqs)

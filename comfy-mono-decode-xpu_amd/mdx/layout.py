@@ -206,3 +206,24 @@ def tile_major_bf16(w: torch.Tensor) -> torch.Tensor:
     N, K = w.shape
     assert N % 16 == 0 and K % 32 == 0
     return w.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous().reshape(N, K)
+
+
+def int4_scoring_copy(w: torch.Tensor, group_size: int = 128) -> W4:
+    """An int4 copy of a bf16 or int8 head [N, K] for the first stage of the two-stage draft lm_head
+    (comfy_mono_decode_xpu/draft_lmhead.py:80-95 makes the same kind of copy of its int8 head): per group of
+    `group_size` along K, symmetric codes q = clamp(rint(w / s_g), -8, 7) with s_g = amax_g / 7, packed by
+    the integral GPTQ packer and laid out tile-major. Its products are scores for choosing candidates,
+    never logits. Built in row blocks (bounded temporary memory)."""
+    N, K = w.shape
+    assert K % group_size == 0
+    codes, scales = [], []
+    for n0 in range(0, N, 16384):
+        b = w[n0:n0 + 16384].float().view(-1, K // group_size, group_size)
+        sg = (b.abs().amax(-1) / 7.0).clamp_min(1e-30)
+        codes.append((b / sg[..., None]).round().clamp(-8, 7).to(torch.int8).view(-1, K))
+        scales.append(sg)
+    q = torch.cat(codes)
+    sg = torch.cat(scales).clamp(max=65504.0).to(torch.float16)
+    packed, s_rel, sch, _ = gptq_pack(q, sg, group_size, integral=True)
+    del q
+    return W4(tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE, _lib.DECODE_INTEGRAL)

@@ -367,6 +367,35 @@ int mdx_draft_silu_mul(const uint16_t* gu, int64_t gu_row_stride, const uint16_t
 int mdx_draft_norm_rot_quant(uint16_t* x, const uint16_t* h, const uint16_t* w, float eps, int32_t rot, uint16_t* xr,
                              int8_t* qx, float* sx, int64_t rows, int64_t H, void* stream);
 
+/* Bytes of device workspace the draft pick needs (zeroed once before its first use; every call leaves
+ * its counter at zero again). */
+size_t mdx_draft_pick_workspace(void);
+
+/* Second stage of the two-stage draft lm_head: from approximate scores approx bf16 [N] of the whole
+ * vocabulary, the exact logits of candidates -- bf16((float(acc) * x_scale) * w_scale[n]), acc the int32 dot
+ * of the int8 row w[n] [K] with qx int8 [K] -- and of them the top-nout in torch topk's tie order and the
+ * argmax (torch argmax rules). With w == NULL the scores are the logits. Candidates: the 32 best scores of
+ * each of 32 contiguous segments. Writes top[:nout] and ranks_row[:nout] (each may be NULL), the draft
+ * token (the argmax if argmax_first, else top[0]) to token[0] and vtok[children[0]], top[j] to
+ * vtok[children[j]] (1 <= j < nchildren <= nout <= 8), and adds 1 to calls[0] (may be NULL).
+ * 8192 <= N <= 262144; K % 64 == 0, K <= 16384.
+ * Replaces: _C.draft_pick, csrc/draft_lmhead.sycl:82-291 (bindings.cpp:66-68, 86). */
+int mdx_draft_pick(const uint16_t* approx, int64_t N, const int8_t* qx, const float* x_scale, const int8_t* w,
+                   const float* w_scale, int64_t K, int64_t nout, int32_t argmax_first, int64_t* top, int64_t* ranks_row,
+                   int64_t* token, int64_t* vtok, int64_t nvtok, const int64_t* children, int64_t nchildren,
+                   int64_t* calls, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The draft pick of a bf16 lm_head: as mdx_draft_pick, the exact logits being those mdx_bf16_linear
+ * gives for the row x bf16 [K] and the head w bf16 [N, K] (layout MDX_LAYOUT_TILE or _ROW), recomputed
+ * for 16 candidates per segment with the same per-output MFMA chain and K split, so the result equals
+ * mdx_bf16_linear + mdx_fast_topk whenever their top-nout lies within the candidates. top_values
+ * (bf16 [nout], may be NULL) receives the top-nout logits. K % 32 == 0, K <= 4096. No counterpart in the
+ * reference (whose draft head is int8); it serves the synthetic model's bf16 head. */
+int mdx_draft_pick_bf16(const uint16_t* approx, const uint16_t* x, const uint16_t* w, int32_t layout, int64_t N, int64_t K,
+                        int64_t nout, int32_t argmax_first, int64_t* top, uint16_t* top_values, int64_t* token,
+                        int64_t* vtok, int64_t nvtok, const int64_t* children, int64_t nchildren, int64_t* calls,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Calibration: one streaming read of `bytes` (a multiple of 1024) from `src` with the W4A8 GEMV's load
  * pattern (1 KiB per wave instruction, four loads in flight per wave), over `work_groups` work-groups
  * of 256 threads; `sink` (4 bytes) is written only if the data hashes to a marker value. It has no

@@ -815,3 +815,30 @@ def draft_norm_rot_quant(x_bits, h_bits, w_bits, eps, rot="h256"):
     div = bfround(scale)
     q = np.clip(np.rint((xr / div[:, None]).astype(np.float32)), -128, 127).astype(np.int8)
     return xn, f32_to_bf16(xr), q, scale
+
+
+# ---------------------------------------------------------------------------------------------
+# two-stage draft lm_head, second stage (csrc/draft_lmhead.sycl:82-291)
+# ---------------------------------------------------------------------------------------------
+
+
+def int8_head_logits(qx, sx, w8, sw):
+    """Exact int8 head logits bf16((float(acc) * sx) * sw[n]), acc the int32 dot of the int8 row with qx
+    (csrc/draft_lmhead.sycl:217-220): int64 sums (exact), one rounding to fp32, two fp32 products."""
+    acc = np.asarray(w8, dtype=np.int64) @ np.asarray(qx, dtype=np.int64).reshape(-1)
+    f = (acc.astype(np.float32) * np.float32(np.asarray(sx, dtype=np.float32).reshape(-1)[0])).astype(np.float32)
+    f = (f * np.asarray(sw, dtype=np.float32).reshape(-1)).astype(np.float32)
+    return f32_to_bf16(f)
+
+
+def draft_pick(logit_bits, nout, argmax_first, children, nvtok):
+    """The draft's outputs from the exact logits (csrc/draft_lmhead.sycl:263-284): top-nout in torch topk
+    order, the token (argmax, or top[0]), vtok[children[0]] = token, vtok[children[j]] = top[j]; vtok is
+    returned with -1 elsewhere."""
+    _, top = fast_topk(logit_bits, nout)
+    tok = argmax_bf16(logit_bits) if argmax_first else int(top[0])
+    vtok = np.full(nvtok, -1, dtype=np.int64)
+    vtok[children[0]] = tok
+    for j, c in enumerate(children[1:], 1):
+        vtok[c] = top[j]
+    return top, tok, vtok

@@ -48,3 +48,29 @@ def test_graph_replay_matches_eager(dev):
     torch.cuda.synchronize()
     assert torch.equal(a.st, b.st) and torch.equal(a.nt, b.nt) and torch.equal(a.result, b.result)
     assert torch.equal(a.hbuf, b.hbuf)
+
+
+def test_two_stage_drafts_equal_one_stage(dev):
+    """The two-stage draft head (int4 scores + the draft pick) gives the same decode as the full bf16 head:
+    counters, accept records, next tokens and hidden rows after eager steps and a graph replay."""
+    from mdx import hybrid
+    ms = []
+    for two in (False, True):
+        cfg = hybrid.HybridConfig(layers=4, inter=4096, vocab=32768, cap=256, greedy=True, two_stage=two)
+        m = hybrid.HybridModel(cfg, dev, seed=7)
+        m.prefill(torch.randint(0, cfg.vocab, (37,), generator=torch.Generator().manual_seed(2)))
+        ms.append(m)
+    for step in range(3):
+        print(f"case two-stage eager step {step}", flush=True)
+        for m in ms:
+            m.step(m.parity)
+            m.parity ^= 1
+        torch.cuda.synchronize()
+        a, b = ms
+        assert torch.equal(a.vtok, b.vtok) and torch.equal(a.result, b.result) and torch.equal(a.nt, b.nt)
+    for m in ms:
+        m.capture()
+        m.replay(2)
+    torch.cuda.synchronize()
+    a, b = ms
+    assert torch.equal(a.st, b.st) and torch.equal(a.result, b.result) and torch.equal(a.hbuf, b.hbuf)
