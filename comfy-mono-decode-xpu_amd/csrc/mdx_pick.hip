@@ -205,17 +205,32 @@ __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
             if (lane == 0 && q < a.S) logit[q] = f2bf(__fmul_rn(__fmul_rn(float(v), xs), a.sw[sel[q]]));
         }
     } else {
-        // PICK_BF16, S = 16: piece (chunk j, lane 16 g + c) = candidate c's k [32 j + 8 g, + 8), the
-        // A-operand layout of the lm_head kernel; then x
-        const int NC = a.K / 32, pieces = NC * 64;
-        uint8_t* xl = rows_lds + size_t(pieces) * 16;
-        for (int p0 = wave * 64; p0 < pieces; p0 += PK_T) {
-            const int p = p0 + lane, j = p >> 6, l = p & 63, g = l >> 4, c = l & 15;
-            const int64_t n = sel[c];
-            const uint16_t* src = a.layout == MDX_LAYOUT_TILE
-                                      ? a.wb + ((n >> 4) * int64_t(NC) + j) * 512 + (16 * g + (n & 15)) * 8
-                                      : a.wb + n * a.K + 32 * j + 8 * g;
-            __builtin_amdgcn_global_load_lds((const PK_G uint8_t*)(src), PK_LDS(rows_lds + size_t(p0) * 16), 16, 0, 0);
+        // PICK_BF16, S = 16. Row-major head with K % 512 == 0: each candidate row lands in LDS contiguously
+        // (1 KiB contiguous per DMA instruction), rows 2 K + 16 bytes apart (the 16 rows of one MFMA operand
+        // read fall on different banks); otherwise piece (chunk j, lane 16 g + c) = candidate c's k
+        // [32 j + 8 g, + 8) in the MFMA A-operand layout. Then x.
+        const int NC = a.K / 32;
+        const bool rowl = a.layout == MDX_LAYOUT_ROW && a.K % 512 == 0;
+        const int rstride = 2 * a.K + 16;
+        const size_t rows_bytes = rowl ? size_t(16) * rstride : size_t(NC) * 64 * 16;
+        uint8_t* xl = rows_lds + rows_bytes;
+        if (rowl) {
+            const int per = a.K / 8;  // 16-byte pieces per row (a multiple of 64)
+            for (int p0 = wave * 64; p0 < 16 * per; p0 += PK_T) {
+                const int c = p0 / per, q0 = p0 - c * per;
+                __builtin_amdgcn_global_load_lds((const PK_G uint8_t*)(a.wb + int64_t(sel[c]) * a.K + 8 * (q0 + lane)),
+                                                 PK_LDS(rows_lds + size_t(c) * rstride + size_t(q0) * 16), 16, 0, 0);
+            }
+        } else {
+            const int pieces = NC * 64;
+            for (int p0 = wave * 64; p0 < pieces; p0 += PK_T) {
+                const int p = p0 + lane, j = p >> 6, l = p & 63, g = l >> 4, c = l & 15;
+                const int64_t n = sel[c];
+                const uint16_t* src = a.layout == MDX_LAYOUT_TILE
+                                          ? a.wb + ((n >> 4) * int64_t(NC) + j) * 512 + (16 * g + (n & 15)) * 8
+                                          : a.wb + n * a.K + 32 * j + 8 * g;
+                __builtin_amdgcn_global_load_lds((const PK_G uint8_t*)(src), PK_LDS(rows_lds + size_t(p0) * 16), 16, 0, 0);
+            }
         }
         for (int p0 = wave * 64; p0 < a.K / 8; p0 += PK_T)
             if (p0 + lane < a.K / 8)  // (a lane past the row would write past the LDS block)
@@ -230,7 +245,8 @@ __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
                 const int c0 = ks * NC / a.KS, c1 = (ks + 1) * NC / a.KS;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                 for (int j = c0; j < c1; ++j) {
-                    const u32x4 wv = *reinterpret_cast<const u32x4*>(rows_lds + (size_t(j) * 64 + lane) * 16);
+                    const u32x4 wv = *reinterpret_cast<const u32x4*>(
+                        rowl ? rows_lds + size_t(c) * rstride + (32 * j + 8 * g) * 2 : rows_lds + (size_t(j) * 64 + lane) * 16);
                     u32x4 xv = *reinterpret_cast<const u32x4*>(xl + (size_t(j) * 4 + g) * 16);
                     if (c != 0) xv = u32x4{0u, 0u, 0u, 0u};  // activation rows past the first are zero
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv), __builtin_bit_cast(bf16x8, xv),
@@ -320,7 +336,9 @@ int launch_pick(PickArgs& a, const int64_t* children, int64_t nch, int64_t nvtok
     a.amax = base + PK_WG * PK_MAXN;
     a.counter = reinterpret_cast<unsigned*>(base + PK_WG * PK_MAXN + PK_WG);
     size_t lds = 0;
-    if (a.mode == PICK_BF16) lds = size_t(a.K / 32) * 64 * 16 + size_t(a.K) * 2;
+    if (a.mode == PICK_BF16)
+        lds = (a.layout == MDX_LAYOUT_ROW && a.K % 512 == 0 ? size_t(16) * (2 * a.K + 16) : size_t(a.K / 32) * 64 * 16) +
+              size_t(a.K) * 2;
     if (a.mode == PICK_I8) lds = size_t(a.S + 1) * std::min(a.K, PK_KB);
     if (lds > 64 * 1024) allow_smem(reinterpret_cast<const void*>(&draft_pick_kernel), lds);
     hipLaunchKernelGGL(draft_pick_kernel, dim3(PK_WG), dim3(PK_T), lds, st, a);

@@ -116,8 +116,11 @@ class HybridModel:
         self.embed = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.5).bfloat16()
         head = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.02).bfloat16()
         self.lm_head = layout.tile_major_bf16(head)
-        # the draft head's first stage: an int4 copy of the lm_head scored by the W4A8 GEMV
-        self.lm4 = layout.int4_scoring_copy(head)
+        # the two-stage draft head: an int4 copy of the lm_head scored by the W4A8 GEMV, and the row-major
+        # head the draft pick reads its candidates from (8 KiB contiguous per row; the tile-major copy
+        # serves the full-vocabulary passes)
+        self.lm4 = layout.int4_scoring_copy(head) if c.two_stage else None
+        self.lm_rows = head if c.two_stage else None
         del head
         self.final_norm = _norm(H, gen, dev)
         self.h256 = layout.regular_hadamard(dev)
@@ -330,8 +333,8 @@ class HybridModel:
         if c.two_stage:
             q, s = _C.quant_rows(xf)
             _C.stream_gemv(q, s.view(-1), [self.lm4], [self.dlogits])
-            _C.draft_pick_bf16(self.dlogits.view(-1), xf.view(-1), self.lm_head, width, False, self.dtop[k], None,
-                               self.dtok[k], self.vtok.view(-1), T["fill_rows"][k])
+            _C.draft_pick_bf16(self.dlogits.view(-1), xf.view(-1), self.lm_rows, width, False, self.dtop[k], None,
+                               self.dtok[k], self.vtok.view(-1), T["fill_rows"][k], tiled=False)
             return self.dtok[k]
         _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
         top = _C.fast_topk(self.dlogits, width, False)[1]
