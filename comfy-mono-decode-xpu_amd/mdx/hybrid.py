@@ -46,9 +46,10 @@ class HybridConfig:
     two_stage: bool = False       # drafts: int4 scores + the draft pick instead of the full bf16 lm_head
     eps: float = 1e-6
     cap: int = 2048
+    attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
 
     def attention(self, i):
-        return i % 4 == 3
+        return i % self.attn_every == self.attn_every - 1
 
 
 def _gptq(N, K, gen, dev):
@@ -143,9 +144,9 @@ class HybridModel:
                          g_decay=-torch.exp(torch.rand(hv, generator=gen, device=dev) * 1.5 - 1),
                          gnorm=_norm(128, gen, dev, 0.1))
             self.layers.append(L)
-        # the MTP draft block (bf16)
+        # the MTP draft block (bf16; gated attention: the q projection holds [query | gate] per head)
         self.mtp = dict(norm_e=_norm(H, gen, dev), norm_h=_norm(H, gen, dev), fc=_bf16w(H, 2 * H, gen, dev, 0.02),
-                        norm_in=_norm(H, gen, dev), qkv=_bf16w(qd + 2 * kd, H, gen, dev, 0.02),
+                        norm_in=_norm(H, gen, dev), qkv=_bf16w(2 * qd + 2 * kd, H, gen, dev, 0.02),
                         qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1),
                         o=_bf16w(H, qd, gen, dev, 0.02), norm_post=_norm(H, gen, dev),
                         gu=_bf16w(2 * I, H, gen, dev, 0.02), d=_bf16w(H, I, gen, dev, 0.02), norm_f=_norm(H, gen, dev))
@@ -201,13 +202,14 @@ class HybridModel:
         self.dcat = torch.zeros(S, 2 * c.hidden, **bf)
         self.dx = torch.zeros(S, c.hidden, **bf)
         self.dxn = torch.zeros(S, c.hidden, **bf)
-        self.dqkv = torch.zeros(S, qd + 2 * kd, **bf)
+        self.dqkv = torch.zeros(S, 2 * qd + 2 * kd, **bf)
         self.dy = torch.zeros(S, qd, **bf)
-        self.dx1 = torch.zeros(S, c.hidden, **bf)
+        self.dgy = torch.zeros(S, qd, **bf)
+        self.do = torch.zeros(S, c.hidden, **bf)
         self.dgu = torch.zeros(S, 2 * c.inter, **bf)
         self.dact = torch.zeros(S, c.inter, **bf)
-        self.dg = torch.zeros(S, c.inter, **bf)
-        self.du = torch.zeros(S, c.inter, **bf)
+        self.dd = torch.zeros(S, c.hidden, **bf)
+        self.dxf = torch.zeros(S, c.hidden, **bf)
         self.dlogits = torch.zeros(1, c.vocab, **bf)
         self.dtop = torch.zeros(len(c.widths), 8, **i64)
         self.dtok = torch.zeros(len(c.widths), 1, **i64)
@@ -216,6 +218,12 @@ class HybridModel:
         # host-side upper bound of the committed position st[0]: every KV write of a step lands at
         # most R - 1 past it, and each step commits at most len(widths) + 1 tokens
         self.pos_bound = None
+        # a list to receive (name, copy) of the step's intermediates (eager steps only; None: off)
+        self.trace = None
+
+    def _tr(self, name, t):
+        if self.trace is not None and not torch.cuda.is_current_stream_capturing():
+            self.trace.append((name, t.detach().clone()))
 
     def _reserve(self, steps):
         """Raise before launching `steps` decode steps whose KV writes could pass the cache capacity."""
@@ -237,6 +245,8 @@ class HybridModel:
         qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
         qkv = [torch.empty(R, n, dtype=torch.bfloat16, device=self.dev) for n in (qd, kd, kd)]
         _C.stream_gemv(q, s, [L["q"], L["k"], L["v"]], qkv)
+        for nm, t in zip(("q", "k", "v"), qkv):
+            self._tr(f"L{i}.{nm}", t)
         qv = qkv[0].view(1, R, c.heads, c.head_dim)
         kv_ = qkv[1].view(1, R, c.kv_heads, c.head_dim)
         vv = qkv[2].view(1, R, c.kv_heads, c.head_dim)
@@ -245,6 +255,9 @@ class HybridModel:
         _C.qk_norm_rope_kv(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, outs=(qo, ko))
         y = torch.empty(1, R, qd, dtype=torch.bfloat16, device=self.dev)
         _C.attn_dpas(qo, key, value, seq, ko, vv.transpose(1, 2), mask, 0, out=y)
+        self._tr(f"L{i}.qo", qo)
+        self._tr(f"L{i}.ko", ko)
+        self._tr(f"L{i}.y", y)
         _C._layer_post(x, y.view(R, qd), None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"],
                        L["d"], 6)
 
@@ -257,68 +270,83 @@ class HybridModel:
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
         _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
+        self._tr(f"L{i}.proj", proj)
+        self._tr(f"L{i}.z", z)
         core = _C._buf(sc["core"], R, hv * 128)
         _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
                     G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
+        self._tr(f"L{i}.core_raw", core)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6,
                        gnorm=(z, L["gnorm"], c.eps))
+        self._tr(f"L{i}.core", core)
 
     def verify_layers(self, x, R, mask, seq, pos, freqs):
         for i in range(self.cfg.layers):
+            self._tr(f"L{i}.in", x)
             if self.cfg.attention(i):
                 self._attn_layer(i, x, R, mask, seq, pos, freqs)
             else:
                 self._gdn_layer(i, x, R)
+            self._tr(f"L{i}.out", x)
 
     def mtp_block(self, n, tok, h, freqs, kvpos, seq, mask):
-        """The MTP block over n rows (tokens `tok` [n], hidden rows `h` [n, H]): writes the MTP KV at
-        kvpos, attends the MTP cache prefix [0, seq) (and, with a mask, the block's own rows); leaves
-        the output hidden rows in self.dh[:n]."""
+        """The MTP block over n rows (tokens `tok` [n], hidden rows `h` [n, H]), in the fused-op structure
+        of comfy_mono_decode_xpu/draft_head.py:179-212: cat(RMSNorm_e(embed[tok]), RMSNorm_h(h)) -> fc -> x;
+        RMSNorm_in -> q|gate, k, v -> Q/K norm + RoPE + the MTP KV write at kvpos -> attention over the MTP
+        cache prefix [0, seq) (and, with a mask, the block's own rows) -> times sigmoid(gate) -> o_proj;
+        x += o, RMSNorm_post -> gate|up -> SiLU(gate) * up -> down; x += down, RMSNorm_f. Leaves the new
+        hidden rows x in self.dh[:n] and their final norm (the lm_head input) in self.dxf[:n]."""
         c, M = self.cfg, self.mtp
-        H = c.hidden
-        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        H, D = c.hidden, c.head_dim
+        qd, kd = c.heads * D, c.kv_heads * D
         cat = _C._buf(self.dcat, n, 2 * H)
         e = torch.index_select(self.embed, 0, tok.view(-1))
-        ca = cat.view(n, 2, H)
-        if n == 1:  # one row: the two halves of the concatenated row are contiguous outputs
-            _C.rmsnorm(e, M["norm_e"], c.eps, out=ca[0, 0].view(1, H))
-            _C.rmsnorm(h, M["norm_h"], c.eps, out=ca[0, 1].view(1, H))
-        else:
-            ea, hb = (torch.empty(n, H, dtype=torch.bfloat16, device=self.dev) for _ in range(2))
-            _C.rmsnorm(e, M["norm_e"], c.eps, out=ea)
-            _C.rmsnorm(h, M["norm_h"], c.eps, out=hb)
-            ca[:, 0].copy_(ea)
-            ca[:, 1].copy_(hb)
-        x = _C._buf(self.dx, n, H)
+        _C.draft_embed_norm_cat(None, None, None, None, e, h, M["norm_e"], M["norm_h"], c.eps, c.eps, cat)
+        x = _C._buf(self.dh, n, H)
         xn = _C._buf(self.dxn, n, H)
         _C.bf16_linear(cat, M["fc"], out=x)
-        _C.rmsnorm(x, M["norm_in"], c.eps, out=xn)
-        qkv = _C._buf(self.dqkv, n, qd + 2 * kd)
+        self._tr("mtp.cat", cat)
+        self._tr("mtp.x_fc", x)
+        _C.draft_add_rmsnorm(x, None, M["norm_in"], c.eps, xn)
+        self._tr("mtp.xn_in", xn)
+        qkv = _C._buf(self.dqkv, n, 2 * qd + 2 * kd)
         _C.bf16_linear(xn, M["qkv"], out=qkv)
-        qv = qkv[:, :qd].view(1, n, c.heads, c.head_dim)
-        kv_ = qkv[:, qd:qd + kd].view(1, n, c.kv_heads, c.head_dim)
-        vv = qkv[:, qd + kd:].view(1, n, c.kv_heads, c.head_dim)
+        self._tr("mtp.qkv", qkv)
+        qg = qkv[:, :2 * qd]
+        qv = qg.reshape(n, c.heads, 2 * D)[:, :, :D]
+        kv_ = qkv[:, 2 * qd:2 * qd + kd].view(1, n, c.kv_heads, D)
+        vv = qkv[:, 2 * qd + kd:].view(1, n, c.kv_heads, D)
         mk, mv = self.mkv
-        qo = torch.empty(1, c.heads, n, c.head_dim, dtype=torch.bfloat16, device=self.dev)
-        ko = torch.empty(1, c.kv_heads, n, c.head_dim, dtype=torch.bfloat16, device=self.dev)
+        qo = torch.empty(1, c.heads, n, D, dtype=torch.bfloat16, device=self.dev)
+        ko = torch.empty(1, c.kv_heads, n, D, dtype=torch.bfloat16, device=self.dev)
         _C.qk_norm_rope_kv(qv, kv_, vv, M["qn"], M["kn"], freqs, mk, mv, kvpos, c.eps, c.eps, c.rotary, outs=(qo, ko))
         y = _C._buf(self.dy, n, qd)
         _C.attn_dpas(qo, mk, mv, seq, ko, vv.transpose(1, 2), self.empty_mask if mask is None else mask, 0,
                      out=y.view(1, n, qd))
-        x1 = _C._buf(self.dx1, n, H)
-        _C.bf16_linear(y, M["o"], residual=x, out=x1)
-        _C.rmsnorm(x1, M["norm_post"], c.eps, out=xn)
+        gy = _C._buf(self.dgy, n, qd)
+        _C.draft_sigmoid_mul(y, qg if n > 1 else qg.view(-1), D, gy)
+        self._tr("mtp.qo", qo)
+        self._tr("mtp.ko", ko)
+        self._tr("mtp.y", y)
+        self._tr("mtp.gy", gy)
+        o = _C._buf(self.do, n, H)
+        _C.bf16_linear(gy, M["o"], out=o)
+        self._tr("mtp.o", o)
+        _C.draft_add_rmsnorm(x, o, M["norm_post"], c.eps, xn)
+        self._tr("mtp.x_post", x)
+        self._tr("mtp.xn_post", xn)
         gu = _C._buf(self.dgu, n, 2 * c.inter)
         _C.bf16_linear(xn, M["gu"], out=gu)
         act = _C._buf(self.dact, n, c.inter)
-        if n == 1:  # one row: the gate and up halves are contiguous as they lie
-            g_, u_ = gu[0, :c.inter], gu[0, c.inter:]
-        else:
-            g_, u_ = _C._buf(self.dg, n, c.inter), _C._buf(self.du, n, c.inter)
-            g_.copy_(gu[:, :c.inter])
-            u_.copy_(gu[:, c.inter:])
-        _C.silu_mul(g_, u_, self.silu, out=act)
-        _C.bf16_linear(act, M["d"], residual=x1, out=_C._buf(self.dh, n, H))
+        _C.draft_silu_mul(gu, act)
+        d = _C._buf(self.dd, n, H)
+        _C.bf16_linear(act, M["d"], out=d)
+        self._tr("mtp.gu", gu)
+        self._tr("mtp.act", act)
+        self._tr("mtp.d", d)
+        _C.draft_norm_rot_quant(x, d, M["norm_f"], c.eps, None, _C._buf(self.dxf, n, H), None, None)
+        self._tr("mtp.x_out", x)
+        self._tr("mtp.xf", _C._buf(self.dxf, n, H))
 
     def draft(self, k, tok, h, width):
         """Draft depth k: the MTP block on the chain token `tok` [1] and hidden row `h` [1, H] at the
@@ -329,7 +357,7 @@ class HybridModel:
         c, T = self.cfg, self.tree
         _C.mtp_prep_draft(self.st, k, self.ftab.view(1, 1, c.cap, c.rotary // 2, 2, 2), self.dfreqs, self.mpos, self.mseq)
         self.mtp_block(1, tok, h, self.dfreqs.view(1, c.rotary // 2, 2, 2), self.mpos[:1], self.mseq, None)
-        xf = _C.rmsnorm(self.dh[:1], self.mtp["norm_f"], c.eps)
+        xf = self.dxf[:1]
         if c.two_stage:
             q, s = _C.quant_rows(xf)
             _C.stream_gemv(q, s.view(-1), [self.lm4], [self.dlogits])
@@ -337,6 +365,7 @@ class HybridModel:
                                self.dtok[k], self.vtok.view(-1), T["fill_rows"][k], tiled=False)
             return self.dtok[k]
         _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
+        self._tr("draft.logits", self.dlogits)
         top = _C.fast_topk(self.dlogits, width, False)[1]
         self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
         return top.view(-1)[:1]
@@ -357,15 +386,25 @@ class HybridModel:
         _C.mtp_prep_verify(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0)
         torch.index_select(self.ftab, 0, self.vpos.view(-1), out=self.vfreqs)
         torch.index_select(self.embed, 0, self.vtok.view(-1), out=self.x)
+        self._tr("verify.vtok", self.vtok)
         self.verify_layers(self.x, R, T["mask"], self.aseq, self.apos, self.vfreqs)
         xf = _C.rmsnorm(self.x, self.final_norm, c.eps)
         _C.bf16_linear(xf, self.lm_head, out=self.logits)
+        self._tr("verify.xf", xf)
+        self._tr("verify.logits", self.logits)
         vals, idx = _C.topk_rows(self.logits, c.top_k)
+        self._tr("verify.vals", vals)
+        self._tr("verify.idx", idx)
         if c.greedy:
             self.toks.copy_(idx[:, :1].reshape(1, R))
         else:
             # Gumbel-max over the top-k: a sample of softmax(vals / T) restricted to the top k
             _C.topk_sample(vals, idx, torch.rand(R, c.top_k, device=self.dev), c.temperature, out=self.toks.view(R))
+        self._tr("verify.toks", self.toks)
+        for i, kv in enumerate(self.kv):
+            if kv is not None:
+                self._tr(f"L{i}.key_pre_accept", kv[0])
+                self._tr(f"L{i}.value_pre_accept", kv[1])
         _C.mtp_accept(self.st, self.toks, self.vtok, None, T["children"], R, T["depth"], self.x, self.nt,
                       self.hbuf.view(1, 1, -1), self.ctl, self.kv_ptrs, c.kv_heads, c.cap, c.head_dim, self.result)
 
