@@ -28,6 +28,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "comfy-mono-decode-xpu_amd"))
 
 PEAK_HBM_GBS = 8000.0
+PEAK_I8_OPS = 5.0e15      # dense int8 MFMA, MI355X
+PEAK_BF16_FLOPS = 2.5e15  # dense bf16 MFMA, MI355X
 METRIC = "W4A8 GEMV achieved HBM GB/s (% of peak); decode tok/s at 9B hybrid, 8-draft tree"
 
 
@@ -226,6 +228,12 @@ def bench_mlp(args, dev):
                      "algorithmic_bytes_per_launch": gu_b, "avg_launch_us": round(t_gu * 1e6, 3),
                      "single_launch_read_roof_gbs": read_roof("52MB")},
     }
+    if M >= 2:
+        # the MFMA path (v_mfma_i32_16x16x32_i8 on rows padded to 16): issued int8 operations of the gate/up
+        # launch per second against the dense int8 peak (counters: profiles/mfma_mlp8_attn16.md)
+        ops = 2 * 16 * -(-M // 16) * 2 * I * H
+        res["roofline"]["mfma_util"] = round(ops / t_gu / PEAK_I8_OPS, 4)
+        res["roofline"]["mfma_useful_util"] = round(2 * M * 2 * I * H / t_gu / PEAK_I8_OPS, 4)
     # the same block with the fp16-faithful packer (group scales kept as fp16 ratios, per-weight rint decode)
     del ring
     torch.cuda.empty_cache()
@@ -346,7 +354,9 @@ def bench_attn(args, dev):
                               f"{ring_n}-copy KV ring", "ctx": L, "rows": S, "algorithmic_bytes_per_step": per},
                  {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
                   "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                  "avg_launch_us": round(t * 1e6, 3)})
+                  "avg_launch_us": round(t * 1e6, 3),
+                  # S^T = K Q^T and O^T = V^T P^T on bf16 MFMA: 4 H S L D flops per call against the dense peak
+                  "mfma_util": round(4 * H * S * L * D / t / PEAK_BF16_FLOPS, 4)})
 
 
 def bench_stack(args, dev, tokens=0, two_stage=False):

@@ -101,19 +101,20 @@ size_t mdx_mono_mlp_workspace(int64_t rows, int64_t K1, int64_t N1);
  * gate/up: N1 x K1, down: N2 x N1; one codebook for all three; 1 <= rows <= 16. With residual (bf16
  * [rows, N2], may equal xn): out = bf16(float(residual) + float(bf16(down))) (layer_post's last phase,
  * csrc/mono_layer.sycl:303-313).
- * workspace: >= mdx_mono_mlp_workspace(rows, K1, N1) bytes, 256-byte aligned, ZERO-FILLED before its
- * first use (its control words and int32 accumulators; every call leaves them zero again). Calls that
- * share a workspace must be ordered (one stream). Four launches: row prep of x, gate/up, row prep of h,
- * down. With MDX_MLP_FUSED=1 in the environment (opt-in: slower on MI355X), shapes with K1 <= 4096,
- * N1 % 256 == 0 and rot != MATRIX whose grid is resident at once run as two: the row prep, then
- * gate/up + rotation of h + K-split down in one launch. */
+ * workspace: >= mdx_mono_mlp_workspace(rows, K1, N1) bytes, 256-byte aligned (the intermediates: the
+ * gate/up work-groups' |h| maxima, q1, q2, row scales, h; zero-filling it once is recommended for the
+ * diagnostic word of mdx_mono_mlp_error_offset, which no launch of this library sets). Calls that share a
+ * workspace must be ordered (one stream). Four launches: row prep of x, gate/up, row prep of h, down;
+ * without rotation at 1 row two (the row prep in the gate/up prologue, h quantised in the down
+ * prologue), at 2 rows three. */
 int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float eps, const uint16_t* h, int32_t rot,
                  const uint16_t* silu_lut, const mdx_w4* gate, const mdx_w4* up, const mdx_w4* down,
                  const uint16_t* residual, uint16_t* out, int64_t rows, void* workspace, size_t workspace_bytes,
                  void* stream);
 
-/* Byte offset in the mdx_mono_mlp workspace of a word that a call sets to 1 if one of its in-kernel
- * waits gave up (a diagnostic; zero in correct operation). No counterpart in the reference. */
+/* Byte offset in the mdx_mono_mlp workspace of a diagnostic word reserved for in-kernel waits that give
+ * up; no launch of this library waits on another work-group, so it stays as the caller left it (zero).
+ * No counterpart in the reference. */
 size_t mdx_mono_mlp_error_offset(void);
 
 /* One launch of the stream GEMV engine over up to three W4 matrices sharing K (outputs per matrix),

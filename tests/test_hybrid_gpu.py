@@ -74,3 +74,34 @@ def test_two_stage_drafts_equal_one_stage(dev):
     torch.cuda.synchronize()
     a, b = ms
     assert torch.equal(a.st, b.st) and torch.equal(a.result, b.result) and torch.equal(a.hbuf, b.hbuf)
+
+
+def test_full_stack_steps(dev):
+    """The full decode stack (32 layers: 24 GDN + 8 attention, hidden 4096, MLP 12288, vocab 151936, tree
+    (4, 3)): eager steps give finite logits, advance the counters by the accepted count and commit only
+    tree tokens; a captured graph replayed from the same state reproduces the eager steps."""
+    from mdx import hybrid
+    ms = []
+    for _ in range(2):
+        cfg = hybrid.HybridConfig(cap=256, greedy=True)
+        m = hybrid.HybridModel(cfg, dev, seed=9)
+        m.prefill(torch.randint(0, cfg.vocab, (41,), generator=torch.Generator().manual_seed(4)))
+        ms.append(m)
+    a, b = ms
+    for step in range(3):
+        print(f"case full stack eager step {step}", flush=True)
+        st0 = a.st[0].item()
+        a.step(a.parity)
+        a.parity ^= 1
+        torch.cuda.synchronize()
+        assert torch.isfinite(a.logits.float()).all()
+        n = a.result[0].item()
+        assert 1 <= n <= a.R and a.st[0].item() == st0 + n
+        committed = a.result[1:1 + n].tolist()
+        assert all(t in a.vtok[0].tolist() or t == a.nt.item() for t in committed)
+    print("case full stack graph replay", flush=True)
+    b.capture()  # two eager warm-up steps, one per parity
+    b.replay(1)
+    torch.cuda.synchronize()
+    assert torch.equal(a.st, b.st) and torch.equal(a.nt, b.nt) and torch.equal(a.result, b.result)
+    assert torch.equal(a.hbuf, b.hbuf) and torch.equal(a.logits, b.logits)
