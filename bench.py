@@ -301,11 +301,29 @@ def _line(args, value, unit, t, steps, dtype, data, config, roofline=None):
 
 
 def bench_lmhead(args, dev):
-    """bf16 lm_head of the hybrid stack: vocab 151936 x hidden 4096, `rows` decode rows."""
+    """bf16 lm_head of the hybrid stack: vocab 151936 x hidden 4096, `rows` decode rows (--head int8: the
+    int8 ConvRot head through the W8A8 linear)."""
     import torch
     from mdx import _C, layout
     gen = torch.Generator(device=dev).manual_seed(5)
     V, H, M = 151936, 4096, args.rows
+    if args.head == "int8":
+        per = V * H + V * 4 + M * (H + 4) + M * V * 2
+        w8 = layout.tile_major_i8(torch.randint(-127, 128, (V, H), generator=gen, device=dev, dtype=torch.int8))
+        s8 = torch.rand(V, generator=gen, device=dev) * 1e-3 + 1e-4
+        x8 = torch.randint(-128, 128, (M, H), generator=gen, device=dev, dtype=torch.int8)
+        xs = torch.rand(M, generator=gen, device=dev) * 0.05 + 0.01
+        out = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+        steps = max(1, args.steps // 5)
+        t = ring_time(lambda i: _C.int8_linear_prequantized(x8, xs, w8, s8, tiled=True, out=out), 1, steps, args.warmup)
+        gbs = per / t / 1e9
+        return _line(args, round(gbs, 2), "GB/s", t, steps, "int8 x int8 -> int32 (MFMA), bf16 out",
+                     "synthetic (seeded int8 weights and rows, per-row scales)",
+                     {"workload": f"int8 ConvRot lm_head 151936x4096, rows={M}, tile-major", "rows": M,
+                      "algorithmic_bytes_per_step": per},
+                     {"bound": "hbm", "kernel": "int8_linear_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                      "avg_launch_us": round(t * 1e6, 3)})
     per = V * H * 2 + M * H * 2 + M * V * 2
     w = layout.tile_major_bf16((torch.randn(V, H, generator=gen, device=dev) * 0.02).bfloat16())
     x = torch.randn(M, H, generator=gen, device=dev).bfloat16()
@@ -359,20 +377,21 @@ def bench_attn(args, dev):
                   "mfma_util": round(4 * H * S * L * D / t / PEAK_BF16_FLOPS, 4)})
 
 
-def bench_stack(args, dev, tokens=0, two_stage=False):
+def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     """The full synthetic 32-layer hybrid stack (3 GDN : 1 attention, hidden 4096, MLP 12288, W4A8
     GPTQ G128), 1-layer bf16 MTP draft block, bf16 lm_head over 151936, tree_spec (4, 3) (8 rows, 2
     drafts per step), top-k 20 sampling; a seeded random prompt is prefilled (not timed), then each
     decode step is one replayed HIP graph. value = accepted tokens per second. tokens > 0: decode
     until that many tokens are committed (chunks of 64 steps, each timed by events, the committed
-    count read between chunks); else exactly `steps` steps."""
+    count read between chunks); else exactly `steps` steps. head "int8": the int8 ConvRot lm_head (W8A8) for
+    the verify and the drafts instead of the bf16 one."""
     import torch
     from mdx import hybrid
     steps, warm = args.steps, max(args.warmup, 2)
     per = 3  # at most len(widths) + 1 tokens committed per step
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
-    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage)
+    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -398,10 +417,11 @@ def bench_stack(args, dev, tokens=0, two_stage=False):
         got = int(m.st[0].item()) - st0
     per_step = t / done
     what = f"{got} tokens decoded" if tokens else f"{done} decode steps"
-    return _line(args, round(got / t, 2), "tok/s", per_step, done, "W4A8 int8 x int4 -> int32; bf16 draft, lm_head",
+    hd = "int8 ConvRot lm_head (W8A8)" if head == "int8" else "bf16 lm_head"
+    return _line(args, round(got / t, 2), "tok/s", per_step, done, f"W4A8 int8 x int4 -> int32; bf16 draft block, {hd}",
                  "synthetic (random-init weights, seeded random prompt)",
-                 {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936, "
-                              f"MTP draft{' (two-stage head)' if two_stage else ''}, tree (4, 3), top-k 20, "
+                 {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936 "
+                              f"({hd}), MTP draft{' (two-stage head)' if two_stage else ''}, tree (4, 3), top-k 20, "
                               f"prompt {args.prompt}, {what}",
                   "prompt": args.prompt, "steps": done, "tokens": got,
                   "accepted_per_step": round(got / done, 3), "ms_per_step": round(per_step * 1e3, 4),
@@ -603,6 +623,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=0, help="stack: decode until this many tokens are committed")
     ap.add_argument("--two-stage", action="store_true", help="stack: drafts score the vocabulary with an int4 copy "
                                                                "of the lm_head and recompute their candidates exactly")
+    ap.add_argument("--head", choices=["bf16", "int8"], default="bf16",
+                    help="stack / lmhead: the bf16 lm_head or the int8 ConvRot one (W8A8)")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -620,7 +642,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     if args.workload == "stack":
-        res = bench_stack(args, dev, tokens=args.tokens, two_stage=args.two_stage)
+        res = bench_stack(args, dev, tokens=args.tokens, two_stage=args.two_stage, head=args.head)
     else:
         res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
                "attn": bench_attn, "read": bench_read, "attn_layer": bench_attn_layer,

@@ -441,6 +441,29 @@ def bf16_linear(x, w, tiled=True, residual=None, out=None):
     return out
 
 
+def int8_linear_prequantized(x, x_scale, w, w_scale, bias=None, out_dtype=2, tiled=False, out=None):
+    """W8A8 linear of the int8 ConvRot lm_head (omni_xpu_kernel's int8_linear_prequantized, called at
+    comfy_mono_decode_xpu/draft_head.py:228): bf16((float(acc) * x_scale[m]) * w_scale[n]) with acc the exact
+    int32 dot of the int8 rows. x int8 [rows, K] (1..16 rows), x_scale f32 [rows] (or [rows, 1]), w int8
+    [N, K] (tile-major, layout.tile_major_i8, when tiled), w_scale f32 [N]. Only bf16 out (out_dtype 2)
+    and no bias, the forms the reference's head uses."""
+    _dev(x, "x")
+    _check(bias is None, "bias is not supported (the int8 head has none)")
+    _check(out_dtype == 2, "out_dtype 2 (bf16) only")
+    _check(x.dtype == torch.int8 and x.is_contiguous() and x.dim() == 2, "x: contiguous int8 [rows, K]")
+    rows, K = x.shape
+    _check(x_scale.dtype == torch.float32 and x_scale.is_contiguous() and x_scale.numel() == rows, "x_scale f32 [rows]")
+    _check(w.dtype == torch.int8 and w.is_contiguous() and w.dim() == 2 and w.shape[1] == K, "w: contiguous int8 [N, K]")
+    N = w.shape[0]
+    _check(w_scale.dtype == torch.float32 and w_scale.is_contiguous() and w_scale.numel() == N, "w_scale f32 [N]")
+    if out is None:
+        out = torch.empty(rows, N, dtype=torch.bfloat16, device=x.device)
+    _check(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == rows * N, "out bf16 [rows, N]")
+    _lib.call("mdx_int8_linear", _lib.ptr(x), _lib.ptr(x_scale), _lib.ptr(w), _lib.ptr(w_scale),
+              _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW, _lib.ptr(out), rows, N, K, _lib.stream_of(x))
+    return out
+
+
 def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
              sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None, raw=False):
     """The Gated-DeltaNet core of csrc/mono_gdn.sycl:313-607 (layer_gdn phases P3-P5; layer_gdn_core's

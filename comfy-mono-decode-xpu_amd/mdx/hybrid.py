@@ -43,7 +43,8 @@ class HybridConfig:
     top_k: int = 20
     temperature: float = 1.0
     greedy: bool = False          # take the top-1 instead of sampling
-    two_stage: bool = False       # drafts: int4 scores + the draft pick instead of the full bf16 lm_head
+    two_stage: bool = False       # drafts: int4 scores + the draft pick instead of the full lm_head
+    head: str = "bf16"            # "int8": the int8 ConvRot lm_head (W8A8) for the verify and the drafts
     eps: float = 1e-6
     cap: int = 2048
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
@@ -116,15 +117,30 @@ class HybridModel:
         self.gdn_ch = 2 * hk * 128 + hv * 128
         self.embed = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.5).bfloat16()
         head = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.02).bfloat16()
-        self.lm_head = layout.tile_major_bf16(head)
-        # the two-stage draft head: an int4 copy of the lm_head scored by the W4A8 GEMV, and the row-major
-        # head the draft pick reads its candidates from (8 KiB contiguous per row; the tile-major copy
-        # serves the full-vocabulary passes)
-        self.lm4 = layout.int4_scoring_copy(head) if c.two_stage else None
-        self.lm_rows = head if c.two_stage else None
-        del head
+        if c.head not in ("bf16", "int8"):
+            raise ValueError("head: 'bf16' or 'int8'")
+        self.lm_head = self.lm_rows = self.lm8 = self.lm8_rows = self.lm8_s = None
+        if c.head == "int8":
+            # the int8 ConvRot head (rows rotated by H256 per 256 group, per-row scales), tile-major for the
+            # W8A8 linear; the two-stage drafts score an int4 copy of it and the pick recomputes its
+            # candidates from the row-major int8 rows (comfy_mono_decode_xpu/draft_lmhead.py:68-84)
+            q8, self.lm8_s = layout.int8_convrot_head(head)
+            del head
+            self.lm8 = layout.tile_major_i8(q8)
+            self.lm4 = layout.int4_scoring_copy(q8.float() * self.lm8_s[:, None]) if c.two_stage else None
+            self.lm8_rows = q8 if c.two_stage else None
+            del q8
+        else:
+            self.lm_head = layout.tile_major_bf16(head)
+            # the two-stage draft head: an int4 copy of the lm_head scored by the W4A8 GEMV, and the row-major
+            # head the draft pick reads its candidates from (8 KiB contiguous per row; the tile-major copy
+            # serves the full-vocabulary passes)
+            self.lm4 = layout.int4_scoring_copy(head) if c.two_stage else None
+            self.lm_rows = head if c.two_stage else None
+            del head
         self.final_norm = _norm(H, gen, dev)
         self.h256 = layout.regular_hadamard(dev)
+        self.h256f = layout.regular_hadamard(dev, torch.float32)  # the draft ops take the f32 matrix
         self.silu = layout.silu_lut(dev)
         self.sig = torch.sigmoid(layout.bf16_all(dev)).contiguous()
         self.layers = []
@@ -210,6 +226,9 @@ class HybridModel:
         self.dact = torch.zeros(S, c.inter, **bf)
         self.dd = torch.zeros(S, c.hidden, **bf)
         self.dxf = torch.zeros(S, c.hidden, **bf)
+        self.dqx = torch.zeros(S, c.hidden, dtype=torch.int8, device=dev)
+        self.dsx = torch.zeros(S, dtype=torch.float32, device=dev)
+        self.pick_calls = torch.zeros(1, **i64)
         self.dlogits = torch.zeros(1, c.vocab, **bf)
         self.dtop = torch.zeros(len(c.widths), 8, **i64)
         self.dtok = torch.zeros(len(c.widths), 1, **i64)
@@ -344,7 +363,14 @@ class HybridModel:
         self._tr("mtp.gu", gu)
         self._tr("mtp.act", act)
         self._tr("mtp.d", d)
-        _C.draft_norm_rot_quant(x, d, M["norm_f"], c.eps, None, _C._buf(self.dxf, n, H), None, None)
+        if c.head == "int8":
+            # the int8 head's input: the final norm rotated by H256 and quantised per row
+            _C.draft_norm_rot_quant(x, d, M["norm_f"], c.eps, self.h256f, _C._buf(self.dxf, n, H), self.dqx[:n],
+                                    self.dsx[:n])
+            self._tr("mtp.qx", self.dqx[:n])
+            self._tr("mtp.sx", self.dsx[:n])
+        else:
+            _C.draft_norm_rot_quant(x, d, M["norm_f"], c.eps, None, _C._buf(self.dxf, n, H), None, None)
         self._tr("mtp.x_out", x)
         self._tr("mtp.xf", _C._buf(self.dxf, n, H))
 
@@ -358,6 +384,18 @@ class HybridModel:
         _C.mtp_prep_draft(self.st, k, self.ftab.view(1, 1, c.cap, c.rotary // 2, 2, 2), self.dfreqs, self.mpos, self.mseq)
         self.mtp_block(1, tok, h, self.dfreqs.view(1, c.rotary // 2, 2, 2), self.mpos[:1], self.mseq, None)
         xf = self.dxf[:1]
+        if c.head == "int8":
+            qx, sx = self.dqx[:1], self.dsx[:1]
+            if c.two_stage:
+                _C.stream_gemv(qx, sx, [self.lm4], [self.dlogits])
+                _C.draft_pick(self.dlogits.view(-1), qx.view(-1), sx, self.lm8_rows, self.lm8_s, width, False,
+                              self.dtop[k], None, self.dtok[k], self.vtok.view(-1), T["fill_rows"][k], self.pick_calls)
+                return self.dtok[k]
+            _C.int8_linear_prequantized(qx, sx, self.lm8, self.lm8_s, tiled=True, out=self.dlogits)
+            self._tr("draft.logits", self.dlogits)
+            top = _C.fast_topk(self.dlogits, width, False)[1]
+            self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
+            return top.view(-1)[:1]
         if c.two_stage:
             q, s = _C.quant_rows(xf)
             _C.stream_gemv(q, s.view(-1), [self.lm4], [self.dlogits])
@@ -388,9 +426,15 @@ class HybridModel:
         torch.index_select(self.embed, 0, self.vtok.view(-1), out=self.x)
         self._tr("verify.vtok", self.vtok)
         self.verify_layers(self.x, R, T["mask"], self.aseq, self.apos, self.vfreqs)
-        xf = _C.rmsnorm(self.x, self.final_norm, c.eps)
-        _C.bf16_linear(xf, self.lm_head, out=self.logits)
-        self._tr("verify.xf", xf)
+        if c.head == "int8":
+            q, s = _C.rms_rot_quant(self.x, self.final_norm, c.eps, _lib.ROT_H256, self.h256)
+            _C.int8_linear_prequantized(q, s, self.lm8, self.lm8_s, tiled=True, out=self.logits)
+            self._tr("verify.q", q)
+            self._tr("verify.s", s)
+        else:
+            xf = _C.rmsnorm(self.x, self.final_norm, c.eps)
+            _C.bf16_linear(xf, self.lm_head, out=self.logits)
+            self._tr("verify.xf", xf)
         self._tr("verify.logits", self.logits)
         vals, idx = _C.topk_rows(self.logits, c.top_k)
         self._tr("verify.vals", vals)

@@ -208,6 +208,51 @@ def tile_major_bf16(w: torch.Tensor) -> torch.Tensor:
     return w.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous().reshape(N, K)
 
 
+def tile_major_i8(w: torch.Tensor) -> torch.Tensor:
+    """int8 [N, K] -> the W8A8 linear's tile-major order [N/16][K/64][64 lanes][16] (lane 16 g + c holds
+    row 16 t + c, k in [64 j + 16 g, 64 j + 16 g + 16) of block (t, j)), returned as [N, K]."""
+    N, K = w.shape
+    assert w.dtype == torch.int8 and N % 16 == 0 and K % 64 == 0
+    return w.reshape(N // 16, 16, K // 64, 4, 16).permute(0, 2, 3, 1, 4).contiguous().reshape(N, K)
+
+
+def row_major_i8(t: torch.Tensor) -> torch.Tensor:
+    """Inverse of tile_major_i8."""
+    N, K = t.shape
+    return t.reshape(N // 16, K // 64, 4, 16, 16).permute(0, 3, 1, 2, 4).contiguous().reshape(N, K)
+
+
+def convrot_rotate(w: torch.Tensor) -> torch.Tensor:
+    """w [N, K] (K % 256 == 0) -> float32 w . H256 per 256-column group, H256 = kron(H4, H4, H4, H4) / 16 (the
+    ConvRot rotation, comfy_mono_decode_xpu/layer.py:74-90; orthogonal, so (x H)(w H)^T = x w^T), computed
+    in float64 (exact for bf16 inputs up to one rounding to float32)."""
+    N, K = w.shape
+    assert K % 256 == 0
+    h = regular_hadamard(w.device, torch.float64)
+    out = torch.empty(N, K, dtype=torch.float32, device=w.device)
+    for n0 in range(0, N, 8192):
+        b = w[n0:n0 + 8192].to(torch.float64).reshape(-1, K // 256, 256)
+        out[n0:n0 + 8192] = (b @ h).reshape(-1, K).float()
+    return out
+
+
+def int8_convrot_head(w: torch.Tensor):
+    """An int8 ConvRot lm_head from a bf16 / float head [N, K]: the rows rotated by H256 per 256 group
+    (convrot_rotate), then quantised per row, s = max(amax / 127, 1e-30) (f32), q = clamp(rint(w_rot / s),
+    -127, 127) int8 -- the weight form comfy-kitchen's TensorWiseINT8Layout with convrot (group size 256)
+    holds and draft_lmhead._plain accepts (comfy_mono_decode_xpu/draft_lmhead.py:33-46). Returns (q int8
+    [N, K] row-major, s f32 [N])."""
+    N, K = w.shape
+    q = torch.empty(N, K, dtype=torch.int8, device=w.device)
+    s = torch.empty(N, dtype=torch.float32, device=w.device)
+    for n0 in range(0, N, 16384):
+        r = convrot_rotate(w[n0:n0 + 16384])
+        sc = (r.abs().amax(1) / 127.0).clamp_min(1e-30)
+        q[n0:n0 + 16384] = torch.round(r / sc[:, None]).clamp(-127, 127).to(torch.int8)
+        s[n0:n0 + 16384] = sc
+    return q, s
+
+
 def int4_scoring_copy(w: torch.Tensor, group_size: int = 128) -> W4:
     """An int4 copy of a bf16 or int8 head [N, K] for the first stage of the two-stage draft lm_head
     (comfy_mono_decode_xpu/draft_lmhead.py:80-95 makes the same kind of copy of its int8 head): per group of

@@ -265,6 +265,19 @@ int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stri
 int mdx_bf16_linear(const uint16_t* x, const uint16_t* w, int32_t layout, const uint16_t* residual, uint16_t* out,
                     int64_t rows, int64_t N, int64_t K, void* stream);
 
+/* W8A8 linear (the int8 ConvRot lm_head): out[m, n] = bf16((float(acc) * x_scale[m]) * w_scale[n]), acc the
+ * exact int32 dot of the int8 row x[m] with the int8 weight row w[n] (two fp32 roundings, no FMA).
+ * Replaces: omni_xpu_kernel int8_linear_prequantized(qx, sx, q, s, None, 2) (third-party, 0.2.0b3) as
+ * called for the int8 head at comfy_mono_decode_xpu/draft_head.py:228 and by the verify's F.linear on that
+ * head (comfy_mono_decode_xpu/mtp_loop.py:221-225); the logit formula is the draft pick's
+ * (csrc/draft_lmhead.sycl:217-220).
+ * x int8 [rows, K], x_scale f32 [rows], w int8 [N, K] row-major (MDX_LAYOUT_ROW) or tile-major
+ * (MDX_LAYOUT_TILE: [N/16][K/64][64][16 B], lane 16 g + c holding row 16 t + c, k in [64 j + 16 g, + 16) of
+ * block (t, j)), w_scale f32 [N], out bf16 [rows, N]. 1 <= rows <= 16, N % 16 == 0, K % 64 == 0,
+ * K <= 65536. */
+int mdx_int8_linear(const int8_t* x, const float* x_scale, const int8_t* w, const float* w_scale, int32_t layout,
+                    uint16_t* out, int64_t rows, int64_t N, int64_t K, void* stream);
+
 /* Gated-DeltaNet decode core of one layer with deferred replay, for 1..slots tree-verify rows.
  * Replaces: the GDN phases of _C.layer_gdn (csrc/mono_gdn.sycl:313-607) and _C.layer_gdn_core
  * (csrc/mono_gdn.sycl:702-704).

@@ -50,13 +50,15 @@ def test_graph_replay_matches_eager(dev):
     assert torch.equal(a.hbuf, b.hbuf)
 
 
-def test_two_stage_drafts_equal_one_stage(dev):
-    """The two-stage draft head (int4 scores + the draft pick) gives the same decode as the full bf16 head:
-    counters, accept records, next tokens and hidden rows after eager steps and a graph replay."""
+@pytest.mark.parametrize("head", ["bf16", "int8"])
+def test_two_stage_drafts_equal_one_stage(dev, head):
+    """The two-stage draft head (int4 scores + the draft pick) gives the same decode as the full lm_head (bf16,
+    or the int8 ConvRot head): counters, accept records, next tokens and hidden rows after eager steps and
+    a graph replay."""
     from mdx import hybrid
     ms = []
     for two in (False, True):
-        cfg = hybrid.HybridConfig(layers=4, inter=4096, vocab=32768, cap=256, greedy=True, two_stage=two)
+        cfg = hybrid.HybridConfig(layers=4, inter=4096, vocab=32768, cap=256, greedy=True, two_stage=two, head=head)
         m = hybrid.HybridModel(cfg, dev, seed=7)
         m.prefill(torch.randint(0, cfg.vocab, (37,), generator=torch.Generator().manual_seed(2)))
         ms.append(m)

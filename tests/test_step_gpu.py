@@ -53,9 +53,10 @@ def _attn_bound(got, q, k, v, L, xk, xv, mask, what):
     assert err.mean() <= 1.5 * e_ref.mean() + 1e-5, (what, err.mean(), e_ref.mean())
 
 
-def test_decode_step_matches_oracle(C, dev):
+@pytest.mark.parametrize("head", ["bf16", "int8"])
+def test_decode_step_matches_oracle(C, dev, head):
     from mdx import hybrid, layout
-    cfg = hybrid.HybridConfig(layers=2, attn_every=2, cap=128, greedy=True)
+    cfg = hybrid.HybridConfig(layers=2, attn_every=2, cap=128, greedy=True, head=head)
     m = hybrid.HybridModel(cfg, dev, seed=11)
     m.prefill(torch.randint(0, cfg.vocab, (24,), generator=torch.Generator().manual_seed(3)))
     torch.cuda.synchronize()
@@ -84,7 +85,12 @@ def test_decode_step_matches_oracle(C, dev):
     mk, mv = snap["mk"].copy(), snap["mv"].copy()
     tok, h = snap["nt"], snap["hbuf"]
     cols = np.random.default_rng(1).choice(cfg.vocab, 2048, replace=False)
-    lm_rows = rowmaj(m.lm_head)
+    cols_d = torch.from_numpy(cols).to(dev)
+    if head == "int8":
+        q8 = layout.row_major_i8(m.lm8)[cols_d].cpu().numpy()
+        s8 = m.lm8_s[cols_d].cpu().numpy()
+    else:
+        lm_cols = _np(rowmaj(m.lm_head)[cols_d])
     for k, width in enumerate(cfg.widths):
         print(f"case step draft {k}", flush=True)
         g = lambda n: _np(tr[f"mtp.{n}"][k])
@@ -113,11 +119,17 @@ def test_decode_step_matches_oracle(C, dev):
         _bf16_bound(g("gu"), g("xn_post"), _np(rowmaj(M["gu"])), f"draft {k} gate|up")
         assert_bits_equal(g("act"), ref.draft_silu_mul(g("gu"), lut), f"draft {k} silu")
         _bf16_bound(g("d"), g("act"), _np(rowmaj(M["d"])), f"draft {k} down")
-        xo, xr, _, _ = ref.draft_norm_rot_quant(g("x_post"), g("d"), _np(M["norm_f"]), eps, rot="none")
+        xo, xr, qx, sx = ref.draft_norm_rot_quant(g("x_post"), g("d"), _np(M["norm_f"]), eps,
+                                                  rot="h256" if head == "int8" else "none")
         assert_bits_equal(g("x_out"), xo, f"draft {k} x + down")
         assert_bits_equal(g("xf"), xr, f"draft {k} final norm")
         logits = _np(tr["draft.logits"][k])
-        _bf16_bound(logits[:, cols], g("xf"), _np(lm_rows[torch.from_numpy(cols).to(dev)]), f"draft {k} lm_head")
+        if head == "int8":
+            assert_bits_equal(g("qx"), qx, f"draft {k} head activation")
+            assert_bits_equal(g("sx"), sx.view(np.uint32), f"draft {k} head activation scale")
+            assert_bits_equal(logits[0, cols], ref.int8_head_logits(qx[0], sx, q8, s8), f"draft {k} int8 lm_head")
+        else:
+            _bf16_bound(logits[:, cols], g("xf"), lm_cols, f"draft {k} lm_head")
         _, top = ref.fast_topk(logits[0], width)
         vt = m.vtok.cpu().numpy()[0]
         assert vt[T["fill_rows"][k]].tolist() == top.tolist(), f"draft {k} tree tokens"
@@ -183,9 +195,16 @@ def test_decode_step_matches_oracle(C, dev):
     # ---- head, pick, accept ---------------------------------------------------------------------------
     print("case step head and accept", flush=True)
     xf = ref.rmsnorm(_np(tr["L1.out"][0]), _np(m.final_norm), eps)
-    assert_bits_equal(_np(tr["verify.xf"][0]), xf, "final norm")
     logits = _np(tr["verify.logits"][0])
-    _bf16_bound(logits[:, cols], xf, _np(lm_rows[torch.from_numpy(cols).to(dev)]), "verify lm_head")
+    if head == "int8":
+        q, s = ref.rot_quant(xf, "h256")
+        assert_bits_equal(_np(tr["verify.q"][0]), q, "verify head activation")
+        assert_bits_equal(_np(tr["verify.s"][0]), s.view(np.uint32), "verify head activation scales")
+        for r in range(R):
+            assert_bits_equal(logits[r, cols], ref.int8_head_logits(q[r], s[r:r + 1], q8, s8), f"verify int8 lm_head row {r}")
+    else:
+        assert_bits_equal(_np(tr["verify.xf"][0]), xf, "final norm")
+        _bf16_bound(logits[:, cols], xf, lm_cols, "verify lm_head")
     wv, wi = ref.topk_rows(logits, cfg.top_k)
     assert np.array_equal(_np(tr["verify.idx"][0]), wi), "top-20 indices"
     assert_bits_equal(_np(tr["verify.vals"][0]), wv.view(np.uint32), "top-20 values")
