@@ -48,6 +48,7 @@ class HybridConfig:
     eps: float = 1e-6
     cap: int = 2048
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
+    rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
 
     def attention(self, i):
         return i % self.attn_every == self.attn_every - 1
@@ -141,6 +142,8 @@ class HybridModel:
         self.final_norm = _norm(H, gen, dev)
         self.h256 = layout.regular_hadamard(dev)
         self.h256f = layout.regular_hadamard(dev, torch.float32)  # the draft ops take the f32 matrix
+        # the W4 activation preps: plain absmax (GPTQ weights) or H256 first (ConvRot-packed weights)
+        self.rot, self.hrot = (_lib.ROT_H256, self.h256) if c.rotate else (_lib.ROT_NONE, None)
         self.silu = layout.silu_lut(dev)
         self.sig = torch.sigmoid(layout.bf16_all(dev)).contiguous()
         self.layers = []
@@ -168,6 +171,23 @@ class HybridModel:
                         gu=_bf16w(2 * I, H, gen, dev, 0.02), d=_bf16w(H, I, gen, dev, 0.02), norm_f=_norm(H, gen, dev))
         self.ftab = rope_table(c, dev)
         self._state(gen)
+
+    def load_w4(self, weights, plan):
+        """Replace the W4 linears of the layers in `plan` ({layer: {role: prefix}}, as checkpoint.plan_hybrid
+        returns) by packed checkpoint linears (`weights`: {prefix: layout.W4}). The layer's three MLP
+        projections must share one codebook (the MLP block decodes them with one table); the attention
+        q_proj must be ungated ([heads * head_dim, hidden]). Weights packed with a ConvRot rotation
+        (comfy-kitchen's W4A8 layout) need cfg.rotate."""
+        c = self.cfg
+        qd = c.heads * c.head_dim
+        for i, roles in plan.items():
+            ws = {r: weights[p] for r, p in roles.items()}
+            if "q" in ws and ws["q"].n != qd:
+                raise ValueError(f"layer {i}: a gated q_proj ({ws['q'].n} rows) is not supported here")
+            cbs = [ws[r].cb for r in ("g", "u", "d")]
+            if not (all(cb is None for cb in cbs) or all(cb is not None and torch.equal(cb, cbs[0]) for cb in cbs)):
+                raise ValueError(f"layer {i}: gate / up / down codebooks differ")
+            self.layers[i].update(ws)
 
     # ---- decode state --------------------------------------------------------------------------
     def _state(self, gen):
@@ -260,7 +280,7 @@ class HybridModel:
         c, L = self.cfg, self.layers[i]
         key, value = self.kv[i]
         xn = torch.empty(R, c.hidden, dtype=torch.bfloat16, device=self.dev)
-        q, s = _C.rms_rot_quant(x, L["norm_in"], c.eps, _lib.ROT_NONE, None, xn_out=xn)
+        q, s = _C.rms_rot_quant(x, L["norm_in"], c.eps, self.rot, self.hrot, xn_out=xn)
         qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
         qkv = [torch.empty(R, n, dtype=torch.bfloat16, device=self.dev) for n in (qd, kd, kd)]
         _C.stream_gemv(q, s, [L["q"], L["k"], L["v"]], qkv)
@@ -277,15 +297,15 @@ class HybridModel:
         self._tr(f"L{i}.qo", qo)
         self._tr(f"L{i}.ko", ko)
         self._tr(f"L{i}.y", y)
-        _C._layer_post(x, y.view(R, qd), None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"],
+        _C._layer_post(x, y.view(R, qd), None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"],
                        L["d"], 6)
 
     def _gdn_layer(self, i, x, R):
         c, L, G = self.cfg, self.layers[i], self.gdn[i]
         sc = _C._scratch(self.dev)
         xn, q, s = _C._buf(sc["xn"], R, c.hidden), _C._buf(sc["q1"], R, c.hidden), sc["s"][:R]
-        _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn), None,
-                  _lib.ROT_NONE, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
+        _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn), _lib.ptr(self.hrot),
+                  self.rot, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
         _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
@@ -295,7 +315,7 @@ class HybridModel:
         _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
                     G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
         self._tr(f"L{i}.core_raw", core)
-        _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, None, self.silu, L["g"], L["u"], L["d"], 6,
+        _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"], L["d"], 6,
                        gnorm=(z, L["gnorm"], c.eps))
         self._tr(f"L{i}.core", core)
 

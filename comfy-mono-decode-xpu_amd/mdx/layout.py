@@ -78,12 +78,13 @@ def gptq_pack(q: torch.Tensor, scales: torch.Tensor, group_size: int = 128, inte
     n, k = q.shape
     assert k % group_size == 0 and scales.shape == (n, k // group_size)
     s = scales.float()
-    smax = s.abs().amax(dim=1).clamp_min(1e-30)
+    # the channel scales on the host: a GPU division by a scalar is a multiplication by its reciprocal,
+    # so the same weights would pack differently on the two devices (the rest is elementwise IEEE)
+    smax = s.abs().amax(dim=1).clamp_min(1e-30).cpu()
+    sch = (smax / 15.0 if integral else smax * 8.0 / 127.0).to(s.device)
     if integral:
-        sch = smax / 15.0
         s_rel = torch.round(s / sch[:, None]).clamp(1, 15)
     else:
-        sch = smax * 8.0 / 127.0
         s_rel = (s / sch[:, None]).clamp(max=127.0 / 8.0)
     packed = pack_codes(q.to(torch.int32) + 8)
     return packed, s_rel.to(torch.float16).contiguous(), sch.float().contiguous(), None
