@@ -428,6 +428,42 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
                   "setup_s": round(setup, 1)})
 
 
+def bench_stack_auto(args, dev, tokens=512):
+    """The full stack with the adaptive tree (auto): decode until `tokens` are committed; each step replays the
+    current tree's draft and verify graphs with events between them, every 32 steps the acceptance ranks and
+    device times choose the tree. value = committed tokens per second of wall time (the adaptive
+    bookkeeping, its host reads and any new tree's capture included)."""
+    import torch
+    from mdx import hybrid
+    cap = args.prompt + 8 * (tokens + 64) + 64
+    cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head)
+    t0 = time.perf_counter()
+    m = hybrid.HybridModel(cfg, dev, seed=5)
+    m.prefill(torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5)))
+    m.decode_auto(64)  # warm: the first trees captured, the clock past its warm-up
+    torch.cuda.synchronize()
+    setup = time.perf_counter() - t0
+    got = steps = 0
+    widths = []
+    t1 = time.perf_counter()
+    while got < tokens:
+        out = m.decode_auto(64)
+        got += out["tokens"]
+        steps += out["steps"]
+        widths += out["widths"]
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t1
+    final = widths[-1]
+    return _line(args, round(got / t, 2), "tok/s", t / steps, steps, "W4A8 int8 x int4 -> int32; bf16 draft block",
+                 "synthetic (random-init weights, seeded random prompt)",
+                 {"workload": f"32-layer W4A8 hybrid, vocab 151936, MTP draft, adaptive tree (auto), top-k 20, prompt "
+                              f"{args.prompt}, {got} tokens decoded", "prompt": args.prompt, "steps": steps,
+                  "tokens": got, "accepted_per_step": round(got / steps, 3), "final_widths": list(final),
+                  "trees_used": sorted({str(list(w)) for w in widths}), "ms_per_step": round(t / steps * 1e3, 4),
+                  "draft_ms": round(out["draft_ms"], 4), "verify_ms": round(out["verify_ms"], 4),
+                  "setup_s": round(setup, 1)})
+
+
 def w4_bytes(w):
     return w.q.numel() + w.s.numel() * w.s.element_size() + w.sc.numel() * 4
 
@@ -623,6 +659,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=0, help="stack: decode until this many tokens are committed")
     ap.add_argument("--two-stage", action="store_true", help="stack: drafts score the vocabulary with an int4 copy "
                                                                "of the lm_head and recompute their candidates exactly")
+    ap.add_argument("--auto", action="store_true", help="stack: the adaptive tree (decode_auto)")
     ap.add_argument("--head", choices=["bf16", "int8"], default="bf16",
                     help="stack / lmhead: the bf16 lm_head or the int8 ConvRot one (W8A8)")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")
@@ -642,7 +679,10 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     if args.workload == "stack":
-        res = bench_stack(args, dev, tokens=args.tokens, two_stage=args.two_stage, head=args.head)
+        if args.auto:
+            res = bench_stack_auto(args, dev, tokens=args.tokens or 512)
+        else:
+            res = bench_stack(args, dev, tokens=args.tokens, two_stage=args.two_stage, head=args.head)
     else:
         res = {"mlp": bench_mlp, "linear": bench_linear, "copy": bench_copy, "lmhead": bench_lmhead,
                "attn": bench_attn, "read": bench_read, "attn_layer": bench_attn_layer,

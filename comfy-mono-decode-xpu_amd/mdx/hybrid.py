@@ -48,6 +48,7 @@ class HybridConfig:
     eps: float = 1e-6
     cap: int = 2048
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
+    auto: bool = False            # adaptive tree: drafts keep 7 candidates, the accept records their ranks
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
 
     def attention(self, i):
@@ -193,8 +194,6 @@ class HybridModel:
     def _state(self, gen):
         c, dev = self.cfg, self.dev
         S = c.slots
-        self.tree = tree_tensors(c.widths, S, dev)
-        R = self.R = self.tree["R"]
         bf = dict(dtype=torch.bfloat16, device=dev)
         self.kv = [None] * c.layers
         self.gdn = [None] * c.layers
@@ -221,14 +220,11 @@ class HybridModel:
         self.result = torch.zeros(S + 24, **i64)
         self.nt = torch.zeros(1, 1, **i64)
         self.hbuf = torch.zeros(1, c.hidden, **bf)
-        self.vtok = torch.zeros(1, R, **i64)
-        self.toks = torch.zeros(1, R, **i64)
-        self.apos = torch.zeros(R, **i64)
+        # the tree rows' buffers at the slot capacity; _set_tree takes views of the first R rows
+        self._rows = dict(vtok=torch.zeros(1, S, **i64), toks=torch.zeros(1, S, **i64), apos=torch.zeros(S, **i64),
+                          vpos=torch.zeros(1, S, **i64), vfreqs=torch.zeros(S, c.rotary // 2, 2, 2, device=dev),
+                          x=torch.zeros(S, c.hidden, **bf), logits=torch.zeros(S, c.vocab, **bf))
         self.aseq = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.vpos = torch.zeros(1, R, **i64)
-        self.vfreqs = torch.zeros(R, c.rotary // 2, 2, 2, device=dev)
-        self.x = torch.zeros(R, c.hidden, **bf)
-        self.logits = torch.zeros(R, c.vocab, **bf)
         qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
         # MTP block buffers (up to `slots` rows: one per draft, a chain of rows in the prefill)
         self.dfreqs = torch.zeros(1, 1, 1, c.rotary // 2, 2, 2, device=dev)
@@ -250,8 +246,11 @@ class HybridModel:
         self.dsx = torch.zeros(S, dtype=torch.float32, device=dev)
         self.pick_calls = torch.zeros(1, **i64)
         self.dlogits = torch.zeros(1, c.vocab, **bf)
-        self.dtop = torch.zeros(len(c.widths), 8, **i64)
-        self.dtok = torch.zeros(len(c.widths), 1, **i64)
+        self.dtop = torch.zeros(7, 8, **i64)
+        self.dtok = torch.zeros(7, 1, **i64)
+        # auto: the 7 candidates of chain node k (the draft at depth k) at [7 k, 7 k + 7) for the accept's ranks
+        self.cand = torch.zeros(7 * 7, **i64)
+        self._set_tree(c.widths)
         self.empty_mask = torch.empty(0, dtype=torch.int32, device=dev)
         self.graphs = {}
         # host-side upper bound of the committed position st[0]: every KV write of a step lands at
@@ -259,6 +258,21 @@ class HybridModel:
         self.pos_bound = None
         # a list to receive (name, copy) of the step's intermediates (eager steps only; None: off)
         self.trace = None
+
+    def _set_tree(self, widths):
+        """Use the tree tree_spec(widths) from the next step on (views of the first R tree-row buffers)."""
+        c = self.cfg
+        widths = tuple(int(w) for w in widths)
+        if not (1 <= len(widths) <= 7 and all(1 <= w <= (7 if c.auto else 8) for w in widths)
+                and 1 + sum(widths) <= c.slots):
+            raise ValueError(f"widths {widths}: 1..7 depths of 1..{7 if c.auto else 8} candidates within "
+                             f"{c.slots} slots")
+        self.widths = widths
+        self.tree = tree_tensors(widths, c.slots, self.dev)
+        R = self.R = self.tree["R"]
+        b = self._rows
+        self.vtok, self.toks, self.vpos = b["vtok"][:, :R], b["toks"][:, :R], b["vpos"][:, :R]
+        self.apos, self.vfreqs, self.x, self.logits = b["apos"][:R], b["vfreqs"][:R], b["x"][:R], b["logits"][:R]
 
     def _tr(self, name, t):
         if self.trace is not None and not torch.cuda.is_current_stream_capturing():
@@ -268,7 +282,7 @@ class HybridModel:
         """Raise before launching `steps` decode steps whose KV writes could pass the cache capacity."""
         if self.pos_bound is None:
             raise RuntimeError("prefill() first")
-        per = len(self.cfg.widths) + 1
+        per = len(self.widths) + 1
         need = self.pos_bound + steps * per + self.R
         if need > self.cfg.cap:
             raise RuntimeError(f"{steps} more decode steps may write KV position {need - 1}, past the cache capacity "
@@ -399,47 +413,62 @@ class HybridModel:
         device positions of mtp_prep_draft, then the final norm, the lm_head and the top-`width`, written
         to the tree rows of depth k + 1 (chain child first). Returns the chain token [1].
         two_stage: the lm_head's int4 copy scores the vocabulary and the draft pick recomputes the exact
-        bf16 logits of its candidates (the same result whenever the exact top-width is among them)."""
+        logits of its candidates (the same result whenever the exact top-width is among them).
+        auto: the draft keeps its 7 best candidates in self.cand[7 k, 7 k + 7) (the accept records the rank
+        of the verify's token among them), the first `width` become tree rows."""
         c, T = self.cfg, self.tree
+        nout = 7 if c.auto else width
         _C.mtp_prep_draft(self.st, k, self.ftab.view(1, 1, c.cap, c.rotary // 2, 2, 2), self.dfreqs, self.mpos, self.mseq)
         self.mtp_block(1, tok, h, self.dfreqs.view(1, c.rotary // 2, 2, 2), self.mpos[:1], self.mseq, None)
         xf = self.dxf[:1]
+        picked = None
         if c.head == "int8":
             qx, sx = self.dqx[:1], self.dsx[:1]
             if c.two_stage:
                 _C.stream_gemv(qx, sx, [self.lm4], [self.dlogits])
-                _C.draft_pick(self.dlogits.view(-1), qx.view(-1), sx, self.lm8_rows, self.lm8_s, width, False,
+                _C.draft_pick(self.dlogits.view(-1), qx.view(-1), sx, self.lm8_rows, self.lm8_s, nout, False,
                               self.dtop[k], None, self.dtok[k], self.vtok.view(-1), T["fill_rows"][k], self.pick_calls)
-                return self.dtok[k]
-            _C.int8_linear_prequantized(qx, sx, self.lm8, self.lm8_s, tiled=True, out=self.dlogits)
-            self._tr("draft.logits", self.dlogits)
-            top = _C.fast_topk(self.dlogits, width, False)[1]
-            self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
-            return top.view(-1)[:1]
-        if c.two_stage:
+                picked = self.dtop[k]
+            else:
+                _C.int8_linear_prequantized(qx, sx, self.lm8, self.lm8_s, tiled=True, out=self.dlogits)
+        elif c.two_stage:
             q, s = _C.quant_rows(xf)
             _C.stream_gemv(q, s.view(-1), [self.lm4], [self.dlogits])
-            _C.draft_pick_bf16(self.dlogits.view(-1), xf.view(-1), self.lm_rows, width, False, self.dtop[k], None,
+            _C.draft_pick_bf16(self.dlogits.view(-1), xf.view(-1), self.lm_rows, nout, False, self.dtop[k], None,
                                self.dtok[k], self.vtok.view(-1), T["fill_rows"][k], tiled=False)
+            picked = self.dtop[k]
+        else:
+            _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
+        if picked is not None:
+            if c.auto:
+                self.cand[7 * k:7 * k + 7].copy_(picked[:7])
             return self.dtok[k]
-        _C.bf16_linear(xf, self.lm_head, out=self.dlogits)
         self._tr("draft.logits", self.dlogits)
-        top = _C.fast_topk(self.dlogits, width, False)[1]
-        self.vtok[0].index_copy_(0, T["fill"][k], top.view(-1))
-        return top.view(-1)[:1]
+        top = _C.fast_topk(self.dlogits, nout, False)[1].view(-1)
+        self.vtok[0].index_copy_(0, T["fill"][k], top[:width])
+        if c.auto:
+            self.cand[7 * k:7 * k + 7].copy_(top)
+        return top[:1]
+
+    def draft_part(self):
+        """The step's drafts: depth k proposes the children of chain node k."""
+        tok, h = self.nt.view(-1), self.hbuf
+        self.vtok[0, 0:1].copy_(self.nt.view(-1))
+        for k, w in enumerate(self.widths):
+            tok, h = self.draft(k, tok, h, w), self.dh[:1]
 
     def step(self, parity):
         """One decode step on the device (drafts, verify, sampling, accept). An eager step checks the
         KV capacity itself; a captured one is checked when its graph is replayed."""
         if not torch.cuda.is_current_stream_capturing():
             self._reserve(1)
+        self.draft_part()
+        self.verify_part(parity)
+
+    def verify_part(self, parity):
+        """The step's verify: the tree rows through the layers, lm_head, top-k, sampling, accept."""
         c, T = self.cfg, self.tree
         R = self.R
-        # drafts: depth k proposes the children of chain node k
-        tok, h = self.nt.view(-1), self.hbuf
-        self.vtok[0, 0:1].copy_(self.nt.view(-1))
-        for k, w in enumerate(c.widths):
-            tok, h = self.draft(k, tok, h, w), self.dh[:1]
         # verify
         _C.mtp_prep_verify(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0)
         torch.index_select(self.ftab, 0, self.vpos.view(-1), out=self.vfreqs)
@@ -469,8 +498,9 @@ class HybridModel:
             if kv is not None:
                 self._tr(f"L{i}.key_pre_accept", kv[0])
                 self._tr(f"L{i}.value_pre_accept", kv[1])
-        _C.mtp_accept(self.st, self.toks, self.vtok, None, T["children"], R, T["depth"], self.x, self.nt,
-                      self.hbuf.view(1, 1, -1), self.ctl, self.kv_ptrs, c.kv_heads, c.cap, c.head_dim, self.result)
+        _C.mtp_accept(self.st, self.toks, self.vtok, self.cand if c.auto else None, T["children"], R, T["depth"], self.x,
+                      self.nt, self.hbuf.view(1, 1, -1), self.ctl, self.kv_ptrs, c.kv_heads, c.cap, c.head_dim,
+                      self.result)
 
     # ---- prefill (not timed) -------------------------------------------------------------------
     def prefill(self, prompt):
@@ -516,22 +546,105 @@ class HybridModel:
         self.pos_bound = body.numel()
 
     # ---- graphs ----------------------------------------------------------------------------------
-    def capture(self):
-        """Capture one step per parity (after an eager warm-up of each)."""
-        s = torch.cuda.Stream(self.dev)
-        s.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(s):
+    def _warm(self):
+        """Two eager steps (one per parity) on a side stream: workspaces reach their sizes before capture.
+        They are real decode steps of the current tree."""
+        st = torch.cuda.Stream(self.dev)
+        st.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(st):
             for p in (self.parity, self.parity ^ 1):
                 self.step(p)
-        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.current_stream(self.dev).wait_stream(st)
+
+    def capture(self):
+        """Capture one whole step per parity for the current tree (after an eager warm-up of each)."""
+        self._warm()
         for p in (0, 1):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 self.step(p)
-            self.graphs[p] = g
+            self.graphs[(self.widths, p)] = g
 
     def replay(self, steps):
         self._reserve(steps)
         for _ in range(steps):
-            self.graphs[self.parity].replay()
+            self.graphs[(self.widths, self.parity)].replay()
             self.parity ^= 1
+
+    def capture_parts(self):
+        """Capture the current tree's step as two graphs, the drafts and (per parity) the verify, so that
+        device events between them time each part (the adaptive tree's inputs)."""
+        self._warm()
+        gd = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gd):
+            self.draft_part()
+        gv = {}
+        for p in (0, 1):
+            gv[p] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gv[p]):
+                self.verify_part(p)
+        self.graphs[(self.widths, "parts")] = (gd, gv)
+
+    def decode_auto(self, steps, fold_every=32):
+        """`steps` decode steps with the adaptive tree (cfg.auto): each step replays the current tree's
+        draft and verify graphs with HIP events around them and copies its accept record to the host;
+        every `fold_every` steps the records' ranks and the events' times are folded in
+        (autotree.Hits / Clock) and autotree.best_widths may change the tree (a new tree is captured on
+        first use; its two warm-up steps are decode steps too). Returns {"steps", "tokens", "widths"
+        (the tree of every step), "draft_ms", "verify_ms"}."""
+        from . import autotree
+        if not self.cfg.auto:
+            raise RuntimeError("decode_auto needs HybridConfig(auto=True) (the drafts keep 7 candidates)")
+        if not hasattr(self, "auto_hits"):
+            self.auto_hits, self.auto_clock = autotree.Hits(), autotree.Clock()
+        S = self.cfg.slots
+        host = torch.zeros(fold_every, S + 24, dtype=torch.int64).pin_memory()
+        out = {"steps": 0, "tokens": 0, "widths": []}
+        pending = []
+
+        def fold():
+            torch.cuda.synchronize()
+            for ev, slot, nd in pending:
+                r = host[slot].tolist()
+                n, nranks = int(r[0]), int(r[S + 3])
+                self.auto_hits.add(r[S + 4:S + 4 + nranks])
+                out["tokens"] += n
+                self.auto_clock.add(ev[0].elapsed_time(ev[1]) / nd, ev[1].elapsed_time(ev[2]))
+            pending.clear()
+            if self.auto_clock.ready:
+                best = autotree.best_widths(self.widths, self.auto_hits, self.auto_clock.draft_ms,
+                                            self.auto_clock.verify_ms, S)
+                if best != self.widths:
+                    self._set_tree(best)
+
+        done = 0
+        while done < steps:
+            if (self.widths, "parts") not in self.graphs:
+                st0 = int(self.st[0].item())
+                self.capture_parts()  # two eager steps of this tree
+                torch.cuda.synchronize()
+                out["tokens"] += int(self.st[0].item()) - st0
+                out["widths"] += [self.widths] * 2
+                done += 2
+                continue
+            gd, gv = self.graphs[(self.widths, "parts")]
+            self._reserve(1)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            ev[0].record()
+            gd.replay()
+            ev[1].record()
+            gv[self.parity].replay()
+            ev[2].record()
+            slot = len(pending)
+            host[slot].copy_(self.result, non_blocking=True)
+            pending.append((ev, slot, len(self.widths)))
+            out["widths"].append(self.widths)
+            self.parity ^= 1
+            done += 1
+            if len(pending) == fold_every:
+                fold()
+        if pending:
+            fold()
+        out["steps"] = done
+        out["draft_ms"], out["verify_ms"] = self.auto_clock.draft_ms, self.auto_clock.verify_ms
+        return out

@@ -107,3 +107,38 @@ def test_full_stack_steps(dev):
     torch.cuda.synchronize()
     assert torch.equal(a.st, b.st) and torch.equal(a.nt, b.nt) and torch.equal(a.result, b.result)
     assert torch.equal(a.hbuf, b.hbuf) and torch.equal(a.logits, b.logits)
+
+
+def test_auto_tree_records_ranks_and_adapts(dev):
+    """auto: the drafts keep 7 candidates and the accept records the verify token's rank among them, the
+    decode itself unchanged; decode_auto folds ranks and device times and, with random weights (no draft is
+    ever accepted), shrinks the tree to one draft."""
+    from mdx import hybrid
+    ms = []
+    for auto in (False, True):
+        cfg = hybrid.HybridConfig(layers=4, inter=4096, vocab=32768, cap=1024, greedy=True, auto=auto)
+        m = hybrid.HybridModel(cfg, dev, seed=5)
+        m.prefill(torch.randint(0, cfg.vocab, (37,), generator=torch.Generator().manual_seed(1)))
+        ms.append(m)
+    a, b = ms
+    S = a.cfg.slots
+    for step in range(3):
+        print(f"case auto eager step {step}", flush=True)
+        for m in ms:
+            m.step(m.parity)
+            m.parity ^= 1
+        torch.cuda.synchronize()
+        ra, rb = a.result.tolist(), b.result.tolist()
+        assert ra[:S + 3] == rb[:S + 3] and ra[S + 11:S + 13] == rb[S + 11:S + 13]
+        nranks = rb[S + 3]
+        assert ra[S + 3] == 0 and 1 <= nranks <= 2
+        cand = b.cand.view(7, 7)[0].tolist()
+        tok0 = b.toks[0, 0].item()
+        assert rb[S + 4] == (cand.index(tok0) if tok0 in cand else 7)
+    print("case auto decode", flush=True)
+    st0 = b.st[0].item()
+    out = b.decode_auto(72, fold_every=16)
+    torch.cuda.synchronize()
+    assert out["steps"] == 72 and len(out["widths"]) == 72 and out["tokens"] == b.st[0].item() - st0
+    assert out["widths"][0] == (4, 3) and out["widths"][-1] == (1,)
+    assert out["draft_ms"] > 0 and out["verify_ms"] > 0
