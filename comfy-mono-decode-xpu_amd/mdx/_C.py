@@ -10,6 +10,8 @@ plans its own launches. There is no CPU path: without libmdx.so every call raise
 from __future__ import annotations
 
 import ctypes
+import math
+import os
 
 import torch
 
@@ -390,11 +392,49 @@ def _attn_ws(dev, nbytes):
     return ws
 
 
+# MDX_ATTN=exact routes attn_dpas through the exact attention (the A/B switch of the reference's
+# MONO_DECODE_XPU_ATTN, comfy_mono_decode_xpu/layer.py:43); set_attention changes it at run time
+_ATTN_MODE = [os.environ.get("MDX_ATTN", "fast")]
+
+
+def set_attention(mode):
+    """"fast" (flash decoding on MFMA, tolerance parity) or "exact" (one canonical fp32 order)."""
+    _check(mode in ("fast", "exact"), "attention mode: 'fast' or 'exact'")
+    _ATTN_MODE[0] = mode
+
+
+def attn_exact(q, key, value, seqlen, xk, xv, mask, out=None):
+    """The exact attention (mdx_attn_exact): attn_dpas's operands and output, one canonical fp32 order."""
+    for t, n in ((q, "q"), (key, "key"), (value, "value"), (xk, "xk"), (xv, "xv")):
+        _dev(t, n)
+        _check(t.dtype == torch.bfloat16 and t.dim() == 4 and t.shape[0] == 1 and t.stride(3) == 1, f"{n}: bf16 [1, ., ., D]")
+    _, H, S, D = q.shape
+    _check(key.is_contiguous() and value.is_contiguous() and key.shape == value.shape and key.shape[3] == D,
+           "cache bf16 [1, Hk, cap, D]")
+    Hk, cap = key.shape[1], key.shape[2]
+    _check(seqlen.dtype == torch.int32 and seqlen.numel() >= 1, "int32 seqlen")
+    _check(mask.dtype == torch.int32 and mask.is_contiguous(), "int32 mask")
+    merge = mask.numel() > 0
+    _check(1 <= S <= 16 and H % Hk == 0 and (mask.numel() == S if merge else S == 1), "batch 1, 1..16 rows")
+    _check(xk.shape == xv.shape and xk.shape[1] == Hk and xk.shape[2] == S and xk.shape[3] == D,
+           "xk / xv [1, Hk, S, D]")
+    if out is None:
+        out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=q.device)
+    _check(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == S * H * D, "out bf16 [1, S, H * D]")
+    _lib.call("mdx_attn_exact", _lib.ptr(q), q.stride(1), q.stride(2), _lib.ptr(key), _lib.ptr(value), _lib.ptr(seqlen),
+              _lib.ptr(xk), xk.stride(1), xk.stride(2), _lib.ptr(xv), xv.stride(1), xv.stride(2),
+              _lib.ptr(mask) if merge else None, _lib.ptr(out), H, Hk, S, D, cap, float(1.0 / math.sqrt(D)),
+              _lib.stream_of(q))
+    return out
+
+
 def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0, out=None):
     """Reference csrc/attn_dpas.sycl:269-342: decode attention of the tree-verify rows (mask int32 [S])
     or the draft row (empty mask, S = 1) over the cache prefix [0, seqlen[0]) and the admitted tree rows.
     q bf16 [1, H, S, D]; key/value bf16 [1, Hk, cap, D]; xk/xv bf16 [1, Hk, S, D]. Returns bf16
     [1, S, H * D]. chunks_hint: 0 plans the context split; n > 0 caps it at n chunks per kv head."""
+    if _ATTN_MODE[0] == "exact":
+        return attn_exact(q, key, value, seqlen, xk, xv, mask, out)
     for t, n in ((q, "q"), (key, "key"), (value, "value"), (xk, "xk"), (xv, "xv")):
         _dev(t, n)
         _check(t.dtype == torch.bfloat16 and t.dim() == 4 and t.shape[0] == 1 and t.stride(3) == 1, f"{n}: bf16 [1, ., ., D]")

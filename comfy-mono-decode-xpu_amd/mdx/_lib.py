@@ -72,6 +72,9 @@ SIGNATURES = {
                                        c_int64, c_int64, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
     "mdx_bf16_linear": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                        c_void_p]),
+    "mdx_attn_exact": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                      c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                      c_int64, c_int64, c_int64, ctypes.c_float, c_void_p]),
     "mdx_int8_linear": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int64,
                                        c_int64, c_void_p]),
     "mdx_gdn_core": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,

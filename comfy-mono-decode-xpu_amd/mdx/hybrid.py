@@ -49,6 +49,7 @@ class HybridConfig:
     cap: int = 2048
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
     auto: bool = False            # adaptive tree: drafts keep 7 candidates, the accept records their ranks
+    attn: str = "fast"            # "exact": attention in one canonical fp32 order (mdx_attn_exact)
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
 
     def attention(self, i):
@@ -274,6 +275,12 @@ class HybridModel:
         self.vtok, self.toks, self.vpos = b["vtok"][:, :R], b["toks"][:, :R], b["vpos"][:, :R]
         self.apos, self.vfreqs, self.x, self.logits = b["apos"][:R], b["vfreqs"][:R], b["x"][:R], b["logits"][:R]
 
+    def _attend(self, q, key, value, seq, xk, xv, mask, out):
+        if self.cfg.attn == "exact":
+            _C.attn_exact(q, key, value, seq, xk, xv, mask, out=out)
+        else:
+            _C.attn_dpas(q, key, value, seq, xk, xv, mask, 0, out=out)
+
     def _tr(self, name, t):
         if self.trace is not None and not torch.cuda.is_current_stream_capturing():
             self.trace.append((name, t.detach().clone()))
@@ -307,7 +314,7 @@ class HybridModel:
         ko = torch.empty(1, c.kv_heads, R, c.head_dim, dtype=torch.bfloat16, device=self.dev)
         _C.qk_norm_rope_kv(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, outs=(qo, ko))
         y = torch.empty(1, R, qd, dtype=torch.bfloat16, device=self.dev)
-        _C.attn_dpas(qo, key, value, seq, ko, vv.transpose(1, 2), mask, 0, out=y)
+        self._attend(qo, key, value, seq, ko, vv.transpose(1, 2), mask, y)
         self._tr(f"L{i}.qo", qo)
         self._tr(f"L{i}.ko", ko)
         self._tr(f"L{i}.y", y)
@@ -374,8 +381,8 @@ class HybridModel:
         ko = torch.empty(1, c.kv_heads, n, D, dtype=torch.bfloat16, device=self.dev)
         _C.qk_norm_rope_kv(qv, kv_, vv, M["qn"], M["kn"], freqs, mk, mv, kvpos, c.eps, c.eps, c.rotary, outs=(qo, ko))
         y = _C._buf(self.dy, n, qd)
-        _C.attn_dpas(qo, mk, mv, seq, ko, vv.transpose(1, 2), self.empty_mask if mask is None else mask, 0,
-                     out=y.view(1, n, qd))
+        self._attend(qo, mk, mv, seq, ko, vv.transpose(1, 2), self.empty_mask if mask is None else mask,
+                     y.view(1, n, qd))
         gy = _C._buf(self.dgy, n, qd)
         _C.draft_sigmoid_mul(y, qg if n > 1 else qg.view(-1), D, gy)
         self._tr("mtp.qo", qo)

@@ -410,6 +410,19 @@ int mdx_draft_pick_bf16(const uint16_t* approx, const uint16_t* x, const uint16_
                         int64_t* vtok, int64_t nvtok, const int64_t* children, int64_t nchildren, int64_t* calls,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Exact tree-verify decode attention (the exactness fallback of mdx_attn_decode): the same operands and
+ * output, computed in one canonical fp32 order (scores in dimension order, weights by a fixed exp
+ * sequence, the normaliser by 64 ordered lane partials and a halving tree, o in token order; the oracle's
+ * attention_exact restates it bit for bit). scale: the score scale (1/sqrt(D) in the callers).
+ * Replaces: the role of the bit-identical attention port, csrc/attn_port.sycl:1-12 (selected by
+ * MONO_DECODE_XPU_ATTN, comfy_mono_decode_xpu/layer.py:43,409); not its arithmetic (its upstream is
+ * third-party). D in {64, 128, 256}, 1..16 rows, cap + rows <= 16384. */
+int mdx_attn_exact(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
+                   const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, int64_t xk_head_stride,
+                   int64_t xk_row_stride, const uint16_t* xv, int64_t xv_head_stride, int64_t xv_row_stride,
+                   const int32_t* mask, uint16_t* out, int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap,
+                   float scale, void* stream);
+
 /* Calibration: one streaming read of `bytes` (a multiple of 1024) from `src` with the W4A8 GEMV's load
  * pattern (1 KiB per wave instruction, four loads in flight per wave), over `work_groups` work-groups
  * of 256 threads; `sink` (4 bytes) is written only if the data hashes to a marker value. It has no

@@ -842,3 +842,70 @@ def draft_pick(logit_bits, nout, argmax_first, children, nvtok):
     for j, c in enumerate(children[1:], 1):
         vtok[c] = top[j]
     return top, tok, vtok
+
+
+# ---------------------------------------------------------------------------------------------
+# exact attention (the exactness fallback beside attn_dpas; the reference's bit-identical port of its
+# upstream attention, csrc/attn_port.sycl:1-12, has the same role): one canonical fp32 order
+# ---------------------------------------------------------------------------------------------
+_EXP_C = [np.float32(float.fromhex(h)) for h in ("0x1.a01a02p-13", "0x1.6c16c2p-10", "0x1.111112p-7",
+                                                 "0x1.555556p-5", "0x1.555556p-3", "0x1.0p-1", "0x1.0p0", "0x1.0p0")]
+_LOG2E = np.float32(float.fromhex("0x1.715476p+0"))
+_LN2_HI = np.float32(float.fromhex("0x1.62e4p-1"))
+_LN2_LO = np.float32(float.fromhex("0x1.7f7d1cp-20"))
+
+
+def exp_c(x):
+    """e^x (x <= 0) as the exact attention computes it: n = rint(fl(x log2e)), r = fl(fl(x - fl(n ln2_hi)) -
+    fl(n ln2_lo)), Horner over the fp32 Taylor coefficients 1/7! .. 1/0!, times 2^n; 0 below -80 or for NaN."""
+    f32 = np.float32
+    x = np.asarray(x, dtype=f32)
+    n = np.rint((x * _LOG2E).astype(f32)).astype(f32)
+    r = ((x - (n * _LN2_HI).astype(f32)).astype(f32) - (n * _LN2_LO).astype(f32)).astype(f32)
+    p = np.full_like(r, _EXP_C[0])
+    for c in _EXP_C[1:]:
+        p = ((p * r).astype(f32) + c).astype(f32)
+    with np.errstate(invalid="ignore"):
+        out = np.ldexp(p, np.where(x > -80, n, 0).astype(np.int32)).astype(f32)
+    return np.where(x > -80, out, f32(0)).astype(f32)
+
+
+def attention_exact(q_bits, key_bits, value_bits, L, xk_bits, xv_bits, mask, scale):
+    """The exact attention's result bits [S, H * D] for q [H, S, D], caches [Hk, cap, D], tree rows xk / xv
+    [Hk, S, D] (bf16 bits), L cached tokens, mask (list or None), scale (fp32). Tokens: the prefix [0, L),
+    then the admitted tree rows ascending. score = fl(dot * scale), the dot in dimension order; weights
+    e = exp_c(score - max); l = 64 lane partials (lane j: tokens j, j + 64, .. in order) reduced by a halving
+    tree; o[d] in token order; out = bf16(o / l), 0 for no tokens."""
+    f32 = np.float32
+    qf, kf, vf = bf16_to_f32(q_bits), bf16_to_f32(key_bits), bf16_to_f32(value_bits)
+    xkf, xvf = bf16_to_f32(xk_bits), bf16_to_f32(xv_bits)
+    H, S, D = qf.shape
+    Hk = kf.shape[0]
+    scale = f32(scale)
+    out = np.zeros((S, H, D), dtype=np.uint16)
+    for h in range(H):
+        kh = h // (H // Hk)
+        for s in range(S):
+            rows = [t for t in range(S) if mask is not None and (int(mask[s]) >> t) & 1]
+            K = np.concatenate([kf[kh, :L], xkf[kh, rows]]).astype(f32)
+            V = np.concatenate([vf[kh, :L], xvf[kh, rows]]).astype(f32)
+            n = K.shape[0]
+            if n == 0:
+                continue
+            acc = np.zeros(n, dtype=f32)
+            for d in range(D):
+                acc = (acc + (qf[h, s, d] * K[:, d]).astype(f32)).astype(f32)
+            sc = (acc * scale).astype(f32)
+            e = exp_c((sc - sc.max()).astype(f32))
+            ep = np.zeros(-(-n // 64) * 64, dtype=f32)
+            ep[:n] = e
+            parts = np.zeros(64, dtype=f32)
+            for i in range(ep.size // 64):
+                parts = (parts + ep[64 * i:64 * i + 64]).astype(f32)
+            for o in (32, 16, 8, 4, 2, 1):
+                parts[:o] = (parts[:o] + parts[o:2 * o]).astype(f32)
+            o = np.zeros(D, dtype=f32)
+            for u in range(n):
+                o = (o + (e[u] * V[u]).astype(f32)).astype(f32)
+            out[s, h] = f32_to_bf16((o / parts[0]).astype(f32))
+    return out.reshape(S, H * D)
