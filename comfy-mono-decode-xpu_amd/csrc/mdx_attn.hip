@@ -24,6 +24,7 @@
 // Work-group ids are laid out so the row tiles of one (kv head, chunk) share an XCD (ids are dealt
 // round-robin over the 8 XCDs): the 4x re-read of a K/V chunk hits that XCD's L2.
 #include <math.h>
+#include <stdlib.h>
 
 #include "mdx_common.hpp"
 
@@ -37,7 +38,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int AT_WAVES = 4;
 constexpr int AT_STEP = 32;        // tokens per MFMA step
 constexpr int AT_VT_ROW = 72;      // bytes per [dim] row of the transposed V tile (64 + 8: conflict-free writes)
-constexpr int AT_MIN_TPW = 128;    // default: at least this many tokens per wave per chunk
+constexpr int AT_MIN_TPW = 64;     // default: at least this many tokens per wave per chunk (swept: 32, 64, 128)
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -329,10 +330,27 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     a.out[(int64_t(sr) * a.H + h) * D + t] = f2bf(s > 0.f ? __fdiv_rn(o, s) : 0.f);
 }
 
+// the context split's tuning (MDX_ATTN_TPW: minimum tokens per wave of a chunk; MDX_ATTN_UNITS: the
+// work-group count the chunk count aims at), read once; sweeps only
+int env_int(const char* name, int dflt, int lo, int hi) {
+    const char* e = getenv(name);
+    const int v = e ? atoi(e) : dflt;
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+int min_tpw_default() {
+    static const int v = env_int("MDX_ATTN_TPW", AT_MIN_TPW, AT_STEP, 4096) / AT_STEP * AT_STEP;
+    return v;
+}
+int target_units() {
+    static const int v = env_int("MDX_ATTN_UNITS", 512, 8, 65536);
+    return v;
+}
+
 int plan_chunks(int Hk, int RT, int cap, int hint) {
     if (hint > 0) return hint > 64 ? 64 : hint;
-    int c = (512 + Hk * RT - 1) / (Hk * RT);
-    const int by_cap = (cap + AT_WAVES * AT_MIN_TPW - 1) / (AT_WAVES * AT_MIN_TPW);
+    const int tpw = min_tpw_default();
+    int c = (target_units() + Hk * RT - 1) / (Hk * RT);
+    const int by_cap = (cap + AT_WAVES * tpw - 1) / (AT_WAVES * tpw);
     c = c > by_cap ? by_cap : c;
     return c < 1 ? 1 : (c > 64 ? 64 : c);  // the merge holds at most 64 + 1 partial weights
 }
@@ -410,7 +428,7 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.rows = int(H / Hk * S);
     a.RT = RT;
     a.C = C;
-    a.min_tpw = chunks_hint > 0 ? AT_STEP : AT_MIN_TPW;
+    a.min_tpw = chunks_hint > 0 ? AT_STEP : min_tpw_default();
     a.zscale = float(1.0 / sqrt(double(D)) * 1.4426950408889634);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (D == 64) return launch<64>(a, st);

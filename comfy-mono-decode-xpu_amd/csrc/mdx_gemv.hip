@@ -261,7 +261,14 @@ __global__ __launch_bounds__(1024) void prep_rows_kernel(PrepArgs a) {
 }
 
 int launch_prep(const PrepArgs& a, int64_t rows, hipStream_t st) {
-    const int G = a.K / 256, W = std::min(16, G), gpw = (G + W - 1) / W;
+    // waves per row (MDX_PREP_WAVES overrides for sweeps; the result does not depend on it: the norm adds
+    // the group sums in group order and the maximum is order-free)
+    static const int pw = [] {
+        const char* e = getenv("MDX_PREP_WAVES");
+        return e ? std::max(1, std::min(16, atoi(e))) : 16;
+    }();
+    const int G = a.K / 256, W = std::min(G, std::max(pw, (G + 3) / 4)), gpw = (G + W - 1) / W;
+    MDX_CHECK(gpw <= 4, "row prep: %d groups over %d waves exceeds 4 per wave", G, W);
     const dim3 grid{unsigned(rows)}, block{unsigned(W * WAVE)};
     switch (gpw) {
         case 1: hipLaunchKernelGGL(prep_rows_kernel<1>, grid, block, 0, st, a); break;

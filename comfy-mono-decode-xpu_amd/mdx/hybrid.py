@@ -50,6 +50,7 @@ class HybridConfig:
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
     auto: bool = False            # adaptive tree: drafts keep 7 candidates, the accept records their ranks
     attn: str = "fast"            # "exact": attention in one canonical fp32 order (mdx_attn_exact)
+    gdn_fused: bool = False       # the GDN core in one launch (mdx_gdn_core_fused, the same bits)
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
 
     def attention(self, i):
@@ -204,7 +205,9 @@ class HybridModel:
                               torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf))
             else:
                 hv, hk = c.gdn_value_heads, c.gdn_key_heads
-                self.gdn[i] = dict(conv=torch.zeros(self.gdn_ch, 3, **bf), pb=torch.zeros(2, S, self.gdn_ch, **bf),
+                # the one-launch core double-buffers the conv history by parity (reads [1 - p], writes [p])
+                conv = torch.zeros(2, self.gdn_ch, 3, **bf) if c.gdn_fused else torch.zeros(self.gdn_ch, 3, **bf)
+                self.gdn[i] = dict(conv=conv, pb=torch.zeros(2, S, self.gdn_ch, **bf),
                                    qb=torch.zeros(2, S, self.gdn_ch, **bf),
                                    rec=torch.randn(hv, 128, 128, generator=gen, device=dev) * 0.1,
                                    gates=torch.zeros(2, S, hv, 2, device=dev), sums=torch.zeros(2, S, hk, 2, device=dev))
@@ -334,7 +337,8 @@ class HybridModel:
         self._tr(f"L{i}.z", z)
         core = _C._buf(sc["core"], R, hv * 128)
         _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
-                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
+                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True,
+                    fused=c.gdn_fused)
         self._tr(f"L{i}.core_raw", core)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"], L["d"], 6,
                        gnorm=(z, L["gnorm"], c.eps))

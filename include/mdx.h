@@ -314,6 +314,17 @@ int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* w
                      float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
                      void* stream);
 
+/* The core of mdx_gdn_core_raw in one launch, bit for bit the same outputs and buffers, with the conv
+ * history double-buffered by parity: conv_state2 bf16 [2][C][3], the step of parity p (ctl[1]) reading
+ * [1 - p] and writing [p] (each work-group runs the conv of the channels it reads, so no work-group may
+ * advance a history another one still reads). No counterpart in the reference (whose GDN core is one
+ * persistent launch with in-kernel barriers, csrc/mono_gdn.sycl:87-699). */
+int mdx_gdn_core_fused(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
+                       const uint16_t* conv_w, uint16_t* conv_state2, uint16_t* proj_buf, uint16_t* qkv_buf,
+                       const int32_t* ctl, const float* dt_bias, const float* g_decay, float* rec_state, float* gates,
+                       float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
+                       void* stream);
+
 /* Gated RMSNorm per 128-element head, then the rotation + row quantisation of mdx_rot_quant:
  * y' = bf16(bf16((y gnorm_w) / sqrt(mean_head(y^2) + eps)) * bf16(silu(z))). y_out (optional, may be y)
  * receives y'; with q = scale = NULL and rot = MDX_ROT_NONE only y' is written. y, z, y_out bf16
