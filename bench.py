@@ -391,7 +391,8 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     per = 3  # at most len(widths) + 1 tokens committed per step
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
-    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, gdn_fused=args.gdn_fused)
+    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, gdn_fused=args.gdn_fused,
+                              gdn_side_gates=args.side_gates)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -662,6 +663,7 @@ def main():
                                                                "of the lm_head and recompute their candidates exactly")
     ap.add_argument("--auto", action="store_true", help="stack: the adaptive tree (decode_auto)")
     ap.add_argument("--gdn-fused", action="store_true", help="gdn_layer / stack: the one-launch GDN core")
+    ap.add_argument("--side-gates", action="store_true", help="stack: GDN gates on a second stream")
     ap.add_argument("--head", choices=["bf16", "int8"], default="bf16",
                     help="stack / lmhead: the bf16 lm_head or the int8 ConvRot one (W8A8)")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")

@@ -220,6 +220,11 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     }
 }
 
+// This step's gates alone (four work-groups per value head), for a launch beside the projection GEMV.
+__global__ __launch_bounds__(256) void gdn_gates_kernel(GdnArgs a) {
+    gdn_gates_part(a, blockIdx.x / 4, blockIdx.x % 4);
+}
+
 // The delta rule of value head h over the columns [16 cs, 16 cs + 16) of its state (eight work-groups
 // per head, one per CU: the columns are independent, and a thread's serial work per entry is 8 rows).
 // Wave w owns columns 4 w .. 4 w + 3; lane l holds state rows 8 rg .. 8 rg + 7 (rg = l / 4) of column
@@ -685,7 +690,7 @@ namespace {
 int gdn_run(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
             const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
             const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums, float qscale,
-            uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, hipStream_t st) {
+            uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, hipStream_t st, bool gates_too = true) {
     MDX_CHECK(proj && xn && wa && wb && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
                   rec_state && gates && sums && core,
               "null pointer");
@@ -717,7 +722,7 @@ int gdn_run(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const 
     a.HV = int(HV);
     a.C = int(2 * HK * DH + HV * DH);
     a.slots = int(slots);
-    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + 4 * a.HV), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + (gates_too ? 4 * a.HV : 0)), dim3(256), 0, st, a);
     MDX_LAUNCHED();
     hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV * NSPLIT), dim3(HT), 0, st, a);
     MDX_LAUNCHED();
@@ -787,6 +792,41 @@ extern "C" int mdx_gdn_core_fused(const uint16_t* proj, const uint16_t* xn, cons
     a.C = int(2 * HK * DH + HV * DH);
     a.slots = int(slots);
     hipLaunchKernelGGL(gdn_fused_kernel, dim3(a.HV * NSPLIT), dim3(2 * HT), 0, static_cast<hipStream_t>(stream), a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
+extern "C" int mdx_gdn_core_split(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
+                                  int64_t K, const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf,
+                                  uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias, const float* g_decay,
+                                  float* rec_state, float* gates, float* sums, float qscale, uint16_t* core,
+                                  int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    return gdn_run(proj, xn, wa, wb, K, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates,
+                   sums, qscale, core, rows, HK, HV, slots, static_cast<hipStream_t>(stream), false);
+}
+
+extern "C" int mdx_gdn_gates(const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K, const int32_t* ctl,
+                             const float* dt_bias, const float* g_decay, float* gates, int64_t rows, int64_t HV,
+                             int64_t slots, void* stream) {
+    MDX_CHECK(xn && wa && wb && ctl && dt_bias && g_decay && gates, "null pointer");
+    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
+    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
+    MDX_CHECK(HV >= 1 && HV <= 128, "1..128 value heads");
+    MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
+              "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
+    GdnArgs a{};
+    a.xn = xn;
+    a.wa = wa;
+    a.wb = wb;
+    a.K = int(K);
+    a.ctl = ctl;
+    a.dt_bias = dt_bias;
+    a.g_decay = g_decay;
+    a.gates = gates;
+    a.R = int(rows);
+    a.HV = int(HV);
+    a.slots = int(slots);
+    hipLaunchKernelGGL(gdn_gates_kernel, dim3(4 * a.HV), dim3(256), 0, static_cast<hipStream_t>(stream), a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
