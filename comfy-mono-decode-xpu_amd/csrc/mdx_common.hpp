@@ -44,15 +44,27 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 // ---- scalar conversions (device) ---------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// round-to-nearest-even fp32 -> bf16; NaN becomes the canonical quiet NaN 0x7FC0
+// Round-to-nearest-even fp32 -> bf16 by the hardware conversion (v_cvt_pk_bf16_f32, two values per
+// instruction): on gfx950 it gives the RNE result of the bit pattern for every non-NaN fp32 input,
+// subnormals included (checked over all 2^32 patterns against the integer formulation
+// u + 0x7FFF + ((u >> 16) & 1)), and a NaN for a NaN. f2bf makes every NaN the canonical quiet NaN
+// 0x7FC0; bfround (the fp32 value of the bf16 rounding) keeps a NaN a NaN of unspecified payload,
+// which no fp32 operation distinguishes.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
+    const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+    return f != f ? uint16_t(0x7FC0u) : h;
 }
 
-__device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ float bfround(float f) { return bf2f(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))); }
+
+// bfround of two values by one conversion instruction
+typedef float mdx_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mdx_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bfround2(float& a, float& b) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(mdx_f32x2{a, b}, mdx_bf16x2));
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xFFFF0000u);
+}
 
 __device__ __forceinline__ float fp16_to_f32(uint16_t h) {
     return float(__builtin_bit_cast(_Float16, h));

@@ -788,12 +788,15 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 const float rr = r ? rcp[1] : rcp[0];
                 const uint32_t w[4] = {hraw[k].x, hraw[k].y, hraw[k].z, hraw[k].w};
                 uint32_t o[2] = {0u, 0u};
+                float d[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float v = __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
-                    const float d = bfround(__fmul_rn(v, rr));
-                    o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
-                }
+                for (int e = 0; e < 8; ++e)
+                    d[e] = __fmul_rn(__uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16)), rr);
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) bfround2(d[e], d[e + 1]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    o[e >> 2] |= (uint32_t(int(fminf(fmaxf(rintf(d[e]), -128.f), 127.f))) & 0xFFu) << (8 * (e & 3));
                 *reinterpret_cast<uint2*>(xl + r * Kr + 8 * j) = make_uint2(o[0], o[1]);
             }
         }
@@ -830,7 +833,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 float wv[4];
                 unpack4(reinterpret_cast<const uint2*>(xs_l + 2 * K)[64 * min(wave + nwv * gi, G - 1) + lane], wv);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], rr), wv[e]));
+                for (int e = 0; e < 4; ++e) v[gi][e] = __fmul_rn(__fmul_rn(v[gi][e], rr), wv[e]);
+                bfround2(v[gi][0], v[gi][1]);
+                bfround2(v[gi][2], v[gi][3]);
             }
         }
         float m = 0.f;
@@ -854,11 +859,14 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             const int g = wave + nwv * gi;
             if (g < G) {
                 uint32_t o = 0;
+                float d[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float d = bfround(__fmul_rn(v[gi][e], rr));
-                    o |= (uint32_t(int(fminf(fmaxf(rintf(d), -128.f), 127.f))) & 0xFFu) << (8 * e);
-                }
+                for (int e = 0; e < 4; ++e) d[e] = __fmul_rn(v[gi][e], rr);
+                bfround2(d[0], d[1]);
+                bfround2(d[2], d[3]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o |= (uint32_t(int(fminf(fmaxf(rintf(d[e]), -128.f), 127.f))) & 0xFFu) << (8 * e);
                 *reinterpret_cast<uint32_t*>(xl + 256 * g + 4 * lane) = o;
             }
         }
