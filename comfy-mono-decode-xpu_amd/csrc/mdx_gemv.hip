@@ -660,8 +660,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // SRC_HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the maxima entries (thread t:
     // entries t, t + threads, ... of both rows) are one-shot operands too
     constexpr int HRP = HR ? 16 : 1;
+    constexpr int HMV = HR ? HMW : 1;
     uint4 hraw[HRP];
     float hmx[2] = {0.f, 0.f};
+    float hv[2][HMV];  // SRC_HR with every maximum per wave: this lane's maxima (reduced behind the ring)
     const int nwv = a.TPW * a.KS;
     if (HR) {
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
@@ -671,25 +673,15 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             hraw[k] = make_uint4(0u, 0u, 0u, 0u);
             if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
         }
-        if (a.hmax_n <= WAVE * HMW) {
-            // every wave reads all the maxima itself (HMW per lane, contiguous per row, issued at
-            // once): the rows' maxima need no exchange between the waves
-            float hv[2][HMW];
+        // every wave reads the maxima itself (HMW per lane, contiguous per row, issued at once; all
+        // of them when hmax_n <= WAVE * HMW, so that the rows' maxima need no exchange between the
+        // waves). They are reduced after the weight ring is issued, so that its first round does
+        // not wait for them.
 #pragma unroll
-            for (int j = 0; j < HMW; ++j)
+        for (int j = 0; j < HMV; ++j)
 #pragma unroll
-                for (int r = 0; r < 2; ++r)
-                    hv[r][j] = __uint_as_float(a.hmax[min(r, a.rows - 1) * a.hmax_n + min(lane + WAVE * j, a.hmax_n - 1)]);
-#pragma unroll
-            for (int j = 0; j < HMW; ++j)
-#pragma unroll
-                for (int r = 0; r < 2; ++r) hmx[r] = fmaxf(hmx[r], hv[r][j]);
-        } else {
-            for (int w = t; w < a.hmax_n; w += nthr)
-#pragma unroll
-                for (int r = 0; r < 2; ++r)
-                    if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[r * a.hmax_n + w]));
-        }
+            for (int r = 0; r < 2; ++r)
+                hv[r][j] = __uint_as_float(a.hmax[min(r, a.rows - 1) * a.hmax_n + min(lane + WAVE * j, a.hmax_n - 1)]);
     }
     // SRC_XP: the bf16 row and its norm weights land in LDS by DMA with the other one-shot operands,
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
@@ -758,7 +750,15 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // stays in flight: bf16(v / sb) as bf16(v * fl32(1 / sb)) (quant_rcp)
         float* wm = reinterpret_cast<float*>(red);  // [2][16 waves] (the reduction block is free here)
         const bool whole = a.hmax_n <= WAVE * HMW;  // (uniform) each wave holds every maximum
+#pragma unroll
+        for (int j = 0; j < HMV; ++j)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) hmx[r] = fmaxf(hmx[r], hv[r][j]);
         if (!whole) {
+            for (int w = t; w < a.hmax_n; w += nthr)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+                    if (r < a.rows) hmx[r] = fmaxf(hmx[r], __uint_as_float(a.hmax[r * a.hmax_n + w]));
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const float m = wave_max_nn(hmx[r]);

@@ -34,10 +34,41 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* base, i
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// The integer formulation of round-to-nearest-even fp32 -> bf16 (NaN -> 0x7FC0), against which the
+// library's f2bf / bfround (the hardware conversion) are checked over every fp32 bit pattern.
+__device__ __forceinline__ uint16_t rne_bits(uint32_t u) {
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__global__ __launch_bounds__(256) void bf16_round_check_kernel(unsigned long long* mismatches, uint32_t* first) {
+    const uint64_t nthr = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < (1ull << 32); i += nthr) {
+        const uint32_t u = uint32_t(i);
+        const float f = __uint_as_float(u);
+        const uint16_t want = rne_bits(u);
+        const float r = bfround(f);
+        const bool nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
+        const bool ok = f2bf(f) == want && (nan ? r != r : __float_as_uint(r) == uint32_t(want) << 16);
+        if (!ok) {
+            atomicAdd(mismatches, 1ull);
+            atomicMin(first, u);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace mdx
 
 using namespace mdx;
+
+extern "C" int mdx_check_bf16_round(unsigned long long* mismatches, uint32_t* first, void* stream) {
+    MDX_CHECK(mismatches && first, "null pointer");
+    hipLaunchKernelGGL(bf16_round_check_kernel, dim3(1024), dim3(256), 0, static_cast<hipStream_t>(stream), mismatches,
+                       first);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
 
 extern "C" int mdx_stream_read(const void* src, int64_t bytes, int32_t work_groups, uint32_t* sink, void* stream) {
     MDX_CHECK(src && sink, "null pointer");

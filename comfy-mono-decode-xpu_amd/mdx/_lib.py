@@ -111,6 +111,7 @@ SIGNATURES = {
     "mdx_draft_norm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int32, c_void_p,
                                                 c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_stream_read": (ctypes.c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
+    "mdx_check_bf16_round": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
     "mdx_draft_pick_workspace": (c_size_t, []),
     "mdx_draft_pick": (ctypes.c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int32,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p,

@@ -458,6 +458,12 @@ int mdx_attn_exact(const uint16_t* q, int64_t q_head_stride, int64_t q_row_strid
  * beside the 8 TB/s spec figure. */
 int mdx_stream_read(const void* src, int64_t bytes, int32_t work_groups, uint32_t* sink, void* stream);
 
+/* Self-check of this library's fp32 -> bf16 rounding (the hardware conversion behind every bf16 result):
+ * compares it with the integer round-to-nearest-even formulation (NaN -> 0x7FC0) over all 2^32 fp32 bit
+ * patterns, adding the number of disagreements to *mismatches (caller zeroes it) and lowering *first
+ * (caller sets 0xFFFFFFFF) to the smallest disagreeing pattern. No counterpart in the reference. */
+int mdx_check_bf16_round(unsigned long long* mismatches, uint32_t* first, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,3 +60,15 @@ def test_lm_head_151936(C, dev, rows):
     v, i = C.topk_rows(logits, 20)
     wv, wi = ref.topk_rows(bits(logits), 20)
     assert np.array_equal(i.cpu().numpy(), wi)
+
+
+def test_bf16_rounding_matches_integer_rne_everywhere(C, dev):
+    """The library rounds fp32 to bf16 with the hardware conversion; mdx_check_bf16_round compares it on
+    the device with the integer round-to-nearest-even formulation over all 2^32 fp32 patterns
+    (subnormals, infinities, ties; NaN -> 0x7FC0 for stored bits, any NaN for in-register values)."""
+    from mdx import _lib
+    n = torch.zeros(1, dtype=torch.int64, device=dev)
+    first = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    _lib.call("mdx_check_bf16_round", _lib.ptr(n), _lib.ptr(first), _lib.stream_of(n))
+    torch.cuda.synchronize()
+    assert int(n.item()) == 0, f"{int(n.item())} patterns disagree, first 0x{int(first.item()) & 0xFFFFFFFF:08x}"
