@@ -314,7 +314,7 @@ struct GemvArgs {
     int out_dt;
     const uint16_t* lut;  // EPI_SILU
     // EPI_SILU with hmax_out (one gate/up pair per work-group): work-group wg also stores its rows'
-    // |h| maxima (fp32 bits) at hmax_out[wg * 16 + row]
+    // |h| maxima (fp32 bits) at hmax_out[row * (number of work-groups) + wg]
     uint32_t* hmax_out;
     // SRC_HR units: the activation is hr (bf16 [rows, K]) quantised in the prologue with the row
     // scale max(absmax / 127, 1e-30), absmax = the maximum of hmax[row * hmax_n + w] over w < hmax_n
@@ -673,15 +673,21 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             hraw[k] = make_uint4(0u, 0u, 0u, 0u);
             if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
         }
-        // every wave reads the maxima itself (HMW per lane, contiguous per row, issued at once; all
-        // of them when hmax_n <= WAVE * HMW, so that the rows' maxima need no exchange between the
-        // waves). They are reduced after the weight ring is issued, so that its first round does
-        // not wait for them.
+        // every wave reads the maxima itself (HMW per lane in 16-byte pieces, issued at once; all of
+        // them when hmax_n <= WAVE * HMW, so that the rows' maxima need no exchange between the
+        // waves; hmax_n is a multiple of 4). They are reduced after the weight ring is issued, so
+        // that its first round does not wait for them.
 #pragma unroll
-        for (int j = 0; j < HMV; ++j)
+        for (int j = 0; j < HMV / 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                hv[r][j] = __uint_as_float(a.hmax[min(r, a.rows - 1) * a.hmax_n + min(lane + WAVE * j, a.hmax_n - 1)]);
+            for (int r = 0; r < 2; ++r) {
+                const uint4 m4 = *reinterpret_cast<const uint4*>(
+                    a.hmax + min(r, a.rows - 1) * a.hmax_n + min(4 * lane + 4 * WAVE * j, a.hmax_n - 4));
+                hv[r][4 * j] = __uint_as_float(m4.x);
+                hv[r][4 * j + 1] = __uint_as_float(m4.y);
+                hv[r][4 * j + 2] = __uint_as_float(m4.z);
+                hv[r][4 * j + 3] = __uint_as_float(m4.w);
+            }
     }
     // SRC_XP: the bf16 row and its norm weights land in LDS by DMA with the other one-shot operands,
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
@@ -706,13 +712,21 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         if (a.xp_nw) dma_rows_to_lds(as_global(reinterpret_cast<const uint8_t*>(a.xp_nw)), 0, 2 * K, 1, xs_l + 2 * K, nthr);
     }
 
+    // the codebook by scalar loads (it is read-only for the whole launch): one instruction instead
+    // of sixteen vector loads per wave in the memory pipeline ahead of the ring
+    typedef __attribute__((address_space(4))) const float* const_f32p;
     float cb[16];
     bool cbdef = true;
+    if (a.cb) {
+        const const_f32p cbc = (const_f32p)(a.cb);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        cb[i] = a.cb ? a.cb[i] : float(i - 8);
-        cbdef = cbdef && cb[i] == float(i - 8);
+        for (int i = 0; i < 16; ++i) cb[i] = cbc[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cb[i] = float(i - 8);
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cbdef = cbdef && cb[i] == float(i - 8);
 
     // 2. the weight ring: every slot issues one load; reads past the slice repeat its last chunk. A
     // tile slot past the matrix's last tile (a work-group's share can end inside its tile slots)
@@ -1164,7 +1178,7 @@ int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, con
 // work-group): the smallest split that puts >= 3072 waves on the chip (12 per CU), but no slice
 // shorter than 4 chunks, measured best on MI355X for the 8-52 MB matrices of this model (longer
 // streams per wave beat more, shorter waves: 4096 x 4096 takes 6.4 us at 8 slices against 7.6 at 12).
-void gemv_geometry(int total, int K, bool pair, int& TPW, int& KS) {
+void gemv_geometry(int total, int K, bool pair, int rows, int& TPW, int& KS) {
     TPW = pair ? 2 : 1;
     const int NC = K / CHUNK_K;
     const int maxks = 16 / TPW;
@@ -1192,7 +1206,7 @@ void gemv_geometry(int total, int K, bool pair, int& TPW, int& KS) {
 // of a down GEMV would read 50 MB of h between them and lose more than the prep launch costs.
 bool gemv_hr_fits(const mdx_w4* w, int rows) {
     int TPW, KS;
-    gemv_geometry(int(w->n / 16), int(w->k), false, TPW, KS);
+    gemv_geometry(int(w->n / 16), int(w->k), false, rows, TPW, KS);
     return rows <= 2 && TPW * KS <= 12 && int64_t(rows) * (w->k / 8) <= int64_t(16) * TPW * KS * WAVE;
 }
 
@@ -1202,7 +1216,7 @@ bool gemv_xp_fits(const mdx_w4* const* ws, int nm, bool pair) {
     int total = 0;
     for (int i = 0; i < nm; ++i) total += int(ws[i]->n / 16);
     int TPW, KS;
-    gemv_geometry(total, int(ws[0]->k), pair, TPW, KS);
+    gemv_geometry(total, int(ws[0]->k), pair, 1, TPW, KS);
     return ws[0]->k % 256 == 0 && ws[0]->k / 256 <= int64_t(XP_GPW) * TPW * KS;
 }
 
@@ -1221,7 +1235,8 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
              void* const* outs, const void* const* res, int out_dt, const uint16_t* lut, hipStream_t st,
              const GemvExtra& ex = GemvExtra{}) {
     MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16 (got %d)", rows);
-    MDX_CHECK(!ex.hr || (nm == 1 && !pair && ex.hmax && ex.hmax_n > 0 && gemv_hr_fits(ws[0], rows)),
+    MDX_CHECK(!ex.hr || (nm == 1 && !pair && ex.hmax && ex.hmax_n >= 4 && ex.hmax_n % 4 == 0 && aligned(ex.hmax, 16) &&
+                         gemv_hr_fits(ws[0], rows)),
               "bf16-row GEMV geometry");
     MDX_CHECK(!ex.hmax_out || (pair && rows <= 16), "|h| maxima need a gate/up pair");
     MDX_CHECK(!ex.xp_x || (rows == 1 && gemv_xp_fits(ws, nm, pair)), "row-prep GEMV geometry");
@@ -1245,7 +1260,7 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     int rc = setup_gemv(ws, nm, pair, ex.hr || ex.xp_x ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
     if (rc) return rc;
     const bool mfma = rows >= MFMA_MIN_ROWS;
-    gemv_geometry(total, a.K, pair, a.TPW, a.KS);
+    gemv_geometry(total, a.K, pair, rows, a.TPW, a.KS);
     MDX_CHECK(!ex.hmax_out || a.TPW == 2, "|h| maxima need one gate/up pair per work-group");
     a.hmax_out = ex.hmax_out;
     a.hr = ex.hr;
@@ -1452,7 +1467,7 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     // the down GEMV quantises h in its prologue (the same scale and codes as the row prep), when
     // its geometry holds the rows (MDX_MLP_HPREP=1 forces the prep launch).
     const char* hp = getenv("MDX_MLP_HPREP");
-    const bool hr = rot == MDX_ROT_NONE && gemv_hr_fits(down, int(rows)) && !(hp && atoi(hp) != 0);
+    const bool hr = rot == MDX_ROT_NONE && N1 % 64 == 0 && gemv_hr_fits(down, int(rows)) && !(hp && atoi(hp) != 0);
     const mdx_w4* gu[2] = {gate, up};
     // one row: the gate/up GEMV prepares x itself (no row prep launch); MDX_MLP_HPREP=1 keeps both
     // prep launches
