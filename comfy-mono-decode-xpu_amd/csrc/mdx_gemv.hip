@@ -1180,6 +1180,19 @@ int setup_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, con
 // streams per wave beat more, shorter waves: 4096 x 4096 takes 6.4 us at 8 slices against 7.6 at 12).
 void gemv_geometry(int total, int K, bool pair, int rows, int& TPW, int& KS) {
     TPW = pair ? 2 : 1;
+    // more than 8 rows: about one work-group per CU (up to six tiles each). Every work-group stages
+    // all of its rows' K range, so wider work-groups stage less per CU: the 16-row MLP 46.3 -> 41.3 us
+    // (gate/up pair 20.0 -> 15.4 us). At 8 rows the same geometry loses (MLP 30.8 -> 31.1 us, stack
+    // 3.243 -> 3.272 ms). MDX_WIDE_ROWS moves the threshold (tuning sweeps).
+    static const int wide_rows = [] {
+        const char* e = getenv("MDX_WIDE_ROWS");
+        return e ? atoi(e) : 9;
+    }();
+    if (rows >= wide_rows) {
+        int t = std::min(6, total / 256);
+        if (pair) t &= ~1;
+        TPW = std::max(TPW, t);
+    }
     const int NC = K / CHUNK_K;
     const int maxks = 16 / TPW;
     KS = 1;
