@@ -55,6 +55,8 @@ def test_lm_head_151936(C, dev, rows):
     x = torch.randn(rows, H, generator=g, device=dev).bfloat16()
     wt = layout.tile_major_bf16(w)
     logits = C.bf16_linear(x, wt, tiled=True)
+    # the streaming kernel (tile-major, many tiles) against the split-K kernel that reads row-major
+    assert_bits_equal(bits(logits), bits(C.bf16_linear(x, w, tiled=False)), "tile vs row layout")
     cols = np.random.default_rng(0).choice(V, 4096, replace=False)
     _check(logits.cpu(), x.cpu(), w.cpu(), cols=cols)
     v, i = C.topk_rows(logits, 20)
@@ -72,3 +74,23 @@ def test_bf16_rounding_matches_integer_rne_everywhere(C, dev):
     _lib.call("mdx_check_bf16_round", _lib.ptr(n), _lib.ptr(first), _lib.stream_of(n))
     torch.cuda.synchronize()
     assert int(n.item()) == 0, f"{int(n.item())} patterns disagree, first 0x{int(first.item()) & 0xFFFFFFFF:08x}"
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16])
+def test_many_tiles_partial_last_wave(C, dev, rows):
+    """8195 tiles (more than one resident grid of single-tile waves: two tiles per wave in the
+    streaming kernel, the last wave one): tile-major against row-major bits, with and without a
+    residual, and within the float64 bound on sampled rows."""
+    from mdx import layout
+    g = torch.Generator(device=dev).manual_seed(11 + rows)
+    N, K = 16 * 8195, 4096
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.02).bfloat16()
+    x = torch.randn(rows, K, generator=g, device=dev).bfloat16()
+    res = torch.randn(rows, N, generator=g, device=dev).bfloat16()
+    wt = layout.tile_major_bf16(w)
+    for r in (None, res):
+        print(f"case many tiles rows={rows} residual={r is not None}", flush=True)
+        got = C.bf16_linear(x, wt, tiled=True, residual=r)
+        assert_bits_equal(bits(got), bits(C.bf16_linear(x, w, tiled=False, residual=r)), "tile vs row layout")
+    cols = np.concatenate([np.arange(N - 64, N), np.random.default_rng(1).choice(N - 64, 960, replace=False)])
+    _check(C.bf16_linear(x, wt, tiled=True).cpu(), x.cpu(), w.cpu(), cols=cols)
