@@ -308,6 +308,7 @@ struct GemvArgs {
     int force_exact;      // MDX_DECODE_EXACT: never take the integral form
     int assume_int;       // MDX_DECODE_INTEGRAL (every matrix): the integral form without the check
     int pwo;              // per-wave one-shots (one int8 row, G128, assume_int): no work-group barrier
+    int tbl;              // per-weight decode tables built once per work-group into LDS (gemv_tables)
     int epi;
     void* out[3];
     const void* res[3];
@@ -332,6 +333,10 @@ struct GemvArgs {
 // Where a unit's activation comes from: int8 rows a.xq (DMA to LDS), bf16 rows quantised with
 // given maxima (SRC_HR), or one bf16 row prepared from scratch (SRC_XP).
 enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
+// Added to a source: the kernel variant with the integral decode only (scales asserted integral, the
+// default codebook, groups the integral form takes). Without the per-weight decode's code the
+// integral path keeps its registers and schedule (the 1-row MLP 24.6 -> 23.x us).
+constexpr int SRC_INT_ONLY = 4;
 constexpr int XP_GPW = 4;
 constexpr int HMW = 16;  // SRC_HR: maxima per lane when every wave reads them all (<= 1024 work-groups)  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
 
@@ -355,6 +360,29 @@ __device__ __forceinline__ Lut make_lut(float s, const float* cb) {
     return L;
 }
 
+// The table of the default codebook (c - 8) from its eight magnitudes: rint and the clamp are odd
+// functions and (-k) s = -(k s) exactly, so entry 8 - k is the negation of q(k s) = clamp(rint(k s),
+// +-127) (NaN -> 0) and entry 8 is 0 (0 * s rounds to 0, or is NaN -> 0): eight products instead of
+// sixteen, the same bytes as make_lut.
+__device__ __forceinline__ Lut make_lut_c8(float s) {
+    int q[9];
+    q[0] = 0;
+#pragma unroll
+    for (int k = 1; k <= 8; ++k) {
+        const float r = rintf(__fmul_rn(float(k), s));
+        q[k] = (r != r) ? 0 : int(fminf(fmaxf(r, -127.f), 127.f));
+    }
+    auto pk = [](int b0, int b1, int b2, int b3) {
+        return (uint32_t(b0) & 0xFFu) | ((uint32_t(b1) & 0xFFu) << 8) | ((uint32_t(b2) & 0xFFu) << 16) | (uint32_t(b3) << 24);
+    };
+    Lut L;
+    L.w[0] = pk(-q[8], -q[7], -q[6], -q[5]);
+    L.w[1] = pk(-q[4], -q[3], -q[2], -q[1]);
+    L.w[2] = pk(0, q[1], q[2], q[3]);
+    L.w[3] = pk(q[4], q[5], q[6], q[7]);
+    return L;
+}
+
 // four codes (one per byte, values 0..15) -> four int8 via the 16-byte table
 __device__ __forceinline__ uint32_t lut4(const Lut& L, uint32_t c) {
     const uint32_t sel = c & 0x07070707u;
@@ -364,14 +392,30 @@ __device__ __forceinline__ uint32_t lut4(const Lut& L, uint32_t c) {
     return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
-// per-weight decode of one chunk's four code dwords (two scales: dwords 0-1 and 2-3)
-__device__ __forceinline__ void decode_exact(const uint32_t* wd, float s0, float s1, const float* cb, uint32_t* lo,
-                                             uint32_t* hi) {
-    const Lut L0 = make_lut(s0, cb);
-    const Lut L1 = (__float_as_uint(s1) == __float_as_uint(s0)) ? L0 : make_lut(s1, cb);
+// per-weight decode of one chunk's four code dwords (two scales: dwords 0-1 and 2-3; one when the
+// group spans the lane's 32 k, `one`, uniform); cbdef (uniform): the default codebook c - 8
+__device__ __forceinline__ void decode_exact(const uint32_t* wd, float s0, float s1, bool one, bool cbdef,
+                                             const float* cb, uint32_t* lo, uint32_t* hi) {
+    const Lut L0 = cbdef ? make_lut_c8(s0) : make_lut(s0, cb);
+    Lut L1 = L0;
+    if (!one) L1 = (__float_as_uint(s1) == __float_as_uint(s0)) ? L0 : (cbdef ? make_lut_c8(s1) : make_lut(s1, cb));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const Lut& L = j < 2 ? L0 : L1;
+        lo[j] = lut4(L, wd[j] & 0x0F0F0F0Fu);
+        hi[j] = lut4(L, (wd[j] >> 4) & 0x0F0F0F0Fu);
+    }
+}
+
+// per-weight decode of one chunk's four code dwords through one table (a group spans the chunk)
+__device__ __forceinline__ void decode_tbl(const uint32_t* wd, const uint4 T, uint32_t* lo, uint32_t* hi) {
+    Lut L;
+    L.w[0] = T.x;
+    L.w[1] = T.y;
+    L.w[2] = T.z;
+    L.w[3] = T.w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
         lo[j] = lut4(L, wd[j] & 0x0F0F0F0Fu);
         hi[j] = lut4(L, (wd[j] >> 4) & 0x0F0F0F0Fu);
     }
@@ -615,15 +659,17 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     const int lgG = a.lgG;
 
     // 1. one-shot operands: activation rows (unless produced in this launch), tile scales, channel scales
-    constexpr bool HR = SRC == SRC_HR, XP = SRC == SRC_XP;
-    const bool own_x = SRC == SRC_Q8;  // int8 rows a.xq staged by this prologue
+    constexpr int SRCK = SRC & 3;
+    constexpr bool IO = (SRC & SRC_INT_ONLY) != 0;  // the integral decode only
+    constexpr bool HR = SRCK == SRC_HR, XP = SRCK == SRC_XP;
+    const bool own_x = SRCK == SRC_Q8;  // int8 rows a.xq staged by this prologue
     // Per-wave one-shots (a.pwo): each wave stages only what it reads, its slice's activation run
     // (the TPW waves of a slice write the same bytes) and its tile's scales of its slice's groups
     // into a region of its own, so no wave waits for another before its loop.
     const bool pwo = a.pwo && !MFMA;  // (uniform)
     const int sbw = (ncu / a.KS) * ESZ;                               // pwo: scale bytes per tile row
     uint8_t* swv = sl + wave * 16 * sbw;                              // pwo: [16][sbw]
-    if (pwo && SRC == SRC_Q8) {
+    if (pwo && SRCK == SRC_Q8) {
         const MDX_G uint8_t* xsrc = as_global(reinterpret_cast<const uint8_t*>(a.xq)) + c0 * CHUNK_K;
         const int xp = nch * (CHUNK_K / 16);
         for (int i0 = 0; i0 < xp; i0 += WAVE)
@@ -693,6 +739,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
     // round of weights); the prep runs from LDS while that round streams in
     uint8_t* xs_l = zeros + 32;  // SRC_XP: [K] bf16 row, then [K] bf16 norm weights
+    // per-weight decode tables [g1 - g0][TPW x 16 rows] x 16 bytes (after the SRC_XP region; the rows of
+    // a group adjacent, so the 16 rows a wave reads at once fall in distinct banks)
+    uint4* tbl = reinterpret_cast<uint4*>(xs_l + (XP ? 4 * K : 0));
+    const bool tbl_on = a.tbl != 0;  // (uniform; groups of at least one chunk, scales not asserted integral)
+    const int ngr = g1 - g0;
     if (XP && pwo) {
         // per wave: the 256-groups its prep reads (group g: 512 bytes of the row, 512 of the weights)
         const int G = K / 256, nw4 = a.TPW * a.KS;
@@ -746,6 +797,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 #pragma unroll
     for (int p = 0; p < RING; ++p) buf[p] = ldg_stream(wp + (live ? min(p, last) : 0) * wstride);
     const bool can_int = !a.force_exact && cbdef && (lgG >= (MFMA ? 7 : 5));
+    const bool one_scale = lgG >= 5;  // (uniform) a lane's 32-k run lies in one group
     if (t == 0) *mixed = 0;
     if (t < 8) reinterpret_cast<uint32_t*>(zeros)[t] = 0u;
 
@@ -890,7 +942,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // MDX_DECODE_INTEGRAL the caller asserts it: no check, and no barrier unless this prologue wrote
     // the activation rows to LDS itself (SRC_HR, SRC_XP).
     bool integ;
-    if (pwo) {
+    if (IO) {
+        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
+        }
+        integ = true;
+    } else if (pwo) {
         if (HR || XP) {  // (the rows this prologue wrote to LDS)
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
@@ -915,10 +973,31 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_barrier();
         integ = can_int && *mixed == 0;  // uniform over the unit
     }
+    if (!integ && tbl_on) {
+        // every (tile row, group) table once (make_lut's bytes), from the staged scales
+        const int nr = a.TPW * 16, ntab = nr * ngr;
+        for (int j = t; j < ntab; j += nthr) {
+            const int gg = j / nr, rw = j - gg * nr;
+            const float sv = rd_scale<SDT>(sl + rw * seg + gg * ESZ);
+            const Lut L = cbdef ? make_lut_c8(sv) : make_lut(sv, cb);
+            tbl[j] = make_uint4(L.w[0], L.w[1], L.w[2], L.w[3]);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+    }
     // the tile-major layout keeps k 0..3 of a code word in its low nibbles and k 4..7 in its high
     // ones (natural activation order); the checkpoint layout interleaves them (even k low, odd k high)
     const bool split = a.layout == MDX_LAYOUT_TILE;
     const uint8_t* scol = pwo ? swv + c * sbw - c0 * ESZ : sl + (ts * 16 + c) * seg - g0 * ESZ;
+    const uint4* tcol = tbl + (ts * 16 + c) - g0 * (a.TPW * 16);  // this lane's row's table of group g: tcol[g TPW 16]
+    // the tables travel in a ring beside the weights: slot p's table is read from LDS when the slot's
+    // weights are requested, a round ahead of its use (an LDS read right before the lookups would
+    // expose its latency at every chunk)
+    const bool tring = !integ && tbl_on;  // (uniform)
+    auto tbl_of = [&](int i) { return tcol[(((c0 + min(i, last)) * CHUNK_K + klane) >> lgG) * (a.TPW * 16)]; };
+    uint4 tq[RING];
+#pragma unroll
+    for (int p = 0; p < RING; ++p) tq[p] = tring ? tbl_of(p) : make_uint4(0u, 0u, 0u, 0u);
 
     if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
@@ -961,7 +1040,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 #pragma unroll
                         for (int j = 0; j < 8; ++j) xd[j] = 0;
                     uint32_t lo[4], hi[4];
-                    decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
+                    if (tbl_on)
+                        decode_tbl(wd, tq[p], lo, hi);
+                    else
+                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), one_scale, cbdef, cb, lo, hi);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         uint32_t n0 = lo[j], n1 = hi[j];
@@ -973,6 +1055,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 // refill the slot only now: its old and new contents never live at once, so the ring
                 // keeps its registers across rounds (no copies, and no wait, at the loop end)
                 buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
+                if (tring) tq[p] = tbl_of(i + RING);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1001,7 +1084,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                         hi[j] = sx16_hi(wd[j]);
                     }
                 } else {
-                    decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), cb, lo, hi);
+                    if (tbl_on)
+                        decode_tbl(wd, tq[p], lo, hi);
+                    else
+                        decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), one_scale, cbdef, cb, lo, hi);
                 }
                 if (!split)
 #pragma unroll
@@ -1024,6 +1110,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                     }
                 }
                 buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);  // refill after use (see above)
+                if (tring) tq[p] = tbl_of(i + RING);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1048,12 +1135,17 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 // SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
 // SIMD.
 template <bool MFMA, int R, int SDT, int RING, int SRC = SRC_Q8>
-__global__ __launch_bounds__(SRC == SRC_HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__((SRC & 3) == SRC_HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     gemv_unit<MFMA, R, SDT, RING, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds);
 }
 
 // LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
+// Whether units build their per-weight decode tables once into LDS (groups of at least one chunk,
+// scales not asserted integral): one 16-byte table per (tile row, group) instead of one per lane and
+// chunk in the loop.
+bool gemv_tables(const GemvArgs& a) { return a.tbl != 0; }
+
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     const int ng = a.K >> a.lgG;
     int g0 = (cu0 * CHUNK_K) >> a.lgG, g1 = ((cu0 + ncu) * CHUNK_K + (1 << a.lgG) - 1) >> a.lgG;
@@ -1065,7 +1157,9 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
     s += 128 * 4 + 16 + 32;  // parameters, flag, zeros
-    return a.xp_x ? s + size_t(4) * a.K : s;  // SRC_XP: the bf16 row and its norm weights
+    if (a.xp_x) s += size_t(4) * a.K;  // SRC_XP: the bf16 row and its norm weights
+    if (gemv_tables(a)) s += size_t(a.TPW) * 16 * (g1 - g0) * 16;  // per-weight decode tables
+    return s;
 }
 
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mfma, esz, 0, a.K / CHUNK_K); }
@@ -1085,6 +1179,13 @@ int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
 
 template <bool MFMA, int R, int SDT, int RING>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
+    // the integral-only variant when the caller asserts integral scales that the integral form takes
+    const bool io = a.assume_int && !a.cb && !a.force_exact && a.lgG >= (MFMA ? 7 : 5);
+    if (io) {
+        if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR + SRC_INT_ONLY>(a, wgs, st);
+        if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_INT_ONLY>(a, wgs, st);
+        return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY>(a, wgs, st);
+    }
     if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR>(a, wgs, st);
     if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP>(a, wgs, st);
     return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8>(a, wgs, st);
@@ -1285,6 +1386,16 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
+    // per-weight decode tables in LDS when the scales are not asserted integral, a group spans a chunk
+    // and the larger footprint still holds the grid's work-groups per CU (else fewer resident: at 8
+    // rows the gate/up pair would drop from three work-groups per CU to two and lose more than the
+    // tables save; there the lanes build their tables in the loop)
+    if (!a.assume_int && a.lgG >= 7) {
+        a.tbl = 1;
+        const size_t sm = gemv_smem(a, mfma, esz);
+        const int per_cu = (wgs + 255) / 256;
+        a.tbl = sm <= 160 * 1024 && int64_t(per_cu) * sm <= 160 * 1024;
+    }
     // per-wave one-shots: one int8 row, caller-asserted integral scales with the default codebook,
     // G128, 16-byte runs of scales per slice and per row (MDX_GEMV_PWO=0 turns them off)
     const char* pe = getenv("MDX_GEMV_PWO");
