@@ -308,7 +308,7 @@ struct GemvArgs {
     int force_exact;      // MDX_DECODE_EXACT: never take the integral form
     int assume_int;       // MDX_DECODE_INTEGRAL (every matrix): the integral form without the check
     int pwo;              // per-wave one-shots (one int8 row, G128, assume_int): no work-group barrier
-    int tbl;              // per-weight decode tables built once per work-group into LDS (gemv_tables)
+    int tbl;              // per-weight decode tables built once per work-group into LDS: 1 16-byte, 2 8-byte (gemv_table_bytes)
     int epi;
     void* out[3];
     const void* res[3];
@@ -383,6 +383,33 @@ __device__ __forceinline__ Lut make_lut_c8(float s) {
     return L;
 }
 
+// The eight magnitudes q(k s), k = 1..8, of the default codebook's table as int8 bytes (q1..q4, q5..q8).
+__device__ __forceinline__ uint2 make_q8(float s) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 1; k <= 8; ++k) {
+        const float r = rintf(__fmul_rn(float(k), s));
+        const int q = (r != r) ? 0 : int(fminf(fmaxf(r, -127.f), 127.f));
+        w[(k - 1) >> 2] |= (uint32_t(q) & 0xFFu) << (8 * ((k - 1) & 3));
+    }
+    return make_uint2(w[0], w[1]);
+}
+
+// The default codebook's 16-byte table from its magnitudes (make_lut_c8's bytes): byte reversal and
+// a carry-free negation of four int8 at once (~b + 1 per byte; no byte is -128 after the clamp).
+__device__ __forceinline__ Lut lut_from_q8(uint32_t qa, uint32_t qb) {
+    auto neg4 = [](uint32_t b) {
+        const uint32_t n = ~b;
+        return ((n & 0x7F7F7F7Fu) + 0x01010101u) ^ (n & 0x80808080u);
+    };
+    Lut L;
+    L.w[0] = neg4(__builtin_amdgcn_perm(0u, qb, 0x00010203u));  // -q8, -q7, -q6, -q5
+    L.w[1] = neg4(__builtin_amdgcn_perm(0u, qa, 0x00010203u));  // -q4 .. -q1
+    L.w[2] = __builtin_amdgcn_perm(0u, qa, 0x0201000Cu);        // 0, q1, q2, q3
+    L.w[3] = __builtin_amdgcn_perm(qb, qa, 0x06050403u);        // q4 .. q7
+    return L;
+}
+
 // four codes (one per byte, values 0..15) -> four int8 via the 16-byte table
 __device__ __forceinline__ uint32_t lut4(const Lut& L, uint32_t c) {
     const uint32_t sel = c & 0x07070707u;
@@ -408,12 +435,17 @@ __device__ __forceinline__ void decode_exact(const uint32_t* wd, float s0, float
 }
 
 // per-weight decode of one chunk's four code dwords through one table (a group spans the chunk)
-__device__ __forceinline__ void decode_tbl(const uint32_t* wd, const uint4 T, uint32_t* lo, uint32_t* hi) {
+// (q8: T holds the default codebook's eight magnitudes in .x, .y)
+__device__ __forceinline__ void decode_tbl(const uint32_t* wd, const uint4 T, bool q8, uint32_t* lo, uint32_t* hi) {
     Lut L;
-    L.w[0] = T.x;
-    L.w[1] = T.y;
-    L.w[2] = T.z;
-    L.w[3] = T.w;
+    if (q8) {
+        L = lut_from_q8(T.x, T.y);
+    } else {
+        L.w[0] = T.x;
+        L.w[1] = T.y;
+        L.w[2] = T.z;
+        L.w[3] = T.w;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         lo[j] = lut4(L, wd[j] & 0x0F0F0F0Fu);
@@ -743,6 +775,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // a group adjacent, so the 16 rows a wave reads at once fall in distinct banks)
     uint4* tbl = reinterpret_cast<uint4*>(xs_l + (XP ? 4 * K : 0));
     const bool tbl_on = a.tbl != 0;  // (uniform; groups of at least one chunk, scales not asserted integral)
+    const bool tbl8 = a.tbl == 2;    // (uniform) 8-byte tables: the default codebook's magnitudes
     const int ngr = g1 - g0;
     if (XP && pwo) {
         // per wave: the 256-groups its prep reads (group g: 512 bytes of the row, 512 of the weights)
@@ -979,8 +1012,12 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         for (int j = t; j < ntab; j += nthr) {
             const int gg = j / nr, rw = j - gg * nr;
             const float sv = rd_scale<SDT>(sl + rw * seg + gg * ESZ);
-            const Lut L = cbdef ? make_lut_c8(sv) : make_lut(sv, cb);
-            tbl[j] = make_uint4(L.w[0], L.w[1], L.w[2], L.w[3]);
+            if (tbl8) {
+                reinterpret_cast<uint2*>(tbl)[j] = make_q8(sv);
+            } else {
+                const Lut L = cbdef ? make_lut_c8(sv) : make_lut(sv, cb);
+                tbl[j] = make_uint4(L.w[0], L.w[1], L.w[2], L.w[3]);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
@@ -989,12 +1026,18 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // ones (natural activation order); the checkpoint layout interleaves them (even k low, odd k high)
     const bool split = a.layout == MDX_LAYOUT_TILE;
     const uint8_t* scol = pwo ? swv + c * sbw - c0 * ESZ : sl + (ts * 16 + c) * seg - g0 * ESZ;
-    const uint4* tcol = tbl + (ts * 16 + c) - g0 * (a.TPW * 16);  // this lane's row's table of group g: tcol[g TPW 16]
     // the tables travel in a ring beside the weights: slot p's table is read from LDS when the slot's
     // weights are requested, a round ahead of its use (an LDS read right before the lookups would
     // expose its latency at every chunk)
     const bool tring = !integ && tbl_on;  // (uniform)
-    auto tbl_of = [&](int i) { return tcol[(((c0 + min(i, last)) * CHUNK_K + klane) >> lgG) * (a.TPW * 16)]; };
+    auto tbl_of = [&](int i) {
+        const int o = (ts * 16 + c) + ((((c0 + min(i, last)) * CHUNK_K + klane) >> lgG) - g0) * (a.TPW * 16);
+        if (tbl8) {
+            const uint2 q = reinterpret_cast<const uint2*>(tbl)[o];
+            return make_uint4(q.x, q.y, 0u, 0u);
+        }
+        return tbl[o];
+    };
     uint4 tq[RING];
 #pragma unroll
     for (int p = 0; p < RING; ++p) tq[p] = tring ? tbl_of(p) : make_uint4(0u, 0u, 0u, 0u);
@@ -1041,7 +1084,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                         for (int j = 0; j < 8; ++j) xd[j] = 0;
                     uint32_t lo[4], hi[4];
                     if (tbl_on)
-                        decode_tbl(wd, tq[p], lo, hi);
+                        decode_tbl(wd, tq[p], tbl8, lo, hi);
                     else
                         decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), one_scale, cbdef, cb, lo, hi);
 #pragma unroll
@@ -1085,7 +1128,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                     }
                 } else {
                     if (tbl_on)
-                        decode_tbl(wd, tq[p], lo, hi);
+                        decode_tbl(wd, tq[p], tbl8, lo, hi);
                     else
                         decode_exact(wd, s0, rd_scale<SDT>(scol + ((k0 + 16) >> lgG) * ESZ), one_scale, cbdef, cb, lo, hi);
                 }
@@ -1140,12 +1183,11 @@ __global__ __launch_bounds__((SRC & 3) == SRC_HR ? 768 : 1024) void gemv_kernel(
     gemv_unit<MFMA, R, SDT, RING, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds);
 }
 
-// LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
-// Whether units build their per-weight decode tables once into LDS (groups of at least one chunk,
-// scales not asserted integral): one 16-byte table per (tile row, group) instead of one per lane and
-// chunk in the loop.
-bool gemv_tables(const GemvArgs& a) { return a.tbl != 0; }
+// Bytes of a per-weight decode table in LDS (0: none): 16 (the table), 8 (the default codebook's
+// eight magnitudes, expanded per chunk by four byte permutes and two carry-free negations).
+int gemv_table_bytes(const GemvArgs& a) { return a.tbl == 1 ? 16 : (a.tbl == 2 ? 8 : 0); }
 
+// LDS bytes of a unit over `ncu` chunks starting at chunk cu0 (the layout of gemv_unit)
 size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     const int ng = a.K >> a.lgG;
     int g0 = (cu0 * CHUNK_K) >> a.lgG, g1 = ((cu0 + ncu) * CHUNK_K + (1 << a.lgG) - 1) >> a.lgG;
@@ -1158,7 +1200,7 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
     s += 128 * 4 + 16 + 32;  // parameters, flag, zeros
     if (a.xp_x) s += size_t(4) * a.K;  // SRC_XP: the bf16 row and its norm weights
-    if (gemv_tables(a)) s += size_t(a.TPW) * 16 * (g1 - g0) * 16;  // per-weight decode tables
+    s += size_t(a.TPW) * 16 * (g1 - g0) * gemv_table_bytes(a);  // per-weight decode tables
     return s;
 }
 
@@ -1391,10 +1433,14 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     // rows the gate/up pair would drop from three work-groups per CU to two and lose more than the
     // tables save; there the lanes build their tables in the loop)
     if (!a.assume_int && a.lgG >= 7) {
-        a.tbl = 1;
-        const size_t sm = gemv_smem(a, mfma, esz);
         const int per_cu = (wgs + 255) / 256;
-        a.tbl = sm <= 160 * 1024 && int64_t(per_cu) * sm <= 160 * 1024;
+        for (int tb = 1; tb <= 2; ++tb) {  // 16-byte tables, else (default codebook) 8-byte ones
+            if (tb == 2 && a.cb) break;
+            a.tbl = tb;
+            const size_t sm = gemv_smem(a, mfma, esz);
+            if (int64_t(per_cu) * sm <= 160 * 1024) break;
+            a.tbl = 0;
+        }
     }
     // per-wave one-shots: one int8 row, caller-asserted integral scales with the default codebook,
     // G128, 16-byte runs of scales per slice and per row (MDX_GEMV_PWO=0 turns them off)
