@@ -335,7 +335,7 @@ def bench_lmhead(args, dev):
                  "synthetic (seeded N(0, 0.02) weights, N(0,1) rows)",
                  {"workload": f"bf16 lm_head 151936x4096, rows={M}, tile-major", "rows": M,
                   "algorithmic_bytes_per_step": per},
-                 {"bound": "hbm", "kernel": "bf16_linear_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                 {"bound": "hbm", "kernel": "bf16_stream_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
                   "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                   "avg_launch_us": round(t * 1e6, 3)})
 
