@@ -171,6 +171,69 @@ def cpu_baseline_mlp(ring0, rows, xb, nwb, lutb, budget_s=25.0):
     return float(np.median(times)), len(times), model, threads
 
 
+def cpu_decode_estimate(mlp_s, mlp_algo_bytes, budget_s=20.0):
+    """Config-5 CPU tok/s, composed from timed pieces of the numpy oracle on the host (a whole 32-layer
+    step on the CPU takes tens of seconds): every W4A8 GEMV of a step at the MLP chain's measured rate
+    per weight byte (the same decode + int dot), the bf16 lm_head (verify + 2 drafts) and the MTP
+    block's bf16 GEMMs at the rate of a timed 8-row slice of the float64 bf16 linear, 24 timed GDN
+    steps (8 tree rows) and 8 timed attention calls (8 rows over a 1024-token context); norms,
+    RoPE, top-k and the accept walk are left out. One accepted token per step, as in the GPU line."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    sys.path.insert(0, ROOT)
+    from oracle import ref
+    rng = np.random.default_rng(5)
+    H, I, V = 4096, 12288, 151936
+    bf = lambda *shape: ref.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * 0.05)
+
+    def med(fn, n=3):
+        ts = []
+        t_end = time.perf_counter() + budget_s / 4
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end:
+                break
+        return float(np.median(ts))
+
+    w4_layer = {"mlp": 3 * H * I, "gdn": (2 * 16 * 128 + 32 * 128 + 32 * 128) * H + H * 32 * 128,
+                "attn": (2 * 32 * 128 + 2 * 8 * 128) * H + H * 32 * 128}
+    w4_bytes = (32 * w4_layer["mlp"] + 24 * w4_layer["gdn"] + 8 * w4_layer["attn"]) * (0.5 + 2 / 128)
+    w4_s = mlp_s * w4_bytes / mlp_algo_bytes
+    _, threads = cpu_info()
+    with threadpool_limits(limits=threads):
+        xs, ws = bf(8, H), bf(16384, H)
+        bf_rate = 16384 * H * 2 / med(lambda: ref.bf16_linear_f64(xs, ws))
+        mtp_bytes = 486.5e6
+        bf_s = (3 * V * H * 2 + 2 * mtp_bytes) / bf_rate
+        HK, HV, R, slots = 16, 32, 8, 8
+        C = 2 * HK * 128 + HV * 128
+        tree = ref.tree_from_spec(ref.spec_of_widths((4, 3)), slots)
+        parents = tree[0][:R]
+        ctl = np.array([0, 0] + [0] * slots + parents + ref.verify_program(parents, R))
+        st = dict(conv_state=ref.bf16_to_f32(bf(C, 3)), pb=np.zeros((2, slots, C), np.float32),
+                  qb=np.zeros((2, slots, C), np.float32), rec=(rng.standard_normal((HV, 128, 128)) * 0.1).astype(np.float32),
+                  gates=np.zeros((2, slots, HV, 2), np.float32), sums=np.zeros((2, slots, HK, 2), np.float32))
+        a, b = ref.gdn_ab(bf(R, H), bf(HV, H), bf(HV, H))
+        args_g = (ref.bf16_to_f32(bf(R, C)), ref.bf16_to_f32(bf(R, HV * 128)), a, b, ref.bf16_to_f32(bf(C, 4)),
+                  rng.uniform(-1, 1, HV).astype(np.float32), -np.exp(rng.uniform(-1, 0.5, HV)).astype(np.float32),
+                  ref.bf16_to_f32(bf(128)), 1e-6, 128 ** -0.5, ctl, R, HK, slots)
+        gdn_s = med(lambda: ref.gdn_step({k: v.copy() for k, v in st.items()}, *args_g))
+        L = 1024
+        q, k, v = (rng.standard_normal(sh).astype(np.float32) for sh in ((32, R, 128), (8, L + 64, 128), (8, L + 64, 128)))
+        xk, xv = (rng.standard_normal((8, R, 128)).astype(np.float32) for _ in range(2))
+        attn_s = med(lambda: ref.attention_f64(q, k, v, L, xk, xv, ref.tree_mask(tree[0][:R])))
+    step_s = w4_s + bf_s + 24 * gdn_s + 8 * attn_s
+    return {"value": round(1.0 / step_s, 5), "unit": "tok/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(step_s * 1e3, 1),
+            "components_ms": {"w4a8_gemvs": round(w4_s * 1e3, 1), "bf16_gemms": round(bf_s * 1e3, 1),
+                              "gdn_steps": round(24 * gdn_s * 1e3, 1), "attention": round(8 * attn_s * 1e3, 1)},
+            "sample": "composed from timed oracle pieces: W4A8 GEMVs at the MLP chain's rate, one 8-row 16384-row "
+                      "slice of the bf16 linear, one GDN step and one attention call (medians of up to 3), "
+                      "scaled to a 32-layer step; norms, RoPE and top-k left out"}
+
+
 def bench_mlp(args, dev):
     import torch
     from mdx import _C, _lib, layout
@@ -248,6 +311,7 @@ def bench_mlp(args, dev):
         nwb = nw.view(torch.int16).cpu().numpy().view("uint16")
         lutb = lut.view(torch.int16).cpu().numpy().view("uint16")
         t_cpu, n, model, threads = cpu_baseline_mlp(ring_f[0], M, xb, nwb, lutb)
+        res["_cpu_mlp_s"] = t_cpu
         res["cpu_baseline"] = {"value": round(per / t_cpu / 1e9, 4), "unit": "GB/s", "cores": threads,
                                "kind": "port", "ms_per_step": round(t_cpu * 1e3, 1), "cpu_model": model,
                                "sample": f"median of {n} MLP calls (after 3 warm-up calls) of the numpy oracle chain "
@@ -705,6 +769,9 @@ def main():
         res["decode_two_stage_drafts"] = {"value": d2["value"], "unit": "tok/s", "ms_per_step": d2["config"]["ms_per_step"],
                                           "accepted_per_step": d2["config"]["accepted_per_step"],
                                           "workload": d2["config"]["workload"]}
+        if "_cpu_mlp_s" in res:
+            res["decode"]["cpu_baseline"] = cpu_decode_estimate(res["_cpu_mlp_s"], mlp_bytes(1))
+    res.pop("_cpu_mlp_s", None)
     print(json.dumps(res), flush=True)
 
 
