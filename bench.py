@@ -456,7 +456,7 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
     cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, gdn_fused=args.gdn_fused,
-                              gdn_side_gates=args.side_gates)
+                              gdn_side_gates=args.side_gates, predictable=getattr(args, "predictable", False))
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -723,6 +723,8 @@ def main():
     ap.add_argument("--workload", choices=["mlp", "linear", "copy", "lmhead", "attn", "stack", "read", "attn_layer",
                                            "gdn_layer"], default="mlp")
     ap.add_argument("--tokens", type=int, default=0, help="stack: decode until this many tokens are committed")
+    ap.add_argument("--predictable", action="store_true", help="stack: synthetic weights whose next token is "
+                    "predictable (t -> t + 1), so the drafts are accepted (HybridConfig.predictable)")
     ap.add_argument("--two-stage", action="store_true", help="stack: drafts score the vocabulary with an int4 copy "
                                                                "of the lm_head and recompute their candidates exactly")
     ap.add_argument("--auto", action="store_true", help="stack: the adaptive tree (decode_auto)")
@@ -769,6 +771,13 @@ def main():
         res["decode_two_stage_drafts"] = {"value": d2["value"], "unit": "tok/s", "ms_per_step": d2["config"]["ms_per_step"],
                                           "accepted_per_step": d2["config"]["accepted_per_step"],
                                           "workload": d2["config"]["workload"]}
+        # the same decode on weights whose next token is predictable: the drafts are accepted, every step
+        # commits len(widths) + 1 tokens (the same kernels on the same shapes)
+        sub.predictable = True
+        d3 = bench_stack(sub, dev, tokens=512)
+        res["decode_predictable_weights"] = {"value": d3["value"], "unit": "tok/s", "ms_per_step": d3["config"]["ms_per_step"],
+                                             "accepted_per_step": d3["config"]["accepted_per_step"],
+                                             "workload": d3["config"]["workload"] + ", predictable synthetic weights"}
         if "_cpu_mlp_s" in res:
             res["decode"]["cpu_baseline"] = cpu_decode_estimate(res["_cpu_mlp_s"], mlp_bytes(1))
     res.pop("_cpu_mlp_s", None)

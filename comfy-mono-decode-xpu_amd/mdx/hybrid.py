@@ -53,6 +53,12 @@ class HybridConfig:
     gdn_fused: bool = False       # the GDN core in one launch (mdx_gdn_core_fused, the same bits)
     gdn_side_gates: bool = False  # the GDN gates on a second stream beside the projection GEMV (the same bits)
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
+    # synthetic weights with a predictable next token (token t -> t + 1 mod vocab) for the verify and the
+    # drafts: the lm_head row v is the embedding of v - 1, the layers' and the MTP block's output
+    # projections are scaled down (the residual stream stays the embedding) and the MTP block's fc passes
+    # the embedding half through. Every kernel does the same work on the same shapes; the drafts are
+    # accepted, so a step commits len(widths) + 1 tokens.
+    predictable: bool = False
 
     def attention(self, i):
         return i % self.attn_every == self.attn_every - 1
@@ -122,6 +128,9 @@ class HybridModel:
         self.gdn_ch = 2 * hk * 128 + hv * 128
         self.embed = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.5).bfloat16()
         head = (torch.randn(c.vocab, H, generator=gen, device=dev) * 0.02).bfloat16()
+        if c.predictable:
+            # logit of t + 1 at an embedding e_t: 0.015 |e_t|^2 / rms(e_t) ~ 31, the others ~ N(0, 0.5)
+            head = (torch.roll(self.embed.float(), shifts=1, dims=0) * 0.015).bfloat16()
         if c.head not in ("bf16", "int8"):
             raise ValueError("head: 'bf16' or 'int8'")
         self.lm_head = self.lm_rows = self.lm8 = self.lm8_rows = self.lm8_s = None
@@ -174,6 +183,14 @@ class HybridModel:
                         qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1),
                         o=_bf16w(H, qd, gen, dev, 0.02), norm_post=_norm(H, gen, dev),
                         gu=_bf16w(2 * I, H, gen, dev, 0.02), d=_bf16w(H, I, gen, dev, 0.02), norm_f=_norm(H, gen, dev))
+        if c.predictable:
+            for L in self.layers:
+                for r in ("o", "d"):
+                    L[r].sc.mul_(1e-6)  # (1e-3 is not enough: the GDN layers' outputs grow along the stack)
+            M = self.mtp
+            M["fc"] = layout.tile_major_bf16(torch.cat([torch.eye(H, device=dev), torch.zeros(H, H, device=dev)], 1).bfloat16())
+            M["o"] = layout.tile_major_bf16((torch.randn(H, qd, generator=gen, device=dev) * 2e-5).bfloat16())
+            M["d"] = layout.tile_major_bf16((torch.randn(H, I, generator=gen, device=dev) * 2e-5).bfloat16())
         self.ftab = rope_table(c, dev)
         self._state(gen)
 

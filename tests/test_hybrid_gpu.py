@@ -142,3 +142,43 @@ def test_auto_tree_records_ranks_and_adapts(dev):
     assert out["steps"] == 72 and len(out["widths"]) == 72 and out["tokens"] == b.st[0].item() - st0
     assert out["widths"][0] == (4, 3) and out["widths"][-1] == (1,)
     assert out["draft_ms"] > 0 and out["verify_ms"] > 0
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_predictable_weights_commit_every_draft(dev, greedy):
+    """Synthetic weights whose next token is predictable (t -> t + 1 mod vocab, HybridConfig.predictable):
+    the drafts follow the chain, the verify (sampled or greedy) accepts them, and every step commits
+    len(widths) + 1 consecutive tokens, eagerly and from a replayed graph."""
+    from mdx import hybrid
+    cfg = hybrid.HybridConfig(layers=4, inter=4096, vocab=32768, cap=512, greedy=greedy, predictable=True)
+    m = hybrid.HybridModel(cfg, dev, seed=3)
+    m.prefill(torch.randint(0, cfg.vocab, (37,), generator=torch.Generator().manual_seed(6)))
+    torch.cuda.synchronize()
+    want_n = len(cfg.widths) + 1
+    root = m.nt.item()
+
+    def check(step):
+        nonlocal root
+        n = m.result[0].item()
+        got = m.result[1:1 + n].tolist()
+        assert n == want_n, (step, n, got, root)
+        assert got == [(root + 1 + i) % cfg.vocab for i in range(n)], (step, got, root)
+        assert m.nt.item() == got[-1]
+        root = got[-1]
+
+    for step in range(3):
+        print(f"case predictable greedy={greedy} eager step {step}", flush=True)
+        st0 = m.st[0].item()
+        m.step(m.parity)
+        m.parity ^= 1
+        torch.cuda.synchronize()
+        check(step)
+        assert m.st[0].item() == st0 + want_n
+    print(f"case predictable greedy={greedy} replay", flush=True)
+    m.capture()  # two more eager warm-up steps
+    torch.cuda.synchronize()
+    root = m.nt.item()
+    for step in range(3):
+        m.replay(1)
+        torch.cuda.synchronize()
+        check(3 + step)
