@@ -501,7 +501,8 @@ def bench_stack_auto(args, dev, tokens=512):
     import torch
     from mdx import hybrid
     cap = args.prompt + 8 * (tokens + 64) + 64
-    cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head)
+    cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head,
+                              predictable=getattr(args, "predictable", False))
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     m.prefill(torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5)))
@@ -520,7 +521,7 @@ def bench_stack_auto(args, dev, tokens=512):
     t = time.perf_counter() - t1
     final = widths[-1]
     return _line(args, round(got / t, 2), "tok/s", t / steps, steps, "W4A8 int8 x int4 -> int32; bf16 draft block",
-                 "synthetic (random-init weights, seeded random prompt)",
+                 "synthetic (" + ("predictable" if cfg.predictable else "random-init") + " weights, seeded random prompt)",
                  {"workload": f"32-layer W4A8 hybrid, vocab 151936, MTP draft, adaptive tree (auto), top-k 20, prompt "
                               f"{args.prompt}, {got} tokens decoded", "prompt": args.prompt, "steps": steps,
                   "tokens": got, "accepted_per_step": round(got / steps, 3), "final_widths": list(final),
