@@ -34,6 +34,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int AT_WAVES = 4;
 constexpr int AT_STEP = 32;        // tokens per MFMA step
@@ -55,6 +56,7 @@ struct AttnArgs {
     float* part;             // [Hk][RT][C + 1][2 * 16 + 16 * D]
     int H, Hk, S, cap, groups, rows, RT, C;
     int min_tpw;             // a chunk gives each wave at least this many tokens
+    int p2;                  // the streaming form's token parts per chunk (0: the register form)
     float zscale;            // 1/sqrt(D) * log2(e)
 };
 
@@ -282,6 +284,303 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
     }
 }
 
+// ---- The streaming form (head_dim 64 and 128) ---------------------------------------------------
+// One work-group per (kv head, chunk): all of the kv head's query rows (up to 4 row tiles) in one
+// work-group, so each K/V byte leaves HBM once and is read from LDS by every row tile. Wave w owns
+// row tile w % RTW and token part w / RTW of the chunk (P = 4 / RTW parts). A part's K and V stream
+// through an LDS ring of 32-token stages by direct-to-LDS loads (1 KiB per wave instruction, every
+// stage of the ring in flight from the start); the 16-byte units of a token row are stored XOR-
+// swizzled by the token's low bits, so the S^T operand reads (16 tokens, one unit each) and the V^T
+// gathers (8 tokens per lane) hit distinct banks. Per stage a wave computes S^T = K Q^T from LDS
+// (v_mfma_f32_16x16x32_bf16), the online softmax in its lanes, and O^T += V^T P^T with V^T gathered
+// from the natural [token][dim] rows in the k-slot order its S^T accumulators give P^T. The grid is
+// at most 256 work-groups (one round on the chip's 256 CUs: the ring takes most of a CU's LDS).
+constexpr int A2_STEP = 32;
+constexpr int A2_RING = 128 * 1024;  // K/V ring bytes per work-group
+constexpr int A2_MAX_WG = 256;
+
+// ds_read_b64_tr_b16 (gfx950) as inline asm: in each 16-lane group, lane i receives element i % 4 of
+// the 8-byte runs that lanes i / 4 + 4 j (j = 0..3) point at. The builtin form makes the compiler wait
+// for every outstanding direct-to-LDS load (vmcnt(0)) before it, which would drain the ring each stage;
+// here N reads and their lgkmcnt(0) wait form one asm statement, so the results exist (for the
+// compiler) only after the wait. Addresses are LDS byte addresses.
+template <int N>
+__device__ __forceinline__ void ds_read_tr16_n(u32x2 (&r)[N], const uint32_t (&addr)[N]) {
+    static_assert(N == 4 || N == 8, "4 or 8 reads");
+    if constexpr (N == 4) {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %5\n\tds_read_b64_tr_b16 %2, %6\n\t"
+            "ds_read_b64_tr_b16 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]));
+    } else {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %9\n\tds_read_b64_tr_b16 %2, %10\n\t"
+            "ds_read_b64_tr_b16 %3, %11\n\tds_read_b64_tr_b16 %4, %12\n\tds_read_b64_tr_b16 %5, %13\n\t"
+            "ds_read_b64_tr_b16 %6, %14\n\tds_read_b64_tr_b16 %7, %15\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+              "v"(addr[7]));
+    }
+}
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const unsigned char*)p));
+}
+
+// chunk length (tokens, a multiple of 32 P) and active chunk count for context L over C chunks
+__device__ __forceinline__ void split2(int L, int C, int P, int& T, int& active) {
+    const int per = (L + C - 1) / C, q = A2_STEP * P;
+    T = per < 1 ? q : (per + q - 1) / q * q;
+    active = L > 0 ? (L + T - 1) / T : 0;
+}
+
+template <int D, int RTW>
+__global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
+    constexpr int P = 4 / RTW;
+    constexpr int KK = D / 32, DT = D / 16;
+    constexpr int RB = 2 * D;                    // bytes per token row
+    constexpr int SW = D / 8 < 16 ? D / 8 - 1 : 15;  // swizzle mask of the 16-byte units
+    constexpr int STAGE = A2_STEP * RB;          // bytes of K (or V) per stage
+    constexpr int NS = A2_RING / (2 * STAGE * P);  // ring stages per part
+    constexpr int PER = STAGE / 1024 / RTW;      // DMA instructions per wave, stage and matrix
+    static_assert(NS >= 2 && PER >= 1 && (NS - 2) * 2 * PER <= 63, "ring geometry");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
+    const int rt = w % RTW, part = w / RTW;
+    const int kh = blockIdx.x / (a.C + 1), cslot = blockIdx.x % (a.C + 1);
+    const bool tree = cslot == a.C;
+    int L = a.seqlen[0];
+    L = L < 0 ? 0 : (L > a.cap ? a.cap : L);
+    int T, active;
+    split2(L, a.C, P, T, active);
+    if (tree ? a.mask == nullptr : cslot >= active) return;  // no tokens: no partial (the merge skips it)
+    const int nst = tree ? 1 : T / (A2_STEP * P);  // stages per part
+
+    // this lane's query row
+    const int r = rt * 16 + c16;
+    const bool rvalid = r < a.rows;
+    const int rr = rvalid ? r : 0;
+    const int hq = kh * a.groups + rr / a.S, sq = rr % a.S;
+    const uint32_t rmask = (tree && rvalid) ? uint32_t(a.mask[sq]) : 0u;
+
+    // the part's tokens and sources (element strides)
+    int t_begin, t_end;
+    const uint16_t *kb, *vb;
+    int64_t ks, vs;
+    if (tree) {
+        t_begin = 0;
+        t_end = part == 0 ? a.S : 0;
+        kb = a.xk + kh * a.xh;
+        vb = a.xv + kh * a.vh;
+        ks = a.xs;
+        vs = a.vs;
+    } else {
+        t_begin = cslot * T + part * (T / P);
+        t_end = min(L, t_begin + T / P);
+        kb = a.key + int64_t(kh) * a.cap * D;
+        vb = a.value + int64_t(kh) * a.cap * D;
+        ks = vs = D;
+    }
+    const int t_last = t_end > t_begin ? t_end - 1 : (tree ? 0 : min(t_begin, L - 1));
+    const int t_clamp = t_last < 0 ? 0 : t_last;  // a token every load may read (in bounds)
+
+    u32x4 qf[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+        qf[kk] = rvalid ? ld16(a.q + hq * a.qh + sq * a.qs + 32 * kk + 8 * g) : u32x4{0, 0, 0, 0};
+
+    unsigned char* ring = smem + part * NS * 2 * STAGE;
+    // stage s of this part into ring slot s % NS: the wave's PER KiB of K and of V (lane -> LDS byte
+    // o = 1024 j' + 16 lane, token o / RB, stored unit (o % RB) / 16 holding unit ^ (token & SW)); byte
+    // offsets fit 32 bits (cap * D * 2 < 2^31)
+    const unsigned char* kbase = reinterpret_cast<const unsigned char*>(kb);
+    const unsigned char* vbase = reinterpret_cast<const unsigned char*>(vb);
+    const int ksb = int(ks) * 2, vsb = int(vs) * 2;
+    int jt[PER], ju[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int o = (rt * PER + j) * 1024 + lane * 16;
+        jt[j] = o / RB;
+        ju[j] = (((o % RB) / 16) ^ (jt[j] & SW)) * 16;
+    }
+    auto issue = [&](int s) {
+        unsigned char* kd = ring + (s % NS) * 2 * STAGE;
+        const int t0 = t_begin + s * A2_STEP;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int o0 = (rt * PER + j) * 1024;
+            const int tok = min(t0 + jt[j], t_clamp);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kbase + (tok * ksb + ju[j])),
+                                             (__attribute__((address_space(3))) void*)(kd + o0), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vbase + (tok * vsb + ju[j])),
+                                             (__attribute__((address_space(3))) void*)(kd + STAGE + o0), 16, 0, 0);
+        }
+    };
+
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+    for (int s = 0; s < nst; ++s) {
+        // stage s landed (this wave's share), then everyone's share and everyone done with stage s - 1
+        if (s + NS - 2 < nst) {
+            __builtin_amdgcn_s_waitcnt(((((NS - 2) * 2 * PER) & 15)) | ((((NS - 2) * 2 * PER) >> 4) << 14) | (7 << 4) | (15 << 8));
+        } else {
+            __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the ring's tail
+        }
+        // s_barrier alone: __syncthreads' release fence would wait for the whole ring (vmcnt(0))
+        __builtin_amdgcn_s_barrier();
+        if (s + NS - 1 < nst) issue(s + NS - 1);
+        const unsigned char* kd = ring + (s % NS) * 2 * STAGE;
+        const unsigned char* vd = kd + STAGE;
+        const int t0 = t_begin + s * A2_STEP;
+        // the S^T operands of the stage (16 tokens x one 16-byte unit per lane), all issued before the
+        // first use
+        u32x4 kf[2][KK];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 16 * tt + c16;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk)
+                kf[tt][kk] = *reinterpret_cast<const u32x4*>(kd + t * RB + (((4 * kk + g) ^ (t & SW)) * 16));
+        }
+        f32x4 st[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            st[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk)
+                st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[tt][kk]), as_bf16x8(qf[kk]), st[tt], 0, 0, 0);
+        }
+        // the stage's admitted tokens (bit j: token t0 + j); whole stages of the prefix skip the mask
+        const int nvalid = t_end - t0;
+        uint32_t mbits = nvalid >= 32 ? ~0u : (nvalid > 0 ? (1u << nvalid) - 1u : 0u);
+        if (tree) mbits &= rmask;
+        float z[2][4], mx = -INFINITY;
+        if (__builtin_amdgcn_ballot_w64(mbits != ~0u) == 0) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    z[tt][i] = st[tt][i] * a.zscale;
+                    mx = fmaxf(mx, z[tt][i]);
+                }
+        } else {
+            const uint32_t lb = mbits >> (4 * g);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    z[tt][i] = ((lb >> (16 * tt + i)) & 1u) ? st[tt][i] * a.zscale : -INFINITY;
+                    mx = fmaxf(mx, z[tt][i]);
+                }
+        }
+        mx = max_x32(max_x16(mx));
+        const float mnew = fmaxf(m, mx);
+        // v_exp_f32 directly (2^-inf = 0; a result below 2^-126 flushes to 0, far inside the bound);
+        // a row with nothing admitted yet subtracts 0, so -inf - -inf never forms
+        const float msub = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m - msub);
+        float p[2][4], ps = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                p[tt][i] = __builtin_amdgcn_exp2f(z[tt][i] - msub);
+                p[tt][i + 1] = __builtin_amdgcn_exp2f(z[tt][i + 1] - msub);
+                bfround2(p[tt][i], p[tt][i + 1]);
+                ps += p[tt][i];
+                ps += p[tt][i + 1];
+            }
+        ps = sum_x32(sum_x16(ps));
+        l = l * alpha + ps;
+        m = mnew;
+        // O^T is rescaled only when some row's maximum moved (x * 1 == x: skipping changes no bit)
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        }
+        // p holds bf16 values: their top halves are the MFMA operand
+        auto top2 = [](float lo, float hi) { return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u); };
+        const u32x4 pf = {top2(p[0][0], p[0][1]), top2(p[0][2], p[0][3]), top2(p[1][0], p[1][1]), top2(p[1][2], p[1][3])};
+        // V^T operands by transposing reads: lane s of group g points at token 4 g + s / 4 (+ 16 for the
+        // second read), dims 16 dt + 4 (s % 4) .. + 3, so lane (dim 16 dt + c16, g) receives the 8 tokens
+        // of its k-slots (4 g .. 4 g + 3, then 16 + 4 g ..), the order its S^T accumulators give P^T
+        u32x2 va[DT], vb2[DT];
+        {
+            const int tv0 = 4 * g + (c16 >> 2), tv1 = tv0 + 16;
+            const int sub = (c16 & 3) >> 1, half = (c16 & 1) * 8;
+            uint32_t a0[DT], a1[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a0[dt] = lds_addr(vd + tv0 * RB + (((2 * dt + sub) ^ (tv0 & SW)) * 16) + half);
+                a1[dt] = lds_addr(vd + tv1 * RB + (((2 * dt + sub) ^ (tv1 & SW)) * 16) + half);
+            }
+            ds_read_tr16_n<DT>(va, a0);
+            ds_read_tr16_n<DT>(vb2, a1);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const u32x4 vf = {va[dt].x, va[dt].y, vb2[dt].x, vb2[dt].y};
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vf), as_bf16x8(pf), acc[dt], 0, 0, 0);
+        }
+    }
+
+    // the work-group's partial per row tile: (m, l, O) of its rows; P parts merge through LDS first
+    float* rec = a.part + (int64_t(kh * a.RT + rt) * (a.C + 1) + cslot) * (32 + 16 * D);
+    if (P == 1) {
+        if (rt >= a.RT) return;
+        if (g == 0) {
+            rec[c16] = m;
+            rec[16 + c16] = l;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(rec + 32 + c16 * D + 16 * dt + 4 * g) = acc[dt];
+        return;
+    }
+    __syncthreads();  // the ring is free
+    constexpr int WREG = (32 + 16 * D) * 4;
+    float* wr = reinterpret_cast<float*>(smem + w * WREG);
+    if (g == 0) {
+        wr[c16] = m;
+        wr[16 + c16] = l;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(wr + 32 + c16 * D + 16 * dt + 4 * g) = acc[dt];
+    __syncthreads();
+    // the row tile's P waves (w = rt + RTW * p) merged in part order by the RTW * 64 threads of part 0
+    if (part != 0 || rt >= a.RT) return;
+    auto part_reg = [&](int p_) { return reinterpret_cast<const float*>(smem + (rt + RTW * p_) * WREG); };
+    float fw[P];
+    float M = -INFINITY;
+#pragma unroll
+    for (int p_ = 0; p_ < P; ++p_) M = fmaxf(M, part_reg(p_)[c16]);
+    float sl = 0.f;
+#pragma unroll
+    for (int p_ = 0; p_ < P; ++p_) {
+        const float mv = part_reg(p_)[c16];
+        fw[p_] = mv == -INFINITY ? 0.f : exp2f(mv - M);
+        sl += part_reg(p_)[16 + c16] * fw[p_];
+    }
+    if (g == 0) {
+        rec[c16] = M;
+        rec[16 + c16] = sl;
+    }
+    // lane (row c16, group g): dims 4g + 16 dt .. + 3 of its row
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p_ = 0; p_ < P; ++p_) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(part_reg(p_) + 32 + c16 * D + 16 * dt + 4 * g);
+            o += v * fw[p_];
+        }
+        *reinterpret_cast<f32x4*>(rec + 32 + c16 * D + 16 * dt + 4 * g) = o;
+    }
+}
+
 // Merge of the chunk partials and the tree partial: one work-group per (kv head, row tile, row), one
 // thread per output dim; the partials' weights are computed once in LDS, the O loads are independent.
 template <int D>
@@ -293,7 +592,10 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a) {
     int L = a.seqlen[0];
     L = L < 0 ? 0 : (L > a.cap ? a.cap : L);
     int tpw, active;
-    split(L, a.C, a.min_tpw, tpw, active);
+    if (a.p2)
+        split2(L, a.C, a.p2, tpw, active);
+    else
+        split(L, a.C, a.min_tpw, tpw, active);
     const bool use_tree = a.mask != nullptr;
     const int np = active + (use_tree ? 1 : 0);
     const float* base = a.part + int64_t(kh * a.RT + rt) * (a.C + 1) * (32 + 16 * D);
@@ -346,6 +648,24 @@ int target_units() {
     return v;
 }
 
+// the streaming form for head_dim 64 / 128 (its ring needs two stages per part; 256 does not fit),
+// unless MDX_ATTN_V1=1 (A/B sweeps only)
+bool use_stream(int D) {
+    static const int v1 = env_int("MDX_ATTN_V1", 0, 0, 1);
+    return !v1 && (D == 64 || D == 128);
+}
+int stream_rtw(int RT) { return RT <= 1 ? 1 : (RT == 2 ? 2 : 4); }
+// chunks per kv head of the streaming form: one work-group per (kv head, chunk) plus the tree
+// work-group within one round of 256, at least 32 tokens per part, at most 64 chunks (the merge)
+int plan_chunks2(int Hk, int RT, int cap, int hint) {
+    const int P = 4 / stream_rtw(RT);
+    int c = A2_MAX_WG / Hk - 1;
+    const int by_cap = (cap + A2_STEP * P - 1) / (A2_STEP * P);
+    c = c > by_cap ? by_cap : c;
+    if (hint > 0 && c > hint) c = hint;
+    return c < 1 ? 1 : (c > 64 ? 64 : c);
+}
+
 int plan_chunks(int Hk, int RT, int cap, int hint) {
     if (hint > 0) return hint > 64 ? 64 : hint;
     const int tpw = min_tpw_default();
@@ -359,8 +679,25 @@ size_t workspace_bytes(int Hk, int RT, int C, int D) {
     return 256 + size_t(Hk) * RT * (C + 1) * (32 + 16 * size_t(D)) * sizeof(float);
 }
 
+template <int D, int RTW>
+int launch2(const AttnArgs& a, hipStream_t st) {
+    allow_smem(reinterpret_cast<const void*>(&attn2_kernel<D, RTW>), A2_RING);
+    hipLaunchKernelGGL((attn2_kernel<D, RTW>), dim3(a.Hk * (a.C + 1)), dim3(256), A2_RING, st, a);
+    MDX_LAUNCHED();
+    hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.Hk * a.RT * 16), dim3(D), 0, st, a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
 template <int D>
 int launch(const AttnArgs& a, hipStream_t st) {
+    if (a.p2) {
+        if constexpr (D == 64 || D == 128) {
+            if (a.p2 == 4) return launch2<D, 1>(a, st);
+            if (a.p2 == 2) return launch2<D, 2>(a, st);
+            return launch2<D, 4>(a, st);
+        }
+    }
     constexpr bool PP = D <= 128;  // register ping-pong fits below 256 VGPRs up to head_dim 128
     const int units = a.Hk * (a.C + 1);
     const int grid = (units + 7) / 8 * 8 * a.RT;
@@ -381,7 +718,9 @@ using namespace mdx;
 extern "C" size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint) {
     if (Hk <= 0 || H % Hk != 0 || S <= 0) return 0;
     const int RT = int((H / Hk * S + 15) / 16);
-    return workspace_bytes(int(Hk), RT, plan_chunks(int(Hk), RT, int(cap), int(chunks_hint)), int(D));
+    const int C = use_stream(int(D)) ? plan_chunks2(int(Hk), RT, int(cap), int(chunks_hint))
+                                     : plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
+    return workspace_bytes(int(Hk), RT, C, int(D));
 }
 
 extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
@@ -401,7 +740,9 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
                   xk_row_stride % 8 == 0 && xv_head_stride % 8 == 0 && xv_row_stride % 8 == 0,
               "16-byte aligned rows");
     const int RT = int((H / Hk * S + 15) / 16);
-    const int C = plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
+    const bool v2 = use_stream(int(D));
+    const int C = v2 ? plan_chunks2(int(Hk), RT, int(cap), int(chunks_hint))
+                     : plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
     MDX_CHECK(workspace && aligned(workspace, 256) && workspace_bytes_ >= workspace_bytes(int(Hk), RT, C, int(D)),
               "workspace: %zu bytes, 256-byte aligned, zeroed once", workspace_bytes(int(Hk), RT, C, int(D)));
     AttnArgs a{};
@@ -429,6 +770,7 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.RT = RT;
     a.C = C;
     a.min_tpw = chunks_hint > 0 ? AT_STEP : min_tpw_default();
+    a.p2 = v2 ? 4 / stream_rtw(RT) : 0;
     a.zscale = float(1.0 / sqrt(double(D)) * 1.4426950408889634);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (D == 64) return launch<64>(a, st);

@@ -66,7 +66,12 @@ def test_attn_hybrid_verify_16_rows(C, dev, L):
 
 
 @pytest.mark.parametrize("H,Hk,D,L,parents", [(8, 8, 64, 300, [-1, 0, 1]), (32, 8, 128, 4000, None),
-                                              (4, 1, 128, 0, [-1, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 6, 7, 7])])
+                                              (4, 1, 128, 0, [-1, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 6, 7, 7]),
+                                              (12, 1, 64, 700, [-1, 0, 1, 2]),
+                                              (16, 8, 64, 2000, [-1, 0, 1, 1, 2, 2, 3, 3]),
+                                              (32, 4, 128, 5000, [-1, 0, 1, 2]),
+                                              (32, 8, 128, 1, [-1, 0, 1, 2, 3, 4, 5, 6]),
+                                              (64, 8, 64, 9000, [-1, 0])])
 def test_attn_other_shapes(C, dev, H, Hk, D, L, parents):
     _case(C, dev, H, Hk, D, L, max(L, 1) + 64, parents, 7 + L)
 
