@@ -434,8 +434,10 @@ def bench_attn(args, dev):
                  "synthetic (seeded N(0,1) KV cache and rows)",
                  {"workload": f"tree-verify decode attention, 32q/8kv heads, head_dim 128, 16 rows, ctx={L}, "
                               f"{ring_n}-copy KV ring", "ctx": L, "rows": S, "algorithmic_bytes_per_step": per},
-                 {"bound": "hbm", "kernel": "attn_kernel", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
-                  "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                 {"bound": "hbm", "kernel": "attn2_kernel + attn_merge_kernel", "achieved": round(gbs, 2),
+                  "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                  # fetched and written bytes of both launches per call (the partials included)
+                  "traffic": pmc_traffic(f"attn_tree16_ctx{L}"),
                   "avg_launch_us": round(t * 1e6, 3),
                   # S^T = K Q^T and O^T = V^T P^T on bf16 MFMA: 4 H S L D flops per call against the dense peak
                   "mfma_util": round(4 * H * S * L * D / t / PEAK_BF16_FLOPS, 4)})
