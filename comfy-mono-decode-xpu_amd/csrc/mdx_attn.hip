@@ -299,32 +299,67 @@ constexpr int A2_STEP = 32;
 constexpr int A2_RING = 128 * 1024;  // K/V ring bytes per work-group
 constexpr int A2_MAX_WG = 256;
 
-// ds_read_b64_tr_b16 (gfx950) as inline asm: in each 16-lane group, lane i receives element i % 4 of
-// the 8-byte runs that lanes i / 4 + 4 j (j = 0..3) point at. The builtin form makes the compiler wait
-// for every outstanding direct-to-LDS load (vmcnt(0)) before it, which would drain the ring each stage;
-// here N reads and their lgkmcnt(0) wait form one asm statement, so the results exist (for the
-// compiler) only after the wait. Addresses are LDS byte addresses.
-template <int N>
-__device__ __forceinline__ void ds_read_tr16_n(u32x2 (&r)[N], const uint32_t (&addr)[N]) {
-    static_assert(N == 4 || N == 8, "4 or 8 reads");
-    if constexpr (N == 4) {
-        asm volatile(
-            "ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %5\n\tds_read_b64_tr_b16 %2, %6\n\t"
-            "ds_read_b64_tr_b16 %3, %7\n\ts_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]));
-    } else {
-        asm volatile(
-            "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %9\n\tds_read_b64_tr_b16 %2, %10\n\t"
-            "ds_read_b64_tr_b16 %3, %11\n\tds_read_b64_tr_b16 %4, %12\n\tds_read_b64_tr_b16 %5, %13\n\t"
-            "ds_read_b64_tr_b16 %6, %14\n\tds_read_b64_tr_b16 %7, %15\n\ts_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
-              "v"(addr[7]));
-    }
-}
+// LDS layout of a ring stage (32 tokens; no swizzle: every read below covers contiguous bytes)
+//   K: [kk < D/32][token 32][g 4][16 B]  -- unit 4 kk + g of each token row; the S^T operand of
+//      (16-token tile tt, kk) is one contiguous KiB: lane (c16, g) at kk * 2048 + (16 tt + c16) * 64 + g * 16
+//   V: [dt < D/16][token 32][2][16 B]    -- dims 16 dt .. 16 dt + 15 of each token row; a transposing
+//      read of (dt, tokens 16 h ..) is 512 contiguous bytes at dt * 1024 + h * 512
+// so one base address per lane and immediate offsets reach every operand of the stage. The reads are
+// inline asm: the builtins make the compiler wait for every outstanding direct-to-LDS load (vmcnt(0))
+// before them, which would drain the ring each stage. Each asm statement ends with its lgkmcnt(0)
+// wait, so its results exist (for the compiler) only after the wait. ds_read_b64_tr_b16 (gfx950): in
+// each 16-lane group, lane i receives element i % 4 of the 8-byte runs that lanes i / 4 + 4 j point
+// at (j = 0..3).
 __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const unsigned char*)p));
+}
+template <int D>
+__device__ __forceinline__ void stage_k(u32x4 (&kf)[2][D / 32], uint32_t base) {
+    if constexpr (D == 128) {
+        asm volatile(
+            "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:2048\n\tds_read_b128 %2, %8 offset:4096\n\t"
+            "ds_read_b128 %3, %8 offset:6144\n\tds_read_b128 %4, %8 offset:1024\n\tds_read_b128 %5, %8 offset:3072\n\t"
+            "ds_read_b128 %6, %8 offset:5120\n\tds_read_b128 %7, %8 offset:7168\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(kf[0][0]), "=&v"(kf[0][1]), "=&v"(kf[0][2]), "=&v"(kf[0][3]), "=&v"(kf[1][0]), "=&v"(kf[1][1]),
+              "=&v"(kf[1][2]), "=&v"(kf[1][3])
+            : "v"(base));
+    } else {
+        static_assert(D == 64, "head_dim 64 or 128");
+        asm volatile(
+            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:2048\n\tds_read_b128 %2, %4 offset:1024\n\t"
+            "ds_read_b128 %3, %4 offset:3072\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(kf[0][0]), "=&v"(kf[0][1]), "=&v"(kf[1][0]), "=&v"(kf[1][1])
+            : "v"(base));
+    }
+}
+template <int D>
+__device__ __forceinline__ void stage_v(u32x2 (&va)[D / 16], u32x2 (&vb)[D / 16], uint32_t base) {
+    if constexpr (D == 128) {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %16\n\tds_read_b64_tr_b16 %1, %16 offset:1024\n\t"
+            "ds_read_b64_tr_b16 %2, %16 offset:2048\n\tds_read_b64_tr_b16 %3, %16 offset:3072\n\t"
+            "ds_read_b64_tr_b16 %4, %16 offset:4096\n\tds_read_b64_tr_b16 %5, %16 offset:5120\n\t"
+            "ds_read_b64_tr_b16 %6, %16 offset:6144\n\tds_read_b64_tr_b16 %7, %16 offset:7168\n\t"
+            "ds_read_b64_tr_b16 %8, %16 offset:512\n\tds_read_b64_tr_b16 %9, %16 offset:1536\n\t"
+            "ds_read_b64_tr_b16 %10, %16 offset:2560\n\tds_read_b64_tr_b16 %11, %16 offset:3584\n\t"
+            "ds_read_b64_tr_b16 %12, %16 offset:4608\n\tds_read_b64_tr_b16 %13, %16 offset:5632\n\t"
+            "ds_read_b64_tr_b16 %14, %16 offset:6656\n\tds_read_b64_tr_b16 %15, %16 offset:7680\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(va[0]), "=&v"(va[1]), "=&v"(va[2]), "=&v"(va[3]), "=&v"(va[4]), "=&v"(va[5]), "=&v"(va[6]),
+              "=&v"(va[7]), "=&v"(vb[0]), "=&v"(vb[1]), "=&v"(vb[2]), "=&v"(vb[3]), "=&v"(vb[4]), "=&v"(vb[5]),
+              "=&v"(vb[6]), "=&v"(vb[7])
+            : "v"(base));
+    } else {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %8 offset:1024\n\t"
+            "ds_read_b64_tr_b16 %2, %8 offset:2048\n\tds_read_b64_tr_b16 %3, %8 offset:3072\n\t"
+            "ds_read_b64_tr_b16 %4, %8 offset:512\n\tds_read_b64_tr_b16 %5, %8 offset:1536\n\t"
+            "ds_read_b64_tr_b16 %6, %8 offset:2560\n\tds_read_b64_tr_b16 %7, %8 offset:3584\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(va[0]), "=&v"(va[1]), "=&v"(va[2]), "=&v"(va[3]), "=&v"(vb[0]), "=&v"(vb[1]), "=&v"(vb[2]),
+              "=&v"(vb[3])
+            : "v"(base));
+    }
 }
 
 // chunk length (tokens, a multiple of 32 P) and active chunk count for context L over C chunks
@@ -339,7 +374,6 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
     constexpr int P = 4 / RTW;
     constexpr int KK = D / 32, DT = D / 16;
     constexpr int RB = 2 * D;                    // bytes per token row
-    constexpr int SW = D / 8 < 16 ? D / 8 - 1 : 15;  // swizzle mask of the 16-byte units
     constexpr int STAGE = A2_STEP * RB;          // bytes of K (or V) per stage
     constexpr int NS = A2_RING / (2 * STAGE * P);  // ring stages per part
     constexpr int PER = STAGE / 1024 / RTW;      // DMA instructions per wave, stage and matrix
@@ -390,18 +424,21 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
         qf[kk] = rvalid ? ld16(a.q + hq * a.qh + sq * a.qs + 32 * kk + 8 * g) : u32x4{0, 0, 0, 0};
 
     unsigned char* ring = smem + part * NS * 2 * STAGE;
-    // stage s of this part into ring slot s % NS: the wave's PER KiB of K and of V (lane -> LDS byte
-    // o = 1024 j' + 16 lane, token o / RB, stored unit (o % RB) / 16 holding unit ^ (token & SW)); byte
-    // offsets fit 32 bits (cap * D * 2 < 2^31)
+    // stage s of this part into ring slot s % NS: the wave's PER instructions of K and of V (instruction
+    // i of a matrix writes LDS bytes [1024 i, 1024 i + 1024) of the stage's block in the layouts above;
+    // lane -> (token within the stage, byte offset within the token row)). Byte offsets fit 32 bits
+    // (cap * D * 2 < 2^31).
     const unsigned char* kbase = reinterpret_cast<const unsigned char*>(kb);
     const unsigned char* vbase = reinterpret_cast<const unsigned char*>(vb);
     const int ksb = int(ks) * 2, vsb = int(vs) * 2;
-    int jt[PER], ju[PER];
+    int ktok[PER], kofs[PER], vtok[PER], vofs[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-        const int o = (rt * PER + j) * 1024 + lane * 16;
-        jt[j] = o / RB;
-        ju[j] = (((o % RB) / 16) ^ (jt[j] & SW)) * 16;
+        const int i = rt * PER + j;
+        ktok[j] = 16 * (i & 1) + (lane >> 2);
+        kofs[j] = (4 * (i >> 1) + (lane & 3)) * 16;
+        vtok[j] = lane >> 1;
+        vofs[j] = (2 * i + (lane & 1)) * 16;
     }
     auto issue = [&](int s) {
         unsigned char* kd = ring + (s % NS) * 2 * STAGE;
@@ -409,10 +446,10 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int o0 = (rt * PER + j) * 1024;
-            const int tok = min(t0 + jt[j], t_clamp);
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kbase + (tok * ksb + ju[j])),
+            const int tk = min(t0 + ktok[j], t_clamp), tv = min(t0 + vtok[j], t_clamp);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kbase + (tk * ksb + kofs[j])),
                                              (__attribute__((address_space(3))) void*)(kd + o0), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vbase + (tok * vsb + ju[j])),
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vbase + (tv * vsb + vofs[j])),
                                              (__attribute__((address_space(3))) void*)(kd + STAGE + o0), 16, 0, 0);
         }
     };
@@ -436,16 +473,9 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
         const unsigned char* kd = ring + (s % NS) * 2 * STAGE;
         const unsigned char* vd = kd + STAGE;
         const int t0 = t_begin + s * A2_STEP;
-        // the S^T operands of the stage (16 tokens x one 16-byte unit per lane), all issued before the
-        // first use
+        // the S^T operands of the stage: lane (token 16 tt + c16, k-group g) reads unit 4 kk + g
         u32x4 kf[2][KK];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int t = 16 * tt + c16;
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk)
-                kf[tt][kk] = *reinterpret_cast<const u32x4*>(kd + t * RB + (((4 * kk + g) ^ (t & SW)) * 16));
-        }
+        stage_k<D>(kf, lds_addr(kd) + c16 * 64 + g * 16);
         f32x4 st[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -454,6 +484,11 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
             for (int kk = 0; kk < KK; ++kk)
                 st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[tt][kk]), as_bf16x8(qf[kk]), st[tt], 0, 0, 0);
         }
+        // V^T operands by transposing reads (issued while the S^T MFMAs run): lane s of group g points at token 4 g + s / 4 (+ 16 for the
+        // second read), dims 16 dt + 4 (s % 4) .. + 3, so lane (dim 16 dt + c16, g) receives the 8 tokens
+        // of its k-slots (4 g .. 4 g + 3, then 16 + 4 g ..), the order its S^T accumulators give P^T
+        u32x2 va[DT], vb2[DT];
+        stage_v<D>(va, vb2, lds_addr(vd) + (4 * g + (c16 >> 2)) * 32 + (c16 & 3) * 8);
         // the stage's admitted tokens (bit j: token t0 + j); whole stages of the prefix skip the mask
         const int nvalid = t_end - t0;
         uint32_t mbits = nvalid >= 32 ? ~0u : (nvalid > 0 ? (1u << nvalid) - 1u : 0u);
@@ -505,22 +540,6 @@ __global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
         // p holds bf16 values: their top halves are the MFMA operand
         auto top2 = [](float lo, float hi) { return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u); };
         const u32x4 pf = {top2(p[0][0], p[0][1]), top2(p[0][2], p[0][3]), top2(p[1][0], p[1][1]), top2(p[1][2], p[1][3])};
-        // V^T operands by transposing reads: lane s of group g points at token 4 g + s / 4 (+ 16 for the
-        // second read), dims 16 dt + 4 (s % 4) .. + 3, so lane (dim 16 dt + c16, g) receives the 8 tokens
-        // of its k-slots (4 g .. 4 g + 3, then 16 + 4 g ..), the order its S^T accumulators give P^T
-        u32x2 va[DT], vb2[DT];
-        {
-            const int tv0 = 4 * g + (c16 >> 2), tv1 = tv0 + 16;
-            const int sub = (c16 & 3) >> 1, half = (c16 & 1) * 8;
-            uint32_t a0[DT], a1[DT];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a0[dt] = lds_addr(vd + tv0 * RB + (((2 * dt + sub) ^ (tv0 & SW)) * 16) + half);
-                a1[dt] = lds_addr(vd + tv1 * RB + (((2 * dt + sub) ^ (tv1 & SW)) * 16) + half);
-            }
-            ds_read_tr16_n<DT>(va, a0);
-            ds_read_tr16_n<DT>(vb2, a1);
-        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             const u32x4 vf = {va[dt].x, va[dt].y, vb2[dt].x, vb2[dt].y};
