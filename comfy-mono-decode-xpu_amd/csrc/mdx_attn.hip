@@ -8,21 +8,24 @@
 // as the reference's own kernel is not bit-identical to the chain it replaces.
 //
 // Query rows of kv head kh: r = (h % groups) * S + s for the heads h of that kv head, 16 rows per
-// row tile (rt). Work-group = (kv head, row tile, chunk) of 4 waves; each wave owns a quarter of the
-// chunk's tokens and runs, per 32-token step:
-//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = 16 K rows (tokens) x 32 dims from HBM, B = Q^T held in
+// row tile (rt). Both forms below compute, per 32-token step of a query row tile:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = 16 K rows (tokens) x 32 dims, B = Q^T held in
 //                 registers; the accumulator gives each lane 4 tokens of one query row (lane % 16), so
 //                 the online softmax state of a row lives in its lanes;
-//   O^T += V^T P^T   A = V^T from LDS (the wave transposes its 32 x D V tile into [dim][token] order,
-//                 tokens permuted so a lane's 8 k-slots are the 8 tokens its S^T accumulators hold),
+//   O^T += V^T P^T   A = V^T, its 8 k-slots per lane in the token order the S^T accumulators hold,
 //                 B = bf16(P^T) straight from the S^T registers -- no shuffle of P.
-// Each wave prefetches its next step's K and V into a second register set while the current step
-// computes (head_dim <= 128). The 4 waves merge in LDS; the work-group's partial (m, l, O) goes to
-// the workspace; attn_merge_kernel (one work-group per query row, one thread per dim) combines the
-// chunks and the tree-row partial and writes bf16. The context split is recomputed on the device
-// from seqlen in both kernels, so a captured graph replays for any context length.
-// Work-group ids are laid out so the row tiles of one (kv head, chunk) share an XCD (ids are dealt
-// round-robin over the 8 XCDs): the 4x re-read of a K/V chunk hits that XCD's L2.
+// Each work-group stores a chunk partial (m, l, O in fp32); attn_merge_kernel (one work-group per
+// query row, one thread per dim) combines the chunks and the tree-row partial and writes bf16. The
+// context split is recomputed on the device from seqlen in both launches, so a captured graph
+// replays for any context length.
+//
+// The streaming form (attn2_kernel, head_dim 64 / 128): one work-group per (kv head, chunk) over all
+// of the kv head's row tiles, K/V read once from HBM into an LDS ring (see the layout note at
+// stage_k). The register form (attn_kernel, head_dim 256): work-group = (kv head, row tile, chunk) of
+// 4 waves, each owning a quarter of the chunk; K rows straight from HBM as the A operand, V transposed
+// into LDS per wave, the next step's K and V prefetched into a second register set (head_dim <= 128);
+// work-group ids dealt so that the row tiles of one (kv head, chunk) share an XCD and re-read the
+// chunk from its L2.
 #include <math.h>
 #include <stdlib.h>
 
@@ -286,15 +289,14 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attn_kernel(AttnArgs a) {
 
 // ---- The streaming form (head_dim 64 and 128) ---------------------------------------------------
 // One work-group per (kv head, chunk): all of the kv head's query rows (up to 4 row tiles) in one
-// work-group, so each K/V byte leaves HBM once and is read from LDS by every row tile. Wave w owns
-// row tile w % RTW and token part w / RTW of the chunk (P = 4 / RTW parts). A part's K and V stream
-// through an LDS ring of 32-token stages by direct-to-LDS loads (1 KiB per wave instruction, every
-// stage of the ring in flight from the start); the 16-byte units of a token row are stored XOR-
-// swizzled by the token's low bits, so the S^T operand reads (16 tokens, one unit each) and the V^T
-// gathers (8 tokens per lane) hit distinct banks. Per stage a wave computes S^T = K Q^T from LDS
-// (v_mfma_f32_16x16x32_bf16), the online softmax in its lanes, and O^T += V^T P^T with V^T gathered
-// from the natural [token][dim] rows in the k-slot order its S^T accumulators give P^T. The grid is
-// at most 256 work-groups (one round on the chip's 256 CUs: the ring takes most of a CU's LDS).
+// work-group, so each K/V byte leaves HBM once and is read from LDS by every row tile. Wave w of NWV
+// owns row tile w % RTW and token part w / RTW of the chunk (P = NWV / RTW parts; eight waves, two per
+// SIMD, wherever each part still gets two ring stages). A part's K and V stream through its share of
+// a 128 KiB LDS ring of 32-token stages by direct-to-LDS loads (1 KiB per wave instruction, the ring's
+// stages in flight from the prologue). Per stage a wave reads its S^T and V^T operands from LDS in two
+// batches (layouts at stage_k), computes S^T = K Q^T, the online softmax in its lanes, and
+// O^T += V^T P^T; the P parts of a row tile merge in LDS. The grid is at most 256 work-groups (one
+// round on the chip's 256 CUs: the ring takes most of a CU's LDS).
 constexpr int A2_STEP = 32;
 constexpr int A2_RING = 128 * 1024;  // K/V ring bytes per work-group
 constexpr int A2_MAX_WG = 256;
@@ -369,9 +371,9 @@ __device__ __forceinline__ void split2(int L, int C, int P, int& T, int& active)
     active = L > 0 ? (L + T - 1) / T : 0;
 }
 
-template <int D, int RTW>
-__global__ __launch_bounds__(256) void attn2_kernel(AttnArgs a) {
-    constexpr int P = 4 / RTW;
+template <int D, int RTW, int NWV>
+__global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
+    constexpr int P = NWV / RTW;
     constexpr int KK = D / 32, DT = D / 16;
     constexpr int RB = 2 * D;                    // bytes per token row
     constexpr int STAGE = A2_STEP * RB;          // bytes of K (or V) per stage
@@ -674,10 +676,18 @@ bool use_stream(int D) {
     return !v1 && (D == 64 || D == 128);
 }
 int stream_rtw(int RT) { return RT <= 1 ? 1 : (RT == 2 ? 2 : 4); }
+// token parts per chunk: eight waves per work-group (two per SIMD, so one wave's LDS and MFMA waits
+// overlap the other's work) where each part still gets two ring stages, else four waves (head_dim 128
+// with one row tile)
+int stream_parts(int D, int RT) {
+    const int rtw = stream_rtw(RT);
+    if (D == 128) return rtw == 4 ? 2 : 4;
+    return 8 / rtw;
+}
 // chunks per kv head of the streaming form: one work-group per (kv head, chunk) plus the tree
 // work-group within one round of 256, at least 32 tokens per part, at most 64 chunks (the merge)
-int plan_chunks2(int Hk, int RT, int cap, int hint) {
-    const int P = 4 / stream_rtw(RT);
+int plan_chunks2(int Hk, int RT, int D, int cap, int hint) {
+    const int P = stream_parts(D, RT);
     int c = A2_MAX_WG / Hk - 1;
     const int by_cap = (cap + A2_STEP * P - 1) / (A2_STEP * P);
     c = c > by_cap ? by_cap : c;
@@ -698,10 +708,10 @@ size_t workspace_bytes(int Hk, int RT, int C, int D) {
     return 256 + size_t(Hk) * RT * (C + 1) * (32 + 16 * size_t(D)) * sizeof(float);
 }
 
-template <int D, int RTW>
+template <int D, int RTW, int NWV>
 int launch2(const AttnArgs& a, hipStream_t st) {
-    allow_smem(reinterpret_cast<const void*>(&attn2_kernel<D, RTW>), A2_RING);
-    hipLaunchKernelGGL((attn2_kernel<D, RTW>), dim3(a.Hk * (a.C + 1)), dim3(256), A2_RING, st, a);
+    allow_smem(reinterpret_cast<const void*>(&attn2_kernel<D, RTW, NWV>), A2_RING);
+    hipLaunchKernelGGL((attn2_kernel<D, RTW, NWV>), dim3(a.Hk * (a.C + 1)), dim3(64 * NWV), A2_RING, st, a);
     MDX_LAUNCHED();
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.Hk * a.RT * 16), dim3(D), 0, st, a);
     MDX_LAUNCHED();
@@ -712,9 +722,10 @@ template <int D>
 int launch(const AttnArgs& a, hipStream_t st) {
     if (a.p2) {
         if constexpr (D == 64 || D == 128) {
-            if (a.p2 == 4) return launch2<D, 1>(a, st);
-            if (a.p2 == 2) return launch2<D, 2>(a, st);
-            return launch2<D, 4>(a, st);
+            const int rtw = stream_rtw(a.RT);
+            if (rtw == 1) return launch2<D, 1, (D == 128 ? 4 : 8)>(a, st);
+            if (rtw == 2) return launch2<D, 2, 8>(a, st);
+            return launch2<D, 4, 8>(a, st);
         }
     }
     constexpr bool PP = D <= 128;  // register ping-pong fits below 256 VGPRs up to head_dim 128
@@ -737,7 +748,7 @@ using namespace mdx;
 extern "C" size_t mdx_attn_workspace(int64_t H, int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint) {
     if (Hk <= 0 || H % Hk != 0 || S <= 0) return 0;
     const int RT = int((H / Hk * S + 15) / 16);
-    const int C = use_stream(int(D)) ? plan_chunks2(int(Hk), RT, int(cap), int(chunks_hint))
+    const int C = use_stream(int(D)) ? plan_chunks2(int(Hk), RT, int(D), int(cap), int(chunks_hint))
                                      : plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
     return workspace_bytes(int(Hk), RT, C, int(D));
 }
@@ -760,7 +771,7 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
               "16-byte aligned rows");
     const int RT = int((H / Hk * S + 15) / 16);
     const bool v2 = use_stream(int(D));
-    const int C = v2 ? plan_chunks2(int(Hk), RT, int(cap), int(chunks_hint))
+    const int C = v2 ? plan_chunks2(int(Hk), RT, int(D), int(cap), int(chunks_hint))
                      : plan_chunks(int(Hk), RT, int(cap), int(chunks_hint));
     MDX_CHECK(workspace && aligned(workspace, 256) && workspace_bytes_ >= workspace_bytes(int(Hk), RT, C, int(D)),
               "workspace: %zu bytes, 256-byte aligned, zeroed once", workspace_bytes(int(Hk), RT, C, int(D)));
@@ -789,7 +800,7 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     a.RT = RT;
     a.C = C;
     a.min_tpw = chunks_hint > 0 ? AT_STEP : min_tpw_default();
-    a.p2 = v2 ? 4 / stream_rtw(RT) : 0;
+    a.p2 = v2 ? stream_parts(int(D), RT) : 0;
     a.zscale = float(1.0 / sqrt(double(D)) * 1.4426950408889634);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (D == 64) return launch<64>(a, st);
