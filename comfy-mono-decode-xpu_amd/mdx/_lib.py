@@ -12,7 +12,8 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmdx.so")
+# MDX_LIB: another build of the library to load (side-by-side A/B timing of two builds in one run)
+LIB_PATH = os.environ.get("MDX_LIB") or os.path.join(HERE, "libmdx.so")
 
 MDX_OK, MDX_EINVAL, MDX_EHIP = 0, 1, 2
 DT_F32, DT_F16, DT_FP8E4M3, DT_BF16 = 0, 1, 2, 3
