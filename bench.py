@@ -786,6 +786,22 @@ def main():
                                              "workload": d3["config"]["workload"] + ", predictable synthetic weights"}
         if "_cpu_mlp_s" in res:
             res["decode"]["cpu_baseline"] = cpu_decode_estimate(res["_cpu_mlp_s"], mlp_bytes(1))
+        # the other configurations' units, each timed by its own workload (weights and caches in rings
+        # larger than twice the Infinity Cache): the 16-row full-attention layer at two context lengths,
+        # the GDN layer step at 1 and 8 rows
+        layers = {}
+        for key, fn, kw in (("attention_layer_16rows_ctx2048", bench_attn_layer, {"ctx": 2048}),
+                            ("attention_layer_16rows_ctx8192", bench_attn_layer, {"ctx": 8192}),
+                            ("gdn_layer_1row", bench_gdn_layer, {"rows": 1}),
+                            ("gdn_layer_8rows", bench_gdn_layer, {"rows": 8})):
+            lsub = argparse.Namespace(**vars(args))
+            lsub.steps, lsub.warmup = 200, 10
+            for k, v in kw.items():
+                setattr(lsub, k, v)
+            r = fn(lsub, dev)
+            layers[key] = {"value": r["value"], "unit": r["unit"], "us_per_step": round(r["ms_per_step"] * 1e3, 2),
+                           "frac_of_peak": round(r["value"] / PEAK_HBM_GBS, 4), "workload": r["config"]["workload"]}
+        res["layers"] = layers
     res.pop("_cpu_mlp_s", None)
     print(json.dumps(res), flush=True)
 
