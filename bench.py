@@ -777,6 +777,12 @@ def main():
         res["decode_one_stage_drafts"] = {"value": d2["value"], "unit": "tok/s", "ms_per_step": d2["config"]["ms_per_step"],
                                           "accepted_per_step": d2["config"]["accepted_per_step"],
                                           "workload": d2["config"]["workload"]}
+        # the same decode with the reference's own head format: an int8 ConvRot lm_head (W8A8) for the verify
+        # and the drafts' exact pick
+        d4 = bench_stack(sub, dev, tokens=512, two_stage=True, head="int8")
+        res["decode_int8_convrot_head"] = {"value": d4["value"], "unit": "tok/s", "ms_per_step": d4["config"]["ms_per_step"],
+                                           "accepted_per_step": d4["config"]["accepted_per_step"],
+                                           "workload": d4["config"]["workload"]}
         # the same decode on weights whose next token is predictable: the drafts are accepted, every step
         # commits len(widths) + 1 tokens (the same kernels on the same shapes)
         sub.predictable = True
