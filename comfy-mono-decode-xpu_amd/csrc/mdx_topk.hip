@@ -16,8 +16,8 @@
 //   3. the candidates are ranked by counting (position = number of larger candidates); the segment's
 //      top-k goes to the workspace as a descending, zero-padded list;
 //   4. the row's last work-group (device-scope counter, reset by that work-group) merges the nseg
-//      lists in two counting stages: each wave keeps the top k of a quarter of the lists, then the 4 k
-//      survivors are ranked among themselves.
+//      lists: theta2 = the k-th largest list head bounds the row's top k from below (k lists hold an
+//      entry >= theta2), and only the entries >= theta2 are ranked among themselves by counting.
 // The counting loops read LDS eight words per round trip (indices clamped, masked).
 // Ranks are never 0 (the radix key of a non-NaN value is nonzero, and a NaN's rank has a nonzero
 // gather word), so 0 marks an empty slot.
@@ -80,9 +80,9 @@ template <int ORD, bool XF32>
 __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
     extern __shared__ __align__(16) uint64_t sm[];
     uint64_t* tmax = sm;             // [256] thread maxima
-    uint64_t* cand = sm + TK_T;      // candidates (k * ceil(seg / 256)) or, in the merge, nseg * k lists
-    __shared__ uint64_t theta_s, am_s[TK_T / 64];
-    __shared__ unsigned ncand, last_s;
+    uint64_t* cand = sm + TK_T;      // candidates (k * ceil(seg / 256)) or, in the merge, nseg * k lists + their survivors
+    __shared__ uint64_t theta_s, theta2_s, am_s[TK_T / 64];
+    __shared__ unsigned ncand, last_s, nc2_s;
     const int t = threadIdx.x;
     const int row = blockIdx.x / a.nseg, sg = blockIdx.x % a.nseg;
     const int K = a.k;
@@ -191,27 +191,38 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
             if (t + TK_T * j < total) cand[t + TK_T * j] = lv[j];
     }
     __syncthreads();
-    // two-stage merge by counting: wave w ranks the entries of its quarter of the lists among that
-    // quarter (all lanes read the same LDS word at a time: broadcasts, no dependent chains) and keeps
-    // its top K; then every thread ranks the 4 K survivors among themselves
-    uint64_t* wtop = cand + total;  // [4][K]
-    {
-        const int w = t >> 6, lane = t & 63;
-        const int l0 = w * a.nseg / 4, l1 = (w + 1) * a.nseg / 4;
-        const int e0 = l0 * K, e1 = l1 * K;
-        for (int j = lane; j < K; j += 64) wtop[w * K + j] = 0;
-        __builtin_amdgcn_wave_barrier();
-        for (int e = e0 + lane; e - lane < e1; e += 64) {
-            const uint64_t v = e < e1 ? cand[e] : 0;
-            const int above = count_above(cand, e0, e1, v);
-            if (v != 0 && above < K) wtop[w * K + above] = v;
+    // the merge: theta2 = the K-th largest list head (the lists are descending, so K lists hold an
+    // entry >= theta2 and every one of the row's top K is >= it), or 1 when at most K heads are nonzero;
+    // only the entries >= theta2 (typically little more than K) are ranked, by counting
+    const uint64_t hd = t < a.nseg ? cand[t * K] : 0;
+    if (t == 0) {
+        theta2_s = 1;
+        nc2_s = 0;
+    }
+    const int nzh = __syncthreads_count(hd != 0);
+    if (nzh > K && hd != 0) {
+        int above = 0;
+        for (int l0 = 0; l0 < a.nseg; l0 += 8) {  // eight heads per LDS round trip
+            uint64_t c[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) c[j] = cand[min(l0 + j, a.nseg - 1) * K];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) above += (l0 + j < a.nseg && c[j] > hd) ? 1 : 0;
         }
+        if (above == K - 1) theta2_s = hd;
     }
     __syncthreads();
-    for (int e = t; e < 4 * K; e += TK_T) {
-        const uint64_t v = wtop[e];
-        if (v == 0) continue;
-        const int pos = count_above(wtop, 0, 4 * K, v);
+    const uint64_t theta2 = theta2_s;
+    uint64_t* c2 = cand + total;  // [total]
+    for (int j = t; j < total; j += TK_T) {
+        const uint64_t v = cand[j];
+        if (v != 0 && v >= theta2) c2[atomicAdd(&nc2_s, 1u)] = v;
+    }
+    __syncthreads();
+    const int nc2 = int(nc2_s);
+    for (int e = t; e < nc2; e += TK_T) {
+        const uint64_t v = c2[e];
+        const int pos = count_above(c2, 0, nc2, v);
         if (pos < K) {
             const uint32_t idx = index_of<ORD>(v);
             a.indices[int64_t(row) * K + pos] = idx;
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(TK_T) void topk_kernel(TopkArgs a) {
 void plan(int64_t rows, int64_t n, int64_t k, int& nseg, int& seg) {
     int64_t s = std::max<int64_t>(1, std::min<int64_t>(TK_MAXSEG, 512 / rows));
     s = std::min<int64_t>(s, std::max<int64_t>(1, n / 1024));
-    s = std::min<int64_t>(s, std::max<int64_t>(4, 640 / k));  // the merge ranks <= 160 entries per wave
+    s = std::min<int64_t>(s, std::max<int64_t>(4, 640 / k));  // the merge holds the lists twice in LDS
     int64_t len = (n + s - 1) / s;
     len = (len + 63) / 64 * 64;
     nseg = int((n + len - 1) / len);
@@ -249,7 +260,7 @@ void plan(int64_t rows, int64_t n, int64_t k, int& nseg, int& seg) {
 
 size_t lds_bytes(int k, int nseg, int seg) {
     const size_t cand = size_t(k) * size_t((seg + TK_T - 1) / TK_T);
-    return (TK_T + std::max(cand, size_t(nseg) * k + 4 * size_t(k))) * sizeof(uint64_t);
+    return (TK_T + std::max(cand, 2 * size_t(nseg) * k)) * sizeof(uint64_t);
 }
 
 size_t workspace_bytes(int64_t rows) {
