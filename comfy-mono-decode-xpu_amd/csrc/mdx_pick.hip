@@ -21,8 +21,9 @@
 //      A-operand layout, then one wave runs the lm_head kernel's chain: v_mfma_f32_16x16x32_bf16 per
 //      32-k chunk over each K slice, the slices added in slice order), or the scores themselves;
 //   3. the work-group's top 8 by topk rank and its best argmax rank go to the workspace (coherent
-//      stores); the last work-group (device-scope counter, reset by it) ranks the 8 x PK_WG entries by
-//      counting and writes the outputs.
+//      stores); the last work-group (device-scope counter, reset by it) takes the nout-th largest list
+//      head as a floor, ranks the entries at or above it (at most 8 nout) by counting and writes the
+//      outputs.
 #include <algorithm>
 
 #include "mdx_common.hpp"
@@ -105,6 +106,57 @@ __device__ __forceinline__ int count_above(const uint64_t* buf, int n, uint64_t 
     return c;
 }
 
+// The bf16 lm_head kernel's MFMA chain over the candidate rows in LDS: chunk j's A operand at
+// w + j * WSTEP, its B operand (the activation) at x + 64 j, zero in the lanes of activation rows past the
+// first (zero_b). Each K slice (chunks [ks NC / KS, (ks + 1) NC / KS)) is one chain and the slices are
+// added in order. The chain runs in groups of 8 chunks: the next group's operand reads are issued before
+// this group's MFMAs (scheduling barriers keep the two apart), so the MFMAs wait on no LDS latency.
+template <int WSTEP>
+__device__ __forceinline__ f32x4 pick_chain(const uint8_t* w, const uint8_t* x, int NC, int KS, bool zero_b) {
+    constexpr int PD = 8;
+    auto mfma = [&](f32x4 acc, u32x4 wv, u32x4 xv) {
+        if (zero_b) xv = u32x4{0u, 0u, 0u, 0u};
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv), __builtin_bit_cast(bf16x8, xv), acc,
+                                                       0, 0, 0);
+    };
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) {
+        const int c0 = ks * NC / KS, c1 = (ks + 1) * NC / KS, cf = c0 + (c1 - c0) / PD * PD;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (cf > c0) {
+            u32x4 wv[PD], xv[PD];
+#pragma unroll
+            for (int i = 0; i < PD; ++i) {
+                wv[i] = *reinterpret_cast<const u32x4*>(w + (c0 + i) * WSTEP);
+                xv[i] = *reinterpret_cast<const u32x4*>(x + (c0 + i) * 64);
+            }
+            for (int j = c0; j < cf; j += PD) {
+                const int jn = j + PD < cf ? j + PD : j;  // the last group reads itself again (in bounds)
+                u32x4 wn[PD], xn[PD];
+#pragma unroll
+                for (int i = 0; i < PD; ++i) {
+                    wn[i] = *reinterpret_cast<const u32x4*>(w + (jn + i) * WSTEP);
+                    xn[i] = *reinterpret_cast<const u32x4*>(x + (jn + i) * 64);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < PD; ++i) acc = mfma(acc, wv[i], xv[i]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < PD; ++i) {
+                    wv[i] = wn[i];
+                    xv[i] = xn[i];
+                }
+            }
+        }
+        for (int j = cf; j < c1; ++j)
+            acc = mfma(acc, *reinterpret_cast<const u32x4*>(w + j * WSTEP), *reinterpret_cast<const u32x4*>(x + j * 64));
+        if (ks == 0) s = acc;
+        else s += acc;
+    }
+    return s;
+}
+
 __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
     extern __shared__ __align__(16) uint8_t rows_lds[];  // PICK_BF16: [K / 32][64 lanes][16 B] rows, then x [K]
     __shared__ uint64_t cand[PK_CAP];
@@ -115,7 +167,9 @@ __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
     __shared__ uint16_t logit[PK_MAXS];
     __shared__ uint64_t rk[PK_MAXS], ra[PK_MAXS];
     __shared__ uint64_t mlist[PK_WG * PK_MAXN + PK_WG];
-    __shared__ int is_last;
+    __shared__ uint64_t m2[PK_MAXN * PK_MAXN];
+    __shared__ uint64_t theta2;
+    __shared__ int is_last, nm2;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int w = blockIdx.x;
     const int64_t s0 = int64_t(w) * a.seg;
@@ -240,21 +294,9 @@ __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
         __syncthreads();
         if (wave == 0) {
             const int g = lane >> 4, c = lane & 15;
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
-            for (int ks = 0; ks < a.KS; ++ks) {
-                const int c0 = ks * NC / a.KS, c1 = (ks + 1) * NC / a.KS;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                for (int j = c0; j < c1; ++j) {
-                    const u32x4 wv = *reinterpret_cast<const u32x4*>(
-                        rowl ? rows_lds + size_t(c) * rstride + (32 * j + 8 * g) * 2 : rows_lds + (size_t(j) * 64 + lane) * 16);
-                    u32x4 xv = *reinterpret_cast<const u32x4*>(xl + (size_t(j) * 4 + g) * 16);
-                    if (c != 0) xv = u32x4{0u, 0u, 0u, 0u};  // activation rows past the first are zero
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv), __builtin_bit_cast(bf16x8, xv),
-                                                                  acc, 0, 0, 0);
-                }
-                if (ks == 0) s = acc;
-                else s += acc;
-            }
+            const uint8_t* wbase = rowl ? rows_lds + size_t(c) * rstride + 16 * g : rows_lds + size_t(lane) * 16;
+            const f32x4 s = rowl ? pick_chain<64>(wbase, xl + 16 * g, NC, a.KS, c != 0)
+                                 : pick_chain<1024>(wbase, xl + 16 * g, NC, a.KS, c != 0);
             // D: lane 16 g + c holds outputs 4 g + i of activation row c (row 0 is the real one)
             if (c == 0)
 #pragma unroll
@@ -286,10 +328,23 @@ __global__ __launch_bounds__(PK_T) void draft_pick_kernel(PickArgs a) {
     if (!is_last) return;
     if (t < PK_WG * PK_MAXN) mlist[t] = ld_c64(a.lists + t);
     if (t < PK_WG) mlist[PK_WG * PK_MAXN + t] = ld_c64(a.amax + t);
+    if (t == 0) nm2 = 0;
     __syncthreads();
-    if (t < PK_WG * PK_MAXN) {
-        const uint64_t r = mlist[t];
-        const int pos = count_above(mlist, PK_WG * PK_MAXN, r);
+    // theta2 = the nout-th largest list head (lists are descending and full, ranks unique): the nout lists
+    // with the largest heads hold nout entries >= theta2, so the top nout are all >= theta2, and only
+    // those nout lists hold such entries (at most 8 nout of them)
+    if (t < PK_WG) {
+        const uint64_t hd = mlist[t * PK_MAXN];
+        int above = 0;
+        for (int q = 0; q < PK_WG; ++q) above += mlist[q * PK_MAXN] > hd ? 1 : 0;
+        if (above == a.nout - 1) theta2 = hd;
+    }
+    __syncthreads();
+    if (t < PK_WG * PK_MAXN && mlist[t] >= theta2) m2[atomicAdd(&nm2, 1)] = mlist[t];
+    __syncthreads();
+    if (t < nm2) {
+        const uint64_t r = m2[t];
+        const int pos = count_above(m2, nm2, r);
         if (pos < a.nout) {
             const int64_t idx = int64_t(index_of<ORDER_BF16>(r));
             if (a.top) a.top[pos] = idx;

@@ -104,3 +104,33 @@ def test_draft_pick_bf16_equals_one_stage_head(C, dev, N, tiled):
             assert vtok[children[0]].item() == want_tok
             for j, c in enumerate(children[1:], 1):
                 assert vtok[c].item() == wi.view(-1)[j].item()
+
+
+@pytest.mark.parametrize("tiled", [False, True])
+def test_draft_pick_bf16_odd_k(C, dev, tiled):
+    """K = 1056 (33 chunks of 32, split into 3 K slices at N = 32768; rows gathered in the MFMA operand
+    layout): the pick against bf16_linear + fast_topk, with the scores the logits themselves and the
+    logits plus a small perturbation."""
+    from mdx import layout
+    N, K = 32768, 1056
+    g = torch.Generator(device=dev).manual_seed(K)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.03).bfloat16()
+    wt = layout.tile_major_bf16(w) if tiled else w
+    for trial in range(3):
+        print(f"case pick bf16 odd K={K} tiled={tiled} trial={trial}", flush=True)
+        x = torch.randn(1, K, generator=g, device=dev).bfloat16()
+        logits = C.bf16_linear(x, wt, tiled=tiled)
+        approx = logits.view(-1).clone() if trial == 0 else (
+            logits.view(-1).float() + 0.002 * torch.randn(N, generator=g, device=dev)).bfloat16()
+        for nout, amf in ((4, False), (8, True)):
+            wv, wi = C.fast_topk(logits, nout, False)
+            top = torch.full((nout,), -1, dtype=torch.long, device=dev)
+            vals = torch.zeros(nout, dtype=torch.bfloat16, device=dev)
+            token = torch.full((1,), -1, dtype=torch.long, device=dev)
+            vtok = torch.full((8,), -1, dtype=torch.long, device=dev)
+            children = list(range(1, nout + 1)) if nout < 8 else list(range(8))
+            C.draft_pick_bf16(approx, x.view(-1), wt, nout, amf, top, vals, token, vtok, children, tiled=tiled)
+            assert top.tolist() == wi.view(-1).tolist(), (trial, nout)
+            assert torch.equal(vals.view(torch.int16), wv.view(-1).view(torch.int16)), (trial, nout)
+            want_tok = C.fast_topk(logits, 1, True)[1].item() if amf else wi.view(-1)[0].item()
+            assert token.item() == want_tok
