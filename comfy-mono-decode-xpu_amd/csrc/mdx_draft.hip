@@ -127,6 +127,10 @@ __global__ __launch_bounds__(1024) void draft_row_kernel(DraftArgs a, int mode) 
             for (int gi = 0; gi < GPW; ++gi)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[gi][e] = bfround(v[gi][e]);  // the embedding row is bf16
+        } else if (a.token) {  // a bf16 table: the row at the token
+            int64_t t = a.token[row];
+            t = t < 0 ? 0 : (t >= a.V ? a.V - 1 : t);
+            load_row<GPW>(a.emb + t * H, G, v, raw);
         } else {
             load_row<GPW>(a.emb + row * H, G, v, raw);
         }
@@ -257,8 +261,8 @@ extern "C" int mdx_draft_embed_norm_cat(const int64_t* token, const int8_t* q, c
                                         uint16_t* out, int64_t rows, int64_t H, void* stream) {
     if (int rc = row_checks(rows, H)) return rc;
     MDX_CHECK(hidden && we && wh && out, "null pointer");
-    MDX_CHECK(q ? (token && s && V >= 1 && aligned(q, 4) && (H % 4) == 0) : emb != nullptr,
-              "an int8 embedding table with token and scales, or a bf16 embedding row");
+    MDX_CHECK(q ? (token && s && V >= 1 && aligned(q, 4) && (H % 4) == 0) : (emb != nullptr && (!token || V >= 1)),
+              "an int8 embedding table with token and scales, a bf16 table with token, or a bf16 embedding row");
     MDX_CHECK(aligned(hidden, 8) && aligned(we, 8) && aligned(wh, 8) && aligned(out, 8) && (!emb || aligned(emb, 8)),
               "8-byte aligned rows");
     if (rows == 0) return MDX_OK;

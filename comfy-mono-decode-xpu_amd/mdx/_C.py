@@ -799,7 +799,9 @@ def _regular_h(hmat, what="hadamard"):
 def draft_embed_norm_cat(token, q, s, hmat, emb, hidden, we, wh, eps_e, eps_h, out):
     """Reference csrc/draft_fused.sycl:76-151: out = cat(RMSNorm_e(emb), RMSNorm_h(hidden)), the embedding
     row gathered from an int8 ConvRot table (q [V, H] int8, s [V] f32, un-rotated by H256 when hmat is
-    given) at token, or given as the bf16 row emb (q empty). Rows: hidden [rows, H] (the reference: one)."""
+    given) at token, or given as the bf16 row emb (q empty), or, with q empty and token given, gathered
+    from the bf16 table emb [V, H] at token (tokens clamped into [0, V) in both gathers). Rows: hidden
+    [rows, H] (the reference: one)."""
     _bf16c(hidden, "hidden")
     _bf16c(we, "we")
     _bf16c(wh, "wh")
@@ -816,6 +818,14 @@ def draft_embed_norm_cat(token, q, s, hmat, emb, hidden, we, wh, eps_e, eps_h, o
         _check(token.dtype == torch.int64 and token.is_contiguous() and token.numel() == rows, "token int64 [rows]")
         unrot = _present(hmat) and _regular_h(hmat)
         _lib.call("mdx_draft_embed_norm_cat", _lib.ptr(token), _lib.ptr(q), _lib.ptr(s), q.shape[0], int(unrot), None,
+                  _lib.ptr(hidden), _lib.ptr(we), _lib.ptr(wh), float(eps_e), float(eps_h), _lib.ptr(out), rows, H,
+                  _lib.stream_of(hidden))
+    elif _present(token):
+        _dev(token, "token")
+        _bf16c(emb, "emb")
+        _check(emb.dim() == 2 and emb.shape[1] == H, "emb bf16 table [V, H]")
+        _check(token.dtype == torch.int64 and token.is_contiguous() and token.numel() == rows, "token int64 [rows]")
+        _lib.call("mdx_draft_embed_norm_cat", _lib.ptr(token), None, None, emb.shape[0], 0, _lib.ptr(emb),
                   _lib.ptr(hidden), _lib.ptr(we), _lib.ptr(wh), float(eps_e), float(eps_h), _lib.ptr(out), rows, H,
                   _lib.stream_of(hidden))
     else:

@@ -392,8 +392,7 @@ class HybridModel:
         H, D = c.hidden, c.head_dim
         qd, kd = c.heads * D, c.kv_heads * D
         cat = _C._buf(self.dcat, n, 2 * H)
-        e = torch.index_select(self.embed, 0, tok.view(-1))
-        _C.draft_embed_norm_cat(None, None, None, None, e, h, M["norm_e"], M["norm_h"], c.eps, c.eps, cat)
+        _C.draft_embed_norm_cat(tok.view(-1), None, None, None, self.embed, h, M["norm_e"], M["norm_h"], c.eps, c.eps, cat)
         x = _C._buf(self.dh, n, H)
         xn = _C._buf(self.dxn, n, H)
         _C.bf16_linear(cat, M["fc"], out=x)

@@ -379,7 +379,8 @@ int mdx_silu_mul(const uint16_t* g, const uint16_t* u, const uint16_t* silu_lut,
 
 /* fc input of the MTP block: out[r] = [RMSNorm_e(e) | RMSNorm_h(hidden[r])] (bf16 [rows, 2 H]), with the
  * embedding row e = bf16(unrotate(q[t] * s[t])), t = token[r] clamped into [0, V) (int8 [V, H] table,
- * f32 scales [V]; unrotate: the group times H256, or none), or, with q == NULL, e = emb[r] (bf16 [rows, H]).
+ * f32 scales [V]; unrotate: the group times H256, or none), or, with q == NULL, e = emb[t] from a bf16 table
+ * [V, H] when token is given (t clamped likewise) and e = emb[r] (bf16 [rows, H]) when it is NULL.
  * Replaces: _C.draft_embed_norm_cat, csrc/draft_fused.sycl:76-151 (bindings.cpp:34-36). */
 int mdx_draft_embed_norm_cat(const int64_t* token, const int8_t* q, const float* s, int64_t V, int32_t unrotate,
                              const uint16_t* emb, const uint16_t* hidden, const uint16_t* we, const uint16_t* wh,

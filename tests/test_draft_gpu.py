@@ -57,6 +57,13 @@ def test_embed_norm_cat(C, dev, rows):
     C.draft_embed_norm_cat(e, e, e, e, emb.to(dev), hidden.to(dev), we.to(dev), wh.to(dev), 1e-6, 1e-6, out2)
     want2 = ref.draft_embed_norm_cat(bits(hidden), bits(we), bits(wh), 1e-6, 1e-6, emb_bits=bits(emb))
     assert_bits_equal(bits(out2), want2, "embed_norm_cat (row)")
+    # the row gathered from a bf16 table at the token (tokens past the table clamp to its last row)
+    table = torch.randn(V, H, generator=g).bfloat16()
+    table[t] = emb
+    out3 = torch.empty_like(out)
+    C.draft_embed_norm_cat(tok.to(dev), e, e, e, table.to(dev), hidden.to(dev), we.to(dev), wh.to(dev), 1e-6, 1e-6,
+                           out3)
+    assert_bits_equal(bits(out3), want2, "embed_norm_cat (bf16 table)")
 
 
 def test_add_rmsnorm_in_place(C, dev):
