@@ -53,11 +53,11 @@ def read_roof(key):
         return None
 
 
-def gptq_weight(N, K, gen, dev, tiled=True, integral=True):
+def gptq_weight(N, K, gen, dev, tiled=True, integral=False):
     """A random GPTQ int4 matrix (q ~ U{-8..7}, fp16 G128 scales ~ U(0.005, 0.02)) in the packed-W4
-    contract. integral=True: the group scales become 4-bit integer multiples of a channel scale (the
-    integral decode; up to smax / (30 s_g) relative scale error per group); False: the fp16 group
-    scales relative to the channel scale, decoded per weight by rint (the reference contract)."""
+    contract. integral=False (default): the fp16 group scales relative to the channel scale, decoded
+    per weight by rint (the reference contract); True: the group scales become 4-bit integer multiples
+    of a channel scale (the integral decode; up to smax / (30 s_g) relative scale error per group)."""
     import torch
     from mdx import _lib, layout
     q = torch.randint(-8, 8, (N, K), generator=gen, device=dev, dtype=torch.int8)
@@ -234,15 +234,38 @@ def cpu_decode_estimate(mlp_s, mlp_algo_bytes, budget_s=20.0):
                       "scaled to a 32-layer step; norms, RoPE and top-k left out"}
 
 
+SCALES_DATA = {
+    "faithful": "fp16 G128 group scales ~U(0.005, 0.02) kept as fp16 ratios to a per-channel scale (the "
+                "reference's W4 contract, the form checkpoint ingestion produces), decoded per weight by rint",
+    "integral": "fp16 G128 group scales ~U(0.005, 0.02) re-quantised to 4-bit integer multiples of a channel "
+                "scale (up to smax / (30 s_g) relative scale error per group), integral decode",
+}
+
+# the gate/up kernel each scale form runs at 1 row (template arguments: MFMA, R, scale dtype, ring, source)
+GATEUP_KERNEL = {
+    "faithful": "gemv_kernel<false, 1, 1, 4, 0> (gate/up pair, int8 activation staged by DMA, per-weight decode)",
+    "integral": "gemv_kernel<false, 1, 1, 4, 4> (gate/up pair, int8 activation staged by DMA, integral decode only)",
+}
+
+
 def bench_mlp(args, dev):
+    """Config 2: the fused MLP block over a weight ring, in the scale form args.scales (faithful by
+    default); the other form is timed beside it as a labelled extra unless --no-extra."""
     import torch
     from mdx import _C, _lib, layout
     gen = torch.Generator(device=dev).manual_seed(2)
     H, I, M = 4096, 12288, args.rows
     per = mlp_bytes(M)
     ring_n = max(2, -(-2 * 256 * 2 ** 20 // (3 * H * I // 2)) + 1)  # > 2x the 256 MB Infinity Cache
-    ring = [(gptq_weight(I, H, gen, dev), gptq_weight(I, H, gen, dev), gptq_weight(H, I, gen, dev))
-            for _ in range(ring_n)]
+    primary = args.scales
+    other = "integral" if primary == "faithful" else "faithful"
+
+    def make_ring(form):
+        integral = form == "integral"
+        return [(gptq_weight(I, H, gen, dev, integral=integral), gptq_weight(I, H, gen, dev, integral=integral),
+                 gptq_weight(H, I, gen, dev, integral=integral)) for _ in range(ring_n)]
+
+    ring = make_ring(primary)
     x = torch.randn(M, H, generator=gen, device=dev).to(torch.bfloat16)
     nw = (1 + 0.02 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
     lut = layout.silu_lut(dev)
@@ -255,16 +278,18 @@ def bench_mlp(args, dev):
             _C.mono_mlp_w4(x, _lib.ROT_NONE, None, lut, g_, u_, d_, norm_w=nw, eps=1e-6, out=out, ws=ws)
         return call
 
-    t_call = ring_time(mlp(ring), ring_n, args.steps, args.warmup)
     # the dominant kernel alone: the gate/up GEMV launch over the same ring
     q1, s1 = _C.rms_rot_quant(x, nw, 1e-6)
     hbuf = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
 
-    def gateup(i):
-        g_, u_, _ = ring[i]
-        _C.stream_gemv(q1, s1, [g_, u_], [hbuf], gate_up=True, silu_lut=lut)
+    def gateup(r):
+        def call(i):
+            g_, u_, _ = r[i]
+            _C.stream_gemv(q1, s1, [g_, u_], [hbuf], gate_up=True, silu_lut=lut)
+        return call
 
-    t_gu = ring_time(gateup, ring_n, args.steps, args.warmup)
+    t_call = ring_time(mlp(ring), ring_n, args.steps, args.warmup)
+    t_gu = ring_time(gateup(ring), ring_n, args.steps, args.warmup)
     gu_b = gateup_bytes(M)
     res = {
         "metric": METRIC,
@@ -278,16 +303,15 @@ def bench_mlp(args, dev):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xint4->int32, bf16 out",
-        "data": "synthetic (seeded GPTQ int4 weights; fp16 G128 group scales ~U(0.005, 0.02) packed as 4-bit "
-                "integer multiples of a channel scale (integral decode); N(0,1) activations)",
+        "data": f"synthetic (seeded GPTQ int4 weights; {SCALES_DATA[primary]}; N(0,1) activations)",
         "config": {"workload": f"fused W4A8 SwiGLU MLP 4096->2x12288->4096, RMSNorm 1e-6, rows={M}, "
                                f"tile-major weights, {ring_n}-copy weight ring",
-                   "rows": M, "hidden": H, "intermediate": I, "group_size": 128,
+                   "rows": M, "hidden": H, "intermediate": I, "group_size": 128, "scales": primary,
                    "algorithmic_bytes_per_step": per, "frac_of_peak": round(per / t_call / 1e9 / PEAK_HBM_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel (gate/up pair, SiLU epilogue)",
+        "roofline": {"bound": "hbm", "kernel": GATEUP_KERNEL[primary] if M == 1 else "gemv_kernel (gate/up pair)",
                      "achieved": round(gu_b / t_gu / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gu_b / t_gu / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": pmc_traffic("mlp_gateup_rows1") if M == 1 else None,
+                     "traffic": pmc_traffic(f"mlp_gateup_rows1_{primary}") if M == 1 else None,
                      "algorithmic_bytes_per_launch": gu_b, "avg_launch_us": round(t_gu * 1e6, 3),
                      "single_launch_read_roof_gbs": read_roof("52MB")},
     }
@@ -297,26 +321,32 @@ def bench_mlp(args, dev):
         ops = 2 * 16 * -(-M // 16) * 2 * I * H
         res["roofline"]["mfma_util"] = round(ops / t_gu / PEAK_I8_OPS, 4)
         res["roofline"]["mfma_useful_util"] = round(2 * M * 2 * I * H / t_gu / PEAK_I8_OPS, 4)
-    # the same block with the fp16-faithful packer (group scales kept as fp16 ratios, per-weight rint decode)
-    del ring
-    torch.cuda.empty_cache()
-    ring_f = [(gptq_weight(I, H, gen, dev, integral=False), gptq_weight(I, H, gen, dev, integral=False),
-               gptq_weight(H, I, gen, dev, integral=False)) for _ in range(ring_n)]
-    t_f = ring_time(mlp(ring_f), ring_n, args.steps, args.warmup)
-    res["faithful_scales"] = {"value": round(per / t_f / 1e9, 2), "unit": "GB/s", "ms_per_step": round(t_f * 1e3, 5),
-                              "data": "fp16 G128 group scales kept as fp16 ratios to the channel scale (reference "
-                                      "contract), per-weight rint decode"}
+    cpu_ring = ring[0]
+    if not args.no_extra:
+        # the same block and gate/up launch in the other scale form (a labelled extra, not the headline)
+        del ring
+        torch.cuda.empty_cache()
+        ring_o = make_ring(other)
+        t_o = ring_time(mlp(ring_o), ring_n, args.steps, args.warmup)
+        t_ogu = ring_time(gateup(ring_o), ring_n, args.steps, args.warmup)
+        res[f"{other}_scales"] = {
+            "value": round(per / t_o / 1e9, 2), "unit": "GB/s", "ms_per_step": round(t_o * 1e3, 5),
+            "gateup_us": round(t_ogu * 1e6, 3), "gateup_gbs": round(gu_b / t_ogu / 1e9, 2),
+            "gateup_kernel": GATEUP_KERNEL[other] if M == 1 else "gemv_kernel (gate/up pair)",
+            "data": SCALES_DATA[other]}
+        if primary == "integral":
+            cpu_ring = ring_o[0]
     if not args.no_cpu:
         xb = x.view(torch.int16).cpu().numpy().view("uint16")
         nwb = nw.view(torch.int16).cpu().numpy().view("uint16")
         lutb = lut.view(torch.int16).cpu().numpy().view("uint16")
-        t_cpu, n, model, threads = cpu_baseline_mlp(ring_f[0], M, xb, nwb, lutb)
+        t_cpu, n, model, threads = cpu_baseline_mlp(cpu_ring, M, xb, nwb, lutb)
         res["_cpu_mlp_s"] = t_cpu
         res["cpu_baseline"] = {"value": round(per / t_cpu / 1e9, 4), "unit": "GB/s", "cores": threads,
                                "kind": "port", "ms_per_step": round(t_cpu * 1e3, 1), "cpu_model": model,
                                "sample": f"median of {n} MLP calls (after 3 warm-up calls) of the numpy oracle chain "
-                                         f"(decode + float64 int dot), one weight set, same rows; BLAS threads "
-                                         f"pinned to {threads}"}
+                                         f"(decode + float64 int dot) on one weight set of the fp16-faithful form, "
+                                         f"same rows; BLAS threads pinned to {threads}"}
     return res
 
 
@@ -328,7 +358,7 @@ def bench_linear(args, dev):
     M = args.rows
     per = linear_bytes(M)
     ring_n = -(-2 * 256 * 2 ** 20 // (N * K // 2)) + 1
-    ring = [gptq_weight(N, K, gen, dev) for _ in range(ring_n)]
+    ring = [gptq_weight(N, K, gen, dev, integral=args.scales == "integral") for _ in range(ring_n)]
     x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
     q, s = _C.quant_rows(x)
     s = s.view(-1)
@@ -339,13 +369,12 @@ def bench_linear(args, dev):
         "metric": METRIC, "value": round(per / t / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8xint4->int32, bf16 out",
-        "data": "synthetic (seeded GPTQ int4 weights; fp16 G128 scales packed as 4-bit integer multiples of a "
-                "channel scale)",
+        "data": f"synthetic (seeded GPTQ int4 weights; {SCALES_DATA[args.scales]})",
         "config": {"workload": f"single W4A8 linear M={M} K=N=4096 G128, {ring_n}-copy weight ring", "rows": M,
-                   "algorithmic_bytes_per_step": per},
+                   "scales": args.scales, "algorithmic_bytes_per_step": per},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel", "achieved": round(per / t / 1e9, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(per / t / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": pmc_traffic("linear_rows1") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3),
+                     "traffic": pmc_traffic(f"linear_rows1_{args.scales}") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3),
                      "single_launch_read_roof_gbs": read_roof("8.7MB")},
     }
 
@@ -458,7 +487,8 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
     cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, gdn_fused=args.gdn_fused,
-                              gdn_side_gates=args.side_gates, predictable=getattr(args, "predictable", False))
+                              gdn_side_gates=args.side_gates, predictable=getattr(args, "predictable", False),
+                              scales=args.scales)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -486,11 +516,11 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     what = f"{got} tokens decoded" if tokens else f"{done} decode steps"
     hd = "int8 ConvRot lm_head (W8A8)" if head == "int8" else "bf16 lm_head"
     return _line(args, round(got / t, 2), "tok/s", per_step, done, f"W4A8 int8 x int4 -> int32; bf16 draft block, {hd}",
-                 "synthetic (random-init weights, seeded random prompt)",
+                 f"synthetic (random-init weights, GPTQ int4 with {SCALES_DATA[args.scales]}; seeded random prompt)",
                  {"workload": f"32-layer W4A8 hybrid (24 GDN + 8 attention), hidden 4096, MLP 12288, vocab 151936 "
                               f"({hd}), MTP draft{' (two-stage head)' if two_stage else ''}, tree (4, 3), top-k 20, "
                               f"prompt {args.prompt}, {what}",
-                  "prompt": args.prompt, "steps": done, "tokens": got,
+                  "prompt": args.prompt, "steps": done, "tokens": got, "scales": args.scales,
                   "accepted_per_step": round(got / done, 3), "ms_per_step": round(per_step * 1e3, 4),
                   "setup_s": round(setup, 1)})
 
@@ -504,7 +534,7 @@ def bench_stack_auto(args, dev, tokens=512):
     from mdx import hybrid
     cap = args.prompt + 8 * (tokens + 64) + 64
     cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head,
-                              predictable=getattr(args, "predictable", False))
+                              predictable=getattr(args, "predictable", False), scales=args.scales)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     m.prefill(torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5)))
@@ -545,6 +575,7 @@ def bench_attn_layer(args, dev):
     import torch
     from mdx import _C, _lib, hybrid
     gen = torch.Generator(device=dev).manual_seed(3)
+    integ = args.scales == "integral"
     H, Hk, D, S, L, Hd = 32, 8, 128, 16, args.ctx, 4096
     cap = L + S
     cfg = hybrid.HybridConfig(cap=cap + 8)
@@ -559,8 +590,8 @@ def bench_attn_layer(args, dev):
     freqs = torch.index_select(ftab, 0, torch.tensor(depth, device=dev) + L).contiguous()
     seq = torch.tensor([L], dtype=torch.int32, device=dev)
     def layer_w():
-        return dict(q=gptq_weight(H * D, Hd, gen, dev), k=gptq_weight(Hk * D, Hd, gen, dev),
-                    v=gptq_weight(Hk * D, Hd, gen, dev), o=gptq_weight(Hd, H * D, gen, dev),
+        return dict(q=gptq_weight(H * D, Hd, gen, dev, integral=integ), k=gptq_weight(Hk * D, Hd, gen, dev, integral=integ),
+                    v=gptq_weight(Hk * D, Hd, gen, dev, integral=integ), o=gptq_weight(Hd, H * D, gen, dev, integral=integ),
                     key=torch.randn(1, Hk, cap, D, generator=gen, device=dev).bfloat16(),
                     value=torch.randn(1, Hk, cap, D, generator=gen, device=dev).bfloat16())
     first = layer_w()
@@ -596,7 +627,7 @@ def bench_attn_layer(args, dev):
     t = ring_time(call, ring_n, args.steps, args.warmup)
     gbs = per / t / 1e9
     return _line(args, round(gbs, 2), "GB/s", t, args.steps, "W4A8 int8 x int4 -> int32; bf16 attention (MFMA)",
-                 "synthetic (seeded GPTQ int4 weights, integral 4-bit group scales; N(0,1) KV cache and rows)",
+                 f"synthetic (seeded GPTQ int4 weights; {SCALES_DATA[args.scales]}; N(0,1) KV cache and rows)",
                  {"workload": f"full-attention layer mixer, 16 tree rows, 32q/8kv heads, head_dim 128, ctx={L}, "
                               f"{ring_n}-copy weight + KV ring", "ctx": L, "rows": S,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
@@ -612,6 +643,7 @@ def bench_gdn_layer(args, dev):
     import torch
     from mdx import _C, _lib
     gen = torch.Generator(device=dev).manual_seed(4)
+    integ = args.scales == "integral"
     M, Hd, HK, HV, DH, S = args.rows, 4096, 16, 32, 128, 8
     if not 1 <= M <= S:
         raise SystemExit("gdn_layer: --rows must be 1..8")
@@ -619,7 +651,7 @@ def bench_gdn_layer(args, dev):
     bf = dict(dtype=torch.bfloat16, device=dev)
 
     def layer_w():
-        return dict(qkv=gptq_weight(C, Hd, gen, dev), z=gptq_weight(HV * DH, Hd, gen, dev), o=gptq_weight(Hd, HV * DH, gen, dev),
+        return dict(qkv=gptq_weight(C, Hd, gen, dev, integral=integ), z=gptq_weight(HV * DH, Hd, gen, dev, integral=integ), o=gptq_weight(Hd, HV * DH, gen, dev, integral=integ),
                     wa=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
                     wb=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
                     conv_w=(torch.randn(C, 4, generator=gen, device=dev) * 0.5).bfloat16(),
@@ -661,7 +693,7 @@ def bench_gdn_layer(args, dev):
     t = ring_time(call, ring_n, args.steps, args.warmup)
     gbs = per / t / 1e9
     return _line(args, round(gbs, 2), "GB/s", t, args.steps, "W4A8 int8 x int4 -> int32; fp32 recurrent state",
-                 "synthetic (seeded GPTQ int4 weights, integral 4-bit group scales; state N(0, 0.1))",
+                 f"synthetic (seeded GPTQ int4 weights; {SCALES_DATA[args.scales]}; state N(0, 0.1))",
                  {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
                               f"{ring_n}-copy weight + state ring", "rows": M,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
@@ -739,6 +771,10 @@ def main():
     ap.add_argument("--ctx", type=int, default=8192, help="attention context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="mlp: skip the full-stack decode leg")
+    ap.add_argument("--no-extra", action="store_true", help="mlp: skip the other scale form's leg")
+    ap.add_argument("--scales", choices=["faithful", "integral"], default="faithful",
+                    help="W4 group scales: fp16 ratios decoded per weight (the reference contract, default) or "
+                         "the lossy 4-bit integral re-quantisation")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU only: the 9B stack scales as one "
@@ -770,8 +806,16 @@ def main():
         # proposes tokens, the verify decides what is committed
         d = bench_stack(sub, dev, tokens=512, two_stage=True)
         res["decode"] = {"metric": "decode tok/s at 9B hybrid, 8-draft tree", "value": d["value"], "unit": "tok/s",
-                         "ms_per_step": d["config"]["ms_per_step"],
+                         "ms_per_step": d["config"]["ms_per_step"], "scales": args.scales,
                          "accepted_per_step": d["config"]["accepted_per_step"], "workload": d["config"]["workload"]}
+        # the same decode on the other scale form's weights (a labelled extra)
+        osub = argparse.Namespace(**vars(sub))
+        osub.scales = "integral" if args.scales == "faithful" else "faithful"
+        do = bench_stack(osub, dev, tokens=512, two_stage=True)
+        res[f"decode_{osub.scales}_scales"] = {"value": do["value"], "unit": "tok/s",
+                                                "ms_per_step": do["config"]["ms_per_step"],
+                                                "accepted_per_step": do["config"]["accepted_per_step"],
+                                                "data": SCALES_DATA[osub.scales]}
         # the same decode with the drafts' full bf16 lm_head (one stage)
         d2 = bench_stack(sub, dev, tokens=512)
         res["decode_one_stage_drafts"] = {"value": d2["value"], "unit": "tok/s", "ms_per_step": d2["config"]["ms_per_step"],

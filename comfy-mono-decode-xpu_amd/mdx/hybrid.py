@@ -53,6 +53,10 @@ class HybridConfig:
     gdn_fused: bool = False       # the GDN core in one launch (mdx_gdn_core_fused, the same bits)
     gdn_side_gates: bool = False  # the GDN gates on a second stream beside the projection GEMV (the same bits)
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
+    # W4 group scales of the random weights: "faithful" keeps each fp16 G128 group scale as an fp16 ratio to
+    # the channel scale, decoded per weight by rint (the reference contract, what checkpoint ingestion
+    # produces); "integral" re-quantises them to 4-bit integer multiples of the channel scale (lossy)
+    scales: str = "faithful"
     # synthetic weights with a predictable next token (token t -> t + 1 mod vocab) for the verify and the
     # drafts: the lm_head row v is the embedding of v - 1, the layers' and the MTP block's output
     # projections are scaled down (the residual stream stays the embedding) and the MTP block's fc passes
@@ -64,12 +68,13 @@ class HybridConfig:
         return i % self.attn_every == self.attn_every - 1
 
 
-def _gptq(N, K, gen, dev):
+def _gptq(N, K, gen, dev, integral=False):
     q = torch.randint(-8, 8, (N, K), generator=gen, device=dev, dtype=torch.int8)
     s = (torch.rand(N, K // 128, generator=gen, device=dev) * 0.015 + 0.005).half()
-    packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=True)
+    packed, s_rel, sch, _ = layout.gptq_pack(q, s, 128, integral=integral)
     del q
-    return layout.W4(layout.tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE, _lib.DECODE_INTEGRAL)
+    return layout.W4(layout.tile_major_codes(packed), s_rel, sch, None, _lib.LAYOUT_TILE,
+                     _lib.DECODE_INTEGRAL if integral else _lib.DECODE_AUTO)
 
 
 def _norm(n, gen, dev, spread=0.02):
@@ -161,15 +166,18 @@ class HybridModel:
         self.silu = layout.silu_lut(dev)
         self.sig = torch.sigmoid(layout.bf16_all(dev)).contiguous()
         self.layers = []
+        if c.scales not in ("faithful", "integral"):
+            raise ValueError(f"HybridConfig.scales: {c.scales!r} (faithful | integral)")
+        integ = c.scales == "integral"
         for i in range(c.layers):
-            L = dict(norm_in=_norm(H, gen, dev), norm_post=_norm(H, gen, dev), g=_gptq(I, H, gen, dev),
-                     u=_gptq(I, H, gen, dev), d=_gptq(H, I, gen, dev))
+            L = dict(norm_in=_norm(H, gen, dev), norm_post=_norm(H, gen, dev), g=_gptq(I, H, gen, dev, integ),
+                     u=_gptq(I, H, gen, dev, integ), d=_gptq(H, I, gen, dev, integ))
             L["u"].cb = L["d"].cb = L["g"].cb
             if c.attention(i):
-                L.update(q=_gptq(qd, H, gen, dev), k=_gptq(kd, H, gen, dev), v=_gptq(kd, H, gen, dev),
-                         o=_gptq(H, qd, gen, dev), qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1))
+                L.update(q=_gptq(qd, H, gen, dev, integ), k=_gptq(kd, H, gen, dev, integ), v=_gptq(kd, H, gen, dev, integ),
+                         o=_gptq(H, qd, gen, dev, integ), qn=_norm(c.head_dim, gen, dev, 0.1), kn=_norm(c.head_dim, gen, dev, 0.1))
             else:
-                L.update(qkv=_gptq(self.gdn_ch, H, gen, dev), z=_gptq(hv * 128, H, gen, dev), o=_gptq(H, hv * 128, gen, dev),
+                L.update(qkv=_gptq(self.gdn_ch, H, gen, dev, integ), z=_gptq(hv * 128, H, gen, dev, integ), o=_gptq(H, hv * 128, gen, dev, integ),
                          wa=(torch.randn(hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
                          wb=(torch.randn(hv, H, generator=gen, device=dev) * 0.02).bfloat16(),
                          conv_w=(torch.randn(self.gdn_ch, 4, generator=gen, device=dev) * 0.5).bfloat16(),

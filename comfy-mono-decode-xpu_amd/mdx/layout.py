@@ -67,14 +67,17 @@ def unpack_codes(packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def gptq_pack(q: torch.Tensor, scales: torch.Tensor, group_size: int = 128, integral: bool = True):
+def gptq_pack(q: torch.Tensor, scales: torch.Tensor, group_size: int = 128, integral: bool = False):
     """GPTQ int4 symmetric weights (q in [-8, 7] as [N, K], fp16 group scales [N, K/G]) -> the
     packed-W4 contract (packed, s_rel fp16, s_channel fp32, codebook None = code - 8).
 
-    integral=True: s_channel[n] = max_g s_g / 15 and s_rel = round(s_g / s_channel) in 1..15, so
-    w8 = q * s_rel exactly (libmdx then takes its factorised integer path). integral=False: s_channel[n] =
-    max_g s_g * 8 / 127 and s_rel = fp16(s_g / s_channel) <= 127 / 8, decoded per weight by rint.
-    In both, w8 * s_channel approximates q * s_g, |w8| <= 127 (no clamp)."""
+    integral=False (the default; the form checkpoint ingestion produces): s_channel[n] =
+    max_g s_g * 8 / 127 and s_rel = fp16(s_g / s_channel) <= 127 / 8, decoded per weight by rint, the
+    reference's W4 contract (csrc/w4a8_decode.sycl:4-11,35-45). integral=True (lossy, opt-in):
+    s_channel[n] = max_g s_g / 15 and s_rel = round(s_g / s_channel) in 1..15, which re-quantises each
+    group scale (up to smax / (30 s_g) relative error) so that w8 = q * s_rel exactly and libmdx can
+    take its factorised integer path. In both, w8 * s_channel approximates q * s_g, |w8| <= 127 (no
+    clamp)."""
     n, k = q.shape
     assert k % group_size == 0 and scales.shape == (n, k // group_size)
     s = scales.float()
