@@ -314,8 +314,8 @@ struct GemvArgs {
     const void* res[3];
     int out_dt;
     const uint16_t* lut;  // EPI_SILU
-    // EPI_SILU with hmax_out (one gate/up pair per work-group): work-group wg also stores its rows'
-    // |h| maxima (fp32 bits) at hmax_out[row * (number of work-groups) + wg]
+    // EPI_SILU with hmax_out: each gate/up pair (tile) also stores its rows' |h| maxima (fp32 bits) at
+    // hmax_out[row * (number of pairs) + pair]
     uint32_t* hmax_out;
     // SRC_HR units: the activation is hr (bf16 [rows, K]) quantised in the prologue with the row
     // scale max(absmax / 127, 1e-30), absmax = the maximum of hmax[row * hmax_n + w] over w < hmax_n
@@ -337,6 +337,12 @@ enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
 // default codebook, groups the integral form takes). Without the per-weight decode's code the
 // integral path keeps its registers and schedule (the 1-row MLP 24.6 -> 23.x us).
 constexpr int SRC_INT_ONLY = 4;
+// Added to a source (MFMA kernels only): the per-weight table decode only, for groups of at least one
+// chunk with their (tile row, group) tables in LDS: 16-byte tables (SRC_TBL) or the default codebook's
+// eight magnitudes (SRC_TBL8). No per-launch scale check and no scale reads in the loop; the tables ride
+// a ring beside the weights at scalar offsets.
+constexpr int SRC_TBL = 8;
+constexpr int SRC_TBL8 = 16;
 constexpr int XP_GPW = 4;
 constexpr int HMW = 16;  // SRC_HR: maxima per lane when every wave reads them all (<= 1024 work-groups)  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
 
@@ -395,6 +401,25 @@ __device__ __forceinline__ uint2 make_q8(float s) {
     return make_uint2(w[0], w[1]);
 }
 
+// make_q8 for an fp16 scale |s| <= 127 / 8 (bits & 0x7FFF <= 0x4BF0; every fp16-ratio GPTQ scale): four packed
+// half-precision FMAs k s + 1536 (k = 1..8). Each forms k s exactly and rounds once; in [1024, 2048) the
+// spacing of half precision is 1, so the result is 1536 + rint(k s) (ties to even, 1536 being even), and
+// its low byte is rint(k s) as int8. |k s| <= 127: no clamp. Two byte permutes gather the eight bytes.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t F16_FAST_MAX = 0x4BF0u;  // fp16 15.875
+
+__device__ __forceinline__ uint2 make_q8_f16(uint32_t sbits) {
+    const half2_t s2 = __builtin_bit_cast(half2_t, sbits | (sbits << 16));
+    const half2_t magic = {(_Float16)1536.0f, (_Float16)1536.0f};
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2_t kk = {(_Float16)float(2 * i + 1), (_Float16)float(2 * i + 2)};
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(kk, s2, magic));
+    }
+    return make_uint2(__builtin_amdgcn_perm(r[1], r[0], 0x06040200u), __builtin_amdgcn_perm(r[3], r[2], 0x06040200u));
+}
+
 // The default codebook's 16-byte table from its magnitudes (make_lut_c8's bytes): byte reversal and
 // a carry-free negation of four int8 at once (~b + 1 per byte; no byte is -128 after the clamp).
 __device__ __forceinline__ Lut lut_from_q8(uint32_t qa, uint32_t qb) {
@@ -450,6 +475,36 @@ __device__ __forceinline__ void decode_tbl(const uint32_t* wd, const uint4 T, bo
     for (int j = 0; j < 4; ++j) {
         lo[j] = lut4(L, wd[j] & 0x0F0F0F0Fu);
         hi[j] = lut4(L, (wd[j] >> 4) & 0x0F0F0F0Fu);
+    }
+}
+
+// The table-only decode of one chunk's four code dwords (tile-major nibble order: k 8j..8j+3 in the low
+// nibbles of dword j, k 8j+4..8j+7 in the high ones). Per four codes: the byte selectors (c & 7) index
+// both 8-byte halves of the table by v_perm_b32, and a third v_perm_b32 picks per byte by bit 3 of the
+// code (selector i or 4 + i, built by one bitop3 from the shifted codes): 13 VALU per code dword.
+// Q8: T.x, T.y hold the default codebook's eight magnitudes (expanded once per chunk).
+template <bool Q8>
+__device__ __forceinline__ void decode_tb(const uint4 w, const uint4 T, uint32_t* lo, uint32_t* hi) {
+    Lut L;
+    if (Q8) {
+        L = lut_from_q8(T.x, T.y);
+    } else {
+        L.w[0] = T.x;
+        L.w[1] = T.y;
+        L.w[2] = T.z;
+        L.w[3] = T.w;
+    }
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t m4 = 0x04040404u, id = 0x03020100u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t v = wd[j];
+        const uint32_t sl = v & 0x07070707u, sh = (v >> 4) & 0x07070707u;
+        // (a & b) | c: bitop3 truth table 0xEA (index 4 a + 2 b + c)
+        const uint32_t pl = __builtin_amdgcn_bitop3_b32(v >> 1, m4, id, 0xEA);
+        const uint32_t ph = __builtin_amdgcn_bitop3_b32(v >> 5, m4, id, 0xEA);
+        lo[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.w[3], L.w[2], sl), __builtin_amdgcn_perm(L.w[1], L.w[0], sl), pl);
+        hi[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L.w[3], L.w[2], sh), __builtin_amdgcn_perm(L.w[1], L.w[0], sh), ph);
     }
 }
 
@@ -577,13 +632,13 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
             uint32_t* o = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out[0]) + r * a.m[0].n + tile * 16 + c);
             *o = v;
             if (a.hmax_out) {
-                // the row's |h| maximum over the 8 threads of this row (the work-group's one pair; NaN
-                // counts as 0, as in the row prep's fmaxf from 0), stored as this work-group's entry
+                // the row's |h| maximum over the 8 threads that hold this pair's 16 columns of the row (NaN
+                // counts as 0, as in the row prep's fmaxf from 0), stored as this pair's entry
                 float m = fmaxf(fabsf(bf2f(uint16_t(v))), fabsf(bf2f(uint16_t(v >> 16))));
                 m = fmaxf(m, __shfl_xor(m, 1, 8));
                 m = fmaxf(m, __shfl_xor(m, 2, 8));
                 m = fmaxf(m, __shfl_xor(m, 4, 8));
-                if ((rem & 7) == 0) a.hmax_out[r * gridDim.x + wg] = __float_as_uint(m != m ? 0.f : m);
+                if ((rem & 7) == 0) a.hmax_out[r * a.m[0].tiles + tile] = __float_as_uint(m != m ? 0.f : m);
             }
         }
         return;
@@ -694,6 +749,9 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     constexpr int SRCK = SRC & 3;
     constexpr bool IO = (SRC & SRC_INT_ONLY) != 0;  // the integral decode only
     constexpr bool HR = SRCK == SRC_HR, XP = SRCK == SRC_XP;
+    constexpr bool TB = (SRC & (SRC_TBL | SRC_TBL8)) != 0;  // the table decode only
+    constexpr bool TB8 = (SRC & SRC_TBL8) != 0;
+    static_assert(!TB || (MFMA && !IO), "the table-only variants are MFMA kernels");
     const bool own_x = SRCK == SRC_Q8;  // int8 rows a.xq staged by this prologue
     // Per-wave one-shots (a.pwo): each wave stages only what it reads, its slice's activation run
     // (the TPW waves of a slice write the same bytes) and its tile's scales of its slice's groups
@@ -774,8 +832,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // per-weight decode tables [g1 - g0][TPW x 16 rows] x 16 bytes (after the SRC_XP region; the rows of
     // a group adjacent, so the 16 rows a wave reads at once fall in distinct banks)
     uint4* tbl = reinterpret_cast<uint4*>(xs_l + (XP ? 4 * K : 0));
-    const bool tbl_on = a.tbl != 0;  // (uniform; groups of at least one chunk, scales not asserted integral)
-    const bool tbl8 = a.tbl == 2;    // (uniform) 8-byte tables: the default codebook's magnitudes
+    const bool tbl_on = TB || a.tbl != 0;  // (uniform; groups of at least one chunk, scales not asserted integral)
+    const bool tbl8 = TB ? TB8 : a.tbl == 2;  // (uniform) 8-byte tables: the default codebook's magnitudes
     const int ngr = g1 - g0;
     if (XP && pwo) {
         // per wave: the 256-groups its prep reads (group g: 512 bytes of the row, 512 of the weights)
@@ -800,17 +858,17 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // of sixteen vector loads per wave in the memory pipeline ahead of the ring
     typedef __attribute__((address_space(4))) const float* const_f32p;
     float cb[16];
-    bool cbdef = true;
+    bool cbdef = true;  // (uniform) the codebook is code - 8: a null one, or loaded values that equal it
     if (a.cb) {
         const const_f32p cbc = (const_f32p)(a.cb);
 #pragma unroll
         for (int i = 0; i < 16; ++i) cb[i] = cbc[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cbdef = cbdef && cb[i] == float(i - 8);
     } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i) cb[i] = float(i - 8);
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) cbdef = cbdef && cb[i] == float(i - 8);
 
     // 2. the weight ring: every slot issues one load; reads past the slice repeat its last chunk. A
     // tile slot past the matrix's last tile (a work-group's share can end inside its tile slots)
@@ -843,6 +901,37 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_waitcnt((RING & 15) | ((RING >> 4) << 14) | (7 << 4) | (15 << 8));  // vmcnt(RING) only
         __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0): LDS writes of this wave
         __builtin_amdgcn_s_barrier();
+    }
+    // a (tile row, group) table from the staged scales: 16 bytes (make_lut's), or the default codebook's eight
+    // magnitudes (8 bytes)
+    auto build_table = [&](int rw, int gg) {
+        const int j = gg * (a.TPW * 16) + rw;
+        const uint8_t* sp = sl + rw * seg + gg * ESZ;
+        uint2 q8;
+        bool have = false;
+        if (SDT == MDX_DT_F16 && cbdef) {
+            const uint32_t sb = *reinterpret_cast<const uint16_t*>(sp);
+            if ((sb & 0x7FFFu) <= F16_FAST_MAX) {
+                q8 = make_q8_f16(sb);
+                have = true;
+            }
+        }
+        if (tbl8) {
+            reinterpret_cast<uint2*>(tbl)[j] = have ? q8 : make_q8(rd_scale<SDT>(sp));
+        } else {
+            const Lut L = have ? lut_from_q8(q8.x, q8.y) : (cbdef ? make_lut_c8(rd_scale<SDT>(sp)) : make_lut(rd_scale<SDT>(sp), cb));
+            tbl[j] = make_uint4(L.w[0], L.w[1], L.w[2], L.w[3]);
+        }
+    };
+    if (TB) {
+        // each wave builds the tables it reads itself (its tile's 16 rows x its slice's groups: lane l takes
+        // row l % 16 of every fourth group), so no work-group barrier follows; a group shared by two slices
+        // is built by both with the same bytes
+        if (nch > 0) {
+            const int gsh = lgG - 7, ga = c0 >> gsh, gb = ((c1 - 1) >> gsh) + 1;
+            for (int gg = ga + (lane >> 4); gg < gb; gg += 4) build_table(ts * 16 + c, gg - g0);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's table writes are done before its reads
     }
     if (HR) {
         // the rows' scales (the row prep's formula), then the rows quantised into LDS while the ring
@@ -975,7 +1064,13 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // MDX_DECODE_INTEGRAL the caller asserts it: no check, and no barrier unless this prologue wrote
     // the activation rows to LDS itself (SRC_HR, SRC_XP).
     bool integ;
-    if (IO) {
+    if (TB) {
+        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __builtin_amdgcn_s_barrier();
+        }
+        integ = false;
+    } else if (IO) {
         if (HR || XP) {  // (the rows this prologue wrote to LDS)
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
@@ -1006,19 +1101,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         __builtin_amdgcn_s_barrier();
         integ = can_int && *mixed == 0;  // uniform over the unit
     }
-    if (!integ && tbl_on) {
-        // every (tile row, group) table once (make_lut's bytes), from the staged scales
-        const int nr = a.TPW * 16, ntab = nr * ngr;
-        for (int j = t; j < ntab; j += nthr) {
-            const int gg = j / nr, rw = j - gg * nr;
-            const float sv = rd_scale<SDT>(sl + rw * seg + gg * ESZ);
-            if (tbl8) {
-                reinterpret_cast<uint2*>(tbl)[j] = make_q8(sv);
-            } else {
-                const Lut L = cbdef ? make_lut_c8(sv) : make_lut(sv, cb);
-                tbl[j] = make_uint4(L.w[0], L.w[1], L.w[2], L.w[3]);
-            }
-        }
+    if (!TB && !integ && tbl_on) {
+        // every (tile row, group) table once, from the staged scales: thread t takes row t % nr of groups
+        // t / nr, t / nr + nthr / nr, ... (nthr is a multiple of nr = 16 TPW)
+        const int nr = a.TPW * 16, gstep = nthr / nr;
+        for (int gg = t / nr; gg < ngr; gg += gstep) build_table(t % nr, gg);
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
     }
@@ -1031,7 +1118,10 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // expose its latency at every chunk)
     const bool tring = !integ && tbl_on;  // (uniform)
     auto tbl_of = [&](int i) {
-        const int o = (ts * 16 + c) + ((((c0 + min(i, last)) * CHUNK_K + klane) >> lgG) - g0) * (a.TPW * 16);
+        // (TB: groups of at least one chunk, so a chunk's group is a uniform shift of its index and the
+        // offset a scalar; the generic path also serves smaller groups through klane)
+        const int o = TB ? (ts * 16 + c) + (((c0 + min(i, last)) >> (lgG - 7)) - g0) * (a.TPW * 16)
+                         : (ts * 16 + c) + ((((c0 + min(i, last)) * CHUNK_K + klane) >> lgG) - g0) * (a.TPW * 16);
         if (tbl8) {
             const uint2 q = reinterpret_cast<const uint2*>(tbl)[o];
             return make_uint4(q.x, q.y, 0u, 0u);
@@ -1042,7 +1132,40 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 #pragma unroll
     for (int p = 0; p < RING; ++p) tq[p] = tring ? tbl_of(p) : make_uint4(0u, 0u, 0u, 0u);
 
-    if (MFMA) {
+    if constexpr (TB) {
+        // the table decode only: per chunk the lane's four code dwords through its (row, group) table,
+        // four MFMAs against the activation rows (rows past the last repeat the last row: their sums are
+        // never stored); a chunk past the slice adds nothing (a uniform branch)
+        v4i acc = {0, 0, 0, 0};
+        const uint8_t* xrow = xl + min(lane & 15, a.rows - 1) * Kr + klane - cu0 * CHUNK_K;
+        for (int i0 = 0; i0 < nch; i0 += RING) {
+#pragma unroll
+            for (int p = 0; p < RING; ++p) {
+                const int i = i0 + p;
+                const int ch = c0 + min(i, last);
+                const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
+                const uint4 xa = x4[0], xb = x4[1];
+                const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                uint32_t lo[4], hi[4];
+                decode_tb<TB8>(buf[p], tq[p], lo, hi);
+                if (!split)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], lo[j], hi[j]);
+                if (i < nch) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                    long(uint64_t(lo[j]) | (uint64_t(hi[j]) << 32)), acc, 0, 0, 0);
+                }
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);  // refill after use
+                tq[p] = tbl_of(i + RING);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        int32_t* dst = red + ((ts * a.KS + slice) * 64 + lane) * 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r] = acc[r];
+    } else if (MFMA) {
         v4i accE = {0, 0, 0, 0};        // per-weight decoded chunks: one running MFMA sum
         int32_t tot[4] = {0, 0, 0, 0};  // integral chunks: sum of s * (chunk dot - 8 sum x)
         // rows past the last read 32 zero bytes at every chunk (stride 0)
@@ -1208,8 +1331,26 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz) { return gemv_smem(a, mf
 
 int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1); }
 
+// The kernel variants this thread's GEMV launches took since the last mdx_gemv_trace call (a diagnostic for
+// tests: which source, decode form and product path a shape reaches).
+constexpr int TRACE_MAX = 64;
+thread_local int32_t g_trace[TRACE_MAX][6];
+thread_local int g_trace_n = 0;
+
+void trace_launch(bool mfma, int src, int sdt, const GemvArgs& a) {
+    if (g_trace_n >= TRACE_MAX) return;
+    int32_t* r = g_trace[g_trace_n++];
+    r[0] = mfma;
+    r[1] = src;
+    r[2] = sdt;
+    r[3] = a.rows;
+    r[4] = a.TPW;
+    r[5] = a.KS;
+}
+
 template <bool MFMA, int R, int SDT, int RING, int SRC>
 int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
+    trace_launch(MFMA, SRC, SDT, a);
     const size_t smem = gemv_smem(a, MFMA, esz_of(SDT));
     const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING, SRC>);
     if (smem > 64 * 1024) allow_smem(fn, smem);
@@ -1219,8 +1360,22 @@ int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
     return MDX_OK;
 }
 
+constexpr int TB_RING = 4;  // weight ring depth of the table-only variants
+
+template <bool MFMA, int R, int SDT, int RING, int TB>
+int launch_gemv_tb(const GemvArgs& a, int wgs, hipStream_t st) {
+    if (a.hr) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_HR + TB>(a, wgs, st);
+    if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_XP + TB>(a, wgs, st);
+    return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB>(a, wgs, st);
+}
+
 template <bool MFMA, int R, int SDT, int RING>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
+    if constexpr (MFMA) {
+        // per-weight decode tables in LDS: the table-only variants
+        if (a.tbl == 1) return launch_gemv_tb<MFMA, R, SDT, RING, SRC_TBL>(a, wgs, st);
+        if (a.tbl == 2) return launch_gemv_tb<MFMA, R, SDT, RING, SRC_TBL8>(a, wgs, st);
+    }
     // the integral-only variant when the caller asserts integral scales that the integral form takes
     const bool io = a.assume_int && !a.cb && !a.force_exact && a.lgG >= (MFMA ? 7 : 5);
     if (io) {
@@ -1344,7 +1499,22 @@ void gemv_geometry(int total, int K, bool pair, int rows, int& TPW, int& KS) {
         KS = d;
         if (int64_t(total) * d >= 3072) break;
     }
-    // MDX_GEMV_TPW / MDX_GEMV_KS override the geometry (tuning sweeps)
+    // MDX_GEMV_TPW / MDX_GEMV_KS override the geometry (tuning sweeps); MDX_GEMV_PAIR_TPW / _KS only that of
+    // gate/up pairs
+    if (const char* env = pair ? getenv("MDX_GEMV_PAIR_TPW") : nullptr) {
+        const int tpw = atoi(env);
+        if (tpw >= 2 && tpw <= 6 && tpw % 2 == 0) TPW = tpw;
+        KS = 1;
+        for (int d = 1; d <= 16 / TPW && 4 * d <= NC; ++d) {
+            if (NC % d) continue;
+            KS = d;
+            if (int64_t(total) * d >= 3072) break;
+        }
+    }
+    if (const char* env = pair ? getenv("MDX_GEMV_PAIR_KS") : nullptr) {
+        const int ks = atoi(env);
+        if (ks >= 1 && ks * TPW <= 16 && NC % ks == 0) KS = ks;
+    }
     if (const char* env = getenv("MDX_GEMV_TPW")) {
         const int tpw = atoi(env);
         if (tpw >= 1 && tpw <= 6 && (!pair || tpw % 2 == 0)) TPW = tpw;  // the parameter block holds 6 tiles
@@ -1415,9 +1585,8 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     int total = 0;
     int rc = setup_gemv(ws, nm, pair, ex.hr || ex.xp_x ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
     if (rc) return rc;
-    const bool mfma = rows >= MFMA_MIN_ROWS;
+    bool mfma = rows >= MFMA_MIN_ROWS;
     gemv_geometry(total, a.K, pair, rows, a.TPW, a.KS);
-    MDX_CHECK(!ex.hmax_out || a.TPW == 2, "|h| maxima need one gate/up pair per work-group");
     a.hmax_out = ex.hmax_out;
     a.hr = ex.hr;
     a.hmax = ex.hmax;
@@ -1431,17 +1600,21 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     // per-weight decode tables in LDS when the scales are not asserted integral, a group spans a chunk
     // and the larger footprint still holds the grid's work-groups per CU (else fewer resident: at 8
     // rows the gate/up pair would drop from three work-groups per CU to two and lose more than the
-    // tables save; there the lanes build their tables in the loop)
+    // tables save; there the lanes build their tables in the loop). Tables select the table-only
+    // variants, which run on the MFMA kernel at every row count (at one row too: the products leave
+    // the VALU to the decode).
     if (!a.assume_int && a.lgG >= 7) {
         const int per_cu = (wgs + 255) / 256;
         for (int tb = 1; tb <= 2; ++tb) {  // 16-byte tables, else (default codebook) 8-byte ones
             if (tb == 2 && a.cb) break;
             a.tbl = tb;
-            const size_t sm = gemv_smem(a, mfma, esz);
+            const size_t sm = gemv_smem(a, true, esz);
             if (int64_t(per_cu) * sm <= 160 * 1024) break;
             a.tbl = 0;
         }
+        if (a.tbl) mfma = true;
     }
+    MDX_CHECK(!(mfma && a.xp_x) || a.tbl, "row-prep GEMV geometry (one row takes the VALU kernel or the tables)");
     // per-wave one-shots: one int8 row, caller-asserted integral scales with the default codebook,
     // G128, 16-byte runs of scales per slice and per row (MDX_GEMV_PWO=0 turns them off)
     const char* pe = getenv("MDX_GEMV_PWO");
@@ -1470,6 +1643,14 @@ int prep_checks(int64_t rows, int64_t K, int32_t rot, const void* h, const void*
 }  // namespace mdx
 
 using namespace mdx;
+
+extern "C" int32_t mdx_gemv_trace(int32_t* out, int32_t max_records) {
+    const int n = g_trace_n;
+    for (int i = 0; i < n && i < max_records; ++i)
+        for (int j = 0; j < 6; ++j) out[6 * i + j] = g_trace[i][j];
+    g_trace_n = 0;
+    return n;
+}
 
 extern "C" int mdx_w4a8_decode_linear(const int8_t* x, const float* x_scale, const mdx_w4* w, const void* residual,
                                       void* out, int32_t out_dtype, int64_t rows, void* stream) {
@@ -1641,8 +1822,10 @@ extern "C" int mdx_mono_mlp(const uint16_t* xn, const uint16_t* norm_w, float ep
     const mdx_w4* gu[2] = {gate, up};
     // one row: the gate/up GEMV prepares x itself (no row prep launch); MDX_MLP_HPREP=1 keeps both
     // prep launches
+    const char* xpe = getenv("MDX_MLP_XPREP");  // MDX_MLP_XPREP=1: the x prep launch at one row too (A/B)
     const bool xp = hr && rows == 1 && gemv_xp_fits(gu, 2, true) && aligned(xn, 16) &&
-                    (!norm_w || aligned(norm_w, 16));  // (the row and its weights are DMA'd in 16-byte pieces)
+                    (!norm_w || aligned(norm_w, 16)) &&  // (the row and its weights are DMA'd in 16-byte pieces)
+                    !(xpe && atoi(xpe) != 0);
     if (!xp) {
         PrepArgs pa{xn, norm_w, eps, nullptr, h, rot, w.q1, w.s, int(K1)};
         if ((rc = launch_prep(pa, rows, st))) return rc;

@@ -12,6 +12,7 @@ from __future__ import annotations
 import ctypes
 import math
 import os
+import weakref
 
 import torch
 
@@ -30,6 +31,27 @@ def _dev(t, what):
     _check(isinstance(t, torch.Tensor) and t.is_cuda, f"{what} must be a tensor on the ROCm device")
 
 
+_CB_SEEN = {}  # id(codebook tensor) -> (weak reference to it, its _version, holds code - 8)
+_CB_DEFAULT = torch.arange(-8, 8, dtype=torch.float32)
+
+
+def _codebook(cb):
+    """cb, or None when it holds the default codebook code - 8: libmdx then knows the table's symmetry (the
+    8-byte magnitude tables, the integral form). The values are read once per tensor object and version
+    (a host sync); while a graph is being captured an unseen tensor is passed as it is."""
+    if cb is None:
+        return None
+    hit = _CB_SEEN.get(id(cb))
+    if hit is None or hit[0]() is not cb or hit[1] != cb._version:
+        if cb.is_cuda and torch.cuda.is_current_stream_capturing():
+            return cb
+        if len(_CB_SEEN) > 4096:
+            _CB_SEEN.clear()
+        hit = (weakref.ref(cb), cb._version, bool(torch.equal(cb.detach().cpu(), _CB_DEFAULT)))
+        _CB_SEEN[id(cb)] = hit
+    return None if hit[2] else cb
+
+
 def _w4(q, s, sc, cb, tiled=False) -> W4:
     _dev(q, "packed W4")
     _check(q.dtype in (torch.int8, torch.uint8) and q.dim() == 2 and q.is_contiguous(),
@@ -40,7 +62,7 @@ def _w4(q, s, sc, cb, tiled=False) -> W4:
     _check(sc.dtype == torch.float32 and sc.is_contiguous() and sc.numel() == q.shape[0], "s_channel f32 [N]")
     if cb is not None:
         _check(cb.dtype == torch.float32 and cb.numel() == 16 and cb.is_contiguous(), "codebook f32 [16]")
-    return W4(q, s, sc, cb, _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW, _lib.DECODE_AUTO)
+    return W4(q, s, sc, _codebook(cb), _lib.LAYOUT_TILE if tiled else _lib.LAYOUT_ROW, _lib.DECODE_AUTO)
 
 
 def w4a8_decode_linear(x, x_scale, packed, s_rel, s_channel, codebook=None, residual=None, group_size=16,
@@ -426,6 +448,16 @@ def attn_exact(q, key, value, seqlen, xk, xv, mask, out=None):
               _lib.ptr(mask) if merge else None, _lib.ptr(out), H, Hk, S, D, cap, float(1.0 / math.sqrt(D)),
               _lib.stream_of(q))
     return out
+
+
+def attn_core(q, key, value, seqlen, xk, xv, mask, nwg=0, out=None):
+    """Reference csrc/attn_port.sycl:355-365 (exported as _C.attn_core, csrc/bindings.cpp:81): the attention
+    that comfy_mono_decode_xpu/layer.py:428 calls when its fused attention path is switched off
+    (MONO_DECODE_XPU_ATTN_DPAS=0), the result that its tests compare bit for bit. Here it is the exact
+    attention (mdx_attn_exact: one canonical fp32 order), with attn_dpas's operands and its bf16
+    [1, S, H * D] output. nwg steers the reference's launch geometry (negative: its phase clocks) and is
+    accepted and ignored."""
+    return attn_exact(q, key, value, seqlen, xk, xv, mask, out)
 
 
 def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0, out=None):

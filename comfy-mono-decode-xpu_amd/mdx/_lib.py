@@ -112,6 +112,7 @@ SIGNATURES = {
     "mdx_draft_norm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int32, c_void_p,
                                                 c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_stream_read": (ctypes.c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
+    "mdx_gemv_trace": (c_int32, [c_void_p, c_int32]),
     "mdx_check_bf16_round": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
     "mdx_draft_pick_workspace": (c_size_t, []),
     "mdx_draft_pick": (ctypes.c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int32,
@@ -150,6 +151,25 @@ def call(name, *args):
         msg = lib().mdx_last_error().decode(errors="replace")
         raise MdxError(f"{name}: {msg}")
     return rc
+
+
+SRC_Q8, SRC_HR, SRC_XP = 0, 1, 2
+SRC_INT_ONLY, SRC_TBL, SRC_TBL8 = 4, 8, 16
+
+
+def gemv_trace():
+    """The GEMV kernel variants this thread launched since the previous call (mdx_gemv_trace): a list of
+    dicts {mfma, src (SRC_Q8 / SRC_HR / SRC_XP), decode ("integral", "table16", "table8" or "generic"),
+    s_dtype, rows, tpw, ks}."""
+    buf = (c_int32 * (6 * 64))()
+    n = lib().mdx_gemv_trace(buf, 64)
+    out = []
+    for i in range(min(n, 64)):
+        mfma, src, sdt, rows, tpw, ks = buf[6 * i:6 * i + 6]
+        dec = ("integral" if src & SRC_INT_ONLY else "table16" if src & SRC_TBL else "table8" if src & SRC_TBL8
+               else "generic")
+        out.append(dict(mfma=bool(mfma), src=src & 3, decode=dec, s_dtype=sdt, rows=rows, tpw=tpw, ks=ks))
+    return out
 
 
 def stream_of(t: torch.Tensor):

@@ -15,11 +15,11 @@ Three pieces, each installed on its own (one that fails to install is logged and
            past_key_value)` for 1..16 decode rows: layer_pre -> Q/K norm + RoPE + KV write -> tree
            attention -> layer_post for attention blocks, layer_gdn for Gated-DeltaNet blocks.
 
-Failures follow the reference's rule (guard.py): an error before any state was modified switches the
-piece off and runs the original; an error after a write (KV rows, the recurrent state, x in place) switches
-it off and re-raises, since replaying the block would apply it twice. A sub-path that has already
-switched itself off raises SubpathError, which leaves the piece on. stats() counts the calls each piece
-took and, per reason, those it left to the host.
+Failures follow the breaker rule of mdx/guard.py (the reference's contract, comfy_mono_decode_xpu/guard.py:
+30-43): an error before any state was modified switches the piece off and runs the original; an error
+after a write (KV rows, the recurrent state, x in place) switches it off and re-raises, since replaying the
+block would apply it twice. A sub-path that has already switched itself off raises SubpathError, which
+leaves the piece on. stats() counts the calls each piece took and, per reason, those it left to the host.
 
 Switches (environment): MDX_DECODE=0 turns every piece off; MDX_DECODE_<PIECE>=1/0 (W4, MONO, LAYER)
 overrides it per piece.
@@ -40,6 +40,7 @@ from __future__ import annotations
 import logging
 import os
 import threading
+from typing import NamedTuple
 
 import torch
 
@@ -51,9 +52,10 @@ PIECES = ("W4", "MONO", "LAYER")
 _lock = threading.Lock()
 _stats = {p: {"fast": 0, "fallback": {}} for p in ("w4", "mono", "layer")}
 _consts = {}
+UNCOUNTED = ""  # a route's miss that stats() does not count (inputs that are plainly not a decode call)
 
 
-class SubpathError(RuntimeError):
+class SubpathError(guard.PassThrough):
     """A sub-path failed after writing state and has switched itself off; the block is not replayed."""
 
 
@@ -69,15 +71,14 @@ def reset_stats():
             d["fallback"].clear()
 
 
-def _fast(piece):
+def _count(piece, why=None):
+    """One call of `piece` taken by the fast path (why None) or left to the host for `why`."""
     with _lock:
-        _stats[piece]["fast"] += 1
-
-
-def _fallback(piece, why):
-    with _lock:
-        f = _stats[piece]["fallback"]
-        f[why] = f.get(why, 0) + 1
+        d = _stats[piece]
+        if why is None:
+            d["fast"] += 1
+        elif why != UNCOUNTED:
+            d["fallback"][why] = d["fallback"].get(why, 0) + 1
 
 
 def _lib_C():
@@ -101,70 +102,112 @@ def _compiling():
     return bool(comp is not None and getattr(comp, "is_compiling", lambda: False)())
 
 
+def _dispatch(piece, why, fast, host):
+    """host() when the piece is switched off or the route missed (`why`: the reason, or UNCOUNTED), else
+    fast(progress) under the piece's breaker, counted when it answers."""
+    if why is not None:
+        _count(piece, why)
+        return host()
+
+    def counted(progress):
+        out = fast(progress)
+        _count(piece)
+        return out
+
+    return guard.shielded(piece, counted, host)
+
+
+def _claim(wrapper, original):
+    setattr(wrapper, CLAIM, True)
+    wrapper.__wrapped__ = original
+    return wrapper
+
+
 # ---------------------------------------------------------------------------------------------------
 # the W4A8 linear entry
 # ---------------------------------------------------------------------------------------------------
-def linear_contract(x, x_scale, packed, s_rel, s_channel, codebook, bias, group_size, out_dtype):
-    """None when libmdx's W4A8 linear takes the call, else the reason (the reference's checks,
-    comfy_mono_decode_xpu/patch.py:32-55, with this library's limits: 1..16 rows, K % 128, power-of-two
-    groups of at least 16, fp32 / fp16 / fp8 group scales)."""
-    if bias is not None:
-        return "bias"
-    if out_dtype not in (torch.bfloat16, torch.float32):
-        return "out_dtype"
-    if x.device.type != DEVICE_TYPE or x.dtype != torch.int8 or not x.is_contiguous():
-        return "x"
-    k = x.shape[-1]
-    rows = x.numel() // k if k else 0
-    if not 1 <= rows <= 16:
-        return "rows"
-    if k % 128 or k > 65536 or group_size < 16 or group_size & (group_size - 1) or k % group_size:
-        return "shape"
-    if (packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2 or not packed.is_contiguous()
-            or packed.shape[1] * 2 != k or packed.shape[0] % 16):
-        return "packed"
-    if packed.data_ptr() % 16 or x.data_ptr() % 16:
-        return "align"
-    if (s_rel.dtype not in (torch.float32, torch.float16, torch.float8_e4m3fn) or not s_rel.is_contiguous()
-            or s_rel.numel() != packed.shape[0] * (k // group_size)):
-        return "s_rel"
-    if s_channel.numel() != packed.shape[0]:
-        return "s_channel"
-    if codebook is not None and (codebook.dtype != torch.float32 or codebook.numel() != 16):
-        return "codebook"
-    if (x_scale.numel() != rows or any(t.device != x.device for t in (x_scale, packed, s_rel, s_channel))
-            or (codebook is not None and codebook.device != x.device)):
-        return "operands"
+class LinearCall(NamedTuple):
+    """The arguments of the host's W4A8 linear entry, by name."""
+    x: torch.Tensor
+    x_scale: torch.Tensor
+    packed: torch.Tensor
+    s_rel: torch.Tensor
+    s_channel: torch.Tensor
+    codebook: torch.Tensor | None
+    bias: torch.Tensor | None
+    group_size: int
+    out_dtype: torch.dtype
+
+    @property
+    def k(self):
+        return self.x.shape[-1]
+
+    @property
+    def rows(self):
+        return self.x.numel() // self.k if self.k else 0
+
+
+_OUT_CODE = {torch.float32: 0, torch.bfloat16: 2}  # libmdx's output dtype codes
+
+
+def _pow2(v):
+    return v > 0 and v & (v - 1) == 0
+
+
+# The linear contract as (reason, test that the call breaks it), checked in this order: the output the
+# host asked for, the activation, the geometry, the weight tensors, then where the operands live
+# (the reference's checks, comfy_mono_decode_xpu/patch.py:32-55, with this library's limits: 1..16 rows,
+# K % 128, power-of-two groups of at least 16, fp32 / fp16 / fp8 group scales).
+_LINEAR_RULES = (
+    ("bias", lambda c: c.bias is not None),
+    ("out_dtype", lambda c: c.out_dtype not in _OUT_CODE),
+    ("x", lambda c: c.x.device.type != DEVICE_TYPE or c.x.dtype != torch.int8 or not c.x.is_contiguous()),
+    ("rows", lambda c: not 1 <= c.rows <= 16),
+    ("shape", lambda c: c.k % 128 or c.k > 65536 or c.group_size < 16 or not _pow2(c.group_size)
+     or c.k % c.group_size),
+    ("packed", lambda c: c.packed.dtype not in (torch.int8, torch.uint8) or c.packed.dim() != 2
+     or not c.packed.is_contiguous() or c.packed.shape[1] * 2 != c.k or c.packed.shape[0] % 16),
+    ("align", lambda c: c.packed.data_ptr() % 16 or c.x.data_ptr() % 16),
+    ("s_rel", lambda c: c.s_rel.dtype not in (torch.float32, torch.float16, torch.float8_e4m3fn)
+     or not c.s_rel.is_contiguous() or c.s_rel.numel() != c.packed.shape[0] * (c.k // c.group_size)),
+    ("s_channel", lambda c: c.s_channel.numel() != c.packed.shape[0]),
+    ("codebook", lambda c: c.codebook is not None and (c.codebook.dtype != torch.float32 or c.codebook.numel() != 16)),
+    ("operands", lambda c: c.x_scale.numel() != c.rows
+     or any(t is not None and t.device != c.x.device for t in (c.x_scale, c.packed, c.s_rel, c.s_channel, c.codebook))),
+)
+
+
+def linear_contract(*args):
+    """None when libmdx's W4A8 linear takes the call (the host's positional arguments), else the first
+    reason it does not."""
+    call = LinearCall(*args)
+    for why, breaks in _LINEAR_RULES:
+        if breaks(call):
+            return why
     return None
+
+
+def _linear_fast(call):
+    """The call through mdx_w4a8_decode_linear: rows flattened, the scales as contiguous f32 vectors."""
+    C = _lib_C()
+    out = C.w4a8_decode_linear(call.x.reshape(call.rows, call.k), call.x_scale.reshape(-1).float().contiguous(),
+                               call.packed, call.s_rel, call.s_channel.reshape(-1).float().contiguous(),
+                               call.codebook, None, call.group_size, _OUT_CODE[call.out_dtype])
+    return out.view(*call.x.shape[:-1], call.packed.shape[0])
 
 
 def wrap_linear(original):
     def w4a8_linear_prequantized(x_int8, x_scale, packed, relative_scale, channel_scale, codebook=None, bias=None,
                                  group_size=16, out_dtype=torch.bfloat16):
-        args = (x_int8, x_scale, packed, relative_scale, channel_scale, codebook, bias, group_size, out_dtype)
-        if guard.off("w4") or _compiling():
-            return original(*args)
-        why = linear_contract(*args)
-        if why is not None:
-            _fallback("w4", why)
-            return original(*args)
-        k = x_int8.shape[-1]
-        try:
-            C = _lib_C()
-            x2 = x_int8.reshape(-1, k)
-            xs = x_scale.reshape(-1).to(torch.float32).contiguous()
-            sc = channel_scale.reshape(-1).to(torch.float32).contiguous()
-            out = C.w4a8_decode_linear(x2, xs, packed, relative_scale, sc, codebook, None, group_size,
-                                       0 if out_dtype == torch.float32 else 2)
-        except Exception as e:  # a pure function of its inputs: the original recomputes it
-            guard.failed("w4", e)
-            return original(*args)
-        _fast("w4")
-        return out.reshape(*x_int8.shape[:-1], packed.shape[0])
+        call = LinearCall(x_int8, x_scale, packed, relative_scale, channel_scale, codebook, bias, group_size,
+                          out_dtype)
+        host = lambda: original(*call)  # noqa: E731
+        if not guard.BOARD.allows("w4") or _compiling():
+            return host()
+        # a pure function of its inputs: on a failure the host's entry recomputes the call
+        return _dispatch("w4", linear_contract(*call), lambda progress: _linear_fast(call), host)
 
-    setattr(w4a8_linear_prequantized, CLAIM, True)
-    w4a8_linear_prequantized.__wrapped__ = original
-    return w4a8_linear_prequantized
+    return _claim(w4a8_linear_prequantized, original)
 
 
 def install_w4(module, name="w4a8_linear_prequantized"):
@@ -209,35 +252,39 @@ def _norm_weight(norm):
 # ---------------------------------------------------------------------------------------------------
 # the MLP block
 # ---------------------------------------------------------------------------------------------------
+def _mlp_route(mod, x, norm):
+    """(None, packed parts) when the MLP block takes the call, else (reason, None)."""
+    if (norm is None or x.device.type != DEVICE_TYPE or x.dtype != torch.bfloat16 or x.shape[-1] != 4096
+            or not 1 <= x.numel() // x.shape[-1] <= 16):
+        return UNCOUNTED, None
+    lins = (mod.gate_proj, mod.up_proj, mod.down_proj)
+    parts = _cached(mod, "_mdx_mlp", tuple(id(getattr(l, "weight", None)) for l in lins),
+                    lambda: [_w4_of(l) for l in lins])
+    if any(p is None for p in parts):
+        return "weights", None
+    cb = parts[0][3]
+    if not all(torch.equal(cb, p[3]) for p in parts[1:]):
+        return "codebook", None  # the block decodes its three projections with one table
+    return None, parts
+
+
 def wrap_mlp(original):
     def forward(self, x, norm=None):
-        if (guard.off("mono") or norm is None or x.device.type != DEVICE_TYPE or x.dtype != torch.bfloat16
-                or x.shape[-1] != 4096 or not 1 <= x.numel() // x.shape[-1] <= 16):
-            return original(self, x, norm=norm)
-        lins = (self.gate_proj, self.up_proj, self.down_proj)
-        key = tuple(id(getattr(l, "weight", None)) for l in lins)
-        parts = _cached(self, "_mdx_mlp", key, lambda: [_w4_of(l) for l in lins])
-        if any(p is None for p in parts):
-            _fallback("mono", "weights")
-            return original(self, x, norm=norm)
-        if not (torch.equal(parts[0][3], parts[1][3]) and torch.equal(parts[0][3], parts[2][3])):
-            _fallback("mono", "codebook")
-            return original(self, x, norm=norm)
-        try:
+        host = lambda: original(self, x, norm=norm)  # noqa: E731
+        if not guard.BOARD.allows("mono"):
+            return host()
+        why, parts = _mlp_route(self, x, norm)
+
+        def fast(progress):  # writes nothing: the host's forward recomputes from x on a failure
             C = _lib_C()
             h, lut, _ = _constants(x.device)
-            xn = norm(x)
-            out = C.mono_mlp(xn.reshape(-1, x.shape[-1]).contiguous(), h, lut, *parts[0], *parts[1], *parts[2], 0, 4,
-                             False)
-        except Exception as e:  # nothing was written: the original recomputes from x
-            guard.failed("mono", e)
-            return original(self, x, norm=norm)
-        _fast("mono")
-        return out.reshape(*x.shape[:-1], out.shape[-1])
+            rows = norm(x).reshape(-1, x.shape[-1]).contiguous()
+            out = C.mono_mlp(rows, h, lut, *parts[0], *parts[1], *parts[2], 0, 4, False)
+            return out.reshape(*x.shape[:-1], out.shape[-1])
 
-    setattr(forward, CLAIM, True)
-    forward.__wrapped__ = original
-    return forward
+        return _dispatch("mono", why, fast, host)
+
+    return _claim(forward, original)
 
 
 def install_mono(MLP):
@@ -297,65 +344,74 @@ def attn_core(mix, q, k, v, freqs, kv):
     return C.attn_dpas(qo, kv.key, kv.value, kv.seqlen, ko, vv.transpose(1, 2), kv.mask, 0).view(S, H * D)
 
 
-def _run(block, plan, x, S, freqs_cis, kv, state):
+def _run_gdn(block, plan, x2, kv, progress):
     C = _lib_C()
-    h, silu, sig = _constants(x.device)
-    x2 = x.view(S, 4096)
+    h, silu, _ = _constants(x2.device)
+    mix, ex = block.linear_attn, plan["extra"]
     (nin, ein), (npo, epo) = plan["norm_in"], plan["norm_post"]
-    if plan["gdn"]:
-        mix, ex = block.linear_attn, plan["extra"]
-        args = (x2, nin, ein, h, plan["pre"] + plan["out"] + plan["mlp"], ex["wa"], ex["wb"], ex["conv_w"],
+    progress.wrote()  # the one launch writes x, the conv history and the recurrent state
+    C.layer_gdn(x2, nin, ein, h, plan["pre"] + plan["out"] + plan["mlp"], ex["wa"], ex["wb"], ex["conv_w"],
                 kv.conv_state, kv.proj_buf, kv.qkv_buf, kv.ctl, kv.dt_bias, kv.g_decay, kv.recurrent_state,
                 kv.gates_buf, kv.sumsq_buf, kv.norm_weight, mix.norm.eps, mix.key_head_dim ** -0.5, mix.num_key_heads,
                 npo, epo, silu, 0, 11, False)
-        state["mutated"] = True  # marked before the launch: a failure does not prove that nothing ran
-        C.layer_gdn(*args)
-        return x, kv
-    outs = C.layer_pre(x2, nin, ein, h, plan["pre"], 0, False)
-    state["mutated"] = True  # the attention core writes KV rows before attending
-    y = attn_core(block.self_attn, outs[1], outs[2], outs[3], freqs_cis, kv)
-    # the gate half of each head's [query | gate] block, as a plain [S, heads * head_dim] gate
+
+
+def _run_attention(block, plan, x2, S, freqs_cis, kv, progress):
+    C = _lib_C()
+    h, silu, sig = _constants(x2.device)
     mix = block.self_attn
-    gate = (outs[1].view(S, mix.num_heads, 2, mix.head_dim)[:, :, 1].reshape(S, -1).contiguous()
-            if plan["gated"] else None)
+    (nin, ein), (npo, epo) = plan["norm_in"], plan["norm_post"]
+    outs = C.layer_pre(x2, nin, ein, h, plan["pre"], 0, False)  # pure: nothing written yet
+    progress.wrote()  # from here on KV rows, then x in place
+    y = attn_core(mix, outs[1], outs[2], outs[3], freqs_cis, kv)
+    gate = None
+    if plan["gated"]:  # the gate half of each head's [query | gate] block, as a plain [S, heads * head_dim] gate
+        gate = outs[1].view(S, mix.num_heads, 2, mix.head_dim)[:, :, 1].reshape(S, -1).contiguous()
     C.layer_post(x2, y.contiguous(), gate, sig, *plan["out"], npo, epo, h, silu, *plan["mlp"], 0, 6, False)
-    return x, kv
+
+
+def _block_route(block, x, attention_mask, kv, max_rows):
+    """(None, plan, rows) when the decoder block takes the call, else (reason, None, 0)."""
+    miss = (UNCOUNTED, None, 0)
+    if kv is None or x.device.type != DEVICE_TYPE or x.dtype != torch.bfloat16 or x.dim() != 3:
+        return miss
+    B, S = x.shape[0], x.shape[1]
+    if B != 1 or not 1 <= S <= max_rows or x.shape[-1] != 4096 or not x.is_contiguous():
+        return miss
+    if getattr(block, "layer_type", None) == "linear_attention":
+        if not kv.decode_step(S):  # the cache's own judgement: a prefill chunk is not a decode step
+            return miss
+    else:
+        mix = block.self_attn
+        if attention_mask is not None or (mix.num_heads // mix.num_kv_heads) * S > 64:
+            return miss
+    key = tuple(id(getattr(m, "weight", None)) for m in _block_linears(block))
+    plan = _cached(block, "_mdx_plan", key, lambda: static_plan(block))
+    if plan is None:
+        return "weights", None, 0
+    return None, plan, S
 
 
 def wrap_block(original, max_rows=16):
     def forward(self, x, attention_mask=None, freqs_cis=None, optimized_attention=None, past_key_value=None):
-        args = (self, x, attention_mask, freqs_cis, optimized_attention, past_key_value)
-        B, S = (x.shape[0], x.shape[1]) if x.dim() == 3 else (0, 0)
-        if (guard.off("layer") or past_key_value is None or x.device.type != DEVICE_TYPE or x.dtype != torch.bfloat16
-                or B != 1 or not 1 <= S <= max_rows or x.shape[-1] != 4096 or not x.is_contiguous()):
-            return original(*args)
-        gdn = getattr(self, "layer_type", None) == "linear_attention"
-        if gdn and not past_key_value.decode_step(S):
-            return original(*args)
-        if not gdn and (attention_mask is not None
-                        or (self.self_attn.num_heads // self.self_attn.num_kv_heads) * S > 64):
-            return original(*args)
-        key = tuple(id(getattr(m, "weight", None)) for m in _block_linears(self))
-        plan = _cached(self, "_mdx_plan", key, lambda: static_plan(self))
-        if plan is None:
-            _fallback("layer", "weights")
-            return original(*args)
-        state = {"mutated": False}
-        try:
-            out = _run(self, plan, x, S, freqs_cis, past_key_value, state)
-        except SubpathError:
-            raise  # that sub-path is already off; state may be written, so the block is not replayed
-        except Exception as e:
-            guard.failed("layer", e, can_fallback=not state["mutated"])
-            if state["mutated"]:
-                raise  # KV rows, the recurrent state or x already changed: replaying would apply them twice
-            return original(*args)
-        _fast("layer")
-        return out
+        host = lambda: original(self, x, attention_mask, freqs_cis, optimized_attention, past_key_value)  # noqa: E731
+        if not guard.BOARD.allows("layer"):
+            return host()
+        why, plan, S = _block_route(self, x, attention_mask, past_key_value, max_rows)
 
-    setattr(forward, CLAIM, True)
-    forward.__wrapped__ = original
-    return forward
+        def fast(progress):
+            x2 = x.view(S, 4096)
+            if plan["gdn"]:
+                _run_gdn(self, plan, x2, past_key_value, progress)
+            else:
+                _run_attention(self, plan, x2, S, freqs_cis, past_key_value, progress)
+            return x, past_key_value
+
+        # a failure after a write re-raises (replaying the block would apply it twice); SubpathError
+        # passes through: that sub-path is off already
+        return _dispatch("layer", why, fast, host)
+
+    return _claim(forward, original)
 
 
 def _block_linears(block):

@@ -281,6 +281,9 @@ class HybridModel:
         self.dtok = torch.zeros(7, 1, **i64)
         # auto: the 7 candidates of chain node k (the draft at depth k) at [7 k, 7 k + 7) for the accept's ranks
         self.cand = torch.zeros(7 * 7, **i64)
+        # every tree's device tensors, kept for the model's lifetime: a captured graph holds their
+        # addresses, and a tree may come back after another one (decode_auto, _set_tree)
+        self._trees = {}
         self._set_tree(c.widths)
         self.empty_mask = torch.empty(0, dtype=torch.int32, device=dev)
         self.graphs = {}
@@ -299,7 +302,9 @@ class HybridModel:
             raise ValueError(f"widths {widths}: 1..7 depths of 1..{7 if c.auto else 8} candidates within "
                              f"{c.slots} slots")
         self.widths = widths
-        self.tree = tree_tensors(widths, c.slots, self.dev)
+        if widths not in self._trees:
+            self._trees[widths] = tree_tensors(widths, c.slots, self.dev)
+        self.tree = self._trees[widths]
         R = self.R = self.tree["R"]
         b = self._rows
         self.vtok, self.toks, self.vpos = b["vtok"][:, :R], b["toks"][:, :R], b["vpos"][:, :R]

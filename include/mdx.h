@@ -443,9 +443,11 @@ int mdx_draft_pick_bf16(const uint16_t* approx, const uint16_t* x, const uint16_
  * output, computed in one canonical fp32 order (scores in dimension order, weights by a fixed exp
  * sequence, the normaliser by 64 ordered lane partials and a halving tree, o in token order; the oracle's
  * attention_exact restates it bit for bit). scale: the score scale (1/sqrt(D) in the callers).
- * Replaces: the role of the bit-identical attention port, csrc/attn_port.sycl:1-12 (selected by
- * MONO_DECODE_XPU_ATTN, comfy_mono_decode_xpu/layer.py:43,409); not its arithmetic (its upstream is
- * third-party). D in {64, 128, 256}, 1..16 rows, cap + rows <= 16384. */
+ * Replaces: _C.attn_core (csrc/bindings.cpp:81, csrc/attn_port.sycl:355-365; called by
+ * comfy_mono_decode_xpu/layer.py:428) in the role of the bit-identical attention port, csrc/attn_port.sycl:1-12
+ * (selected by MONO_DECODE_XPU_ATTN, comfy_mono_decode_xpu/layer.py:43,409); not its arithmetic (its upstream
+ * is third-party). The Python mirror exposes it as _C.attn_core and _C.attn_exact. D in {64, 128, 256},
+ * 1..16 rows, cap + rows <= 16384. */
 int mdx_attn_exact(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* key,
                    const uint16_t* value, const int32_t* seqlen, const uint16_t* xk, int64_t xk_head_stride,
                    int64_t xk_row_stride, const uint16_t* xv, int64_t xv_head_stride, int64_t xv_row_stride,
@@ -458,6 +460,14 @@ int mdx_attn_exact(const uint16_t* q, int64_t q_head_stride, int64_t q_row_strid
  * counterpart in the reference: it measures the read roof a single launch of a given size reaches,
  * beside the 8 TB/s spec figure. */
 int mdx_stream_read(const void* src, int64_t bytes, int32_t work_groups, uint32_t* sink, void* stream);
+
+/* Diagnostics: the GEMV kernel variants this thread launched since the previous call (at most 64 kept),
+ * as records of six int32: [MFMA kernel (0/1), source (0 int8 rows, 1 bf16 rows quantised in the
+ * prologue, 2 one row prepared in the prologue; + 4 integral decode only, + 8 per-weight 16-byte tables
+ * only, + 16 per-weight 8-byte tables only), scale dtype (MDX_DT_*), rows, tiles per work-group, K
+ * slices]. Up to max_records records are copied to out; returns how many launches were recorded, and
+ * starts a new record. No counterpart in the reference: it lets tests name the decode path a shape takes. */
+int32_t mdx_gemv_trace(int32_t* out, int32_t max_records);
 
 /* Self-check of this library's fp32 -> bf16 rounding (the hardware conversion behind every bf16 result):
  * compares it with the integer round-to-nearest-even formulation (NaN -> 0x7FC0) over all 2^32 fp32 bit

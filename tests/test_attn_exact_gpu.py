@@ -72,3 +72,21 @@ def test_decode_with_exact_attention(dev):
     m.capture()
     m.replay(2)
     torch.cuda.synchronize()
+
+
+def test_attn_core_is_the_reference_name_of_the_exact_attention(C, dev):
+    """_C.attn_core with the reference's positional arguments (q, key, value, seqlen, xk, xv, mask, nwg), as
+    comfy_mono_decode_xpu/layer.py:428 calls it: the exact attention, bit for bit against the oracle, for a
+    tree-verify call and a draft row (empty mask)."""
+    g = torch.Generator().manual_seed(11)
+    for H, Hk, S, D, L, cap, tree in ((32, 8, 8, 128, 400, 420, True), (32, 8, 1, 128, 99, 128, False)):
+        print(f"case attn_core H={H} S={S} L={L}", flush=True)
+        q, k, v, xk, xv = _inputs(g, H, Hk, S, D, cap, dev)
+        mask = ref.tree_mask([-1] + list(range(S - 1))) if tree else None
+        md = torch.tensor(mask if tree else [], dtype=torch.int32, device=dev)
+        seq = torch.tensor([L], dtype=torch.int32, device=dev)
+        out = C.attn_core(q.to(dev), k.to(dev), v.to(dev), seq, xk.to(dev), xv.to(dev), md, 0)
+        assert out.shape == (1, S, H * D) and out.dtype == torch.bfloat16
+        want = ref.attention_exact(bits(q)[0], bits(k)[0], bits(v)[0], L, bits(xk)[0], bits(xv)[0], mask,
+                                   np.float32(1.0 / np.sqrt(D)))
+        assert_bits_equal(bits(out)[0], want, "attn_core")

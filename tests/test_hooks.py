@@ -15,11 +15,12 @@ import torch
 def hk(monkeypatch):
     from mdx import guard, hooks
     monkeypatch.setattr(hooks, "DEVICE_TYPE", "cpu")
-    monkeypatch.setattr(guard, "_off", {})
+    guard.BOARD.clear()
     hooks.reset_stats()
     fake = types.SimpleNamespace(calls=[])
     monkeypatch.setattr(hooks, "_lib_C", lambda: fake)
-    return hooks, guard, fake
+    yield hooks, guard, fake
+    guard.BOARD.clear()
 
 
 def _linear_args(rows=2, N=32, K=256, G=16):
@@ -58,7 +59,7 @@ def test_linear_routes_the_contract_and_counts_reasons(hk):
         assert f(*a) == "host", why
     st = hooks.stats()["w4"]
     assert st["fast"] == 1 and st["fallback"] == {k: 1 for k in cases}
-    assert not guard.off("w4")
+    assert guard.BOARD.allows("w4")
 
 
 def test_linear_failure_falls_back_and_switches_off(hk, caplog):
@@ -74,7 +75,7 @@ def test_linear_failure_falls_back_and_switches_off(hk, caplog):
     with caplog.at_level(logging.WARNING):
         assert f(*_linear_args()) == "host"
         assert f(*_linear_args()) == "host"
-    assert guard.off("w4") and n["fast"] == 1
+    assert not guard.BOARD.allows("w4") and n["fast"] == 1
     assert caplog.text.count("w4 path failed") == 1
 
 
@@ -88,11 +89,11 @@ def test_interrupt_passes_through_and_switches_nothing_off(hk):
     f = hooks.wrap_linear(lambda *a: "host")
     with pytest.raises(KeyboardInterrupt):
         f(*_linear_args())
-    assert not guard.off("w4")
-    # an interrupt-type exception that reaches guard.failed is re-raised unchanged
+    assert guard.BOARD.allows("w4")
+    # an interrupt-type exception that reaches the board is re-raised unchanged
     with pytest.raises(KeyboardInterrupt):
-        guard.failed("w4", KeyboardInterrupt())
-    assert not guard.off("w4")
+        guard.BOARD.trip("w4", KeyboardInterrupt())
+    assert guard.BOARD.allows("w4")
 
 
 class _P:
@@ -143,7 +144,7 @@ def test_mlp_block_routes_and_falls_back(hk):
         raise RuntimeError("LDS overflow")
 
     fake.mono_mlp = broken
-    assert fwd(_MLP(), x, norm) == "host" and guard.off("mono")
+    assert fwd(_MLP(), x, norm) == "host" and not guard.BOARD.allows("mono")
     fake.mono_mlp = lambda *a: pytest.fail("a piece that is off must not be called")
     assert fwd(_MLP(), x, norm) == "host"
 
@@ -237,17 +238,17 @@ def test_decoder_block_state_writes_are_not_replayed(hk, failure):
         if failure is None:
             assert out[0] is x and out[1] is kv and blk.host_calls == 0
             assert fake.calls == [("pre", 12), ("post", True, 4 + 2 + 2 + 12 + 3)]  # gated q: the gate goes in
-            assert hooks.stats()["layer"]["fast"] == 1 and not guard.off("layer")
+            assert hooks.stats()["layer"]["fast"] == 1 and guard.BOARD.allows("layer")
             assert kv.key.max().item() == 1 and x.max().item() == 1
         else:
-            assert out == "host" and blk.host_calls == 1 and guard.off("layer")
+            assert out == "host" and blk.host_calls == 1 and not guard.BOARD.allows("layer")
             assert kv.key.max().item() == 0
         return
     with pytest.raises(RuntimeError, match="after state write"):
         fwd(blk, x, past_key_value=kv)
     assert blk.host_calls == 0 and kv.key.max().item() == 1  # written once, never replayed
     assert x.max().item() == int(failure == "x")
-    assert guard.off("layer") == (failure != "subpath")
+    assert (not guard.BOARD.allows("layer")) == (failure != "subpath")
 
 
 def test_decoder_block_inputs_outside_the_contract_run_the_host(hk):
@@ -326,3 +327,36 @@ def test_install_switches_idempotence_and_isolation(hk, monkeypatch, caplog):
     mod4 = types.SimpleNamespace(w4a8_linear_prequantized=lambda *a: "host")
     assert hooks.install(mod4, None, None, env={}) == {}
     assert not getattr(mod4.w4a8_linear_prequantized, hooks.CLAIM, False)
+
+
+def test_board_rule_directly(caplog):
+    """The breaker rule on its own: a failure before a write answers from the host and trips the piece, one
+    log line per piece however often it fails; after a write the error propagates (still tripping); a
+    PassThrough error and an interrupt trip nothing; clear() switches a piece back on."""
+    from mdx import guard
+    board = guard.Board()
+    calls = []
+
+    def fails(wrote, exc=RuntimeError("boom")):
+        def fast(progress):
+            if wrote:
+                progress.wrote()
+            raise exc
+        return fast
+
+    host = lambda: calls.append("host") or "host"  # noqa: E731
+    with caplog.at_level(logging.WARNING):
+        assert guard.shielded("p", fails(False), host, board) == "host"
+        assert guard.shielded("p", fails(False), host, board) == "host"
+        with pytest.raises(RuntimeError, match="boom"):
+            guard.shielded("q", fails(True), host, board)
+    assert calls == ["host", "host"] and board.failures("p") == 2 and board.failures("q") == 1
+    assert caplog.text.count("p path failed") == 1 and caplog.text.count("q path failed") == 1
+    assert set(board.tripped()) == {"p", "q"} and not board.allows("p")
+    for exc in (guard.PassThrough("sub-path already off"), KeyboardInterrupt()):
+        with pytest.raises(type(exc)):
+            guard.shielded("r", fails(True, exc), host, board)
+    assert board.allows("r") and calls == ["host", "host"]
+    board.clear("p")
+    assert board.allows("p") and not board.allows("q")
+    assert guard.shielded("p", lambda progress: "fast", host, board) == "fast"

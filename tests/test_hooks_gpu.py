@@ -34,7 +34,7 @@ def _dense(lin):
 
 def test_w4_hook_matches_the_oracle(C, dev, monkeypatch):
     from mdx import guard, hooks
-    monkeypatch.setattr(guard, "_off", {})
+    guard.BOARD.clear()
     hooks.reset_stats()
     g = torch.Generator().manual_seed(2)
     lin = _kitchen(g, 1024, 4096, dev)
@@ -53,7 +53,7 @@ def test_w4_hook_matches_the_oracle(C, dev, monkeypatch):
 
 def test_mlp_hook_against_a_float32_host_forward(C, dev, monkeypatch):
     from mdx import guard, hooks, layout
-    monkeypatch.setattr(guard, "_off", {})
+    guard.BOARD.clear()
     hooks.reset_stats()
     g = torch.Generator().manual_seed(3)
     I = 2048
@@ -82,12 +82,12 @@ def test_mlp_hook_against_a_float32_host_forward(C, dev, monkeypatch):
         rel = ((got - want).norm() / want.norm()).item()
         assert rel < 3e-2, rel  # int8 activations (2 quantisations) against float32
         assert hooks.stats()["mono"]["fallback"] == {}
-    assert hooks.stats()["mono"]["fast"] >= 2 and not guard.off("mono")
+    assert hooks.stats()["mono"]["fast"] >= 2 and guard.BOARD.allows("mono")
 
 
 def test_attention_block_hook_equals_the_operators(C, dev, monkeypatch):
     from mdx import guard, hooks, layout
-    monkeypatch.setattr(guard, "_off", {})
+    guard.BOARD.clear()
     hooks.reset_stats()
     g = torch.Generator().manual_seed(4)
     S, H, Hk, D, cap, L = 4, 32, 8, 128, 256, 100

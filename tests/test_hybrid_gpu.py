@@ -182,3 +182,40 @@ def test_predictable_weights_commit_every_draft(dev, greedy):
         m.replay(1)
         torch.cuda.synchronize()
         check(3 + step)
+
+
+def test_tree_switch_and_back_replays_the_first_trees_graphs(dev):
+    """A -> B -> A: a model whose graphs were captured for tree A, then for tree B, replays A's graphs again
+    after switching back. Those graphs hold the addresses of A's tree tensors (masks, children, positions,
+    the verify program), so the tensors must still be A's: the replayed steps equal the same steps run
+    eagerly on a second model, with freed-memory reuse provoked in between."""
+    a, b = _model(dev), _model(dev)
+    A, B = (4, 3), (2, 2, 1)
+
+    def eager(m, n):
+        for _ in range(n):
+            m.step(m.parity)
+            m.parity ^= 1
+
+    print("case tree A capture + replay", flush=True)
+    b.capture()  # two eager warm-up steps, one per parity
+    b.replay(1)
+    eager(a, 3)
+    print("case tree B capture + replay", flush=True)
+    for m in (a, b):
+        m._set_tree(B)
+    # small allocations of every size the tree tensors have, filled with junk: a freed A tensor would be
+    # handed out again here and overwritten
+    junk = [torch.full((n,), -7, dtype=dt, device=dev) for n in (8, 16, 64, 256) for dt in (torch.int32, torch.int64)]
+    b.capture()
+    b.replay(1)
+    eager(a, 3)
+    print("case tree A again: replay of the first graphs", flush=True)
+    for m in (a, b):
+        m._set_tree(A)
+    b.replay(2)
+    eager(a, 2)
+    torch.cuda.synchronize()
+    del junk
+    assert torch.equal(a.st, b.st) and torch.equal(a.nt, b.nt) and torch.equal(a.result, b.result)
+    assert torch.equal(a.hbuf, b.hbuf) and torch.equal(a.ctl, b.ctl)

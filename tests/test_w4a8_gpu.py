@@ -67,7 +67,7 @@ def test_w4a8_decode_linear_matches_oracle(C, dev, N, K, fmt):
         assert_bits_equal(bits(out), oracle_linear(x, xs, w), f"{fmt} M={M}")
 
 
-@pytest.mark.parametrize("fmt", ["fp8g16", "gptq"])
+@pytest.mark.parametrize("fmt", ["fp8g16", "gptq", "gptq_rint"])
 def test_w4a8_residual_and_f32_out(C, dev, fmt):
     g = torch.Generator().manual_seed(11)
     N, K = 1024, 4096
@@ -83,19 +83,20 @@ def test_w4a8_residual_and_f32_out(C, dev, fmt):
         assert_bits_equal(bits(out32), oracle_linear(x, xs, w, None, "f32").view(np.uint32), "f32 out")
 
 
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_rint"])
 @pytest.mark.parametrize("tpw,ks", [(3, 4), (5, 2), (6, 1)])
-def test_w4a8_geometry_with_idle_tile_slots(C, dev, tpw, ks, monkeypatch):
+def test_w4a8_geometry_with_idle_tile_slots(C, dev, tpw, ks, monkeypatch, fmt):
     """Work-group geometries whose last work-group has tile slots past the matrix (256 tiles in
     groups of 3, 5, 6): the idle slots read inside the matrix and add nothing; every output equals
     the oracle's. (Regression: the idle slots once formed their weight addresses past the end.)"""
     g = torch.Generator().manual_seed(29 + tpw)
     N, K = 4096, 4096
-    w = random_w4(N, K, g, "gptq")
+    w = random_w4(N, K, g, fmt)
     wd = [t.to(dev) if t is not None else None for t in w[:4]]
     monkeypatch.setenv("MDX_GEMV_TPW", str(tpw))
     monkeypatch.setenv("MDX_GEMV_KS", str(ks))
     for M in (1, 8):
-        print(f"case idle slots tpw={tpw} ks={ks} M={M}", flush=True)
+        print(f"case idle slots fmt={fmt} tpw={tpw} ks={ks} M={M}", flush=True)
         x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
         xs = torch.rand(M, generator=g) * 0.05 + 1e-3
         out = C.w4a8_decode_linear(x.to(dev), xs.to(dev), *wd, None, w[4], 2, 0, False)
@@ -187,6 +188,35 @@ def test_mono_mlp_matches_oracle(C, dev, fmt, tiled, rot):
         assert_bits_equal(bits(out), want, f"M={M}")
 
 
+@pytest.mark.parametrize("tiled,rot", [(True, "none"), (False, "none"), (True, "h256"), (False, "h256")])
+def test_mono_mlp_faithful_scales_matches_oracle(C, dev, tiled, rot):
+    """The MLP block on the config's own weight format (GPTQ int4, fp16 G128 group scales kept as fp16 ratios
+    to the channel scale, decoded per weight by rint: reference csrc/w4a8_decode.sycl:35-45), 1, 2, 4, 8 and
+    16 rows, tile-major and row-major codes, with and without the rotation of h, against the oracle bit for
+    bit (reference tests/test_mono_mlp.py:14-50). Checks the kernels taken: the table-only MFMA variants,
+    at one row without rotation the gate/up with the row prep in its prologue and the down quantising h in
+    its prologue (16-byte tables), at eight rows the gate/up on 8-byte tables."""
+    from mdx import _lib, layout
+    g = torch.Generator().manual_seed(23)
+    ws, args = _mlp_weights(g, "gptq_rint", dev, tiled)
+    h = layout.regular_hadamard() if rot == "h256" else torch.eye(256).to(torch.bfloat16)
+    lut = layout.silu_lut()
+    d = _oracle_dicts(ws)
+    for M in (1, 2, 4, 8, 16):
+        print(f"case faithful mlp tiled={tiled} rot={rot} M={M}", flush=True)
+        xn = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        _lib.gemv_trace()
+        out = C.mono_mlp(xn.to(dev), h.to(dev), lut.to(dev), *args, 0, 4, tiled)
+        tr = _lib.gemv_trace()
+        want = ref.mono_mlp(bits(xn), rot, bits(h), bits(lut), *d)
+        assert_bits_equal(bits(out), want, f"M={M}")
+        assert tr and all(t["mfma"] and t["decode"] in ("table16", "table8") for t in tr), tr
+        if M == 1 and rot == "none":
+            assert [(t["src"], t["decode"]) for t in tr] == [(_lib.SRC_XP, "table16"), (_lib.SRC_HR, "table16")], tr
+        if M == 8:
+            assert tr[0]["decode"] == "table8" and tr[0]["tpw"] == 2, tr  # the gate/up pair
+
+
 @pytest.mark.parametrize("K", [4096, 12288])
 def test_rms_rot_quant_matches_oracle(C, dev, K):
     from mdx import _lib, layout
@@ -207,17 +237,18 @@ def test_rms_rot_quant_matches_oracle(C, dev, K):
                 assert_bits_equal(bits(s), ws.view(np.uint32), f"scale {kind} {name}")
 
 
-def test_mlp_with_norm_matches_oracle(C, dev):
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_rint"])
+def test_mlp_with_norm_matches_oracle(C, dev, fmt):
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(33)
-    ws, _ = _mlp_weights(g, "gptq", dev, True)
+    ws, _ = _mlp_weights(g, fmt, dev, True)
     handles = [layout.W4(layout.tile_major_codes(q).to(dev), s.to(dev), c.to(dev), None, _lib.LAYOUT_TILE)
                for q, s, c, _, _ in ws]
     lut = layout.silu_lut()
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
     d = _oracle_dicts(ws)
-    for M in (1, 4, 8):
-        print(f"case norm-mlp M={M}", flush=True)
+    for M in (1, 2, 4, 8, 16):
+        print(f"case norm-mlp fmt={fmt} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         out = C.mono_mlp_w4(x.to(dev), _lib.ROT_NONE, None, lut.to(dev), *handles, norm_w=nw.to(dev), eps=1e-6)
         xn = ref.rmsnorm(bits(x), bits(nw), 1e-6)
@@ -235,20 +266,22 @@ def _mlp_handles(g, dev, fmt="gptq"):
     return ws, handles
 
 
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_rint"])
 @pytest.mark.parametrize("rot", ["none", "h256"])
-def test_mlp_with_residual_matches_oracle(C, dev, rot):
+def test_mlp_with_residual_matches_oracle(C, dev, rot, fmt):
     """The MLP block with RMSNorm in front and a residual, for every row count class (one row, two,
-    up to eight, sixteen), with and without the rotation of h, against the oracle bit for bit."""
+    up to eight, sixteen), with and without the rotation of h, on integral and fp16-ratio group scales,
+    against the oracle bit for bit."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(41)
-    ws, handles = _mlp_handles(g, dev)
+    ws, handles = _mlp_handles(g, dev, fmt)
     lut = layout.silu_lut(dev)
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
     code = _lib.ROT_H256 if rot == "h256" else _lib.ROT_NONE
     h = layout.regular_hadamard(dev) if rot == "h256" else None
     d = _oracle_dicts(ws)
-    for M in (1, 2, 5, 8, 16):
-        print(f"case mlp-residual rot={rot} M={M}", flush=True)
+    for M in (1, 2, 4, 5, 8, 16):
+        print(f"case mlp-residual rot={rot} fmt={fmt} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         out = C.mono_mlp_w4(x.to(dev), code, h, lut, *handles, norm_w=nw.to(dev), eps=1e-6, residual=res.to(dev))
@@ -257,19 +290,20 @@ def test_mlp_with_residual_matches_oracle(C, dev, rot):
         assert_bits_equal(bits(out), want, f"M={M}")
 
 
-def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_rint"])
+def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch, fmt):
     """Without a rotation, at one or two rows, the down GEMV quantises h itself from gate/up's |h|
     maxima, and at one row the gate/up GEMV also prepares x itself (RMSNorm or none): the same
     outputs, bit for bit, as the row prep launches (MDX_MLP_HPREP=1), and as the oracle; with a
     residual, one to eight rows, over calls that reuse the workspace."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(47)
-    ws, handles = _mlp_handles(g, dev)
+    ws, handles = _mlp_handles(g, dev, fmt)
     lut = layout.silu_lut(dev)
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
     d = _oracle_dicts(ws)
     for M, norm in ((1, True), (1, False), (2, True), (5, True), (8, True), (3, True)):
-        print(f"case mlp-hr M={M} norm={norm}", flush=True)
+        print(f"case mlp-hr fmt={fmt} M={M} norm={norm}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         res = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
         nwd = nw.to(dev) if norm else None
@@ -285,19 +319,20 @@ def test_mlp_down_quantises_h_equals_row_prep(C, dev, monkeypatch):
         assert_bits_equal(bits(outs[0]), want, f"M={M} norm={norm}")
 
 
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_rint"])
 @pytest.mark.parametrize("rot", ["none", "h256"])
-def test_mlp_graph_replays(C, dev, rot):
+def test_mlp_graph_replays(C, dev, rot, fmt):
     """The MLP block captured once, replayed with new inputs between eager calls of the same block:
     every replay equals the eager result (no launch keeps state between calls)."""
     from mdx import _lib, layout
     g = torch.Generator().manual_seed(43)
-    _, handles = _mlp_handles(g, dev)
+    _, handles = _mlp_handles(g, dev, fmt)
     lut = layout.silu_lut(dev)
     code = _lib.ROT_H256 if rot == "h256" else _lib.ROT_NONE
     hd = layout.regular_hadamard(dev) if rot == "h256" else None
     nw = (1 + torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
     for M in (1, 2, 8):
-        print(f"case mlp graph rot={rot} M={M}", flush=True)
+        print(f"case mlp graph rot={rot} fmt={fmt} M={M}", flush=True)
         x = torch.randn(M, 4096, generator=g).to(torch.bfloat16).to(dev)
         out = torch.empty(M, 4096, dtype=torch.bfloat16, device=dev)
         C.mono_mlp_w4(x, code, hd, lut, *handles, norm_w=nw, eps=1e-6, out=out)
