@@ -309,6 +309,7 @@ struct GemvArgs {
     int assume_int;       // MDX_DECODE_INTEGRAL (every matrix): the integral form without the check
     int pwo;              // per-wave one-shots (one int8 row, G128, assume_int): no work-group barrier
     int tbl;              // per-weight decode tables built once per work-group into LDS: 1 16-byte, 2 8-byte (gemv_table_bytes)
+    int red_alias;        // table-only variants with int8 rows: the split-K partials reuse the table region after the loop
     int epi;
     void* out[3];
     const void* res[3];
@@ -725,8 +726,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // flag | 32 zero bytes (the activation of MFMA rows past the last)
     uint8_t* xl = lds;
     uint8_t* sl = xl + ((a.rows * Kr + 1023) & ~1023);
+    // (table-only variants with int8 rows may keep the split-K partials in the table region, which is dead
+    // after the loop: no region of their own)
+    const bool ralias = (SRC & (SRC_TBL | SRC_TBL8)) != 0 && (SRC & 3) == SRC_Q8 && a.red_alias;
     int32_t* red = reinterpret_cast<int32_t*>(sl + ((a.TPW * 16 * seg + 1023) & ~1023));
-    float* prml = reinterpret_cast<float*>(red + (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows));
+    float* prml = reinterpret_cast<float*>(red + (ralias ? 0 : (MFMA ? a.TPW * a.KS * 64 * 4 : a.TPW * a.KS * 16 * a.rows)));
     int* mixed = reinterpret_cast<int*>(prml + 128);
     uint8_t* zeros = reinterpret_cast<uint8_t*>(mixed + 4);
 
@@ -832,6 +836,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // per-weight decode tables [g1 - g0][TPW x 16 rows] x 16 bytes (after the SRC_XP region; the rows of
     // a group adjacent, so the 16 rows a wave reads at once fall in distinct banks)
     uint4* tbl = reinterpret_cast<uint4*>(xs_l + (XP ? 4 * K : 0));
+    if (ralias) red = reinterpret_cast<int32_t*>(tbl);
     const bool tbl_on = TB || a.tbl != 0;  // (uniform; groups of at least one chunk, scales not asserted integral)
     const bool tbl8 = TB ? TB8 : a.tbl == 2;  // (uniform) 8-byte tables: the default codebook's magnitudes
     const int ngr = g1 - g0;
@@ -1162,6 +1167,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (ralias) __syncthreads();  // every wave is past its last table read
         int32_t* dst = red + ((ts * a.KS + slice) * 64 + lane) * 4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) dst[r] = acc[r];
@@ -1320,7 +1326,7 @@ size_t gemv_smem(const GemvArgs& a, bool mfma, int esz, int cu0, int ncu) {
     }
     const size_t seg = size_t(g1 - g0) * esz;
     size_t s = ((size_t(a.rows) * ncu * CHUNK_K + 1023) & ~size_t(1023)) + ((a.TPW * 16 * seg + 1023) & ~size_t(1023));
-    s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
+    if (!a.red_alias) s += mfma ? size_t(a.TPW) * a.KS * 64 * 4 * 4 : size_t(a.TPW) * a.KS * 16 * a.rows * 4;
     s += 128 * 4 + 16 + 32;  // parameters, flag, zeros
     if (a.xp_x) s += size_t(4) * a.K;  // SRC_XP: the bf16 row and its norm weights
     s += size_t(a.TPW) * 16 * (g1 - g0) * gemv_table_bytes(a);  // per-weight decode tables
@@ -1334,7 +1340,7 @@ int esz_of(int sdt) { return sdt == MDX_DT_F32 ? 4 : (sdt == MDX_DT_F16 ? 2 : 1)
 // The kernel variants this thread's GEMV launches took since the last mdx_gemv_trace call (a diagnostic for
 // tests: which source, decode form and product path a shape reaches).
 constexpr int TRACE_MAX = 64;
-thread_local int32_t g_trace[TRACE_MAX][6];
+thread_local int32_t g_trace[TRACE_MAX][7];
 thread_local int g_trace_n = 0;
 
 void trace_launch(bool mfma, int src, int sdt, const GemvArgs& a) {
@@ -1346,6 +1352,7 @@ void trace_launch(bool mfma, int src, int sdt, const GemvArgs& a) {
     r[3] = a.rows;
     r[4] = a.TPW;
     r[5] = a.KS;
+    r[6] = a.red_alias;
 }
 
 template <bool MFMA, int R, int SDT, int RING, int SRC>
@@ -1605,11 +1612,20 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     // the VALU to the decode).
     if (!a.assume_int && a.lgG >= 7) {
         const int per_cu = (wgs + 255) / 256;
-        for (int tb = 1; tb <= 2; ++tb) {  // 16-byte tables, else (default codebook) 8-byte ones
+        // 16-byte tables, with the split-K partials in the table region when that makes them fit (int8 rows,
+        // a table region at least the partials' size); else (default codebook) 8-byte ones
+        const size_t red_bytes = size_t(a.TPW) * a.KS * 64 * 4 * 4;
+        const int ngr = (a.K >> a.lgG);
+        const char* te = getenv("MDX_GEMV_TBL");  // MDX_GEMV_TBL=8: the 8-byte tier whenever it applies (tests)
+        for (int tb = te && atoi(te) == 8 && !a.cb ? 2 : 1; tb <= 2; ++tb) {
             if (tb == 2 && a.cb) break;
             a.tbl = tb;
-            const size_t sm = gemv_smem(a, true, esz);
-            if (int64_t(per_cu) * sm <= 160 * 1024) break;
+            if (int64_t(per_cu) * gemv_smem(a, true, esz) <= 160 * 1024) break;
+            if (tb == 1 && !ex.hr && !ex.xp_x && size_t(a.TPW) * 16 * ngr * 16 >= red_bytes) {
+                a.red_alias = 1;
+                if (int64_t(per_cu) * gemv_smem(a, true, esz) <= 160 * 1024) break;
+                a.red_alias = 0;
+            }
             a.tbl = 0;
         }
         if (a.tbl) mfma = true;
@@ -1647,7 +1663,7 @@ using namespace mdx;
 extern "C" int32_t mdx_gemv_trace(int32_t* out, int32_t max_records) {
     const int n = g_trace_n;
     for (int i = 0; i < n && i < max_records; ++i)
-        for (int j = 0; j < 6; ++j) out[6 * i + j] = g_trace[i][j];
+        for (int j = 0; j < 7; ++j) out[7 * i + j] = g_trace[i][j];
     g_trace_n = 0;
     return n;
 }

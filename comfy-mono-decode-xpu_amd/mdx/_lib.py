@@ -160,15 +160,16 @@ SRC_INT_ONLY, SRC_TBL, SRC_TBL8 = 4, 8, 16
 def gemv_trace():
     """The GEMV kernel variants this thread launched since the previous call (mdx_gemv_trace): a list of
     dicts {mfma, src (SRC_Q8 / SRC_HR / SRC_XP), decode ("integral", "table16", "table8" or "generic"),
-    s_dtype, rows, tpw, ks}."""
-    buf = (c_int32 * (6 * 64))()
+    s_dtype, rows, tpw, ks, red_alias}."""
+    buf = (c_int32 * (7 * 64))()
     n = lib().mdx_gemv_trace(buf, 64)
     out = []
     for i in range(min(n, 64)):
-        mfma, src, sdt, rows, tpw, ks = buf[6 * i:6 * i + 6]
+        mfma, src, sdt, rows, tpw, ks, alias = buf[7 * i:7 * i + 7]
         dec = ("integral" if src & SRC_INT_ONLY else "table16" if src & SRC_TBL else "table8" if src & SRC_TBL8
                else "generic")
-        out.append(dict(mfma=bool(mfma), src=src & 3, decode=dec, s_dtype=sdt, rows=rows, tpw=tpw, ks=ks))
+        out.append(dict(mfma=bool(mfma), src=src & 3, decode=dec, s_dtype=sdt, rows=rows, tpw=tpw, ks=ks,
+                        red_alias=bool(alias)))
     return out
 
 

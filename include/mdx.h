@@ -462,10 +462,11 @@ int mdx_attn_exact(const uint16_t* q, int64_t q_head_stride, int64_t q_row_strid
 int mdx_stream_read(const void* src, int64_t bytes, int32_t work_groups, uint32_t* sink, void* stream);
 
 /* Diagnostics: the GEMV kernel variants this thread launched since the previous call (at most 64 kept),
- * as records of six int32: [MFMA kernel (0/1), source (0 int8 rows, 1 bf16 rows quantised in the
+ * as records of seven int32: [MFMA kernel (0/1), source (0 int8 rows, 1 bf16 rows quantised in the
  * prologue, 2 one row prepared in the prologue; + 4 integral decode only, + 8 per-weight 16-byte tables
  * only, + 16 per-weight 8-byte tables only), scale dtype (MDX_DT_*), rows, tiles per work-group, K
- * slices]. Up to max_records records are copied to out; returns how many launches were recorded, and
+ * slices, split-K partials kept in the table region (0/1)]. Up to max_records records are copied to out
+ * (7 * max_records int32); returns how many launches were recorded, and
  * starts a new record. No counterpart in the reference: it lets tests name the decode path a shape takes. */
 int32_t mdx_gemv_trace(int32_t* out, int32_t max_records);
 

@@ -213,8 +213,28 @@ def test_mono_mlp_faithful_scales_matches_oracle(C, dev, tiled, rot):
         assert tr and all(t["mfma"] and t["decode"] in ("table16", "table8") for t in tr), tr
         if M == 1 and rot == "none":
             assert [(t["src"], t["decode"]) for t in tr] == [(_lib.SRC_XP, "table16"), (_lib.SRC_HR, "table16")], tr
-        if M == 8:
-            assert tr[0]["decode"] == "table8" and tr[0]["tpw"] == 2, tr  # the gate/up pair
+        if M == 8:  # the gate/up pair: 16-byte tables with the partials in the table region
+            assert tr[0]["decode"] == "table16" and tr[0]["tpw"] == 2 and tr[0]["red_alias"], tr
+
+
+def test_mono_mlp_faithful_scales_8_byte_tables(C, dev, monkeypatch):
+    """The 8-byte table tier (the default codebook's eight magnitudes, expanded per chunk), forced by
+    MDX_GEMV_TBL=8 where it applies: the MLP block on fp16-ratio scales at 1, 8 and 16 rows, bit for bit."""
+    from mdx import _lib, layout
+    monkeypatch.setenv("MDX_GEMV_TBL", "8")
+    g = torch.Generator().manual_seed(27)
+    ws, args = _mlp_weights(g, "gptq_rint", dev, True)
+    h = torch.eye(256).to(torch.bfloat16)
+    lut = layout.silu_lut()
+    d = _oracle_dicts(ws)
+    for M in (1, 8, 16):
+        print(f"case faithful mlp table8 M={M}", flush=True)
+        xn = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+        _lib.gemv_trace()
+        out = C.mono_mlp(xn.to(dev), h.to(dev), lut.to(dev), *args, 0, 4, True)
+        tr = _lib.gemv_trace()
+        assert_bits_equal(bits(out), ref.mono_mlp(bits(xn), "none", bits(h), bits(lut), *d), f"M={M}")
+        assert tr and all(t["decode"] == "table8" for t in tr), tr
 
 
 @pytest.mark.parametrize("K", [4096, 12288])
