@@ -243,8 +243,14 @@ SCALES_DATA = {
 
 # the gate/up kernel each scale form runs at 1 row (template arguments: MFMA, R, scale dtype, ring, source)
 GATEUP_KERNEL = {
-    "faithful": "gemv_kernel<false, 1, 1, 4, 0> (gate/up pair, int8 activation staged by DMA, per-weight decode)",
-    "integral": "gemv_kernel<false, 1, 1, 4, 4> (gate/up pair, int8 activation staged by DMA, integral decode only)",
+    "faithful": "gemv_kernel<true, 4, 1, 4, 8> (gate/up pair, int8 activation staged by DMA, per-weight decode through "
+                "16-byte LDS tables, products on v_mfma_i32_16x16x32_i8)",
+    "integral": "gemv_kernel<false, 1, 1, 4, 4> (gate/up pair, int8 activation staged by DMA, integral decode only, "
+                "v_dot4_i32_i8)",
+}
+LINEAR_KERNEL = {
+    "faithful": "gemv_kernel<true, 4, 1, 4, 8> (per-weight decode through 16-byte LDS tables, MFMA products)",
+    "integral": "gemv_kernel<false, 1, 1, 4, 4> (integral decode only, v_dot4_i32_i8)",
 }
 
 
@@ -372,7 +378,8 @@ def bench_linear(args, dev):
         "data": f"synthetic (seeded GPTQ int4 weights; {SCALES_DATA[args.scales]})",
         "config": {"workload": f"single W4A8 linear M={M} K=N=4096 G128, {ring_n}-copy weight ring", "rows": M,
                    "scales": args.scales, "algorithmic_bytes_per_step": per},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel", "achieved": round(per / t / 1e9, 2),
+        "roofline": {"bound": "hbm", "kernel": LINEAR_KERNEL[args.scales] if M == 1 else "gemv_kernel",
+                     "achieved": round(per / t / 1e9, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(per / t / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": pmc_traffic(f"linear_rows1_{args.scales}") if M == 1 else None, "avg_launch_us": round(t * 1e6, 3),
                      "single_launch_read_roof_gbs": read_roof("8.7MB")},
