@@ -493,8 +493,7 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     per = 3  # at most len(widths) + 1 tokens committed per step
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
-    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, gdn_fused=args.gdn_fused,
-                              gdn_side_gates=args.side_gates, predictable=getattr(args, "predictable", False),
+    cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, predictable=getattr(args, "predictable", False),
                               scales=args.scales)
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
@@ -662,8 +661,7 @@ def bench_gdn_layer(args, dev):
                     wa=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
                     wb=(torch.randn(HV, Hd, generator=gen, device=dev) * 0.02).bfloat16(),
                     conv_w=(torch.randn(C, 4, generator=gen, device=dev) * 0.5).bfloat16(),
-                    conv=torch.randn(2, C, 3, generator=gen, device=dev).bfloat16() if args.gdn_fused else
-                    torch.randn(C, 3, generator=gen, device=dev).bfloat16(),
+                    conv=torch.randn(C, 3, generator=gen, device=dev).bfloat16(),
                     pb=torch.zeros(2, S, C, **bf), qb=torch.zeros(2, S, C, **bf),
                     rec=torch.randn(HV, DH, DH, generator=gen, device=dev) * 0.1,
                     gates=torch.zeros(2, S, HV, 2, device=dev), sums=torch.zeros(2, S, HK, 2, device=dev))
@@ -692,7 +690,7 @@ def bench_gdn_layer(args, dev):
         q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
         _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
         _C.gdn_core(proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay,
-                    w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True, fused=args.gdn_fused)
+                    w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True)
         _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnw), 1e-6, _lib.ptr(core), None,
                   _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), M, HV * DH, _lib.stream_of(core))
         _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
@@ -704,7 +702,7 @@ def bench_gdn_layer(args, dev):
                  {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
                               f"{ring_n}-copy weight + state ring", "rows": M,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                  "launches_per_step": 5 if args.gdn_fused else 6})
+                  "launches_per_step": 6})
 
 
 def bench_read(args, dev):
@@ -770,8 +768,6 @@ def main():
     ap.add_argument("--two-stage", action="store_true", help="stack: drafts score the vocabulary with an int4 copy "
                                                                "of the lm_head and recompute their candidates exactly")
     ap.add_argument("--auto", action="store_true", help="stack: the adaptive tree (decode_auto)")
-    ap.add_argument("--gdn-fused", action="store_true", help="gdn_layer / stack: the one-launch GDN core")
-    ap.add_argument("--side-gates", action="store_true", help="stack: GDN gates on a second stream")
     ap.add_argument("--head", choices=["bf16", "int8"], default="bf16",
                     help="stack / lmhead: the bf16 lm_head or the int8 ConvRot one (W8A8)")
     ap.add_argument("--prompt", type=int, default=1024, help="stack: prompt tokens (prefilled, not timed)")

@@ -220,11 +220,6 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     }
 }
 
-// This step's gates alone (four work-groups per value head), for a launch beside the projection GEMV.
-__global__ __launch_bounds__(256) void gdn_gates_kernel(GdnArgs a) {
-    gdn_gates_part(a, blockIdx.x / 4, blockIdx.x % 4);
-}
-
 // The delta rule of value head h over the columns [16 cs, 16 cs + 16) of its state (eight work-groups
 // per head, one per CU: the columns are independent, and a thread's serial work per entry is 8 rows).
 // Wave w owns columns 4 w .. 4 w + 3; lane l holds state rows 8 rg .. 8 rg + 7 (rg = l / 4) of column
@@ -401,285 +396,6 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     }
 }
 
-// The whole core in one launch (mdx_gdn_core_fused). Work-group (value head h, column slice cs) as in
-// gdn_head_kernel; before its entries it runs, for this step's rows, the conv of the channels it reads --
-// q and k of its key head (256 channels, thread t one channel) and its 16 v columns (threads 0..15) --,
-// the q / k sums of squares of its key head and its head's gates (wave w: rows w, w + 4, ...). The
-// arithmetic of each value is gdn_conv_kernel's and gdn_gates_part's, so the results are those of the
-// two-launch core bit for bit. Stores that several work-groups could make are made by one: the q / k
-// channels (qb, pb, history) and the key head's sums by the first value head of the key head at slice 0,
-// the gates by slice 0 of each head; the v channels belong to one work-group each. The conv history is
-// double-buffered by parity ([2][C][3]: read [1 - p], written [p]), so no work-group reads a history
-// another one has already advanced.
-__global__ __launch_bounds__(2 * HT) void gdn_fused_kernel(GdnArgs a) {
-    __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
-    __shared__ float vvec[2 * MAXS][SC], rawc[MAXS][SC];
-    __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
-    __shared__ int ectl[2 + 3 * MAXS];
-    __shared__ uint32_t anct[MAXS];
-    __shared__ uint16_t prl[MAXS][2 * DH + SC];  // this step's projections of the work-group's channels
-    __shared__ float cq[MAXS][2 * DH];            // conv outputs: q (0..127), k (128..255) of the key head
-    __shared__ float cv[MAXS][SC];                // conv outputs of the work-group's v columns
-    __shared__ float tg[MAXS][2], tsq[MAXS][2];   // this step's gates of head h, sums of key head kh
-    const int t = threadIdx.x, lane = t % 64, wv = t / 64, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
-    const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
-    const int kh = h / (HV / HK);
-    const int64_t C = a.C;
-    const bool qk_writer = (h % (HV / HK)) == 0 && cs == 0;
-    // threads 0 .. HT - 1 run the conv and the head's entries; all 2 HT threads (8 waves) share the gates
-    const bool hd = t < HT;
-    // the state of this work-group's columns first (it does not depend on the control words)
-    const int col = (t / 64) * 4 + (lane & 3), rg = lane >> 2;
-    float st[HRPG];
-    float* rs = a.rec + (int64_t(h) * DH + (hd ? rg : 0) * HRPG) * DH + cs * SC + (hd ? col : 0);
-    if (hd)
-#pragma unroll
-        for (int r = 0; r < HRPG; ++r) st[r] = rs[r * DH];
-    if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
-    // this step's projections of the channels: thread t < 256 its q / k channel, t < 16 also a v column
-    const int cqk = t < DH ? kh * DH + t : KD + kh * DH + (t - DH);
-    const int cvc = 2 * KD + h * DH + cs * SC + (t < SC ? t : 0);
-    if (hd)
-#pragma unroll
-        for (int r = 0; r < MAXS; ++r) {
-            const int rr = (r < R ? r : R - 1) * C;
-            prl[r][t] = a.proj[rr + cqk];
-            if (t < SC) prl[r][2 * DH + t] = a.proj[rr + cvc];
-        }
-    __syncthreads();
-    const int pending = ectl[0], p = ectl[1];
-    if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // (uniform) invalid control words
-    const int* acc = ectl + 2;
-    const int* parent = ectl + 2 + S;
-    const int* prog = ectl + 2 + 2 * S;
-    // this step's gates of head h (wave w: rows w, w + 4, ...; rows R .. S - 1 get zeros)
-    for (int ts = wv; ts < S; ts += 2 * HT / 64) {
-        float decay = 0.f, beta = 0.f;
-        if (ts < R) gate_row(a, h, ts, lane, decay, beta);
-        if (lane == 0) {
-            tg[ts][0] = decay;
-            tg[ts][1] = beta;
-            if (cs == 0) {
-                a.gates[((p * S + ts) * HV + h) * 2] = decay;
-                a.gates[((p * S + ts) * HV + h) * 2 + 1] = beta;
-            }
-        }
-    }
-    // the ancestry of each row (gdn_conv_kernel's table)
-    if (t < R) {
-        int anc = t, miss = 0;
-        uint32_t code = 0;
-#pragma unroll
-        for (int d = 1; d <= CW; ++d) {
-            anc = anc >= 0 ? parent[anc] : -1;
-            anc = anc >= R ? -1 : anc;
-            miss += anc < 0;
-            code |= uint32_t(anc >= 0 ? anc : 16 + CW - miss) << (8 * (d - 1));
-        }
-        anct[t] = code;
-    }
-    __syncthreads();
-    // the conv of one channel (gdn_conv_kernel's arithmetic): history from [1 - p], outputs into LDS, and
-    // the owner's stores (history [p], qb / pb of this parity)
-    auto conv = [&](int c, int li, bool owner, float* outp, int ostride) {
-        uint16_t old[CW], prevacc[CW];
-        const uint16_t* hold = a.conv_state + ((1 - p) * C + c) * CW;
-#pragma unroll
-        for (int r = 0; r < CW; ++r) {
-            old[r] = hold[r];
-            const int j = pending + r - CW;
-            int slot = acc[j < 0 ? 0 : j];
-            slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
-            prevacc[r] = a.pb[((1 - p) * S + slot) * C + c];
-        }
-        float w[CW + 1];
-#pragma unroll
-        for (int d = 0; d <= CW; ++d) w[d] = bf2f(a.conv_w[c * (CW + 1) + d]);
-        uint16_t hist[CW];
-#pragma unroll
-        for (int r = 0; r < CW; ++r) {
-            const int j = pending + r;
-            hist[r] = j == 0 ? old[0] : (j == 1 ? old[1] : (j == 2 ? old[2] : prevacc[r]));
-        }
-        if (owner)
-#pragma unroll
-            for (int r = 0; r < CW; ++r) a.conv_state[(p * C + c) * CW + r] = hist[r];
-        for (int ts = 0; ts < S; ++ts) {
-            uint16_t out = 0;
-            if (ts < R) {
-                const uint32_t code = anct[ts];
-                float sum = fmaf(bf2f(prl[ts][li]), w[CW], 0.f);
-#pragma unroll
-                for (int d = 1; d <= CW; ++d) {
-                    const int src = (code >> (8 * (d - 1))) & 0xFF;
-                    const uint16_t hv = src == 16 ? hist[0] : (src == 17 ? hist[1] : hist[2]);
-                    const float v = src < 16 ? bf2f(prl[src][li]) : bf2f(hv);
-                    sum = fmaf(v, w[CW - d], sum);
-                }
-                const float y = bfround(sum);
-                out = f2bf(__fdiv_rn(y, __fadd_rn(1.f, expf(-y))));
-                outp[ts * ostride] = bf2f(out);
-            }
-            if (owner) {
-                a.qb[(p * S + ts) * C + c] = out;
-                a.pb[(p * S + ts) * C + c] = ts < R ? prl[ts][li] : uint16_t(0);
-            }
-        }
-    };
-    if (hd) conv(cqk, t, qk_writer, &cq[0][t], 2 * DH);
-    if (t < SC) conv(cvc, 2 * DH + t, true, &cv[0][t], SC);
-    __syncthreads();
-    // this step's sums of squares of the key head (wave 0: q, wave 1: k; gdn_conv_kernel's order)
-    if (wv < 2) {
-        for (int ts = 0; ts < R; ++ts) {
-            const float v0 = cq[ts][DH * wv + lane], v1 = cq[ts][DH * wv + 64 + lane];
-            float part = fmaf(v1, v1, __fmul_rn(v0, v0));
-            part = tree_sum64(part);
-            if (lane == 0) {
-                tsq[ts][wv] = part;
-                if (qk_writer) a.sums[((p * S + ts) * HK + kh) * 2 + wv] = part;
-            }
-        }
-    }
-    // the entries: the leading valid accepted slots (replayed when all `pending` are valid), then the
-    // leading program entries with a valid row (each wave ballots the same counts)
-    const bool v0 = lane < pending && acc[lane < S ? lane : 0] >= 0 && acc[lane < S ? lane : 0] < S;
-    const int E0 = __builtin_ctzll(~__ballot(v0));
-    const bool replayed = E0 == pending;
-    const int pl = prog[lane < S ? lane : 0];
-    const bool v1 = replayed && lane < R && pl >= 0 && (pl & 15) < R;
-    const int E1 = replayed ? __builtin_ctzll(~__ballot(v1)) : 0;
-    const int E = E0 + E1;
-    auto slot_of = [&](int e) { return e < E0 ? acc[e] : (prog[e - E0] & 15); };
-    // the replayed entries' k and v from the previous parity's buffers (all loads before the first use)
-    constexpr int KP = 2 * MAXS * 16 / HT;
-    uint4 kraw[KP], vraw = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-    for (int j = 0; j < KP; ++j) kraw[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (E0 > 0 && hd) {  // indices clamped into [0, E0): every slot read is a validated one
-#pragma unroll
-        for (int j = 0; j < KP; ++j) {
-            const int i = min(t + HT * j, E0 * 16 - 1), e = i / 16;
-            kraw[j] = *reinterpret_cast<const uint4*>(a.qb + ((1 - p) * S + acc[e]) * C + KD + kh * DH + (i % 16) * 8);
-        }
-        if (t < E0 * VPE) {
-            const int e = t / VPE;
-            vraw = *reinterpret_cast<const uint4*>(a.qb + ((1 - p) * S + acc[e]) * C + 2 * KD + h * DH + cs * SC +
-                                                   (t % VPE) * 8);
-        }
-    }
-    __syncthreads();  // tsq complete
-    if (t < E) {
-        const int e = t, ts = slot_of(e);
-        float sq, sk;
-        if (e < E0) {
-            const float* sm = a.sums + (((1 - p) * S + ts) * HK + kh) * 2;
-            const float* gt = a.gates + (((1 - p) * S + ts) * HV + h) * 2;
-            sq = sm[0], sk = sm[1];
-            egate[e][0] = gt[0];
-            egate[e][1] = gt[1];
-        } else {
-            sq = tsq[ts][0], sk = tsq[ts][1];
-            egate[e][0] = tg[ts][0];
-            egate[e][1] = tg[ts][1];
-        }
-        egate[e][2] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sk), 1e-12f));
-        egate[e][3] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sq), 1e-12f));
-    }
-    __syncthreads();
-    // scaled into LDS: k * ki, (q * scale) * qi, v -- the replayed entries from their loads, this step's
-    // from the conv outputs (the same bf16 values)
-#pragma unroll
-    for (int j = 0; j < KP; ++j) {
-        const int i = t + HT * j;
-        if (hd && i < E0 * 16) {
-            const int e = i / 16, d0 = (i % 16) * 8;
-            const float ki = egate[e][2];
-            const uint32_t w[4] = {kraw[j].x, kraw[j].y, kraw[j].z, kraw[j].w};
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                kvec[e][d0 + q] = __fmul_rn(__uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16)), ki);
-        }
-    }
-    for (int i = t; i < E1 * DH; i += 2 * HT) {
-        const int e = E0 + i / DH, d = i % DH, ts = slot_of(e);
-        kvec[e][d] = __fmul_rn(cq[ts][DH + d], egate[e][2]);
-        qvec[e - E0][d] = __fmul_rn(__fmul_rn(cq[ts][d], a.qscale), egate[e][3]);
-    }
-    if (t < E0 * VPE) {
-        const int e = t / VPE, d0 = (t % VPE) * 8;
-        const uint32_t w[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            vvec[e][d0 + q] = __uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16));
-    }
-    for (int i = t; i < E1 * SC; i += 2 * HT) {
-        const int e = E0 + i / SC;
-        vvec[e][i % SC] = cv[slot_of(e)][i % SC];
-    }
-    __syncthreads();
-    for (int e = 0; e < (hd ? E : 0); ++e) {
-        const bool verify = e >= E0;
-        const bool commit = !verify || (prog[e - E0] & 32);
-        const float decay = egate[e][0], beta = egate[e][1];
-        float kr[HRPG], qr[HRPG];
-        const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * HRPG);
-#pragma unroll
-        for (int j = 0; j < HRPG / 4; ++j) {
-            const float4 v = k4[j];
-            kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
-        }
-        if (verify) {
-            const float4* q4 = reinterpret_cast<const float4*>(qvec[e - E0] + rg * HRPG);
-#pragma unroll
-            for (int j = 0; j < HRPG / 4; ++j) {
-                const float4 v = q4[j];
-                qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
-            }
-        }
-        float m4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (commit) {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) {
-                st[r] = __fmul_rn(st[r], decay);
-                m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
-        }
-        float kv = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
-        kv = sum_x32(sum_x16(sum_r4(sum_x8(kv))));
-        const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
-        float r4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (commit) {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, st[r]);
-            if (verify)
-#pragma unroll
-                for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
-        }
-        if (verify) {
-            float o = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
-            o = sum_x32(sum_x16(sum_r4(sum_x8(o))));
-            if (rg == 0) rawc[slot_of(e)][col] = bfround(o);
-        }
-        if (e == E0 - 1 && replayed)
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
-    }
-    __syncthreads();
-    unsigned written = 0;
-    for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
-    for (int i = t; i < R * SC; i += 2 * HT) {
-        const int ts = i / SC, c = i % SC;
-        a.core[ts * HV * DH + h * DH + cs * SC + c] = ((written >> ts) & 1) ? f2bf(rawc[ts][c]) : uint16_t(0);
-    }
-}
-
 }  // namespace
 }  // namespace mdx
 
@@ -690,7 +406,7 @@ namespace {
 int gdn_run(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
             const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
             const float* dt_bias, const float* g_decay, float* rec_state, float* gates, float* sums, float qscale,
-            uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, hipStream_t st, bool gates_too = true) {
+            uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, hipStream_t st) {
     MDX_CHECK(proj && xn && wa && wb && conv_w && conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
                   rec_state && gates && sums && core,
               "null pointer");
@@ -722,7 +438,7 @@ int gdn_run(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const 
     a.HV = int(HV);
     a.C = int(2 * HK * DH + HV * DH);
     a.slots = int(slots);
-    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + (gates_too ? 4 * a.HV : 0)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(gdn_conv_kernel, dim3((a.C + 255) / 256 + 4 * a.HV), dim3(256), 0, st, a);
     MDX_LAUNCHED();
     hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV * NSPLIT), dim3(HT), 0, st, a);
     MDX_LAUNCHED();
@@ -753,80 +469,4 @@ extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint1
     // the gated RMSNorm of each head, in place
     return mdx_gnorm_rot_quant(core, z, gnorm_w, gnorm_eps, core, nullptr, MDX_ROT_NONE, nullptr, nullptr, rows,
                                HV * DH, stream);
-}
-
-extern "C" int mdx_gdn_core_fused(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
-                                  int64_t K, const uint16_t* conv_w, uint16_t* conv_state2, uint16_t* proj_buf,
-                                  uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias, const float* g_decay,
-                                  float* rec_state, float* gates, float* sums, float qscale, uint16_t* core,
-                                  int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream) {
-    MDX_CHECK(proj && xn && wa && wb && conv_w && conv_state2 && proj_buf && qkv_buf && ctl && dt_bias && g_decay &&
-                  rec_state && gates && sums && core,
-              "null pointer");
-    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
-    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
-    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV % 2 == 0 && HV <= 128, "heads (HV even, <= 128)");
-    MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
-              "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
-    GdnArgs a{};
-    a.proj = proj;
-    a.xn = xn;
-    a.wa = wa;
-    a.wb = wb;
-    a.K = int(K);
-    a.conv_w = conv_w;
-    a.conv_state = conv_state2;
-    a.pb = proj_buf;
-    a.qb = qkv_buf;
-    a.ctl = ctl;
-    a.dt_bias = dt_bias;
-    a.g_decay = g_decay;
-    a.rec = rec_state;
-    a.gates = gates;
-    a.sums = sums;
-    a.qscale = qscale;
-    a.core = core;
-    a.R = int(rows);
-    a.HK = int(HK);
-    a.HV = int(HV);
-    a.C = int(2 * HK * DH + HV * DH);
-    a.slots = int(slots);
-    hipLaunchKernelGGL(gdn_fused_kernel, dim3(a.HV * NSPLIT), dim3(2 * HT), 0, static_cast<hipStream_t>(stream), a);
-    MDX_LAUNCHED();
-    return MDX_OK;
-}
-
-extern "C" int mdx_gdn_core_split(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
-                                  int64_t K, const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf,
-                                  uint16_t* qkv_buf, const int32_t* ctl, const float* dt_bias, const float* g_decay,
-                                  float* rec_state, float* gates, float* sums, float qscale, uint16_t* core,
-                                  int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream) {
-    return gdn_run(proj, xn, wa, wb, K, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates,
-                   sums, qscale, core, rows, HK, HV, slots, static_cast<hipStream_t>(stream), false);
-}
-
-extern "C" int mdx_gdn_gates(const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K, const int32_t* ctl,
-                             const float* dt_bias, const float* g_decay, float* gates, int64_t rows, int64_t HV,
-                             int64_t slots, void* stream) {
-    MDX_CHECK(xn && wa && wb && ctl && dt_bias && g_decay && gates, "null pointer");
-    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
-    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
-    MDX_CHECK(HV >= 1 && HV <= 128, "1..128 value heads");
-    MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
-              "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
-    GdnArgs a{};
-    a.xn = xn;
-    a.wa = wa;
-    a.wb = wb;
-    a.K = int(K);
-    a.ctl = ctl;
-    a.dt_bias = dt_bias;
-    a.g_decay = g_decay;
-    a.gates = gates;
-    a.R = int(rows);
-    a.HV = int(HV);
-    a.slots = int(slots);
-    hipLaunchKernelGGL(gdn_gates_kernel, dim3(4 * a.HV), dim3(256), 0, static_cast<hipStream_t>(stream), a);
-    MDX_LAUNCHED();
-    return MDX_OK;
 }

@@ -536,31 +536,12 @@ def int8_linear_prequantized(x, x_scale, w, w_scale, bias=None, out_dtype=2, til
     return out
 
 
-def gdn_gates(xn, wa, wb, ctl, dt_bias, g_decay, gates_buf):
-    """This step's GDN gates (mdx_gdn_gates) into gates_buf[ctl parity]: the gates phase of gdn_core as a
-    launch of its own (it can run beside the projection GEMV)."""
-    for t, n in ((xn, "xn"), (wa, "wa"), (wb, "wb")):
-        _dev(t, n)
-        _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
-    slots = _slots_of(ctl)
-    K = xn.shape[-1]
-    R, HV = xn.numel() // K, wa.shape[0]
-    _check(wa.shape == (HV, K) and wb.shape == wa.shape, "wa / wb [HV, K]")
-    _check(dt_bias.dtype == torch.float32 and g_decay.dtype == torch.float32 and gates_buf.dtype == torch.float32
-           and gates_buf.is_contiguous() and gates_buf.numel() == 2 * slots * HV * 2, "gates f32 [2, slots, HV, 2]")
-    _lib.call("mdx_gdn_gates", _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), K, _lib.ptr(ctl), _lib.ptr(dt_bias),
-              _lib.ptr(g_decay), _lib.ptr(gates_buf), R, HV, slots, _lib.stream_of(xn))
-
-
 def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
-             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None, raw=False, fused=False, gates_done=False):
+             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=None, raw=False):
     """The Gated-DeltaNet core of csrc/mono_gdn.sycl:313-607 (layer_gdn phases P3-P5; layer_gdn_core's
     output): deferred conv, gates, sums, replay + verify delta rule, gated RMSNorm. Buffers are updated
     in place; returns core bf16 [R, HV * 128]. raw=True leaves out the gated RMSNorm (core holds the
-    delta rule's bf16 outputs; gnorm_rot_quant applies it later). fused=True (with raw): the whole core in
-    one launch (mdx_gdn_core_fused, the same bits), the conv history double-buffered by parity: conv_state
-    bf16 [2, C, 3], the step of parity p reading [1 - p] and writing [p]. gates_done=True (with raw): this
-    step's gates were computed by gdn_gates (mdx_gdn_core_split: the conv and head launches only)."""
+    delta rule's bf16 outputs; gnorm_rot_quant applies it later)."""
     for t, n in ((proj, "proj"), (z, "z"), (xn, "xn"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"), (conv_state, "conv_state"),
                  (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf"), (gnorm_w, "gnorm_w")):
         _dev(t, n)
@@ -575,15 +556,13 @@ def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt
     _check(xn.numel() == R * xn.shape[-1] and wa.shape == (HV, xn.shape[-1]) and wb.shape == wa.shape,
            "xn [R, K], wa / wb [HV, K]")
     _check(z.shape[-1] == HV * 128 and conv_w.numel() == C * 4
-           and conv_state.numel() == C * 3 * (2 if fused else 1), "GDN operand shapes")
-    _check(raw or not (fused or gates_done), "the fused / split core writes the raw outputs (raw=True)")
-    _check(not (fused and gates_done), "the fused core computes its own gates")
+           and conv_state.numel() == C * 3, "GDN operand shapes")
     _check(proj_buf.numel() == 2 * slots * C and qkv_buf.numel() == 2 * slots * C, "proj / qkv buffers [2, slots, C]")
     _check(gates_buf.numel() == 2 * slots * HV * 2 and sums_buf.numel() == 2 * slots * hk * 2, "gates / sums buffers")
     if core is None:
         core = torch.empty(R, HV * 128, dtype=torch.bfloat16, device=proj.device)
     if raw:
-        _lib.call("mdx_gdn_core_fused" if fused else ("mdx_gdn_core_split" if gates_done else "mdx_gdn_core_raw"), _lib.ptr(proj), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), xn.shape[-1],
+        _lib.call("mdx_gdn_core_raw", _lib.ptr(proj), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), xn.shape[-1],
                   _lib.ptr(conv_w), _lib.ptr(conv_state), _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl),
                   _lib.ptr(dt_bias), _lib.ptr(g_decay), _lib.ptr(rec_state), _lib.ptr(gates_buf), _lib.ptr(sums_buf),
                   float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(proj))

@@ -85,14 +85,6 @@ SIGNATURES = {
     "mdx_gdn_core_raw": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
-    "mdx_gdn_core_fused": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
-                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                          ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
-    "mdx_gdn_core_split": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
-                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                          ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
-    "mdx_gdn_gates": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
-                                     c_int64, c_int64, c_int64, c_void_p]),
     "mdx_gnorm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
                                            ctypes.c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_topk_rows_noalloc": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p,

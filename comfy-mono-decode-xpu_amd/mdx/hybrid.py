@@ -50,8 +50,6 @@ class HybridConfig:
     attn_every: int = 4           # layer i is full attention iff i % attn_every == attn_every - 1
     auto: bool = False            # adaptive tree: drafts keep 7 candidates, the accept records their ranks
     attn: str = "fast"            # "exact": attention in one canonical fp32 order (mdx_attn_exact)
-    gdn_fused: bool = False       # the GDN core in one launch (mdx_gdn_core_fused, the same bits)
-    gdn_side_gates: bool = False  # the GDN gates on a second stream beside the projection GEMV (the same bits)
     rotate: bool = False          # W4 activations rotated by H256 before quantisation (ConvRot-packed weights)
     # W4 group scales of the random weights: "faithful" keeps each fp16 G128 group scale as an fp16 ratio to
     # the channel scale, decoded per weight by rint (the reference contract, what checkpoint ingestion
@@ -160,7 +158,6 @@ class HybridModel:
         self.final_norm = _norm(H, gen, dev)
         self.h256 = layout.regular_hadamard(dev)
         self.h256f = layout.regular_hadamard(dev, torch.float32)  # the draft ops take the f32 matrix
-        self.side = torch.cuda.Stream(dev) if dev.type == "cuda" else None  # default priority
         # the W4 activation preps: plain absmax (GPTQ weights) or H256 first (ConvRot-packed weights)
         self.rot, self.hrot = (_lib.ROT_H256, self.h256) if c.rotate else (_lib.ROT_NONE, None)
         self.silu = layout.silu_lut(dev)
@@ -232,8 +229,7 @@ class HybridModel:
                               torch.zeros(1, c.kv_heads, c.cap, c.head_dim, **bf))
             else:
                 hv, hk = c.gdn_value_heads, c.gdn_key_heads
-                # the one-launch core double-buffers the conv history by parity (reads [1 - p], writes [p])
-                conv = torch.zeros(2, self.gdn_ch, 3, **bf) if c.gdn_fused else torch.zeros(self.gdn_ch, 3, **bf)
+                conv = torch.zeros(self.gdn_ch, 3, **bf)
                 self.gdn[i] = dict(conv=conv, pb=torch.zeros(2, S, self.gdn_ch, **bf),
                                    qb=torch.zeros(2, S, self.gdn_ch, **bf),
                                    rec=torch.randn(hv, 128, 128, generator=gen, device=dev) * 0.1,
@@ -364,22 +360,12 @@ class HybridModel:
                   self.rot, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
-        side = c.gdn_side_gates and not c.gdn_fused
-        if side:
-            # the gates need only xn: their launch runs beside the projection GEMV (joined before the core)
-            main = torch.cuda.current_stream(self.dev)
-            self.side.wait_stream(main)
-            with torch.cuda.stream(self.side):
-                _C.gdn_gates(xn, L["wa"], L["wb"], self.ctl, L["dt_bias"], L["g_decay"], G["gates"])
         _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
-        if side:
-            main.wait_stream(self.side)
         self._tr(f"L{i}.proj", proj)
         self._tr(f"L{i}.z", z)
         core = _C._buf(sc["core"], R, hv * 128)
         _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
-                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True,
-                    fused=c.gdn_fused, gates_done=side)
+                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
         self._tr(f"L{i}.core_raw", core)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"], L["d"], 6,
                        gnorm=(z, L["gnorm"], c.eps))

@@ -314,34 +314,6 @@ int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* w
                      float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
                      void* stream);
 
-/* The core of mdx_gdn_core_raw in one launch, bit for bit the same outputs and buffers, with the conv
- * history double-buffered by parity: conv_state2 bf16 [2][C][3], the step of parity p (ctl[1]) reading
- * [1 - p] and writing [p] (each work-group runs the conv of the channels it reads, so no work-group may
- * advance a history another one still reads). No counterpart in the reference (whose GDN core is one
- * persistent launch with in-kernel barriers, csrc/mono_gdn.sycl:87-699). */
-int mdx_gdn_core_fused(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
-                       const uint16_t* conv_w, uint16_t* conv_state2, uint16_t* proj_buf, uint16_t* qkv_buf,
-                       const int32_t* ctl, const float* dt_bias, const float* g_decay, float* rec_state, float* gates,
-                       float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
-                       void* stream);
-
-/* The core of mdx_gdn_core_raw without this step's gates, which mdx_gdn_gates computes (the pair gives the
- * same bits as mdx_gdn_core_raw): the gates need only the normalised layer input, so their launch can run
- * beside the projection GEMV on a second stream (joined before this one). No counterpart in the reference
- * (its gates are a phase of the one persistent GDN launch, csrc/mono_gdn.sycl:424-450). */
-int mdx_gdn_core_split(const uint16_t* proj, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K,
-                       const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf,
-                       const int32_t* ctl, const float* dt_bias, const float* g_decay, float* rec_state, float* gates,
-                       float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
-                       void* stream);
-
-/* This step's GDN gates: a = bf16(xn . wa[h]), b = bf16(xn . wb[h]), decay = exp(g_decay * softplus(a +
- * dt_bias)), beta = bf16(sigmoid(b)) into gates[ctl[1]][row][h] (rows .. slots - 1: zeros); the arithmetic of
- * the gates inside mdx_gdn_core_raw. Replaces: csrc/mono_gdn.sycl:424-450 (as a launch of its own). */
-int mdx_gdn_gates(const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, int64_t K, const int32_t* ctl,
-                  const float* dt_bias, const float* g_decay, float* gates, int64_t rows, int64_t HV, int64_t slots,
-                  void* stream);
-
 /* Gated RMSNorm per 128-element head, then the rotation + row quantisation of mdx_rot_quant:
  * y' = bf16(bf16((y gnorm_w) / sqrt(mean_head(y^2) + eps)) * bf16(silu(z))). y_out (optional, may be y)
  * receives y'; with q = scale = NULL and rot = MDX_ROT_NONE only y' is written. y, z, y_out bf16

@@ -140,60 +140,3 @@ def test_gdn_invalid_accepted_slot_replays_nothing(C, dev, bad):
                         dt_bias, g_decay, gnw, 1e-6, DH ** -0.5, np.array(ctl), R, HK, slots)
     assert not want.any()
     assert_bits_equal(bits(d["conv_state"]), ref.f32_to_bf16(st["conv_state"]), "conv history")
-
-
-@pytest.mark.parametrize("slots,widths", [(8, (4, 3)), (16, (4, 3, 2, 2, 2)), (8, (1,)), (8, ())])
-def test_fused_core_equals_two_launches(C, dev, slots, widths):
-    """mdx_gdn_core_fused, and mdx_gdn_gates followed by mdx_gdn_core_split, against mdx_gdn_core_raw over
-    four deferred steps from the same state: raw outputs, the conv history (fused: the half of this step's
-    parity), both parities of the projection and conv buffers, gates, sums and the recurrent state, bit for
-    bit; the fused history's other half is left as it was."""
-    g = torch.Generator().manual_seed(70 + slots + len(widths))
-    bf = lambda *s_, sc=1.0: (torch.randn(*s_, generator=g) * sc).bfloat16().to(dev)
-    conv_w, wa, wb = bf(NCH, 4, sc=0.5), bf(HV, 4096, sc=0.02), bf(HV, 4096, sc=0.02)
-    dt_bias = (torch.rand(HV, generator=g) * 2 - 1).to(dev)
-    g_decay = (-torch.exp(torch.rand(HV, generator=g) * 1.5 - 1)).to(dev)
-    hist = bf(NCH, 3)
-    two = dict(conv=hist.clone(), pb=torch.zeros(2, slots, NCH, dtype=torch.bfloat16, device=dev),
-               qb=torch.zeros(2, slots, NCH, dtype=torch.bfloat16, device=dev),
-               rec=(torch.randn(HV, DH, DH, generator=g) * 0.1).to(dev),
-               gates=torch.zeros(2, slots, HV, 2, device=dev), sums=torch.zeros(2, slots, HK, 2, device=dev))
-    one = {k: v.clone() for k, v in two.items()}
-    one["conv"] = torch.stack([hist.clone(), hist.clone()])  # the first step (parity 0) reads half 1
-    split = {k: v.clone() for k, v in two.items()}  # mdx_gdn_gates, then mdx_gdn_core_split
-    tree = ref.tree_from_spec(ref.spec_of_widths(widths), slots)
-    R = 1 + sum(widths)
-    parents = tree[0][:R] + [-1] * (slots - R)
-    prog = ref.verify_program(tree[0][:R], R) + [0] * (slots - R)
-    accepted, pending = [0] * slots, 0
-    for step in range(4):
-        p = step % 2
-        print(f"case fused gdn slots={slots} widths={widths} step={step}", flush=True)
-        ctl = torch.tensor([pending, p] + accepted + parents + prog, dtype=torch.int32, device=dev)
-        proj, z, xn = bf(R, NCH), bf(R, HV * DH), bf(R, 4096)
-        outs = []
-        for st, fused, gates_done in ((two, False, False), (one, True, False), (split, False, True)):
-            other = st["conv"][1 - p].clone() if fused else None
-            if gates_done:
-                C.gdn_gates(xn, wa, wb, ctl, dt_bias, g_decay, st["gates"])
-            outs.append(C.gdn_core(proj, z, xn, wa, wb, conv_w, st["conv"], st["pb"], st["qb"], ctl, dt_bias, g_decay,
-                                   st["rec"], st["gates"], st["sums"], bf(DH), 1e-6, DH ** -0.5, HK, raw=True,
-                                   fused=fused, gates_done=gates_done).clone())
-            if fused:
-                assert torch.equal(st["conv"][1 - p], other), "the other parity's history is untouched"
-        assert_bits_equal(bits(outs[1]), bits(outs[0]), f"raw core step {step}")
-        assert_bits_equal(bits(outs[2]), bits(outs[0]), f"split raw core step {step}")
-        assert_bits_equal(bits(one["conv"][p]), bits(two["conv"]), f"conv history step {step}")
-        for k in ("conv", "pb", "qb", "rec", "gates", "sums"):
-            if k != "conv":
-                assert_bits_equal(bits(one[k]), bits(two[k]), f"{k} step {step}")
-            assert_bits_equal(bits(split[k]), bits(two[k]), f"split {k} step {step}")
-        n = int(torch.randint(1, R + 1, (1,), generator=g)) if R > 1 else 1
-        chain = [0]
-        while len(chain) < R:
-            kids = [r for r in range(R) if parents[r] == chain[-1]]
-            if not kids:
-                break
-            chain.append(kids[0])
-        n = min(n, len(chain))
-        pending, accepted = n, chain[:n] + [0] * (slots - n)

@@ -53,10 +53,10 @@ def _attn_bound(got, q, k, v, L, xk, xv, mask, what):
     assert err.mean() <= 1.5 * e_ref.mean() + 1e-5, (what, err.mean(), e_ref.mean())
 
 
-@pytest.mark.parametrize("head,gdn_fused", [("bf16", False), ("int8", False), ("bf16", True)])
-def test_decode_step_matches_oracle(C, dev, head, gdn_fused):
+@pytest.mark.parametrize("head,scales", [("bf16", "faithful"), ("int8", "faithful"), ("bf16", "integral")])
+def test_decode_step_matches_oracle(C, dev, head, scales):
     from mdx import hybrid, layout
-    cfg = hybrid.HybridConfig(layers=2, attn_every=2, cap=128, greedy=True, head=head, gdn_fused=gdn_fused)
+    cfg = hybrid.HybridConfig(layers=2, attn_every=2, cap=128, greedy=True, head=head, scales=scales)
     m = hybrid.HybridModel(cfg, dev, seed=11)
     m.prefill(torch.randint(0, cfg.vocab, (24,), generator=torch.Generator().manual_seed(3)))
     torch.cuda.synchronize()
@@ -67,8 +67,6 @@ def test_decode_step_matches_oracle(C, dev, head, gdn_fused):
                 hbuf=_np(m.hbuf), mk=_np(m.mkv[0])[0], mv=_np(m.mkv[1])[0],
                 key=_np(m.kv[1][0])[0], value=_np(m.kv[1][1])[0],
                 gdn={k: v.float().cpu().numpy().copy() for k, v in m.gdn[0].items()})
-    if cfg.gdn_fused:
-        snap["gdn"]["conv"] = snap["gdn"]["conv"][1 - m.parity]  # the history this step reads
     parity = m.parity
     m.trace = []
     m.step(parity)
@@ -166,8 +164,7 @@ def test_decode_step_matches_oracle(C, dev, head, gdn_fused):
     core = ref.bf16_to_f32(_np(tr["L0.core"][0])).astype(np.float64)
     e_ref, err = np.abs(c32 - c64), np.abs(core - c64)
     assert err.max() <= 1.5 * e_ref.max() + 1e-3 and err.mean() <= 1.5 * e_ref.mean() + 1e-5, "GDN core"
-    conv_after = m.gdn[0]["conv"][parity] if cfg.gdn_fused else m.gdn[0]["conv"]
-    assert_bits_equal(_np(conv_after), ref.f32_to_bf16(st64["conv_state"]), "GDN conv history")
+    assert_bits_equal(_np(m.gdn[0]["conv"]), ref.f32_to_bf16(st64["conv_state"]), "GDN conv history")
     want, _ = ref.layer_post(x0, _np(tr["L0.core"][0]), None, None, _w4(L0["o"]), _np(L0["norm_post"]), eps, "none", None,
                              lut, _w4(L0["g"]), _w4(L0["u"]), _w4(L0["d"]))
     assert_bits_equal(_np(tr["L0.out"][0]), want, "GDN layer output")
