@@ -1143,30 +1143,36 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         // never stored); a chunk past the slice adds nothing (a uniform branch)
         v4i acc = {0, 0, 0, 0};
         const uint8_t* xrow = xl + min(lane & 15, a.rows - 1) * Kr + klane - cu0 * CHUNK_K;
-        for (int i0 = 0; i0 < nch; i0 += RING) {
+        auto chunk = [&](int p, int i, bool refill) {
+            const int ch = c0 + min(i, last);
+            const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
+            const uint4 xa = x4[0], xb = x4[1];
+            const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            uint32_t lo[4], hi[4];
+            decode_tb<TB8>(buf[p], tq[p], lo, hi);
+            if (!split)
 #pragma unroll
-            for (int p = 0; p < RING; ++p) {
-                const int i = i0 + p;
-                const int ch = c0 + min(i, last);
-                const uint4* x4 = reinterpret_cast<const uint4*>(xrow + ch * CHUNK_K);
-                const uint4 xa = x4[0], xb = x4[1];
-                const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                uint32_t lo[4], hi[4];
-                decode_tb<TB8>(buf[p], tq[p], lo, hi);
-                if (!split)
+                for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], lo[j], hi[j]);
+            if (i < nch) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) nat_order(lo[j], hi[j], lo[j], hi[j]);
-                if (i < nch) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
-                                                                    long(uint64_t(lo[j]) | (uint64_t(hi[j]) << 32)), acc, 0, 0, 0);
-                }
-                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);  // refill after use
-                tq[p] = tbl_of(i + RING);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < 4; ++j)
+                    acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(long(uint64_t(xd[2 * j]) | (uint64_t(xd[2 * j + 1]) << 32)),
+                                                                long(uint64_t(lo[j]) | (uint64_t(hi[j]) << 32)), acc, 0, 0, 0);
             }
-        }
+            if (refill) {  // refill after use
+                buf[p] = ldg_stream(wp + min(i + RING, last) * wstride);
+                tq[p] = tbl_of(i + RING);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // whole rounds that refill their slots, then the last round without refills: no load past the
+        // slice is in flight when the wave leaves its loop
+        int i0 = 0;
+        for (; i0 + RING < nch; i0 += RING)
+#pragma unroll
+            for (int p = 0; p < RING; ++p) chunk(p, i0 + p, true);
+#pragma unroll
+        for (int p = 0; p < RING; ++p) chunk(p, i0 + p, false);
         if (ralias) __syncthreads();  // every wave is past its last table read
         int32_t* dst = red + ((ts * a.KS + slice) * 64 + lane) * 4;
 #pragma unroll
@@ -1302,6 +1308,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
     __syncthreads();
     epilogue<MFMA>(a, wg, red, prml);
+}
 }
 
 // SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
