@@ -1309,7 +1309,6 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     __syncthreads();
     epilogue<MFMA>(a, wg, red, prml);
 }
-}
 
 // SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
 // SIMD.
