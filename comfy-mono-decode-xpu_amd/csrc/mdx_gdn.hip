@@ -11,26 +11,29 @@
 //
 // Buffers (per layer): conv_state bf16 [C, 3]; pb, qb bf16 [2 parities][slots][C] (projections and
 // conv outputs of each step, kept for the next step's replay); rec f32 [HV][128][128] (row-major
-// [head][k row][v col]); gates f32 [2][slots][HV][2] (decay, beta); sums f32 [2][slots][HK][2]
-// (q, k sum of squares); ctl int32 [2 + 3 slots] = pending, parity, accepted slots, parents, program.
+// [head][k row][v col]); gates f32 [2][slots][HV][2] (decay, beta); ctl int32 [2 + 3 slots] = pending,
+// parity, accepted slots, parents, program. The reference keeps the q / k sums of squares of each step
+// in a buffer of its own for the next step's replay; here the delta-rule kernel takes them from the conv
+// outputs it loads anyway (sums [2][slots][HK][2] stays in the argument list, neither read nor written).
 // Channels of proj / qb: q [0, KD), k [KD, 2 KD), v [2 KD, 2 KD + HV 128), KD = HK 128.
 //
-// Launches: gdn_conv_kernel (one thread per channel: owns its conv history; the q / k work-groups also
-// take their heads' sums of squares; extra work-groups, four per value head, compute the gates beside
-// them), then gdn_head_kernel (eight work-groups of 256 per value head, 16 state columns each: thread
-// (row group rg, column col) holds state rows 8 rg .. 8 rg + 7 of its column in registers; raw bf16
-// outputs), then the gated RMSNorm per head in place (the row-prep kernel's head-norm mode, which the
+// Launches: gdn_conv_kernel (one thread per channel: owns its conv history; extra work-groups, four per
+// value head, compute the gates beside them), then gdn_head_kernel (eight work-groups of 256 per value
+// head, 16 state columns each: thread (row group rg, column col) holds state rows 8 rg .. 8 rg + 7 of its
+// column in registers; each entry's |k| and |q| from the pieces it loads: a thread's 8 squares in order,
+// then a halving tree over the 16 threads of a head row; raw bf16 outputs), then the gated RMSNorm per head in place (the row-prep kernel's head-norm mode, which the
 // decode stack instead fuses into the output projection's activation prep: mdx_gdn_core_raw +
 // mdx_gnorm_rot_quant).
 #include <math.h>
 
 #include "mdx_common.hpp"
+#include "mdx_gdn_ops.hpp"
 
 namespace mdx {
 namespace {
 
-constexpr int DH = 128, CW = 3;
-constexpr int MAXS = 16;
+constexpr int DH = GDN_DH, CW = GDN_CW;
+constexpr int MAXS = GDN_MAXS;
 
 struct GdnArgs {
     const uint16_t* proj;   // [R, C]
@@ -54,56 +57,17 @@ struct GdnArgs {
 };
 
 
-// This step's gates of head h: one wave per row computes a = xn . wa[h] and b = xn . wb[h] (lane l
-// sums its elements in order, the 8-element blocks l + 64 j, then a halving tree over the lanes; both
-// rounded to bf16), then decay = exp(g_decay * softplus(a + dt_bias)) and beta = bf16(sigmoid(b)) into
-// gates[p][row][h]; rows R .. slots - 1 get zeros. The four work-groups of a head share its rows.
-__device__ __forceinline__ void gate_row(const GdnArgs& a, int h, int ts, int lane, float& decay, float& beta) {
-    const uint16_t* x = a.xn + int64_t(ts) * a.K;
-    const uint16_t* wa = a.wa + int64_t(h) * a.K;
-    const uint16_t* wb = a.wb + int64_t(h) * a.K;
-    uint4 xv[8], av[8], bv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int b0 = lane + 64 * i;
-        const int bc = b0 < a.K / 8 ? b0 : 0;  // unconditional loads, masked below
-        xv[i] = *reinterpret_cast<const uint4*>(x + 8 * bc);
-        av[i] = *reinterpret_cast<const uint4*>(wa + 8 * bc);
-        bv[i] = *reinterpret_cast<const uint4*>(wb + 8 * bc);
-    }
-    float pa = 0.f, pb = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if (lane + 64 * i >= a.K / 8) continue;
-        const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-        const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
-        const uint32_t bw[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int sh = (e & 1) ? 0 : 16;
-            const uint32_t m = (e & 1) ? 0xFFFF0000u : 0xFFFFFFFFu;
-            const float xe = __uint_as_float((xw[e >> 1] << sh) & m);
-            pa = fmaf(xe, __uint_as_float((aw[e >> 1] << sh) & m), pa);
-            pb = fmaf(xe, __uint_as_float((bw[e >> 1] << sh) & m), pb);
-        }
-    }
-    pa = tree_sum64(pa);  // (lane 0's values are the ones used)
-    pb = tree_sum64(pb);
-    const float avv = __fadd_rn(bfround(pa), a.dt_bias[h]);
-    const float sp = avv > 20.f ? avv : log1pf(expf(avv));
-    decay = expf(__fmul_rn(a.g_decay[h], sp));
-    beta = bfround(__fdiv_rn(1.f, __fadd_rn(1.f, expf(-bfround(pb)))));
-}
-
 __device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int R = a.R, S = a.slots;
     // the control words are checked at the stores only, so that their load overlaps the others
     const int pending = a.ctl[0], p = a.ctl[1];
-    const bool ok = p >= 0 && p <= 1 && pending >= 0 && pending <= S;
+    const bool ok = gdn_ctl_ok(pending, p, S);
     for (int ts = quarter * 4 + wv; ts < S; ts += 16) {
         float decay = 0.f, beta = 0.f;
-        if (ts < R) gate_row(a, h, ts, lane, decay, beta);
+        if (ts < R)
+            gdn_gate_row(a.xn + int64_t(ts) * a.K, a.wa + int64_t(h) * a.K, a.wb + int64_t(h) * a.K, a.K, a.dt_bias[h],
+                         a.g_decay[h], lane, decay, beta);
         if (lane == 0 && ok) {
             a.gates[((p * S + ts) * a.HV + h) * 2] = decay;
             a.gates[((p * S + ts) * a.HV + h) * 2 + 1] = beta;
@@ -112,15 +76,12 @@ __device__ void gdn_gates_part(const GdnArgs& a, int h, int quarter) {
 }
 
 // One thread per channel (it owns the channel's history); the work-group stages its 256 channels'
-// projection rows in LDS, so the ancestors of a tree row are LDS reads by index. A work-group of q or
-// k channels (two heads) also takes the sums of squares of its heads' conv outputs per row (lane l:
-// elements l and l + 64, then a halving tree) into sums[p][row][kh][q / k]. The work-groups after
+// projection rows in LDS, so the ancestors of a tree row are LDS reads by index. The work-groups after
 // the channels' compute this step's gates (four per value head).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     __shared__ int sctl[2 + 3 * MAXS];
     __shared__ uint32_t anct[MAXS];
     __shared__ uint16_t prl[MAXS][256];
-    __shared__ float sq[MAXS][256];
     const int t = threadIdx.x;
     const int nconv = (a.C + 255) / 256;
     if (int(blockIdx.x) >= nconv) {
@@ -131,93 +92,21 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs a) {
     const int c = blockIdx.x * 256 + t;
     if (t < 2 + 3 * a.slots) sctl[t] = a.ctl[t];
     const int R = a.R;
-    const int64_t C = a.C;
     const bool cl = c < a.C;
-    // every load up front (clamped addresses, no branches): this step's projections of the channel,
-    // its history, the previous step's accepted rows, its weights
+    // this step's projections of the channel, every load up front (clamped addresses, no branches)
     uint16_t pr[MAXS];
 #pragma unroll
-    for (int r = 0; r < MAXS; ++r) pr[r] = a.proj[(r < R ? r : R - 1) * C + (cl ? c : 0)];
+    for (int r = 0; r < MAXS; ++r) pr[r] = a.proj[(r < R ? r : R - 1) * int64_t(a.C) + (cl ? c : 0)];
 #pragma unroll
     for (int r = 0; r < MAXS; ++r) prl[r][t] = pr[r];
     __syncthreads();
     const int S = a.slots, pending = sctl[0], p = sctl[1];
-    if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // uniform
-    const int* acc = sctl + 2;
-    const int* parent = sctl + 2 + S;
-    // the ancestry of row t (the same for every channel), walked once: byte d - 1 says where the tap
-    // at distance d reads, an earlier row of this step (0 .. R - 1) or history entry 16 + (CW - the
-    // number of taps so far that fell before this step)
-    if (t < R) {
-        int anc = t, miss = 0;
-        uint32_t code = 0;
-#pragma unroll
-        for (int d = 1; d <= CW; ++d) {
-            anc = anc >= 0 ? parent[anc] : -1;
-            anc = anc >= R ? -1 : anc;  // a parent is an earlier row of this step
-            miss += anc < 0;
-            code |= uint32_t(anc >= 0 ? anc : 16 + CW - miss) << (8 * (d - 1));
-        }
-        anct[t] = code;
-    }
+    if (!gdn_ctl_ok(pending, p, S)) return;  // uniform
+    if (t < R) anct[t] = gdn_ancestry(t, R, sctl + 2 + S);
     __syncthreads();
-    if (!cl) return;  // (only a last, partial work-group of v channels, which takes no sums)
-    uint16_t old[CW], prevacc[CW];
-#pragma unroll
-    for (int r = 0; r < CW; ++r) {
-        old[r] = a.conv_state[c * CW + r];
-        const int j = pending + r - CW;
-        int slot = acc[j < 0 ? 0 : j];
-        slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
-        prevacc[r] = a.pb[((1 - p) * S + slot) * C + c];
-    }
-    float w[CW + 1];
-#pragma unroll
-    for (int d = 0; d <= CW; ++d) w[d] = bf2f(a.conv_w[c * (CW + 1) + d]);
-    // the history shifted by the previous step's accepted rows
-    uint16_t hist[CW];
-#pragma unroll
-    for (int r = 0; r < CW; ++r) {
-        const int j = pending + r;
-        hist[r] = j == 0 ? old[0] : (j == 1 ? old[1] : (j == 2 ? old[2] : prevacc[r]));
-    }
-#pragma unroll
-    for (int r = 0; r < CW; ++r) a.conv_state[c * CW + r] = hist[r];
-#pragma unroll
-    for (int ts = 0; ts < MAXS; ++ts) {
-        if (ts >= S) break;
-        uint16_t out = 0;
-        if (ts < R) {
-            const uint32_t code = anct[ts];
-            float sum = fmaf(bf2f(prl[ts][t]), w[CW], 0.f);
-#pragma unroll
-            for (int d = 1; d <= CW; ++d) {
-                const int src = (code >> (8 * (d - 1))) & 0xFF;
-                const uint16_t hv = src == 16 ? hist[0] : (src == 17 ? hist[1] : hist[2]);
-                const float v = src < 16 ? bf2f(prl[src][t]) : bf2f(hv);
-                sum = fmaf(v, w[CW - d], sum);
-            }
-            const float y = bfround(sum);
-            out = f2bf(__fdiv_rn(y, __fadd_rn(1.f, expf(-y))));
-        }
-        a.qb[(p * S + ts) * C + c] = out;
-        a.pb[(p * S + ts) * C + c] = ts < R ? prl[ts][t] : uint16_t(0);
-        if (ts < R) sq[ts][t] = bf2f(out);
-    }
-    // q / k heads of this work-group: sums of squares per row (the v channels have none)
-    const int KD = a.HK * DH;
-    if (int(blockIdx.x) * 256 >= 2 * KD) return;
-    __syncthreads();
-    const int lane = t & 63, wv = t >> 6;
-    if (wv & 1) return;  // wave 2 j owns head j of the work-group (its elements 0..63; 64..127 from wave 2 j + 1)
-    const int c0 = blockIdx.x * 256 + 128 * (wv >> 1);
-    const int which = c0 >= KD, kh = (c0 - which * KD) / DH;
-    for (int ts = 0; ts < R; ++ts) {
-        const float v0 = sq[ts][64 * wv + lane], v1 = sq[ts][64 * wv + 64 + lane];
-        float part = fmaf(v1, v1, __fmul_rn(v0, v0));
-        part = tree_sum64(part);
-        if (lane == 0) a.sums[((p * S + ts) * a.HK + kh) * 2 + which] = part;
-    }
+    if (!cl) return;  // (only a last, partial work-group of v channels)
+    gdn_conv_channel(c, a.C, R, S, pending, p, sctl + 2, anct, [&](int r) { return prl[r][t]; }, a.conv_w, a.conv_state,
+                     a.pb, a.qb);
 }
 
 // The delta rule of value head h over the columns [16 cs, 16 cs + 16) of its state (eight work-groups
@@ -239,6 +128,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
     __shared__ float vvec[2 * MAXS][SC], rawc[MAXS][SC];
     __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
+    __shared__ float esum[2 * MAXS][2];   // sums of squares of q, k
     __shared__ int ectl[2 + 3 * MAXS];
     const int t = threadIdx.x, lane = t % 64, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
@@ -291,13 +181,42 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     }
     if (t < E) {
         const int e = t, ts = slot_of(e), par = e < E0 ? 1 - p : p;
-        const float* sm = a.sums + ((par * S + ts) * HK + kh) * 2;
         const float* gt = a.gates + ((par * S + ts) * HV + h) * 2;
-        const float sq = sm[0], sk = sm[1];
         egate[e][0] = gt[0];
         egate[e][1] = gt[1];
-        egate[e][2] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sk), 1e-12f));
-        egate[e][3] = __fdiv_rn(1.f, fmaxf(sqrt_rn(sq), 1e-12f));
+    }
+    // the entries' sums of squares of k (every entry) and q (verify entries) from the loaded pieces: each
+    // thread's 8 squares in order, then the 16 pieces of an entry (16 consecutive lanes) by a halving tree
+    auto sq8 = [](const uint4 v) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float s_ = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float f = __uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16));
+            s_ = fmaf(f, f, s_);
+        }
+        return s_;
+    };
+    auto sum16 = [](float v) {
+#pragma unroll
+        for (int d = 8; d >= 1; d >>= 1) v = __fadd_rn(v, __shfl_xor(v, d, 16));
+        return v;
+    };
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const int i = t + HT * j;
+        const float ssum = sum16(sq8(kraw[j]));
+        if (i < E * 16 && (i & 15) == 0) esum[i / 16][1] = ssum;
+    }
+    {
+        const float ssum = sum16(sq8(qraw));
+        if (t < E1 * 16 && (t & 15) == 0) esum[E0 + t / 16][0] = ssum;
+    }
+    __syncthreads();
+    if (t < E) {
+        const int e = t;
+        egate[e][2] = __fdiv_rn(1.f, fmaxf(sqrt_rn(esum[e][1]), 1e-12f));
+        egate[e][3] = __fdiv_rn(1.f, fmaxf(sqrt_rn(e >= E0 ? esum[e][0] : 0.f), 1e-12f));
     }
     __syncthreads();
     // scaled into LDS: k * ki, (q * scale) * qi, v

@@ -294,8 +294,9 @@ int mdx_int8_linear(const int8_t* x, const float* x_scale, const int8_t* w, cons
  * proj bf16 [rows, C] (C = 2 HK 128 + HV 128: q | k | v); z bf16 [rows, HV 128]; xn bf16 [rows, K] (the
  * normalised layer input), wa / wb bf16 [HV, K] (K % 512 == 0, K <= 4096); conv_w bf16 [C, 4]; conv_state bf16 [C, 3]; proj_buf, qkv_buf bf16 [2, slots, C]; ctl int32
  * [2 + 3 slots] = (pending, parity, accepted[slots], parents[slots], prog[slots]); rec_state f32
- * [HV, 128, 128]; gates f32 [2, slots, HV, 2]; sums f32 [2, slots, HK, 2]; gnorm_w bf16 [128]; core bf16
- * [rows, HV 128] (rows without a verify entry are 0). slots in {8, 16}, HV even and <= 128. Tolerance
+ * [HV, 128, 128]; gates f32 [2, slots, HV, 2]; sums f32 [2, slots, HK, 2] (the reference's buffer of
+ * q / k sums of squares, neither read nor written: the norms are taken from qkv_buf); gnorm_w bf16 [128];
+ * core bf16 [rows, HV 128] (rows without a verify entry are 0). slots in {8, 16}, HV even and <= 128. Tolerance
  * parity (float64 bound); the control walk is exact. */
 int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
                  int64_t K, const uint16_t* conv_w,

@@ -666,7 +666,10 @@ def gdn_step(state, proj, z, a, b, conv_w, dt_bias, g_decay, gnorm_w, eps, qscal
             ts = (prog[e - E0] & 15) if verify else acc_slots[e]
             commit = (not verify) or bool(prog[e - E0] & 32)
             src = qb if verify else state["qb"][1 - p].astype(dtype)
-            sq = state["sums"][par][ts, kh] if not verify else sums[ts, kh]
+            # the reference reads a replayed row's sums from the buffer its step stored them in
+            # (csrc/mono_gdn.sycl:464-498); they are the sums of the same qb row, taken again here
+            sq = sums[ts, kh] if verify else [np.sum(src[ts, w * KD + kh * DH:w * KD + (kh + 1) * DH].astype(dtype) ** 2)
+                                              for w in (0, 1)]
             dec, bet = (state["gates"][par][ts, h] if not verify else gates[ts, h])
             q = src[ts, kh * DH:(kh + 1) * DH].astype(dtype)
             k = src[ts, KD + kh * DH:KD + (kh + 1) * DH].astype(dtype)
