@@ -494,7 +494,7 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     budget = tokens + 64 if tokens else steps
     cap = args.prompt + per * (budget + warm + 4) + 64
     cfg = hybrid.HybridConfig(cap=cap, two_stage=two_stage, head=head, predictable=getattr(args, "predictable", False),
-                              scales=args.scales)
+                              scales=args.scales, gdn_fold=not getattr(args, "gdn_split", False))
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5))
@@ -540,7 +540,8 @@ def bench_stack_auto(args, dev, tokens=512):
     from mdx import hybrid
     cap = args.prompt + 8 * (tokens + 64) + 64
     cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head,
-                              predictable=getattr(args, "predictable", False), scales=args.scales)
+                              predictable=getattr(args, "predictable", False), scales=args.scales,
+                              gdn_fold=not getattr(args, "gdn_split", False))
     t0 = time.perf_counter()
     m = hybrid.HybridModel(cfg, dev, seed=5)
     m.prefill(torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(5)))
@@ -685,12 +686,19 @@ def bench_gdn_layer(args, dev):
     ctl = torch.tensor([0, 0] + [0] * S + [r - 1 for r in range(M)] + [-1] * (S - M) + [r | 32 for r in range(M)]
                        + [0] * (S - M), dtype=torch.int32, device=dev)
 
+    fold = not args.gdn_split
+
     def call(i):
         w = ring[i]
         q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
-        _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
-        _C.gdn_core(proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay,
-                    w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True)
+        if fold:
+            _C.gdn_proj(q1, s1, w["qkv"], w["z"], proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"],
+                        ctl, dt_bias, g_decay, w["gates"], HK)
+            _C.gdn_delta(w["qb"], ctl, w["rec"], w["gates"], DH ** -0.5, HK, core)
+        else:
+            _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
+            _C.gdn_core(proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay,
+                        w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True)
         _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnw), 1e-6, _lib.ptr(core), None,
                   _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), M, HV * DH, _lib.stream_of(core))
         _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
@@ -702,7 +710,8 @@ def bench_gdn_layer(args, dev):
                  {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
                               f"{ring_n}-copy weight + state ring", "rows": M,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                  "launches_per_step": 6})
+                  "launches_per_step": 5 if fold else 6,
+                  "gdn_path": "conv and gates in the projection launch" if fold else "conv + gates launch"})
 
 
 def bench_read(args, dev):
@@ -775,6 +784,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="mlp: skip the full-stack decode leg")
     ap.add_argument("--no-extra", action="store_true", help="mlp: skip the other scale form's leg")
+    ap.add_argument("--gdn-split", action="store_true",
+                    help="gdn_layer / stack: the conv + gates as their own launch instead of in the projection launch")
     ap.add_argument("--scales", choices=["faithful", "integral"], default="faithful",
                     help="W4 group scales: fp16 ratios decoded per weight (the reference contract, default) or "
                          "the lossy 4-bit integral re-quantisation")

@@ -389,3 +389,27 @@ extern "C" int mdx_gdn_core(const uint16_t* proj, const uint16_t* z, const uint1
     return mdx_gnorm_rot_quant(core, z, gnorm_w, gnorm_eps, core, nullptr, MDX_ROT_NONE, nullptr, nullptr, rows,
                                HV * DH, stream);
 }
+
+extern "C" int mdx_gdn_delta(const uint16_t* qkv_buf, const int32_t* ctl, float* rec_state, const float* gates,
+                             float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
+                             void* stream) {
+    MDX_CHECK(qkv_buf && ctl && rec_state && gates && core, "null pointer");
+    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
+    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
+    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV % 2 == 0 && HV <= 128, "heads (HV even, <= 128)");
+    GdnArgs a{};
+    a.qb = const_cast<uint16_t*>(qkv_buf);
+    a.ctl = ctl;
+    a.rec = rec_state;
+    a.gates = const_cast<float*>(gates);
+    a.qscale = qscale;
+    a.core = core;
+    a.R = int(rows);
+    a.HK = int(HK);
+    a.HV = int(HV);
+    a.C = int(2 * HK * DH + HV * DH);
+    a.slots = int(slots);
+    hipLaunchKernelGGL(gdn_head_kernel, dim3(a.HV * NSPLIT), dim3(HT), 0, static_cast<hipStream_t>(stream), a);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}

@@ -22,32 +22,38 @@ __device__ __forceinline__ bool gdn_ctl_ok(int pending, int p, int slots) {
 // Row ts's gates for value head h, computed by one wave: a = xn . wa[h] and b = xn . wb[h] (lane l sums its
 // elements in order, the 8-element blocks l + 64 j, then a halving tree over the lanes; both rounded to
 // bf16), then decay = exp(g_decay * softplus(a + dt_bias)) (softplus(x) = x above 20) and beta =
-// bf16(sigmoid(b)). Lane 0's values are the results. K % 8 == 0, K <= 4096.
+// bf16(sigmoid(b)). Lane 0's values are the results. K % 8 == 0, K <= 4096. The loads go out NB blocks
+// at a time (8: all at once; fewer: fewer registers, the same sums).
+template <int NB = 8>
 __device__ __forceinline__ void gdn_gate_row(const uint16_t* xn_row, const uint16_t* wa_h, const uint16_t* wb_h, int K,
                                              float dt_bias, float g_decay, int lane, float& decay, float& beta) {
-    uint4 xv[8], av[8], bv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int b0 = lane + 64 * i;
-        const int bc = b0 < K / 8 ? b0 : 0;  // unconditional loads, masked below
-        xv[i] = *reinterpret_cast<const uint4*>(xn_row + 8 * bc);
-        av[i] = *reinterpret_cast<const uint4*>(wa_h + 8 * bc);
-        bv[i] = *reinterpret_cast<const uint4*>(wb_h + 8 * bc);
-    }
+    static_assert(8 % NB == 0, "NB divides 8");
     float pa = 0.f, pb = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if (lane + 64 * i >= K / 8) continue;
-        const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-        const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
-        const uint32_t bw[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
+    for (int i0 = 0; i0 < 8; i0 += NB) {
+        uint4 xv[NB], av[NB], bv[NB];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int sh = (e & 1) ? 0 : 16;
-            const uint32_t m = (e & 1) ? 0xFFFF0000u : 0xFFFFFFFFu;
-            const float xe = __uint_as_float((xw[e >> 1] << sh) & m);
-            pa = fmaf(xe, __uint_as_float((aw[e >> 1] << sh) & m), pa);
-            pb = fmaf(xe, __uint_as_float((bw[e >> 1] << sh) & m), pb);
+        for (int j = 0; j < NB; ++j) {
+            const int b0 = lane + 64 * (i0 + j);
+            const int bc = b0 < K / 8 ? b0 : 0;  // unconditional loads, masked below
+            xv[j] = *reinterpret_cast<const uint4*>(xn_row + 8 * bc);
+            av[j] = *reinterpret_cast<const uint4*>(wa_h + 8 * bc);
+            bv[j] = *reinterpret_cast<const uint4*>(wb_h + 8 * bc);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if (lane + 64 * (i0 + j) >= K / 8) continue;
+            const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const uint32_t aw[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+            const uint32_t bw[4] = {bv[j].x, bv[j].y, bv[j].z, bv[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int sh = (e & 1) ? 0 : 16;
+                const uint32_t m = (e & 1) ? 0xFFFF0000u : 0xFFFFFFFFu;
+                const float xe = __uint_as_float((xw[e >> 1] << sh) & m);
+                pa = fmaf(xe, __uint_as_float((aw[e >> 1] << sh) & m), pa);
+                pb = fmaf(xe, __uint_as_float((bw[e >> 1] << sh) & m), pb);
+            }
         }
     }
     pa = tree_sum64(pa);

@@ -40,6 +40,7 @@
 #include <stdlib.h>
 
 #include "mdx_common.hpp"
+#include "mdx_gdn_ops.hpp"
 #include "mdx_row.hpp"
 
 namespace mdx {
@@ -293,6 +294,25 @@ struct MatArg {
     int tiles;
 };
 
+// A Gated-DeltaNet projection launch (matrices qkv, z): the tiles of matrix 0 run the deferred causal conv
+// of their 16 channels in the epilogue, and `nside` work-groups after the GEMV's `units` compute the step's
+// gates (buffers as in mdx_gdn.hip).
+struct GdnFold {
+    int on;
+    const uint16_t* conv_w;  // [C, 4]
+    uint16_t* conv_state;    // [C, 3]
+    uint16_t* pb;            // [2][slots][C]
+    uint16_t* qb;            // [2][slots][C]
+    const int32_t* ctl;      // [2 + 3 slots]
+    const uint16_t* xn;      // [rows, K]
+    const uint16_t* wa;      // [HV, K]
+    const uint16_t* wb;      // [HV, K]
+    const float* dt_bias;    // [HV]
+    const float* g_decay;    // [HV]
+    float* gates;            // [2][slots][HV][2]
+    int HV, slots, units, nside;
+};
+
 struct GemvArgs {
     MatArg m[3];
     int nm;
@@ -329,6 +349,7 @@ struct GemvArgs {
     const uint16_t* xp_x;
     const uint16_t* xp_nw;
     float xp_eps;
+    GdnFold gf;
 };
 
 // Where a unit's activation comes from: int8 rows a.xq (DMA to LDS), bf16 rows quantised with
@@ -344,6 +365,10 @@ constexpr int SRC_INT_ONLY = 4;
 // a ring beside the weights at scalar offsets.
 constexpr int SRC_TBL = 8;
 constexpr int SRC_TBL8 = 16;
+// Added to an int8-row source: a Gated-DeltaNet projection launch (GdnFold), its conv epilogue and gate
+// work-groups compiled into these variants only (the gate rows' loads would raise every other variant's
+// registers).
+constexpr int SRC_GDN = 32;
 constexpr int XP_GPW = 4;
 constexpr int HMW = 16;  // SRC_HR: maxima per lane when every wave reads them all (<= 1024 work-groups)  // SRC_XP: 256-groups per wave (K <= 1024 x waves)
 
@@ -655,6 +680,72 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
     }
 }
 
+// The Gated-DeltaNet projection epilogue: both matrices' outputs stored (bf16, no residual), matrix 0's
+// also staged in LDS (stage [TPW][rows][16], in the activation region, dead after the loop) with the
+// control words (gctl: thread t's word, loaded in the prologue), then one thread per qkv channel runs
+// the channel's conv (gdn_conv_channel). The channel's tile owns it: no other work-group reads or writes
+// the channel's conv state or buffers in this launch.
+template <bool MFMA>
+__device__ void gdn_epilogue(const GemvArgs& a, const int wg, const int32_t* red, const float* prml, uint8_t* xl,
+                             int gctl) {
+    const GdnFold& g = a.gf;
+    const int per = 16 * a.rows, t = threadIdx.x;
+    const float* xsl = prml + a.TPW * 16;
+    uint16_t* stage = reinterpret_cast<uint16_t*>(xl);
+    int* sctl = reinterpret_cast<int*>(xl + ((a.TPW * per * 2 + 15) & ~15));
+    for (int ts = 0; ts < a.TPW; ++ts) {  // (the matrix choice stays uniform)
+        int tile;
+        const int mi = which_mat(a, wg * a.TPW + ts, tile);
+        if (tile >= mat_tiles(a, mi)) continue;
+        uint16_t* out = static_cast<uint16_t*>(mi == 0 ? a.out[0] : a.out[1]);
+        const int n = mi == 0 ? a.m[0].n : a.m[1].n;
+        for (int e = t; e < per; e += blockDim.x) {
+            const int r = e >> 4, c = e & 15;
+            const uint16_t v = f2bf(scaleback(reduced<MFMA>(a, red, ts, r, c), xsl[r], prml[ts * 16 + c]));
+            out[r * n + tile * 16 + c] = v;
+            if (mi == 0) stage[(ts * a.rows + r) * 16 + c] = v;
+        }
+    }
+    const int S = g.slots, R = a.rows;
+    if (t < 2 + 3 * S) sctl[t] = gctl;
+    __syncthreads();
+    const int pending = sctl[0], p = sctl[1];
+    if (!gdn_ctl_ok(pending, p, S) || t >= a.TPW * 16) return;  // (the first, uniform)
+    const int ts = t >> 4, c16 = t & 15;
+    int tile;
+    if (which_mat(a, wg * a.TPW + ts, tile) != 0 || tile >= a.m[0].tiles) return;
+    uint32_t anct[GDN_MAXS];
+#pragma unroll
+    for (int r = 0; r < GDN_MAXS; ++r) anct[r] = r < R ? gdn_ancestry(r, R, sctl + 2 + S) : 0u;
+    const uint16_t* st = stage + ts * R * 16 + c16;
+    gdn_conv_channel(tile * 16 + c16, a.m[0].n, R, S, pending, p, sctl + 2, anct, [&](int r) { return st[r * 16]; },
+                     g.conv_w, g.conv_state, g.pb, g.qb);
+}
+
+// The gates of a Gated-DeltaNet projection launch, by side work-group b (< nside): wave w computes row ts,
+// value head h of pair b * waves + w (rows < R; gdn_gate_row); rows R .. slots - 1 get zeros.
+__device__ void gdn_gates_side(const GemvArgs& a, int b) {
+    const GdnFold& g = a.gf;
+    const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6, nthr = blockDim.x;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int R = a.rows, S = g.slots, HV = g.HV;
+    const int pending = g.ctl[0], p = g.ctl[1];
+    const bool ok = gdn_ctl_ok(pending, p, S);
+    const int pair = b * nw + wv;
+    if (pair < R * HV) {
+        const int ts = pair / HV, h = pair - ts * HV;
+        float decay, beta;
+        gdn_gate_row<2>(g.xn + int64_t(ts) * a.K, g.wa + int64_t(h) * a.K, g.wb + int64_t(h) * a.K, a.K, g.dt_bias[h],
+                        g.g_decay[h], lane, decay, beta);
+        if (lane == 0 && ok) {
+            g.gates[((p * S + ts) * HV + h) * 2] = decay;
+            g.gates[((p * S + ts) * HV + h) * 2 + 1] = beta;
+        }
+    }
+    if (ok)
+        for (int i = b * nthr + t; i < (S - R) * HV * 2; i += g.nside * nthr) g.gates[(p * S + R) * HV * 2 + i] = 0.f;
+}
+
 // -------------------------------------------------------------------------------------------------
 // the kernel
 // -------------------------------------------------------------------------------------------------
@@ -797,6 +888,11 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     } else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) {
         prm = a.xs[lane - 16];
     }
+    // a Gated-DeltaNet projection's control words (the epilogue's conv reads them from LDS)
+    constexpr bool GDN = (SRC & SRC_GDN) != 0;
+    static_assert(!GDN || (SRC & 3) == SRC_Q8, "Gated-DeltaNet projections take int8 rows");
+    int gctl = 0;
+    if (GDN && t < 2 + 3 * a.gf.slots) gctl = a.gf.ctl[t];
     // SRC_HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the maxima entries (thread t:
     // entries t, t + threads, ... of both rows) are one-shot operands too
     constexpr int HRP = HR ? 16 : 1;
@@ -1307,7 +1403,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     if (slice == 0 && lane < 16) prml[ts * 16 + lane] = prm;
     else if (own_x && wave == a.TPW * a.KS - 1 && lane >= 16 && lane < 16 + a.rows) prml[a.TPW * 16 + lane - 16] = prm;
     __syncthreads();
-    epilogue<MFMA>(a, wg, red, prml);
+    if constexpr (GDN) gdn_epilogue<MFMA>(a, wg, red, prml, xl, gctl);
+    else epilogue<MFMA>(a, wg, red, prml);
 }
 
 // SRC_HR work-groups have at most 12 waves: their staged pieces need the registers of 3 waves per
@@ -1315,6 +1412,12 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 template <bool MFMA, int R, int SDT, int RING, int SRC = SRC_Q8>
 __global__ __launch_bounds__((SRC & 3) == SRC_HR ? 768 : 1024) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    if constexpr ((SRC & SRC_GDN) != 0) {
+        if (int(blockIdx.x) >= a.gf.units) {  // (uniform) a gate work-group
+            gdn_gates_side(a, int(blockIdx.x) - a.gf.units);
+            return;
+        }
+    }
     gemv_unit<MFMA, R, SDT, RING, SRC>(a, blockIdx.x, 0, a.K / CHUNK_K, lds);
 }
 
@@ -1368,7 +1471,8 @@ int launch_gemv_h(const GemvArgs& a, int wgs, hipStream_t st) {
     const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MFMA, R, SDT, RING, SRC>);
     if (smem > 64 * 1024) allow_smem(fn, smem);
     const int threads = a.TPW * a.KS * WAVE;
-    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING, SRC>), dim3(unsigned(wgs)), dim3(unsigned(threads)), smem, st, a);
+    const int grid = wgs + (a.gf.on ? a.gf.nside : 0);
+    hipLaunchKernelGGL((gemv_kernel<MFMA, R, SDT, RING, SRC>), dim3(unsigned(grid)), dim3(unsigned(threads)), smem, st, a);
     MDX_LAUNCHED();
     return MDX_OK;
 }
@@ -1377,6 +1481,7 @@ constexpr int TB_RING = 4;  // weight ring depth of the table-only variants
 
 template <bool MFMA, int R, int SDT, int RING, int TB>
 int launch_gemv_tb(const GemvArgs& a, int wgs, hipStream_t st) {
+    if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB + SRC_GDN>(a, wgs, st);
     if (a.hr) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_HR + TB>(a, wgs, st);
     if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_XP + TB>(a, wgs, st);
     return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB>(a, wgs, st);
@@ -1392,10 +1497,12 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
     // the integral-only variant when the caller asserts integral scales that the integral form takes
     const bool io = a.assume_int && !a.cb && !a.force_exact && a.lgG >= (MFMA ? 7 : 5);
     if (io) {
+        if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY + SRC_GDN>(a, wgs, st);
         if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR + SRC_INT_ONLY>(a, wgs, st);
         if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_INT_ONLY>(a, wgs, st);
         return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY>(a, wgs, st);
     }
+    if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_GDN>(a, wgs, st);
     if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR>(a, wgs, st);
     if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP>(a, wgs, st);
     return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8>(a, wgs, st);
@@ -1568,6 +1675,7 @@ struct GemvExtra {
     const uint16_t* xp_x = nullptr;    // SRC_XP (gemv_xp_fits): one bf16 row and its prep (no rotation)
     const uint16_t* xp_nw = nullptr;
     float xp_eps = 0.f;
+    const GdnFold* gdn = nullptr;      // a Gated-DeltaNet projection (matrices qkv, z; bf16 outputs)
 };
 
 int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
@@ -1609,6 +1717,18 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     a.xp_eps = ex.xp_eps;
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
+    if (ex.gdn) {
+        MDX_CHECK(nm == 2 && !pair && epi == EPI_STORE && out_dt == MDX_DT_BF16 && !res && rows <= ex.gdn->slots,
+                  "Gated-DeltaNet projection: matrices qkv, z, bf16 outputs, no residual, rows <= slots");
+        // the epilogue's stage and control words fit the activation region
+        MDX_CHECK(((a.TPW * 16 * rows * 2 + 15) & ~15) + 4 * (2 + 3 * ex.gdn->slots) <= rows * a.K,
+                  "Gated-DeltaNet projection stage");
+        a.gf = *ex.gdn;
+        a.gf.on = 1;
+        a.gf.units = wgs;
+        const int nw = a.TPW * a.KS;
+        a.gf.nside = (rows * a.gf.HV + nw - 1) / nw;
+    }
     MDX_CHECK(gemv_smem(a, mfma, esz) <= 160 * 1024, "activation of %d rows x K=%d exceeds LDS", rows, a.K);
     // per-weight decode tables in LDS when the scales are not asserted integral, a group spans a chunk
     // and the larger footprint still holds the grid's work-groups per CU (else fewer resident: at 8
@@ -1887,4 +2007,41 @@ extern "C" int mdx_stream_gemv(const int8_t* x, const float* x_scale, const mdx_
     if (gate_up) MDX_CHECK(nmats == 2 && silu_lut && out_dtype == MDX_DT_BF16, "gate/up needs 2 matrices, bf16 out, a SiLU table");
     return run_gemv(mats, nmats, gate_up != 0, x, x_scale, int(rows), gate_up ? EPI_SILU : EPI_STORE, outs, residuals,
                     out_dtype, silu_lut, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4* w_qkv, const mdx_w4* w_z, uint16_t* proj,
+                            uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
+                            const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf,
+                            const int32_t* ctl, const float* dt_bias, const float* g_decay, float* gates, int64_t rows,
+                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    MDX_CHECK(x && x_scale && w_qkv && w_z && proj && z && xn && wa && wb && conv_w && conv_state && proj_buf &&
+                  qkv_buf && ctl && dt_bias && g_decay && gates,
+              "null pointer");
+    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
+    MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
+    MDX_CHECK(HK >= 1 && HV >= HK && HV % HK == 0 && HV % 2 == 0 && HV <= 128, "heads (HV even, <= 128)");
+    MDX_CHECK(w_qkv->n == (2 * HK + HV) * GDN_DH && w_z->n == HV * GDN_DH, "qkv: N = (2 HK + HV) 128; z: N = HV 128");
+    const int64_t K = w_qkv->k;
+    MDX_CHECK(K >= 512 && K <= 4096 && K % 512 == 0 && aligned(xn, 16) && aligned(wa, 16) && aligned(wb, 16),
+              "a / b input: K % 512 == 0, K <= 4096, 16-byte aligned rows");
+    GdnFold f{};
+    f.conv_w = conv_w;
+    f.conv_state = conv_state;
+    f.pb = proj_buf;
+    f.qb = qkv_buf;
+    f.ctl = ctl;
+    f.xn = xn;
+    f.wa = wa;
+    f.wb = wb;
+    f.dt_bias = dt_bias;
+    f.g_decay = g_decay;
+    f.gates = gates;
+    f.HV = int(HV);
+    f.slots = int(slots);
+    GemvExtra ex;
+    ex.gdn = &f;
+    const mdx_w4* mats[2] = {w_qkv, w_z};
+    void* outs[2] = {proj, z};
+    return run_gemv(mats, 2, false, x, x_scale, int(rows), EPI_STORE, outs, nullptr, MDX_DT_BF16, nullptr,
+                    static_cast<hipStream_t>(stream), ex);
 }

@@ -575,6 +575,51 @@ def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt
     return core
 
 
+def gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
+             gates_buf, hk):
+    """The GDN input projections with the deferred conv and the gates in one launch (mdx_gdn_proj):
+    [proj | z] = W4A8 GEMV of the int8 rows q / s over the W4 handles w_qkv, w_z; the conv runs in the
+    epilogue of the tiles that produce each qkv channel (conv_state, proj_buf, qkv_buf updated as
+    gdn_core's conv phase), and extra work-groups compute the gates (decay, beta) from xn, wa, wb. The
+    in_proj GEMMs + deltanet_conv_step_deferred + the gates of gated_delta_decode_deferred
+    (comfy_mono_decode_xpu/layer.py:216-228, 593). Follow with gdn_delta."""
+    R = q.shape[0]
+    HV = wa.shape[0]
+    slots = _slots_of(ctl)
+    for t, n in ((proj, "proj"), (z, "z"), (xn, "xn"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"),
+                 (conv_state, "conv_state"), (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf")):
+        _dev(t, n)
+        _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
+    for t, n in ((dt_bias, "dt_bias"), (g_decay, "g_decay"), (gates_buf, "gates")):
+        _check(t.dtype == torch.float32 and t.is_contiguous(), f"{n}: contiguous f32")
+    C = w_qkv.n
+    _check(q.dtype == torch.int8 and q.is_contiguous() and s.numel() >= R, "q int8 [R, K], s f32 [R]")
+    _check(proj.numel() == R * C and z.numel() == R * w_z.n and xn.numel() == R * wa.shape[1] and wb.shape == wa.shape,
+           "GDN projection shapes")
+    _check(conv_w.numel() == C * 4 and conv_state.numel() == C * 3 and proj_buf.numel() == 2 * slots * C
+           and qkv_buf.numel() == 2 * slots * C and gates_buf.numel() == 2 * slots * HV * 2, "GDN buffers")
+    _lib.call("mdx_gdn_proj", _lib.ptr(q), _lib.ptr(s), ctypes.pointer(w_qkv.struct()), ctypes.pointer(w_z.struct()),
+              _lib.ptr(proj), _lib.ptr(z), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), _lib.ptr(conv_w),
+              _lib.ptr(conv_state), _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias),
+              _lib.ptr(g_decay), _lib.ptr(gates_buf), R, int(hk), HV, slots, _lib.stream_of(q))
+
+
+def gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, core):
+    """The delta rule after gdn_proj (mdx_gdn_delta): replay + verify entries over rec_state from the
+    conv outputs in qkv_buf and the gates; core [R, HV * 128] receives the raw bf16 outputs (gated
+    RMSNorm not applied)."""
+    slots = _slots_of(ctl)
+    HV = rec_state.shape[-3]
+    R = core.shape[0]
+    _check(qkv_buf.dtype == torch.bfloat16 and core.dtype == torch.bfloat16 and core.is_contiguous()
+           and core.shape[-1] == HV * 128, "qkv_buf bf16, core bf16 [R, HV * 128]")
+    _check(rec_state.dtype == torch.float32 and rec_state.shape[-2:] == (128, 128) and gates_buf.dtype == torch.float32,
+           "rec_state f32 [HV, 128, 128], gates f32")
+    _check(qkv_buf.numel() == 2 * slots * (2 * hk + HV) * 128 and gates_buf.numel() == 2 * slots * HV * 2, "GDN buffers")
+    _lib.call("mdx_gdn_delta", _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(rec_state), _lib.ptr(gates_buf),
+              float(qscale), _lib.ptr(core), R, int(hk), HV, slots, _lib.stream_of(core))
+    return core
+
 
 # ---------------------------------------------------------------------------------------------------
 # decoder-layer segments (csrc/mono_layer.sycl, csrc/mono_gdn.sycl)
@@ -723,11 +768,15 @@ def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj
     _lib.call("mdx_rms_rot_quant", _lib.ptr(x2), _lib.ptr(norm_in), float(eps_in), _lib.ptr(xn), _lib.ptr(hadamard), rot,
               _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(x))
     proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
-    stream_gemv(q, s, [QKV, Z], [proj, z])
-    core = _buf(sc["core"], R, HV * 128)
+    # the projections with the conv and the gates (one launch), then the delta rule; sums_buf is the
+    # reference's, unused here (the norms come from qkv_buf)
+    gdn_proj(q, s, QKV, Z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
+             gates_buf, hk)
+    core = gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, _buf(sc["core"], R, HV * 128))
     full = stop >= 6
-    gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay, rec_state, gates_buf,
-             sums_buf, gnorm_w, gnorm_eps, qscale, hk, core=core, raw=full)
+    if not full:
+        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnorm_w), float(gnorm_eps),
+                  _lib.ptr(core), None, _lib.ROT_NONE, None, None, R, HV * 128, _lib.stream_of(core))
     if full:
         # the gated RMSNorm runs inside the out_proj activation prep (core is normed in place there)
         U.cb = D.cb = G.cb

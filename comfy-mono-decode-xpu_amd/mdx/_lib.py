@@ -85,6 +85,11 @@ SIGNATURES = {
     "mdx_gdn_core_raw": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_gdn_proj": (ctypes.c_int, [c_void_p, c_void_p, W4P, W4P, c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_gdn_delta": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64,
+                                     c_int64, c_int64, c_void_p]),
     "mdx_gnorm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
                                            ctypes.c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_topk_rows_noalloc": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p,
@@ -146,13 +151,13 @@ def call(name, *args):
 
 
 SRC_Q8, SRC_HR, SRC_XP = 0, 1, 2
-SRC_INT_ONLY, SRC_TBL, SRC_TBL8 = 4, 8, 16
+SRC_INT_ONLY, SRC_TBL, SRC_TBL8, SRC_GDN = 4, 8, 16, 32
 
 
 def gemv_trace():
     """The GEMV kernel variants this thread launched since the previous call (mdx_gemv_trace): a list of
     dicts {mfma, src (SRC_Q8 / SRC_HR / SRC_XP), decode ("integral", "table16", "table8" or "generic"),
-    s_dtype, rows, tpw, ks, red_alias}."""
+    s_dtype, rows, tpw, ks, red_alias, gdn (a Gated-DeltaNet projection: conv epilogue, gate work-groups)}."""
     buf = (c_int32 * (7 * 64))()
     n = lib().mdx_gemv_trace(buf, 64)
     out = []
@@ -161,7 +166,7 @@ def gemv_trace():
         dec = ("integral" if src & SRC_INT_ONLY else "table16" if src & SRC_TBL else "table8" if src & SRC_TBL8
                else "generic")
         out.append(dict(mfma=bool(mfma), src=src & 3, decode=dec, s_dtype=sdt, rows=rows, tpw=tpw, ks=ks,
-                        red_alias=bool(alias)))
+                        red_alias=bool(alias), gdn=bool(src & SRC_GDN)))
     return out
 
 

@@ -61,6 +61,10 @@ class HybridConfig:
     # the embedding half through. Every kernel does the same work on the same shapes; the drafts are
     # accepted, so a step commits len(widths) + 1 tokens.
     predictable: bool = False
+    # GDN layers: the conv and the gates in the input projections' launch (mdx_gdn_proj + mdx_gdn_delta);
+    # False: the projections, then the conv + gates and the delta rule as their own launches
+    # (mdx_stream_gemv + mdx_gdn_core_raw). Both give the same bits.
+    gdn_fold: bool = True
 
     def attention(self, i):
         return i % self.attn_every == self.attn_every - 1
@@ -360,12 +364,18 @@ class HybridModel:
                   self.rot, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
-        _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
+        core = _C._buf(sc["core"], R, hv * 128)
+        if c.gdn_fold:
+            _C.gdn_proj(q, s, L["qkv"], L["z"], proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"],
+                        self.ctl, L["dt_bias"], L["g_decay"], G["gates"], c.gdn_key_heads)
+            _C.gdn_delta(G["qb"], self.ctl, G["rec"], G["gates"], 128 ** -0.5, c.gdn_key_heads, core)
+        else:
+            _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
+            _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"],
+                        L["g_decay"], G["rec"], G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads,
+                        core=core, raw=True)
         self._tr(f"L{i}.proj", proj)
         self._tr(f"L{i}.z", z)
-        core = _C._buf(sc["core"], R, hv * 128)
-        _C.gdn_core(proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"], self.ctl, L["dt_bias"], L["g_decay"], G["rec"],
-                    G["gates"], G["sums"], L["gnorm"], c.eps, 128 ** -0.5, c.gdn_key_heads, core=core, raw=True)
         self._tr(f"L{i}.core_raw", core)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"], L["d"], 6,
                        gnorm=(z, L["gnorm"], c.eps))

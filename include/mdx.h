@@ -315,6 +315,29 @@ int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* w
                      float* sums, float qscale, uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
                      void* stream);
 
+/* The Gated-DeltaNet input projections with the conv and the gates, in one launch: [proj | z] =
+ * W4A8 GEMV of the int8 rows x / x_scale over {w_qkv, w_z} (as mdx_stream_gemv, bf16 outputs), with the
+ * deferred causal conv of every qkv channel run by the tile that produced the channel (conv_state,
+ * proj_buf, qkv_buf updated as mdx_gdn_core_raw's conv phase, bit for bit) and this step's gates (decay,
+ * beta of rows < rows; zeros up to slots) computed by extra work-groups of the same launch from xn, wa,
+ * wb, dt_bias, g_decay. Operands as in mdx_gdn_core; w_qkv->n = (2 HK + HV) 128, w_z->n = HV 128, K =
+ * w_qkv->k. Followed by mdx_gdn_delta. Replaces: the in_proj_qkv / in_proj_z GEMMs of
+ * comfy_mono_decode_xpu/layer.py:593 with deltanet_conv_step_deferred and the a / b gates of
+ * gated_delta_decode_deferred (comfy_mono_decode_xpu/layer.py:216-228; csrc/mono_gdn.sycl:313-374,
+ * :424-450). */
+int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4* w_qkv, const mdx_w4* w_z, uint16_t* proj,
+                 uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, const uint16_t* conv_w,
+                 uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
+                 const float* dt_bias, const float* g_decay, float* gates, int64_t rows, int64_t HK, int64_t HV,
+                 int64_t slots, void* stream);
+
+/* The delta rule of a Gated-DeltaNet step after mdx_gdn_proj: the replay of the previous step's accepted
+ * rows and this step's verify program over rec_state, from the conv outputs in qkv_buf and the gates in
+ * gates; core receives the raw bf16 outputs q^ S (as mdx_gdn_core_raw). Replaces: the delta-rule phase of
+ * gated_delta_decode_deferred (comfy_mono_decode_xpu/layer.py:224-228; csrc/mono_gdn.sycl:459-571). */
+int mdx_gdn_delta(const uint16_t* qkv_buf, const int32_t* ctl, float* rec_state, const float* gates, float qscale,
+                  uint16_t* core, int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream);
+
 /* Gated RMSNorm per 128-element head, then the rotation + row quantisation of mdx_rot_quant:
  * y' = bf16(bf16((y gnorm_w) / sqrt(mean_head(y^2) + eps)) * bf16(silu(z))). y_out (optional, may be y)
  * receives y'; with q = scale = NULL and rot = MDX_ROT_NONE only y' is written. y, z, y_out bf16
