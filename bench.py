@@ -679,6 +679,7 @@ def bench_gdn_layer(args, dev):
     xo, xn = torch.empty_like(x), torch.empty_like(x)
     proj = torch.empty(M, C, **bf)
     z = torch.empty(M, HV * DH, **bf)
+    zg = torch.empty(M, HV * DH, **bf)
     core = torch.empty(M, HV * DH, **bf)
     q2 = torch.empty(M, HV * DH, dtype=torch.int8, device=dev)
     s2 = torch.empty(M, dtype=torch.float32, device=dev)
@@ -693,15 +694,18 @@ def bench_gdn_layer(args, dev):
         q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
         if fold:
             _C.gdn_proj(q1, s1, w["qkv"], w["z"], proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"],
-                        ctl, dt_bias, g_decay, w["gates"], HK)
+                        ctl, dt_bias, g_decay, w["gates"], HK, z_gate=zg)
             _C.gdn_delta(w["qb"], ctl, w["rec"], w["gates"], DH ** -0.5, HK, core)
         else:
             _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
             _C.gdn_core(proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay,
                         w["rec"], w["gates"], w["sums"], gnw, 1e-6, DH ** -0.5, HK, core=core, raw=True)
-        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnw), 1e-6, _lib.ptr(core), None,
-                  _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), M, HV * DH, _lib.stream_of(core))
-        _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
+        if fold:  # the gated RMSNorm + quantisation in the out_proj's launch at one or two rows
+            _C.gnorm_linear(core, zg, gnw, 1e-6, w["o"], xo, residual=x, q=q2, scale=s2, z_gated=True)
+        else:
+            _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnw), 1e-6, _lib.ptr(core), None,
+                      _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), M, HV * DH, _lib.stream_of(core))
+            _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
 
     t = ring_time(call, ring_n, args.steps, args.warmup)
     gbs = per / t / 1e9
@@ -710,8 +714,9 @@ def bench_gdn_layer(args, dev):
                  {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
                               f"{ring_n}-copy weight + state ring", "rows": M,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                  "launches_per_step": 5 if fold else 6,
-                  "gdn_path": "conv and gates in the projection launch" if fold else "conv + gates launch"})
+                  "launches_per_step": (4 if M <= 2 else 5) if fold else 6,
+                  "gdn_path": ("conv + gates in the projection launch" + ("; gated RMSNorm + quantisation in the "
+                               "out_proj launch" if M <= 2 else "")) if fold else "six launches"})
 
 
 def bench_read(args, dev):

@@ -93,6 +93,7 @@ struct PrepArgs {
     const uint16_t* hw = nullptr;
     const uint16_t* hz = nullptr;
     float heps = 0.f;
+    int hz_gated = 0;  // hz holds the gate factors gnorm_gate(z) instead of z
 };
 
 // Row prep. One work-group per row, one wave per 256-element group (wave w takes groups w, w + W, ...,
@@ -140,28 +141,10 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
         unpack4(hwraw, hwf);
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
-            float q = __fmul_rn(v[gi][0], v[gi][0]);
-#pragma unroll
-            for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[gi][e], v[gi][e]));
-            q = sum_x16(q);
-            q = __fadd_rn(q, row_shl<8>(q));
-            q = __fadd_rn(q, row_shl<4>(q));
-            q = __fadd_rn(q, row_shl<2>(q));
-            q = __fadd_rn(q, row_shl<1>(q));
-            {
-                const float q0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 0));
-                const float q32 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 32));
-                q = (lane & 32) ? q32 : q0;
-            }
-            const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(q, 128.f), a.heps)));
             float zf[4];
             unpack4(graw[gi], zf);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float normed = bfround(__fmul_rn(__fmul_rn(v[gi][e], hwf[e]), rsq));
-                const float gz = bfround(__fdiv_rn(zf[e], __fadd_rn(1.f, expf(-zf[e]))));
-                v[gi][e] = bfround(__fmul_rn(normed, gz));
-            }
+            if (a.hz_gated) gnorm_pair_g(v[gi], hwf, zf, a.heps, lane);
+            else gnorm_pair(v[gi], hwf, zf, a.heps, lane);
         }
     }
     if (a.nw) {
@@ -227,8 +210,6 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     const float rm = wave_max_nn(lane < W ? wmax[lane] : 0.f);
     const float s = fmaxf(__fdiv_rn(rm, 127.0f), 1e-30f);
     if (threadIdx.x == 0) a.scale[row] = s;
-    uint16_t sb = f2bf(s);
-    if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
     // quant_rcp: the code of v is rint(bf16(v / sb)), the quotient rounded to fp32, then bf16. It is
     // computed as bf16(v * r) with r = fl32(1 / sb): for bf16 v and sb (8-bit significands m_v, m_s)
     // the exact quotient is never a tie of the bf16 rounding (a tie has a 9-bit odd significand, which
@@ -236,20 +217,13 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, const int row, float
     // while the two fp32 roundings of v * r move it by less than 2^-23; r is finite for every sb >=
     // 2^-126, and quotients below the fp32 normal range quantise to 0 either way. (Checked over every
     // bf16 v against 3,256 scales.)
-    const float rr = __fdiv_rn(1.f, bf2f(sb));
+    const float rr = quant_rcp(s);
 #pragma unroll
     for (int gi = 0; gi < GPW; ++gi) {
         const int g = w + W * gi;
         if (g < G) {
-            uint32_t o = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float d = bfround(__fmul_rn(v[gi][e], rr));
-                const int qv = int(fminf(fmaxf(rintf(d), -128.f), 127.f));
-                o |= (uint32_t(qv) & 0xFFu) << (8 * e);
-            }
             uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + int64_t(row) * K + 256 * g + 4 * lane);
-            *qp = o;
+            *qp = quant4(v[gi], rr);
         }
     }
 }
@@ -310,6 +284,7 @@ struct GdnFold {
     const float* dt_bias;    // [HV]
     const float* g_decay;    // [HV]
     float* gates;            // [2][slots][HV][2]
+    uint16_t* zg;            // [rows, HV * 128] or null: the gate factors gnorm_gate(z) of the z outputs
     int HV, slots, units, nside;
 };
 
@@ -349,12 +324,23 @@ struct GemvArgs {
     const uint16_t* xp_x;
     const uint16_t* xp_nw;
     float xp_eps;
+    // SRC_GN units (one or two rows): the activation is the gated RMSNorm per 128-element head of gn_y
+    // (weight gn_w, gate input gn_z; gnorm_pair) quantised in the prologue (no rotation); work-group 0
+    // also stores the normalised rows in gn_out (optional, not aliasing gn_y)
+    const uint16_t* gn_y;
+    const uint16_t* gn_z;
+    const uint16_t* gn_w;
+    float gn_eps;
+    uint16_t* gn_out;
+    int gn_gated;  // gn_z holds the gate factors gnorm_gate(z)
     GdnFold gf;
 };
 
 // Where a unit's activation comes from: int8 rows a.xq (DMA to LDS), bf16 rows quantised with
-// given maxima (SRC_HR), or one bf16 row prepared from scratch (SRC_XP).
-enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2 };
+// given maxima (SRC_HR), one bf16 row prepared from scratch (SRC_XP), or one or two rows of a
+// Gated-DeltaNet's raw outputs gated-normed and quantised (SRC_GN).
+enum Src : int { SRC_Q8 = 0, SRC_HR = 1, SRC_XP = 2, SRC_GN = 3 };
+constexpr int GN_PASSES = 4;  // SRC_GN: head rows per lane (rows x K / 128 <= 8 x waves)
 // Added to a source: the kernel variant with the integral decode only (scales asserted integral, the
 // default codebook, groups the integral form takes). Without the per-weight decode's code the
 // integral path keeps its registers and schedule (the 1-row MLP 24.6 -> 23.x us).
@@ -704,6 +690,7 @@ __device__ void gdn_epilogue(const GemvArgs& a, const int wg, const int32_t* red
             const uint16_t v = f2bf(scaleback(reduced<MFMA>(a, red, ts, r, c), xsl[r], prml[ts * 16 + c]));
             out[r * n + tile * 16 + c] = v;
             if (mi == 0) stage[(ts * a.rows + r) * 16 + c] = v;
+            else if (g.zg) g.zg[r * n + tile * 16 + c] = f2bf(gnorm_gate(bf2f(v)));
         }
     }
     const int S = g.slots, R = a.rows;
@@ -925,6 +912,24 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
                 hv[r][4 * j + 3] = __uint_as_float(m4.w);
             }
     }
+    // SRC_GN: lane l of wave w takes head rows 2 w + l / 32 + 2 waves p (p < GN_PASSES; head row i: row
+    // i / (K / 128), head i % (K / 128)), elements 4 (l % 32) .. + 3: the raw values, the gate inputs and
+    // the norm weights are one-shot operands
+    constexpr bool GN = SRCK == SRC_GN;
+    constexpr int GNP = GN ? GN_PASSES : 1;
+    uint2 gyr[GNP], gzr[GNP], gwr = make_uint2(0u, 0u);
+    if (GN) {
+        const int H = K / 128, nhr = a.rows * H, npass = (nhr + 2 * nwv - 1) / (2 * nwv);
+#pragma unroll
+        for (int p = 0; p < GNP; ++p) {
+            if (p >= npass) break;  // (uniform)
+            const int hr = min(p * 2 * nwv + 2 * wave + (lane >> 5), nhr - 1), row = hr / H;
+            const int64_t off = int64_t(row) * K + (hr - row * H) * 128 + 4 * (lane & 31);
+            gyr[p] = *reinterpret_cast<const uint2*>(a.gn_y + off);
+            gzr[p] = *reinterpret_cast<const uint2*>(a.gn_z + off);
+        }
+        gwr = *reinterpret_cast<const uint2*>(a.gn_w + 4 * (lane & 31));
+    }
     // SRC_XP: the bf16 row and its norm weights land in LDS by DMA with the other one-shot operands,
     // ahead of the weight ring (requested behind it, they would queue behind the whole chip's first
     // round of weights); the prep runs from LDS while that round streams in
@@ -1090,6 +1095,56 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
             }
         }
     }
+    if (GN) {
+        // the gated RMSNorm of every head row (gnorm_pair), the rows' maxima across the waves (the
+        // reduction block holds them), then the row prep's scale and codes into LDS while the ring stays in
+        // flight
+        float* wm = reinterpret_cast<float*>(red);  // [2][16 waves]
+        const int H = K / 128, nhr = a.rows * H, npass = (nhr + 2 * nwv - 1) / (2 * nwv);
+        float hw[4], v[GNP][4], mx[2] = {0.f, 0.f};
+        unpack4(gwr, hw);
+#pragma unroll
+        for (int p = 0; p < GNP; ++p) {
+            if (p >= npass) break;  // (uniform)
+            float z4[4];
+            unpack4(gyr[p], v[p]);
+            unpack4(gzr[p], z4);
+            if (a.gn_gated) gnorm_pair_g(v[p], hw, z4, a.gn_eps, lane);
+            else gnorm_pair(v[p], hw, z4, a.gn_eps, lane);
+            const int hr = p * 2 * nwv + 2 * wave + (lane >> 5);
+            if (hr < nhr) {
+                float m = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[p][e]));
+                if (hr < H) mx[0] = fmaxf(mx[0], m);
+                else mx[1] = fmaxf(mx[1], m);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const float m = wave_max_nn(mx[r]);
+            if (lane == 0) wm[r * 16 + wave] = m;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        float rr[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const float m = wave_max_nn(lane < nwv ? wm[r * 16 + lane] : 0.f);
+            const float s = fmaxf(__fdiv_rn(m, 127.0f), 1e-30f);
+            if (t == 0 && r < a.rows) prml[a.TPW * 16 + r] = s;
+            rr[r] = quant_rcp(s);
+        }
+#pragma unroll
+        for (int p = 0; p < GNP; ++p) {
+            const int hr = p * 2 * nwv + 2 * wave + (lane >> 5);
+            if (p < npass && hr < nhr) {
+                const int row = hr / H, o = (hr - row * H) * 128 + 4 * (lane & 31);
+                *reinterpret_cast<uint32_t*>(xl + row * Kr + o) = quant4(v[p], row ? rr[1] : rr[0]);
+                if (wg == 0 && a.gn_out) *reinterpret_cast<uint2*>(a.gn_out + int64_t(row) * K + o) = pack4(v[p]);
+            }
+        }
+    }
     if (XP) {
         // the row prep of one row (prep_row's arithmetic and order), the barriers without memory
         // waits so that the ring stays in flight; the reduction block holds the group sums / maxima
@@ -1166,25 +1221,25 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     // the activation rows to LDS itself (SRC_HR, SRC_XP).
     bool integ;
     if (TB) {
-        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+        if (HR || XP || GN) {  // (the rows this prologue wrote to LDS)
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
         }
         integ = false;
     } else if (IO) {
-        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+        if (HR || XP || GN) {  // (the rows this prologue wrote to LDS)
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
         }
         integ = true;
     } else if (pwo) {
-        if (HR || XP) {  // (the rows this prologue wrote to LDS)
+        if (HR || XP || GN) {  // (the rows this prologue wrote to LDS)
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
         }
         integ = true;  // (pwo implies assume_int with the default codebook and G128)
     } else if (a.assume_int && can_int) {
-        if (HR || XP) {
+        if (HR || XP || GN) {
             __builtin_amdgcn_s_waitcnt(0xC07F);
             __builtin_amdgcn_s_barrier();
         }
@@ -1482,6 +1537,9 @@ constexpr int TB_RING = 4;  // weight ring depth of the table-only variants
 template <bool MFMA, int R, int SDT, int RING, int TB>
 int launch_gemv_tb(const GemvArgs& a, int wgs, hipStream_t st) {
     if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB + SRC_GDN>(a, wgs, st);
+    if constexpr (SDT == MDX_DT_F16) {  // (gemv_gn_fits: fp16 scales)
+        if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_GN + TB>(a, wgs, st);
+    }
     if (a.hr) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_HR + TB>(a, wgs, st);
     if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_XP + TB>(a, wgs, st);
     return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB>(a, wgs, st);
@@ -1498,11 +1556,17 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
     const bool io = a.assume_int && !a.cb && !a.force_exact && a.lgG >= (MFMA ? 7 : 5);
     if (io) {
         if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY + SRC_GDN>(a, wgs, st);
+        if constexpr (SDT == MDX_DT_F16) {
+            if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, RING, SRC_GN + SRC_INT_ONLY>(a, wgs, st);
+        }
         if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR + SRC_INT_ONLY>(a, wgs, st);
         if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_INT_ONLY>(a, wgs, st);
         return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY>(a, wgs, st);
     }
     if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_GDN>(a, wgs, st);
+    if constexpr (SDT == MDX_DT_F16) {
+        if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, RING, SRC_GN>(a, wgs, st);
+    }
     if (a.hr) return launch_gemv_h<MFMA, R, SDT, RING, SRC_HR>(a, wgs, st);
     if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP>(a, wgs, st);
     return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8>(a, wgs, st);
@@ -1666,6 +1730,17 @@ bool gemv_xp_fits(const mdx_w4* const* ws, int nm, bool pair) {
     return ws[0]->k % 256 == 0 && ws[0]->k / 256 <= int64_t(XP_GPW) * TPW * KS;
 }
 
+// Whether a one-matrix GEMV of `rows` rows takes the gated RMSNorm + quantisation of its activation in its
+// prologue (SRC_GN: one or two rows, fp16 scales, K a multiple of 256, at most GN_PASSES head rows per
+// lane). Every work-group reads both rows and their gate inputs (32 KB at K = 4096), which pays for one or
+// two rows only.
+bool gemv_gn_fits(const mdx_w4* w, int rows) {
+    int TPW, KS;
+    gemv_geometry(int(w->n / 16), int(w->k), false, rows, TPW, KS);
+    return rows >= 1 && rows <= 2 && w->s_dtype == MDX_DT_F16 && w->k % 256 == 0 &&
+           int64_t(rows) * (w->k / 128) <= int64_t(2) * GN_PASSES * TPW * KS;
+}
+
 // Extra activation sources and outputs of one launch (all optional).
 struct GemvExtra {
     uint32_t* hmax_out = nullptr;      // EPI_SILU pair: the work-groups' |h| maxima
@@ -1676,6 +1751,12 @@ struct GemvExtra {
     const uint16_t* xp_nw = nullptr;
     float xp_eps = 0.f;
     const GdnFold* gdn = nullptr;      // a Gated-DeltaNet projection (matrices qkv, z; bf16 outputs)
+    const uint16_t* gn_y = nullptr;    // SRC_GN (gemv_gn_fits): raw rows, gate inputs, norm weights, eps, out
+    const uint16_t* gn_z = nullptr;
+    const uint16_t* gn_w = nullptr;
+    float gn_eps = 0.f;
+    uint16_t* gn_out = nullptr;
+    int gn_gated = 0;
 };
 
 int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const float* xs, int rows, int epi,
@@ -1687,6 +1768,7 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
               "bf16-row GEMV geometry");
     MDX_CHECK(!ex.hmax_out || (pair && rows <= 16), "|h| maxima need a gate/up pair");
     MDX_CHECK(!ex.xp_x || (rows == 1 && gemv_xp_fits(ws, nm, pair)), "row-prep GEMV geometry");
+    MDX_CHECK(!ex.gn_y || (nm == 1 && !pair && ex.gn_z && ex.gn_w && gemv_gn_fits(ws[0], rows)), "gated-norm GEMV geometry");
     // the activation rows live in LDS: above 128 KiB, run the rows in two halves
     if (rows > 8 && int64_t(rows) * ws[0]->k > 128 * 1024) {
         const int ra = 8, rb = rows - 8;
@@ -1704,7 +1786,8 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     }
     GemvArgs a;
     int total = 0;
-    int rc = setup_gemv(ws, nm, pair, ex.hr || ex.xp_x ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut, a, total);
+    int rc = setup_gemv(ws, nm, pair, ex.hr || ex.xp_x || ex.gn_y ? nullptr : xq, xs, rows, epi, outs, res, out_dt, lut,
+                        a, total);
     if (rc) return rc;
     bool mfma = rows >= MFMA_MIN_ROWS;
     gemv_geometry(total, a.K, pair, rows, a.TPW, a.KS);
@@ -1715,6 +1798,12 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
     a.xp_x = ex.xp_x;
     a.xp_nw = ex.xp_nw;
     a.xp_eps = ex.xp_eps;
+    a.gn_y = ex.gn_y;
+    a.gn_z = ex.gn_z;
+    a.gn_w = ex.gn_w;
+    a.gn_eps = ex.gn_eps;
+    a.gn_out = ex.gn_out;
+    a.gn_gated = ex.gn_gated;
     const int wgs = (total + a.TPW - 1) / a.TPW;
     const int esz = esz_of(ws[0]->s_dtype);
     if (ex.gdn) {
@@ -1747,7 +1836,7 @@ int run_gemv(const mdx_w4* const* ws, int nm, bool pair, const int8_t* xq, const
             if (tb == 2 && a.cb) break;
             a.tbl = tb;
             if (int64_t(per_cu) * gemv_smem(a, true, esz) <= 160 * 1024) break;
-            if (tb == 1 && !ex.hr && !ex.xp_x && size_t(a.TPW) * 16 * ngr * 16 >= red_bytes) {
+            if (tb == 1 && !ex.hr && !ex.xp_x && !ex.gn_y && size_t(a.TPW) * 16 * ngr * 16 >= red_bytes) {
                 a.red_alias = 1;
                 if (int64_t(per_cu) * gemv_smem(a, true, esz) <= 160 * 1024) break;
                 a.red_alias = 0;
@@ -1861,6 +1950,42 @@ extern "C" int mdx_gnorm_rot_quant(const uint16_t* y, const uint16_t* z, const u
     a.hz = z;
     a.heps = eps;
     return launch_prep(a, rows, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdx_gnorm_linear(const uint16_t* y, const uint16_t* z, int32_t z_gated, const uint16_t* gnorm_w,
+                                float eps, uint16_t* y_out, const mdx_w4* w, const uint16_t* residual, uint16_t* out,
+                                int8_t* q, float* scale, int64_t rows, void* stream) {
+    MDX_CHECK(y && z && gnorm_w && w && out, "null pointer");
+    int rc = check_w4(w, "weight");
+    if (rc) return rc;
+    const int64_t K = w->k;
+    MDX_CHECK(rows >= 1 && rows <= 16, "rows must be in 1..16");
+    MDX_CHECK(K % 256 == 0 && aligned(y, 8) && aligned(z, 8) && aligned(gnorm_w, 8) && aligned(y_out, 8),
+              "K % 256 == 0, 8-byte aligned rows");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    void* outs[1] = {out};
+    const void* res[1] = {residual};
+    const mdx_w4* ws[1] = {w};
+    const bool overlap = y_out && y_out < y + rows * K && y < y_out + rows * K;
+    if (!overlap && gemv_gn_fits(w, int(rows))) {  // one launch
+        GemvExtra ex;
+        ex.gn_y = y;
+        ex.gn_z = z;
+        ex.gn_w = gnorm_w;
+        ex.gn_eps = eps;
+        ex.gn_out = y_out;
+        ex.gn_gated = z_gated != 0;
+        return run_gemv(ws, 1, false, nullptr, nullptr, int(rows), EPI_STORE, outs, res, MDX_DT_BF16, nullptr, st, ex);
+    }
+    MDX_CHECK(q && scale && aligned(q, 16), "q / scale: the activation of this shape is quantised by its own launch");
+    if ((rc = prep_checks(rows, K, MDX_ROT_NONE, nullptr, y, q, nullptr, y_out))) return rc;
+    PrepArgs pa{y, nullptr, 0.f, y_out, nullptr, MDX_ROT_NONE, q, scale, int(K)};
+    pa.hw = gnorm_w;
+    pa.hz = z;
+    pa.heps = eps;
+    pa.hz_gated = z_gated != 0;
+    if ((rc = launch_prep(pa, rows, st))) return rc;
+    return run_gemv(ws, 1, false, q, scale, int(rows), EPI_STORE, outs, res, MDX_DT_BF16, nullptr, st);
 }
 
 extern "C" int mdx_rmsnorm(const uint16_t* x, const uint16_t* norm_w, float eps, uint16_t* out, int64_t rows, int64_t K,
@@ -2012,8 +2137,8 @@ extern "C" int mdx_stream_gemv(const int8_t* x, const float* x_scale, const mdx_
 extern "C" int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4* w_qkv, const mdx_w4* w_z, uint16_t* proj,
                             uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
                             const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf,
-                            const int32_t* ctl, const float* dt_bias, const float* g_decay, float* gates, int64_t rows,
-                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
+                            const int32_t* ctl, const float* dt_bias, const float* g_decay, float* gates,
+                            uint16_t* z_gate, int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream) {
     MDX_CHECK(x && x_scale && w_qkv && w_z && proj && z && xn && wa && wb && conv_w && conv_state && proj_buf &&
                   qkv_buf && ctl && dt_bias && g_decay && gates,
               "null pointer");
@@ -2036,6 +2161,7 @@ extern "C" int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4*
     f.dt_bias = dt_bias;
     f.g_decay = g_decay;
     f.gates = gates;
+    f.zg = z_gate;
     f.HV = int(HV);
     f.slots = int(slots);
     GemvExtra ex;

@@ -92,4 +92,59 @@ __device__ __forceinline__ float row_rms_factor(const float (&v)[GPW][4], int K,
     return __fdiv_rn(1.f, sqrt_rn(__fadd_rn(mean, eps)));
 }
 
+// bf16(silu(z)) as the gated RMSNorm takes it: bf16(z / (1 + e^-z))
+__device__ __forceinline__ float gnorm_gate(float z) { return bfround(__fdiv_rn(z, __fadd_rn(1.f, expf(-z)))); }
+
+// The gated RMSNorm of two 128-element head rows held by one wave (lanes 0..31 the first, 32..63 the
+// second; lane l holds elements 4 (l % 32) .. + 3 in v, their norm weights in hw and gate factors in gz =
+// gnorm_gate(z)): v <- bf16(bf16(v hw rsq) * gz), rsq = 1 / sqrt(sum(v^2) / 128 + eps). Sum order: the
+// lane partial ((sq0 + sq1) + sq2) + sq3, then a halving tree within each half (l + 16, + 8, ..., + 1),
+// read back from lane 0 / 32. Every lane of the wave must call it.
+__device__ __forceinline__ void gnorm_pair_g(float (&v)[4], const float (&hw)[4], const float (&gz)[4], float eps,
+                                             int lane) {
+    float q = __fmul_rn(v[0], v[0]);
+#pragma unroll
+    for (int e = 1; e < 4; ++e) q = __fadd_rn(q, __fmul_rn(v[e], v[e]));
+    q = sum_x16(q);
+    q = __fadd_rn(q, row_shl<8>(q));
+    q = __fadd_rn(q, row_shl<4>(q));
+    q = __fadd_rn(q, row_shl<2>(q));
+    q = __fadd_rn(q, row_shl<1>(q));
+    {
+        const float q0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 0));
+        const float q32 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(q), 32));
+        q = (lane & 32) ? q32 : q0;
+    }
+    const float rsq = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(q, 128.f), eps)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = bfround(__fmul_rn(bfround(__fmul_rn(__fmul_rn(v[e], hw[e]), rsq)), gz[e]));
+}
+
+// gnorm_pair_g from the gate inputs z
+__device__ __forceinline__ void gnorm_pair(float (&v)[4], const float (&hw)[4], const float (&z)[4], float eps, int lane) {
+    float gz[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gz[e] = gnorm_gate(z[e]);
+    gnorm_pair_g(v, hw, gz, eps, lane);
+}
+
+// The int8 row quantisation of the row prep: scale s = max(absmax / 127, 1e-30) (absmax: the row's
+// maximum |v|, NaN ignored), codes rint(bf16(v * fl32(1 / sb))) clamped to [-128, 127], sb = bf16(s)
+// (0x0080 when that rounds to zero). quant_rcp is 1 / sb.
+__device__ __forceinline__ float quant_rcp(float s) {
+    uint16_t sb = f2bf(s);
+    if ((sb & 0x7FFFu) == 0) sb = 0x0080u;
+    return __fdiv_rn(1.f, bf2f(sb));
+}
+__device__ __forceinline__ uint32_t quant4(const float (&v)[4], float rr) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float d = bfround(__fmul_rn(v[e], rr));
+        const int qv = int(fminf(fmaxf(rintf(d), -128.f), 127.f));
+        o |= (uint32_t(qv) & 0xFFu) << (8 * e);
+    }
+    return o;
+}
+
 }  // namespace mdx

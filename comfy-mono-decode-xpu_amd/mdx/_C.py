@@ -576,13 +576,14 @@ def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt
 
 
 def gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
-             gates_buf, hk):
+             gates_buf, hk, z_gate=None):
     """The GDN input projections with the deferred conv and the gates in one launch (mdx_gdn_proj):
     [proj | z] = W4A8 GEMV of the int8 rows q / s over the W4 handles w_qkv, w_z; the conv runs in the
     epilogue of the tiles that produce each qkv channel (conv_state, proj_buf, qkv_buf updated as
     gdn_core's conv phase), and extra work-groups compute the gates (decay, beta) from xn, wa, wb. The
     in_proj GEMMs + deltanet_conv_step_deferred + the gates of gated_delta_decode_deferred
-    (comfy_mono_decode_xpu/layer.py:216-228, 593). Follow with gdn_delta."""
+    (comfy_mono_decode_xpu/layer.py:216-228, 593). z_gate (optional, like z) receives the gated RMSNorm's
+    gate factors bf16(silu(z)) for gnorm_linear(z_gated=True). Follow with gdn_delta."""
     R = q.shape[0]
     HV = wa.shape[0]
     slots = _slots_of(ctl)
@@ -598,10 +599,12 @@ def gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf
            "GDN projection shapes")
     _check(conv_w.numel() == C * 4 and conv_state.numel() == C * 3 and proj_buf.numel() == 2 * slots * C
            and qkv_buf.numel() == 2 * slots * C and gates_buf.numel() == 2 * slots * HV * 2, "GDN buffers")
+    _check(z_gate is None or (z_gate.dtype == torch.bfloat16 and z_gate.is_contiguous() and z_gate.numel() == z.numel()),
+           "z_gate bf16 like z")
     _lib.call("mdx_gdn_proj", _lib.ptr(q), _lib.ptr(s), ctypes.pointer(w_qkv.struct()), ctypes.pointer(w_z.struct()),
               _lib.ptr(proj), _lib.ptr(z), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), _lib.ptr(conv_w),
               _lib.ptr(conv_state), _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias),
-              _lib.ptr(g_decay), _lib.ptr(gates_buf), R, int(hk), HV, slots, _lib.stream_of(q))
+              _lib.ptr(g_decay), _lib.ptr(gates_buf), _lib.ptr(z_gate), R, int(hk), HV, slots, _lib.stream_of(q))
 
 
 def gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, core):
@@ -637,6 +640,7 @@ def _scratch(dev):
             q1=torch.empty(16, 16384, dtype=torch.int8, device=dev), s=torch.empty(64, dtype=torch.float32, device=dev),
             xn=torch.empty(16, 4096, **bf), x1=torch.empty(16, 4096, **bf), proj=torch.empty(16, 16384, **bf),
             z=torch.empty(16, 8192, **bf), ab=torch.empty(16, 256, **bf), core=torch.empty(16, 8192, **bf),
+            core_n=torch.empty(16, 8192, **bf), zg=torch.empty(16, 8192, **bf),
             mlp_ws=_mlp_workspace(dev),
             wab={})
     return sc
@@ -693,7 +697,28 @@ def layer_pre(x, norm_w, eps, hadamard, mats, nwg=0, tiled=True):
     return [xn] + outs
 
 
-def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop, gnorm=None):
+def gnorm_linear(y, z, gnorm_w, eps, w, out, residual=None, y_out=None, q=None, scale=None, z_gated=False):
+    """out = [residual +] W4A8 GEMV of w over the gated RMSNorm of y (per 128-element head; z the gate input,
+    or with z_gated its gate factors as gdn_proj's z_gate), the rows quantised without rotation
+    (mdx_gnorm_linear): one launch at one or two rows, else the row prep into q / scale (int8 [R, K], f32
+    [R]) then the GEMV. y_out receives the normalised rows."""
+    R, K = y.shape[0], y.shape[-1]
+    for t, n in ((y, "y"), (z, "z"), (gnorm_w, "gnorm_w"), (out, "out")):
+        _dev(t, n)
+        _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
+    _check(z.numel() == R * K and w.k == K and out.numel() == R * w.n and gnorm_w.numel() == 128, "gated-norm linear shapes")
+    _check(residual is None or (residual.dtype == torch.bfloat16 and residual.numel() == R * w.n), "residual bf16 [R, N]")
+    _lib.call("mdx_gnorm_linear", _lib.ptr(y), _lib.ptr(z), int(bool(z_gated)), _lib.ptr(gnorm_w), float(eps),
+              _lib.ptr(y_out),
+              ctypes.pointer(w.struct()), _lib.ptr(residual), _lib.ptr(out), _lib.ptr(q), _lib.ptr(scale), R,
+              _lib.stream_of(y))
+    return out
+
+
+def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D, stop, gnorm=None, gnorm_out=None):
+    """gnorm = (z, weight, eps[, z_gated]): y holds a Gated-DeltaNet's raw outputs, gated-RMSNormed (into
+    gnorm_out, or in place) before the out_proj; z_gated: z holds the gate factors (gdn_proj's z_gate; only
+    without rotation)."""
     R = _rows_of(x)
     _check(stop >= 6, "only the full post block (stop >= 6) is supported")
     _check(y.dtype == torch.bfloat16 and y.is_contiguous() and y.numel() == R * 4096, "y bf16 [R, 4096]")
@@ -701,18 +726,27 @@ def _layer_post(x, y, gate, sig_lut, O, norm_w, eps, hadamard, silu_lut, G, U, D
     x2 = x.view(R, 4096)
     rot = classify_rotation(hadamard)
     q, s = _buf(sc["q1"], R, 4096), sc["s"][:R]
+    x1 = _buf(sc["x1"], R, 4096)
+    if gnorm is not None and rot == _lib.ROT_NONE and gnorm_out is not None:
+        # the gated RMSNorm + quantisation in the out_proj's launch where the shape allows (mdx_gnorm_linear)
+        z, gw, geps = gnorm[:3]
+        gnorm_linear(y.view(R, 4096), z, gw, geps, O, x1, residual=x2, y_out=gnorm_out, q=q, scale=s,
+                     z_gated=len(gnorm) > 3 and gnorm[3])
+        mono_mlp_w4(x1, rot, hadamard, silu_lut, G, U, D, norm_w=norm_w, eps=eps, out=x2, ws=sc["mlp_ws"], residual=x1)
+        return x
     if gnorm is not None:
         # y holds the Gated-DeltaNet's raw outputs: the per-head gated RMSNorm (z, weight, eps), written
-        # back into y, then the rotation + quantisation
-        z, gw, geps = gnorm
-        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(y), _lib.ptr(z), _lib.ptr(gw), float(geps), _lib.ptr(y),
-                  _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(y))
+        # into gnorm_out (or back into y), then the rotation + quantisation
+        z, gw, geps = gnorm[:3]
+        _check(len(gnorm) == 3 or not gnorm[3], "gate factors in place of z need no rotation")
+        _lib.call("mdx_gnorm_rot_quant", _lib.ptr(y), _lib.ptr(z), _lib.ptr(gw), float(geps),
+                  _lib.ptr(y if gnorm_out is None else gnorm_out), _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R,
+                  4096, _lib.stream_of(y))
     elif gate is not None:
         gate_rot_quant(y.view(R, 4096), gate, sig_lut, hadamard, q, s)
     else:
         _lib.call("mdx_rot_quant", _lib.ptr(y), _lib.ptr(hadamard), rot, _lib.ptr(q), _lib.ptr(s), R, 4096,
                   _lib.stream_of(y))
-    x1 = _buf(sc["x1"], R, 4096)
     stream_gemv(q, s, [O], [x1], residuals=[x2])
     mono_mlp_w4(x1, rot, hadamard, silu_lut, G, U, D, norm_w=norm_w, eps=eps, out=x2, ws=sc["mlp_ws"], residual=x1)
     return x
@@ -770,25 +804,27 @@ def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj
     proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
     # the projections with the conv and the gates (one launch), then the delta rule; sums_buf is the
     # reference's, unused here (the norms come from qkv_buf)
+    zg = _buf(sc["zg"], R, Z.n) if rot == _lib.ROT_NONE and stop >= 6 else None
     gdn_proj(q, s, QKV, Z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
-             gates_buf, hk)
+             gates_buf, hk, z_gate=zg)
     core = gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, _buf(sc["core"], R, HV * 128))
-    full = stop >= 6
-    if not full:
+    # the gated RMSNorm writes the layer's core output (layer_gdn_core) into core_n: in the out_proj's
+    # launch or its activation prep (stop >= 6), else on its own
+    core_n = _buf(sc["core_n"], R, HV * 128)
+    if stop < 6:
         _lib.call("mdx_gnorm_rot_quant", _lib.ptr(core), _lib.ptr(z), _lib.ptr(gnorm_w), float(gnorm_eps),
-                  _lib.ptr(core), None, _lib.ROT_NONE, None, None, R, HV * 128, _lib.stream_of(core))
-    if full:
-        # the gated RMSNorm runs inside the out_proj activation prep (core is normed in place there)
+                  _lib.ptr(core_n), None, _lib.ROT_NONE, None, None, R, HV * 128, _lib.stream_of(core))
+    else:
         U.cb = D.cb = G.cb
         _layer_post(x, core, None, None, O, norm_post, eps_post, hadamard, silu_lut, G, U, D, 6,
-                    gnorm=(z, gnorm_w, gnorm_eps))
+                    gnorm=(z, gnorm_w, gnorm_eps) if zg is None else (zg, gnorm_w, gnorm_eps, True), gnorm_out=core_n)
     return x
 
 
 def layer_gdn_core(like, rows):
     """Reference csrc/mono_gdn.sycl:702-704: the GDN core output of the last layer_gdn on this device
     (rows 0..rows-1), valid until the next call."""
-    return _buf(_scratch(like.device)["core"], rows, 4096)
+    return _buf(_scratch(like.device)["core_n"], rows, 4096)
 
 
 def rmsnorm(x, w, eps, out=None):

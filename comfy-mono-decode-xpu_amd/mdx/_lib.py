@@ -87,9 +87,12 @@ SIGNATURES = {
                                         ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "mdx_gdn_proj": (ctypes.c_int, [c_void_p, c_void_p, W4P, W4P, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                    c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                    c_void_p]),
     "mdx_gdn_delta": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_void_p]),
+    "mdx_gnorm_linear": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, ctypes.c_float, c_void_p, W4P,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "mdx_gnorm_rot_quant": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
                                            ctypes.c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_topk_rows_noalloc": (ctypes.c_int, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p,
@@ -150,7 +153,7 @@ def call(name, *args):
     return rc
 
 
-SRC_Q8, SRC_HR, SRC_XP = 0, 1, 2
+SRC_Q8, SRC_HR, SRC_XP, SRC_GN = 0, 1, 2, 3
 SRC_INT_ONLY, SRC_TBL, SRC_TBL8, SRC_GDN = 4, 8, 16, 32
 
 

@@ -365,9 +365,10 @@ class HybridModel:
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
         core = _C._buf(sc["core"], R, hv * 128)
+        zg = _C._buf(sc["zg"], R, hv * 128) if c.gdn_fold and self.rot == _lib.ROT_NONE else None
         if c.gdn_fold:
             _C.gdn_proj(q, s, L["qkv"], L["z"], proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"],
-                        self.ctl, L["dt_bias"], L["g_decay"], G["gates"], c.gdn_key_heads)
+                        self.ctl, L["dt_bias"], L["g_decay"], G["gates"], c.gdn_key_heads, z_gate=zg)
             _C.gdn_delta(G["qb"], self.ctl, G["rec"], G["gates"], 128 ** -0.5, c.gdn_key_heads, core)
         else:
             _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])
@@ -377,9 +378,10 @@ class HybridModel:
         self._tr(f"L{i}.proj", proj)
         self._tr(f"L{i}.z", z)
         self._tr(f"L{i}.core_raw", core)
+        core_n = _C._buf(sc["core_n"], R, hv * 128)
         _C._layer_post(x, core, None, None, L["o"], L["norm_post"], c.eps, self.hrot, self.silu, L["g"], L["u"], L["d"], 6,
-                       gnorm=(z, L["gnorm"], c.eps))
-        self._tr(f"L{i}.core", core)
+                       gnorm=(z, L["gnorm"], c.eps) if zg is None else (zg, L["gnorm"], c.eps, True), gnorm_out=core_n)
+        self._tr(f"L{i}.core", core_n)
 
     def verify_layers(self, x, R, mask, seq, pos, freqs):
         for i in range(self.cfg.layers):

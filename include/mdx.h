@@ -321,15 +321,16 @@ int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* w
  * proj_buf, qkv_buf updated as mdx_gdn_core_raw's conv phase, bit for bit) and this step's gates (decay,
  * beta of rows < rows; zeros up to slots) computed by extra work-groups of the same launch from xn, wa,
  * wb, dt_bias, g_decay. Operands as in mdx_gdn_core; w_qkv->n = (2 HK + HV) 128, w_z->n = HV 128, K =
- * w_qkv->k. Followed by mdx_gdn_delta. Replaces: the in_proj_qkv / in_proj_z GEMMs of
+ * w_qkv->k. z_gate (optional, bf16 [rows, HV 128]) receives the gated RMSNorm's gate factors
+ * bf16(z / (1 + e^-z)) of the z outputs, for mdx_gnorm_linear with z_gated. Followed by mdx_gdn_delta. Replaces: the in_proj_qkv / in_proj_z GEMMs of
  * comfy_mono_decode_xpu/layer.py:593 with deltanet_conv_step_deferred and the a / b gates of
  * gated_delta_decode_deferred (comfy_mono_decode_xpu/layer.py:216-228; csrc/mono_gdn.sycl:313-374,
  * :424-450). */
 int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4* w_qkv, const mdx_w4* w_z, uint16_t* proj,
                  uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, const uint16_t* conv_w,
                  uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
-                 const float* dt_bias, const float* g_decay, float* gates, int64_t rows, int64_t HK, int64_t HV,
-                 int64_t slots, void* stream);
+                 const float* dt_bias, const float* g_decay, float* gates, uint16_t* z_gate, int64_t rows, int64_t HK,
+                 int64_t HV, int64_t slots, void* stream);
 
 /* The delta rule of a Gated-DeltaNet step after mdx_gdn_proj: the replay of the previous step's accepted
  * rows and this step's verify program over rec_state, from the conv outputs in qkv_buf and the gates in
@@ -345,6 +346,20 @@ int mdx_gdn_delta(const uint16_t* qkv_buf, const int32_t* ctl, float* rec_state,
  * (csrc/mono_gdn.sycl:574-607) together with the out_proj activation prep that follows it. */
 int mdx_gnorm_rot_quant(const uint16_t* y, const uint16_t* z, const uint16_t* gnorm_w, float eps, uint16_t* y_out,
                         const uint16_t* h, int32_t rot, int8_t* q, float* scale, int64_t rows, int64_t K, void* stream);
+
+/* The out_proj of a Gated-DeltaNet layer from its raw outputs: y' = the gated RMSNorm of y (z, gnorm_w, eps;
+ * mdx_gnorm_rot_quant's arithmetic; with z_gated, z holds the gate factors bf16(z / (1 + e^-z)) instead, as
+ * mdx_gdn_proj's z_gate), quantised per row without rotation, then out = W4A8 GEMV of w (with
+ * residual as in mdx_w4a8_decode_linear; bf16). At one or two rows with fp16 scales, one launch: every
+ * work-group of the GEMV normalises and quantises the rows in its prologue; otherwise two (the row prep into
+ * q int8 [rows, K] / scale f32 [rows], then the GEMV), and q / scale must be given. y_out (optional)
+ * receives y'; it may alias y only at the shapes that take two launches. y, z, y_out bf16 [rows, K];
+ * gnorm_w bf16 [128]; K = w->k, K % 256 == 0. Replaces: the gated RMSNorm of gated_delta_decode_deferred
+ * (csrc/mono_gdn.sycl:574-607) with layer_post's out_proj activation prep and out_proj
+ * (csrc/mono_layer.sycl:157-318). */
+int mdx_gnorm_linear(const uint16_t* y, const uint16_t* z, int32_t z_gated, const uint16_t* gnorm_w, float eps,
+                     uint16_t* y_out, const mdx_w4* w, const uint16_t* residual, uint16_t* out, int8_t* q, float* scale,
+                     int64_t rows, void* stream);
 
 /* Sigmoid-gated rotation + row quantisation: y' = bf16(y * sig_lut[gate]), then rot_quant(y').
  * Replaces: the first phase of _C.layer_post (csrc/mono_layer.sycl:243-256: the gated attention output,
