@@ -691,10 +691,13 @@ def bench_gdn_layer(args, dev):
 
     def call(i):
         w = ring[i]
-        q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
+        q1 = s1 = None
+        if not (fold and M == 1):  # (one row folded: the row prep runs in the projection launch)
+            q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
         if fold:
-            _C.gdn_proj(q1, s1, w["qkv"], w["z"], proj, z, xn, w["wa"], w["wb"], w["conv_w"], w["conv"], w["pb"], w["qb"],
-                        ctl, dt_bias, g_decay, w["gates"], HK, z_gate=zg)
+            _C.gdn_proj(q1, s1, w["qkv"], w["z"], proj, z, None if M == 1 else xn, w["wa"], w["wb"], w["conv_w"],
+                        w["conv"], w["pb"], w["qb"], ctl, dt_bias, g_decay, w["gates"], HK, z_gate=zg,
+                        x_row=x if M == 1 else None, norm_w=nw, eps=1e-6)
             _C.gdn_delta(w["qb"], ctl, w["rec"], w["gates"], DH ** -0.5, HK, core)
         else:
             _C.stream_gemv(q1, s1, [w["qkv"], w["z"]], [proj, z])
@@ -714,9 +717,10 @@ def bench_gdn_layer(args, dev):
                  {"workload": f"Gated-DeltaNet layer mixer, {M} chain rows, 16 key / 32 value heads of 128, conv 4, "
                               f"{ring_n}-copy weight + state ring", "rows": M,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                  "launches_per_step": (4 if M <= 2 else 5) if fold else 6,
-                  "gdn_path": ("conv + gates in the projection launch" + ("; gated RMSNorm + quantisation in the "
-                               "out_proj launch" if M <= 2 else "")) if fold else "six launches"})
+                  "launches_per_step": (3 if M == 1 else 4 if M <= 2 else 5) if fold else 6,
+                  "gdn_path": (("row prep, " if M == 1 else "") + "conv + gates in the projection launch" +
+                               ("; gated RMSNorm + quantisation in the out_proj launch" if M <= 2 else ""))
+                              if fold else "six launches"})
 
 
 def bench_read(args, dev):

@@ -709,20 +709,56 @@ __device__ void gdn_epilogue(const GemvArgs& a, const int wg, const int32_t* red
                      g.conv_w, g.conv_state, g.pb, g.qb);
 }
 
+// The RMSNorm of a row-prep launch's one row into LDS (xnl, bf16 [K]) by a gate work-group: the row
+// prep's arithmetic (row_rms_factor's order, then bf16((v r) w)), wave w taking the 256-groups w, w +
+// waves, ... (K <= 1024 x waves).
+__device__ void side_row_norm(const GemvArgs& a, uint16_t* xnl, float* gsum) {
+    const int K = a.K, G = K / 256, W = blockDim.x / 64, w = threadIdx.x / 64, lane = threadIdx.x % 64;
+    float v[XP_GPW][4];
+    uint2 wr[XP_GPW];
+#pragma unroll
+    for (int gi = 0; gi < XP_GPW; ++gi) {
+        const int g = min(w + W * gi, G - 1);
+        unpack4(*reinterpret_cast<const uint2*>(a.xp_x + 256 * g + 4 * lane), v[gi]);
+        wr[gi] = *reinterpret_cast<const uint2*>(a.xp_nw + 256 * g + 4 * lane);
+    }
+    const float r = row_rms_factor<XP_GPW>(v, K, a.xp_eps, gsum);
+#pragma unroll
+    for (int gi = 0; gi < XP_GPW; ++gi) {
+        const int g = w + W * gi;
+        if (g < G) {
+            float wv[4];
+            unpack4(wr[gi], wv);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[gi][e] = bfround(__fmul_rn(__fmul_rn(v[gi][e], r), wv[e]));
+            *reinterpret_cast<uint2*>(xnl + 256 * g + 4 * lane) = pack4(v[gi]);
+        }
+    }
+    __syncthreads();
+}
+
 // The gates of a Gated-DeltaNet projection launch, by side work-group b (< nside): wave w computes row ts,
-// value head h of pair b * waves + w (rows < R; gdn_gate_row); rows R .. slots - 1 get zeros.
-__device__ void gdn_gates_side(const GemvArgs& a, int b) {
+// value head h of pair b * waves + w (rows < R; gdn_gate_row); rows R .. slots - 1 get zeros. A row-prep
+// launch (one bf16 row, a.xp_x) has no normalised row in memory: each gate work-group computes it into
+// LDS first.
+__device__ void gdn_gates_side(const GemvArgs& a, int b, uint8_t* lds) {
     const GdnFold& g = a.gf;
     const int t = threadIdx.x, lane = t & 63, nw = blockDim.x >> 6, nthr = blockDim.x;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int R = a.rows, S = g.slots, HV = g.HV;
     const int pending = g.ctl[0], p = g.ctl[1];
     const bool ok = gdn_ctl_ok(pending, p, S);
+    const uint16_t* xn = g.xn;
+    if (a.xp_x) {  // (uniform)
+        uint16_t* xnl = reinterpret_cast<uint16_t*>(lds);
+        side_row_norm(a, xnl, reinterpret_cast<float*>(lds + 2 * a.K));
+        xn = xnl;
+    }
     const int pair = b * nw + wv;
     if (pair < R * HV) {
         const int ts = pair / HV, h = pair - ts * HV;
         float decay, beta;
-        gdn_gate_row<2>(g.xn + int64_t(ts) * a.K, g.wa + int64_t(h) * a.K, g.wb + int64_t(h) * a.K, a.K, g.dt_bias[h],
+        gdn_gate_row<2>(xn + int64_t(ts) * a.K, g.wa + int64_t(h) * a.K, g.wb + int64_t(h) * a.K, a.K, g.dt_bias[h],
                         g.g_decay[h], lane, decay, beta);
         if (lane == 0 && ok) {
             g.gates[((p * S + ts) * HV + h) * 2] = decay;
@@ -877,7 +913,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
     }
     // a Gated-DeltaNet projection's control words (the epilogue's conv reads them from LDS)
     constexpr bool GDN = (SRC & SRC_GDN) != 0;
-    static_assert(!GDN || (SRC & 3) == SRC_Q8, "Gated-DeltaNet projections take int8 rows");
+    static_assert(!GDN || (SRC & 3) == SRC_Q8 || (SRC & 3) == SRC_XP, "Gated-DeltaNet projections take int8 rows or one bf16 row");
     int gctl = 0;
     if (GDN && t < 2 + 3 * a.gf.slots) gctl = a.gf.ctl[t];
     // SRC_HR: the bf16 rows (HRP 16-byte pieces per thread at most) and the maxima entries (thread t:
@@ -1469,7 +1505,7 @@ __global__ __launch_bounds__((SRC & 3) == SRC_HR ? 768 : 1024) void gemv_kernel(
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if constexpr ((SRC & SRC_GDN) != 0) {
         if (int(blockIdx.x) >= a.gf.units) {  // (uniform) a gate work-group
-            gdn_gates_side(a, int(blockIdx.x) - a.gf.units);
+            gdn_gates_side(a, int(blockIdx.x) - a.gf.units, lds);
             return;
         }
     }
@@ -1536,7 +1572,12 @@ constexpr int TB_RING = 4;  // weight ring depth of the table-only variants
 
 template <bool MFMA, int R, int SDT, int RING, int TB>
 int launch_gemv_tb(const GemvArgs& a, int wgs, hipStream_t st) {
-    if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB + SRC_GDN>(a, wgs, st);
+    if (a.gf.on) {
+        if constexpr (SDT == MDX_DT_F16) {  // (mdx_gdn_proj with a bf16 row: fp16 scales)
+            if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_XP + TB + SRC_GDN>(a, wgs, st);
+        }
+        return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_Q8 + TB + SRC_GDN>(a, wgs, st);
+    }
     if constexpr (SDT == MDX_DT_F16) {  // (gemv_gn_fits: fp16 scales)
         if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, TB_RING, SRC_GN + TB>(a, wgs, st);
     }
@@ -1555,7 +1596,12 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
     // the integral-only variant when the caller asserts integral scales that the integral form takes
     const bool io = a.assume_int && !a.cb && !a.force_exact && a.lgG >= (MFMA ? 7 : 5);
     if (io) {
-        if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY + SRC_GDN>(a, wgs, st);
+        if (a.gf.on) {
+            if constexpr (!MFMA && SDT == MDX_DT_F16) {
+                if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_INT_ONLY + SRC_GDN>(a, wgs, st);
+            }
+            return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY + SRC_GDN>(a, wgs, st);
+        }
         if constexpr (SDT == MDX_DT_F16) {
             if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, RING, SRC_GN + SRC_INT_ONLY>(a, wgs, st);
         }
@@ -1563,7 +1609,12 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t st) {
         if (!MFMA && a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_INT_ONLY>(a, wgs, st);
         return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_INT_ONLY>(a, wgs, st);
     }
-    if (a.gf.on) return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_GDN>(a, wgs, st);
+    if (a.gf.on) {
+        if constexpr (!MFMA && SDT == MDX_DT_F16) {
+            if (a.xp_x) return launch_gemv_h<MFMA, R, SDT, RING, SRC_XP + SRC_GDN>(a, wgs, st);
+        }
+        return launch_gemv_h<MFMA, R, SDT, RING, SRC_Q8 + SRC_GDN>(a, wgs, st);
+    }
     if constexpr (SDT == MDX_DT_F16) {
         if (a.gn_y) return launch_gemv_h<MFMA, R, SDT, RING, SRC_GN>(a, wgs, st);
     }
@@ -2138,9 +2189,10 @@ extern "C" int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4*
                             uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb,
                             const uint16_t* conv_w, uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf,
                             const int32_t* ctl, const float* dt_bias, const float* g_decay, float* gates,
-                            uint16_t* z_gate, int64_t rows, int64_t HK, int64_t HV, int64_t slots, void* stream) {
-    MDX_CHECK(x && x_scale && w_qkv && w_z && proj && z && xn && wa && wb && conv_w && conv_state && proj_buf &&
-                  qkv_buf && ctl && dt_bias && g_decay && gates,
+                            uint16_t* z_gate, const uint16_t* x_row, const uint16_t* norm_w, float eps, int64_t rows,
+                            int64_t HK, int64_t HV, int64_t slots, void* stream) {
+    MDX_CHECK(((x && x_scale && xn) || (x_row && norm_w)) && w_qkv && w_z && proj && z && wa && wb && conv_w &&
+                  conv_state && proj_buf && qkv_buf && ctl && dt_bias && g_decay && gates,
               "null pointer");
     MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
     MDX_CHECK(rows >= 1 && rows <= slots, "1 <= rows <= slots");
@@ -2168,6 +2220,14 @@ extern "C" int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4*
     ex.gdn = &f;
     const mdx_w4* mats[2] = {w_qkv, w_z};
     void* outs[2] = {proj, z};
+    if (x_row) {  // one bf16 row, its RMSNorm + quantisation in the launch
+        MDX_CHECK(rows == 1 && w_qkv->s_dtype == MDX_DT_F16 && aligned(x_row, 16) && aligned(norm_w, 16) &&
+                      gemv_xp_fits(mats, 2, false),
+                  "a bf16 row: one row, fp16 scales, 16-byte aligned x_row / norm_w");
+        ex.xp_x = x_row;
+        ex.xp_nw = norm_w;
+        ex.xp_eps = eps;
+    }
     return run_gemv(mats, 2, false, x, x_scale, int(rows), EPI_STORE, outs, nullptr, MDX_DT_BF16, nullptr,
                     static_cast<hipStream_t>(stream), ex);
 }

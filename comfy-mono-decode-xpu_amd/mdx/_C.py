@@ -576,27 +576,34 @@ def gdn_core(proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt
 
 
 def gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
-             gates_buf, hk, z_gate=None):
+             gates_buf, hk, z_gate=None, x_row=None, norm_w=None, eps=0.0):
     """The GDN input projections with the deferred conv and the gates in one launch (mdx_gdn_proj):
     [proj | z] = W4A8 GEMV of the int8 rows q / s over the W4 handles w_qkv, w_z; the conv runs in the
     epilogue of the tiles that produce each qkv channel (conv_state, proj_buf, qkv_buf updated as
     gdn_core's conv phase), and extra work-groups compute the gates (decay, beta) from xn, wa, wb. The
     in_proj GEMMs + deltanet_conv_step_deferred + the gates of gated_delta_decode_deferred
     (comfy_mono_decode_xpu/layer.py:216-228, 593). z_gate (optional, like z) receives the gated RMSNorm's
-    gate factors bf16(silu(z)) for gnorm_linear(z_gated=True). Follow with gdn_delta."""
-    R = q.shape[0]
+    gate factors bf16(silu(z)) for gnorm_linear(z_gated=True). x_row (one bf16 row [1, K]) with norm_w /
+    eps: the row prep (RMSNorm + quantisation, no rotation) runs in the launch; q, s and xn are then
+    unused (None). Follow with gdn_delta."""
+    R = proj.shape[0]
     HV = wa.shape[0]
+    K = wa.shape[1]
     slots = _slots_of(ctl)
-    for t, n in ((proj, "proj"), (z, "z"), (xn, "xn"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"),
+    for t, n in ((proj, "proj"), (z, "z"), (wa, "wa"), (wb, "wb"), (conv_w, "conv_w"),
                  (conv_state, "conv_state"), (proj_buf, "proj_buf"), (qkv_buf, "qkv_buf")):
         _dev(t, n)
         _check(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{n}: contiguous bf16")
     for t, n in ((dt_bias, "dt_bias"), (g_decay, "g_decay"), (gates_buf, "gates")):
         _check(t.dtype == torch.float32 and t.is_contiguous(), f"{n}: contiguous f32")
     C = w_qkv.n
-    _check(q.dtype == torch.int8 and q.is_contiguous() and s.numel() >= R, "q int8 [R, K], s f32 [R]")
-    _check(proj.numel() == R * C and z.numel() == R * w_z.n and xn.numel() == R * wa.shape[1] and wb.shape == wa.shape,
-           "GDN projection shapes")
+    if x_row is None:
+        _check(q.dtype == torch.int8 and q.is_contiguous() and q.shape[0] == R and s.numel() >= R, "q int8 [R, K], s f32 [R]")
+        _check(xn.dtype == torch.bfloat16 and xn.numel() == R * K, "xn bf16 [R, K]")
+    else:
+        _check(R == 1 and x_row.dtype == torch.bfloat16 and x_row.numel() == K and norm_w is not None
+               and norm_w.dtype == torch.bfloat16 and norm_w.numel() == K, "x_row bf16 [1, K] with norm_w bf16 [K]")
+    _check(proj.numel() == R * C and z.numel() == R * w_z.n and wb.shape == wa.shape, "GDN projection shapes")
     _check(conv_w.numel() == C * 4 and conv_state.numel() == C * 3 and proj_buf.numel() == 2 * slots * C
            and qkv_buf.numel() == 2 * slots * C and gates_buf.numel() == 2 * slots * HV * 2, "GDN buffers")
     _check(z_gate is None or (z_gate.dtype == torch.bfloat16 and z_gate.is_contiguous() and z_gate.numel() == z.numel()),
@@ -604,7 +611,8 @@ def gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf
     _lib.call("mdx_gdn_proj", _lib.ptr(q), _lib.ptr(s), ctypes.pointer(w_qkv.struct()), ctypes.pointer(w_z.struct()),
               _lib.ptr(proj), _lib.ptr(z), _lib.ptr(xn), _lib.ptr(wa), _lib.ptr(wb), _lib.ptr(conv_w),
               _lib.ptr(conv_state), _lib.ptr(proj_buf), _lib.ptr(qkv_buf), _lib.ptr(ctl), _lib.ptr(dt_bias),
-              _lib.ptr(g_decay), _lib.ptr(gates_buf), _lib.ptr(z_gate), R, int(hk), HV, slots, _lib.stream_of(q))
+              _lib.ptr(g_decay), _lib.ptr(gates_buf), _lib.ptr(z_gate), _lib.ptr(x_row), _lib.ptr(norm_w), float(eps),
+              R, int(hk), HV, slots, _lib.stream_of(proj))
 
 
 def gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, core):
@@ -799,14 +807,17 @@ def layer_gdn(x, norm_in, eps_in, hadamard, w4, wa, wb, conv_w, conv_state, proj
     x2 = x.view(R, 4096)
     rot = classify_rotation(hadamard)
     xn, q, s = _buf(sc["xn"], R, 4096), _buf(sc["q1"], R, 4096), sc["s"][:R]
-    _lib.call("mdx_rms_rot_quant", _lib.ptr(x2), _lib.ptr(norm_in), float(eps_in), _lib.ptr(xn), _lib.ptr(hadamard), rot,
-              _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(x))
+    # one row without rotation: the row prep runs in the projection launch
+    xrow = R == 1 and rot == _lib.ROT_NONE and QKV.s.dtype == torch.float16
+    if not xrow:
+        _lib.call("mdx_rms_rot_quant", _lib.ptr(x2), _lib.ptr(norm_in), float(eps_in), _lib.ptr(xn), _lib.ptr(hadamard),
+                  rot, _lib.ptr(q), _lib.ptr(s), R, 4096, _lib.stream_of(x))
     proj, z = _buf(sc["proj"], R, QKV.n), _buf(sc["z"], R, Z.n)
     # the projections with the conv and the gates (one launch), then the delta rule; sums_buf is the
     # reference's, unused here (the norms come from qkv_buf)
     zg = _buf(sc["zg"], R, Z.n) if rot == _lib.ROT_NONE and stop >= 6 else None
     gdn_proj(q, s, QKV, Z, proj, z, xn, wa, wb, conv_w, conv_state, proj_buf, qkv_buf, ctl, dt_bias, g_decay,
-             gates_buf, hk, z_gate=zg)
+             gates_buf, hk, z_gate=zg, x_row=x2 if xrow else None, norm_w=norm_in, eps=eps_in)
     core = gdn_delta(qkv_buf, ctl, rec_state, gates_buf, qscale, hk, _buf(sc["core"], R, HV * 128))
     # the gated RMSNorm writes the layer's core output (layer_gdn_core) into core_n: in the out_proj's
     # launch or its activation prep (stop >= 6), else on its own

@@ -87,8 +87,8 @@ SIGNATURES = {
                                         ctypes.c_float, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "mdx_gdn_proj": (ctypes.c_int, [c_void_p, c_void_p, W4P, W4P, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                    c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-                                    c_void_p]),
+                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float,
+                                    c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "mdx_gdn_delta": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_void_p]),
     "mdx_gnorm_linear": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, ctypes.c_float, c_void_p, W4P,

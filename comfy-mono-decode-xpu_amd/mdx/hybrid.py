@@ -360,15 +360,19 @@ class HybridModel:
         c, L, G = self.cfg, self.layers[i], self.gdn[i]
         sc = _C._scratch(self.dev)
         xn, q, s = _C._buf(sc["xn"], R, c.hidden), _C._buf(sc["q1"], R, c.hidden), sc["s"][:R]
-        _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn), _lib.ptr(self.hrot),
-                  self.rot, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
+        # one row without rotation: the row prep runs in the projection launch (fp16 scales)
+        xrow = c.gdn_fold and R == 1 and self.rot == _lib.ROT_NONE and L["qkv"].s.dtype == torch.float16
+        if not xrow:
+            _lib.call("mdx_rms_rot_quant", _lib.ptr(x), _lib.ptr(L["norm_in"]), float(c.eps), _lib.ptr(xn),
+                      _lib.ptr(self.hrot), self.rot, _lib.ptr(q), _lib.ptr(s), R, c.hidden, _lib.stream_of(x))
         hv = c.gdn_value_heads
         proj, z = _C._buf(sc["proj"], R, self.gdn_ch), _C._buf(sc["z"], R, hv * 128)
         core = _C._buf(sc["core"], R, hv * 128)
         zg = _C._buf(sc["zg"], R, hv * 128) if c.gdn_fold and self.rot == _lib.ROT_NONE else None
         if c.gdn_fold:
             _C.gdn_proj(q, s, L["qkv"], L["z"], proj, z, xn, L["wa"], L["wb"], L["conv_w"], G["conv"], G["pb"], G["qb"],
-                        self.ctl, L["dt_bias"], L["g_decay"], G["gates"], c.gdn_key_heads, z_gate=zg)
+                        self.ctl, L["dt_bias"], L["g_decay"], G["gates"], c.gdn_key_heads, z_gate=zg,
+                        x_row=x.view(1, -1) if xrow else None, norm_w=L["norm_in"], eps=c.eps)
             _C.gdn_delta(G["qb"], self.ctl, G["rec"], G["gates"], 128 ** -0.5, c.gdn_key_heads, core)
         else:
             _C.stream_gemv(q, s, [L["qkv"], L["z"]], [proj, z])

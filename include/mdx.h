@@ -322,15 +322,19 @@ int mdx_gdn_core_raw(const uint16_t* proj, const uint16_t* xn, const uint16_t* w
  * beta of rows < rows; zeros up to slots) computed by extra work-groups of the same launch from xn, wa,
  * wb, dt_bias, g_decay. Operands as in mdx_gdn_core; w_qkv->n = (2 HK + HV) 128, w_z->n = HV 128, K =
  * w_qkv->k. z_gate (optional, bf16 [rows, HV 128]) receives the gated RMSNorm's gate factors
- * bf16(z / (1 + e^-z)) of the z outputs, for mdx_gnorm_linear with z_gated. Followed by mdx_gdn_delta. Replaces: the in_proj_qkv / in_proj_z GEMMs of
+ * bf16(z / (1 + e^-z)) of the z outputs, for mdx_gnorm_linear with z_gated. With x_row (one row, bf16
+ * [K], 16-byte aligned; fp16 scales) the launch also runs the row prep of x_row (RMSNorm with norm_w, eps,
+ * then the quantisation: mdx_rms_rot_quant with MDX_ROT_NONE, bit for bit) in its prologue, and x, x_scale
+ * and xn are unused (may be NULL). Followed by mdx_gdn_delta. Replaces: the in_proj_qkv / in_proj_z GEMMs of
  * comfy_mono_decode_xpu/layer.py:593 with deltanet_conv_step_deferred and the a / b gates of
  * gated_delta_decode_deferred (comfy_mono_decode_xpu/layer.py:216-228; csrc/mono_gdn.sycl:313-374,
  * :424-450). */
 int mdx_gdn_proj(const int8_t* x, const float* x_scale, const mdx_w4* w_qkv, const mdx_w4* w_z, uint16_t* proj,
                  uint16_t* z, const uint16_t* xn, const uint16_t* wa, const uint16_t* wb, const uint16_t* conv_w,
                  uint16_t* conv_state, uint16_t* proj_buf, uint16_t* qkv_buf, const int32_t* ctl,
-                 const float* dt_bias, const float* g_decay, float* gates, uint16_t* z_gate, int64_t rows, int64_t HK,
-                 int64_t HV, int64_t slots, void* stream);
+                 const float* dt_bias, const float* g_decay, float* gates, uint16_t* z_gate, const uint16_t* x_row,
+                 const uint16_t* norm_w, float eps, int64_t rows, int64_t HK, int64_t HV, int64_t slots,
+                 void* stream);
 
 /* The delta rule of a Gated-DeltaNet step after mdx_gdn_proj: the replay of the previous step's accepted
  * rows and this step's verify program over rec_state, from the conv outputs in qkv_buf and the gates in

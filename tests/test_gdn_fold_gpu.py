@@ -21,7 +21,7 @@ def _state(gen, dev, slots):
                 sums=torch.zeros(2, slots, HK, 2, device=dev))
 
 
-@pytest.mark.parametrize("slots,widths,integral", [(8, (), False), (8, (4, 3), False), (8, (1,) * 7, True),
+@pytest.mark.parametrize("slots,widths,integral", [(8, (), False), (8, (), True), (8, (4, 3), False), (8, (1,) * 7, True),
                                                    (16, (4, 3, 2, 2, 2, 2), False), (16, (1,) * 15, True)])
 def test_fold_matches_separate_launches(C, dev, slots, widths, integral):
     from mdx import _lib, hybrid
@@ -58,10 +58,13 @@ def test_fold_matches_separate_launches(C, dev, slots, widths, integral):
             if name == "fold":
                 _lib.gemv_trace()
                 zg = torch.empty_like(z)
-                C.gdn_proj(q, s, w_qkv, w_z, proj, z, xn, wa, wb, conv_w, st["conv"], st["pb"], st["qb"], ctl, dt_bias,
-                           g_decay, st["gates"], HK, z_gate=zg)
+                # one row: the row prep in the launch (x itself, no q / s / xn)
+                C.gdn_proj(None if R == 1 else q, None if R == 1 else s, w_qkv, w_z, proj, z, None if R == 1 else xn, wa,
+                           wb, conv_w, st["conv"], st["pb"], st["qb"], ctl, dt_bias, g_decay, st["gates"], HK, z_gate=zg,
+                           x_row=x if R == 1 else None, norm_w=nw, eps=1e-6)
                 tr = _lib.gemv_trace()
                 assert len(tr) == 1 and tr[0]["gdn"] and tr[0]["decode"] == ("integral" if integral else "table16"), tr
+                assert tr[0]["src"] == (_lib.SRC_XP if R == 1 else _lib.SRC_Q8), tr
                 C.gdn_delta(st["qb"], ctl, st["rec"], st["gates"], DH ** -0.5, HK, core)
             else:
                 C.stream_gemv(q, s, [w_qkv, w_z], [proj, z])
