@@ -397,7 +397,17 @@ __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
     const bool rvalid = r < a.rows;
     const int rr = rvalid ? r : 0;
     const int hq = kh * a.groups + rr / a.S, sq = rr % a.S;
-    const uint32_t rmask = (tree && rvalid) ? uint32_t(a.mask[sq]) : 0u;
+    // the tree rows' masks by scalar loads (the tree work-group only): a vector load here would be waited
+    // for with vmcnt(0) at its first use, i.e. behind every stage of the ring issued below
+    uint32_t rmask = 0u;
+    if (tree) {  // (uniform)
+        typedef __attribute__((address_space(4))) const int32_t* const_i32p;
+        const const_i32p mc = (const_i32p)(a.mask);
+        for (int i = 0; i < a.S; ++i) {
+            const uint32_t mi = uint32_t(mc[i]);
+            rmask = (rvalid && sq == i) ? mi : rmask;
+        }
+    }
 
     // the part's tokens and sources (element strides)
     int t_begin, t_end;
@@ -562,14 +572,17 @@ __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
         return;
     }
     __syncthreads();  // the ring is free
-    constexpr int WREG = (32 + 16 * D) * 4;
+    // a wave's (m, l, O) in LDS with O's rows D + 4 floats apart (rows D apart would put the 16 rows a
+    // store or load instruction touches in the same banks)
+    constexpr int OR = D + 4;
+    constexpr int WREG = (32 + 16 * OR) * 4;
     float* wr = reinterpret_cast<float*>(smem + w * WREG);
     if (g == 0) {
         wr[c16] = m;
         wr[16 + c16] = l;
     }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(wr + 32 + c16 * D + 16 * dt + 4 * g) = acc[dt];
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(wr + 32 + c16 * OR + 16 * dt + 4 * g) = acc[dt];
     __syncthreads();
     // the row tile's P waves (w = rt + RTW * p) merged in part order by the RTW * 64 threads of part 0
     if (part != 0 || rt >= a.RT) return;
@@ -595,7 +608,7 @@ __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
         f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int p_ = 0; p_ < P; ++p_) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(part_reg(p_) + 32 + c16 * D + 16 * dt + 4 * g);
+            const f32x4 v = *reinterpret_cast<const f32x4*>(part_reg(p_) + 32 + c16 * OR + 16 * dt + 4 * g);
             o += v * fw[p_];
         }
         *reinterpret_cast<f32x4*>(rec + 32 + c16 * D + 16 * dt + 4 * g) = o;
