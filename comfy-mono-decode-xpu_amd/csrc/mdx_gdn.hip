@@ -124,6 +124,9 @@ __device__ __forceinline__ float sum_r4(float v) {
     return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
 }
 
+// the sum over the column's 16 row groups of a value each lane holds (every lane of the column gets it)
+__device__ __forceinline__ float col_sum(float v) { return sum_x32(sum_x16(sum_r4(sum_x8(v)))); }
+
 __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ __align__(16) float kvec[2 * MAXS][DH], qvec[MAXS][DH];
     __shared__ float vvec[2 * MAXS][SC], rawc[MAXS][SC];
@@ -249,62 +252,61 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             vvec[e][d0 + q] = __uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16));
     }
     __syncthreads();
-    for (int e = 0; e < E; ++e) {
-        const bool verify = e >= E0;
-        const bool commit = !verify || (prog[e - E0] & 32);
-        const float decay = egate[e][0], beta = egate[e][1];
-        float kr[HRPG], qr[HRPG];
+    // The entries in order, each one's operands loaded from LDS one entry ahead. Entry e (decay d, beta b)
+    // on the running state S: kv = k . (d S) = d (k . S), delta = b (v - kv); commit: S <- d S + k delta^T;
+    // verify: out = (d S + k delta^T) . q = d (q . S) + delta (k . q). The column sums of k . S, q . S and
+    // k . q are independent (one exchange chain per entry on the serial path); k . S over the thread's 8
+    // rows in four interleaved accumulators, then ((m0 + m1) + (m2 + m3)), then the column's 16 row groups
+    // (lanes of one residue mod 4): row_ror 8 and 4 inside each row of 16 lanes, then the lane swaps
+    // across rows, so that every lane of the column ends with the same sum.
+    const int Ec = replayed ? E : 0;
+    auto entry_ops = [&](int e, float (&kr)[HRPG], float (&qr)[HRPG], float& vv, float& dd, float& bb, int& pr) {
         const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * HRPG);
+        const float4* q4 = reinterpret_cast<const float4*>(qvec[max(e - E0, 0)] + rg * HRPG);
+        const float4 ka = k4[0], kb = k4[1], qa = q4[0], qb = q4[1];
+        kr[0] = ka.x, kr[1] = ka.y, kr[2] = ka.z, kr[3] = ka.w, kr[4] = kb.x, kr[5] = kb.y, kr[6] = kb.z, kr[7] = kb.w;
+        qr[0] = qa.x, qr[1] = qa.y, qr[2] = qa.z, qr[3] = qa.w, qr[4] = qb.x, qr[5] = qb.y, qr[6] = qb.z, qr[7] = qb.w;
+        vv = vvec[e][col];
+        dd = egate[e][0], bb = egate[e][1];
+        pr = e >= E0 ? prog[e - E0] : 0;
+    };
+    float kr[HRPG], qr[HRPG], vv = 0.f, decay = 0.f, beta = 0.f;
+    int pr = 0;
+    if (Ec > 0) entry_ops(0, kr, qr, vv, decay, beta, pr);
+    for (int e = 0; e < Ec; ++e) {
+        const bool verify = e >= E0;
+        const bool commit = !verify || (pr & 32);
+        float kn[HRPG], qn[HRPG], vn, dn, bn;
+        int prn;
+        entry_ops(min(e + 1, Ec - 1), kn, qn, vn, dn, bn, prn);
+        float m4[4], r4[4], c4[4];
 #pragma unroll
-        for (int j = 0; j < HRPG / 4; ++j) {
-            const float4 v = k4[j];
-            kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
+        for (int r = 0; r < 4; ++r) {
+            m4[r] = __fmul_rn(st[r], kr[r]);
+            r4[r] = __fmul_rn(st[r], qr[r]);
+            c4[r] = __fmul_rn(kr[r], qr[r]);
         }
-        if (verify) {
-            const float4* q4 = reinterpret_cast<const float4*>(qvec[e - E0] + rg * HRPG);
 #pragma unroll
-            for (int j = 0; j < HRPG / 4; ++j) {
-                const float4 v = q4[j];
-                qr[4 * j] = v.x, qr[4 * j + 1] = v.y, qr[4 * j + 2] = v.z, qr[4 * j + 3] = v.w;
-            }
+        for (int r = 4; r < HRPG; ++r) {
+            m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
+            r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
+            c4[r & 3] = fmaf(kr[r], qr[r], c4[r & 3]);
         }
-        // k.S over the thread's 8 rows: four interleaved accumulators, then ((m0 + m1) + (m2 + m3));
-        // then the column's 16 row groups (lanes of one residue mod 4): row_ror 8 and 4 inside each row
-        // of 16 lanes, then the lane swaps across rows; each step adds values that already agree in
-        // pairs, so every lane of the column ends with the same sum
-        float m4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (commit) {
+        // (q . S and k . q of a replayed entry are computed and not used: no branch between the chains)
+        const float ks = col_sum(__fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3])));
+        const float qs = col_sum(__fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3])));
+        const float kq = col_sum(__fadd_rn(__fadd_rn(c4[0], c4[1]), __fadd_rn(c4[2], c4[3])));
+        const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, ks)), beta);
+        if (verify && rg == 0) rawc[pr & 15][col] = bfround(fmaf(delta, kq, __fmul_rn(decay, qs)));
+        if (commit)
 #pragma unroll
-            for (int r = 0; r < HRPG; ++r) {
-                st[r] = __fmul_rn(st[r], decay);
-                m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) m4[r & 3] = fmaf(__fmul_rn(st[r], decay), kr[r], m4[r & 3]);
-        }
-        float kv = __fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3]));
-        kv = sum_x32(sum_x16(sum_r4(sum_x8(kv))));
-        const float delta = __fmul_rn(__fsub_rn(vvec[e][col], kv), beta);
-        float r4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (commit) {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, st[r]);
-            if (verify)
-#pragma unroll
-                for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) r4[r & 3] = fmaf(fmaf(kr[r], delta, __fmul_rn(st[r], decay)), qr[r], r4[r & 3]);
-        }
-        if (verify) {
-            float o = __fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3]));
-            o = sum_x32(sum_x16(sum_r4(sum_x8(o))));
-            if (rg == 0) rawc[slot_of(e)][col] = bfround(o);
-        }
-        if (e == E0 - 1 && replayed)
+            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, __fmul_rn(st[r], decay));
+        if (e == E0 - 1)
 #pragma unroll
             for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
+#pragma unroll
+        for (int r = 0; r < HRPG; ++r) kr[r] = kn[r], qr[r] = qn[r];
+        vv = vn, decay = dn, beta = bn, pr = prn;
     }
     __syncthreads();
     unsigned written = 0;
