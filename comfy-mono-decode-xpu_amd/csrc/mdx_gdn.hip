@@ -133,6 +133,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     __shared__ float egate[2 * MAXS][4];  // decay, beta, 1 / |k|, 1 / |q|
     __shared__ float esum[2 * MAXS][2];   // sums of squares of q, k
     __shared__ int ectl[2 + 3 * MAXS];
+    __shared__ float ekq[MAXS];           // k . q of the verify entries
     const int t = threadIdx.x, lane = t % 64, h = blockIdx.x / NSPLIT, cs = blockIdx.x % NSPLIT;
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
     const int kh = h / (HV / HK);
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     // raw inputs, every load issued before the first use: k (16 pieces of 8 per entry) and v (4 per
     // entry) of every entry, q (16 per entry) of the verify entries; the entries' gates and norms
     constexpr int KP = 2 * MAXS * 16 / HT, VP = 2 * MAXS * VPE;
-    uint4 kraw[KP], qraw = make_uint4(0u, 0u, 0u, 0u), vraw = make_uint4(0u, 0u, 0u, 0u);
+    uint4 kraw[KP], qraw = make_uint4(0u, 0u, 0u, 0u), kqraw = make_uint4(0u, 0u, 0u, 0u), vraw = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int j = 0; j < KP; ++j) kraw[j] = make_uint4(0u, 0u, 0u, 0u);
     if (E > 0) {  // (uniform) indices clamped into [0, E): every slot read is a validated one
@@ -174,7 +175,9 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     }
     {
         const int i = min(t, max(E1 * 16 - 1, 0)), e = E0 + i / 16;
-        qraw = *reinterpret_cast<const uint4*>(a.qb + (p * S + slot_of(min(e, E - 1))) * C + kh * DH + (i % 16) * 8);
+        const uint16_t* row = a.qb + (p * S + slot_of(min(e, E - 1))) * C + kh * DH + (i % 16) * 8;
+        qraw = *reinterpret_cast<const uint4*>(row);
+        kqraw = *reinterpret_cast<const uint4*>(row + KD);  // the same entry's k piece (for k . q)
     }
     if (t < VP) {
         const int i = min(t, E * VPE - 1), e = i / VPE;
@@ -212,14 +215,26 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
         if (i < E * 16 && (i & 15) == 0) esum[i / 16][1] = ssum;
     }
     {
+        // and the raw k . q of the verify entries (it does not depend on the state), the same way
+        const uint32_t wq[4] = {qraw.x, qraw.y, qraw.z, qraw.w}, wk[4] = {kqraw.x, kqraw.y, kqraw.z, kqraw.w};
+        float dkq = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t sh = (q & 1) ? 0u : 16u;
+            dkq = fmaf(__uint_as_float((wk[q >> 1] << sh) & 0xFFFF0000u), __uint_as_float((wq[q >> 1] << sh) & 0xFFFF0000u), dkq);
+        }
         const float ssum = sum16(sq8(qraw));
-        if (t < E1 * 16 && (t & 15) == 0) esum[E0 + t / 16][0] = ssum;
+        dkq = sum16(dkq);
+        if (t < E1 * 16 && (t & 15) == 0) esum[E0 + t / 16][0] = ssum, ekq[t / 16] = dkq;
     }
     __syncthreads();
     if (t < E) {
         const int e = t;
-        egate[e][2] = __fdiv_rn(1.f, fmaxf(sqrt_rn(esum[e][1]), 1e-12f));
-        egate[e][3] = __fdiv_rn(1.f, fmaxf(sqrt_rn(e >= E0 ? esum[e][0] : 0.f), 1e-12f));
+        const float ki = __fdiv_rn(1.f, fmaxf(sqrt_rn(esum[e][1]), 1e-12f));
+        const float qi = __fdiv_rn(1.f, fmaxf(sqrt_rn(e >= E0 ? esum[e][0] : 0.f), 1e-12f));
+        egate[e][2] = ki;
+        egate[e][3] = qi;
+        if (e >= E0) ekq[e - E0] = __fmul_rn(__fmul_rn(ekq[e - E0], ki), __fmul_rn(a.qscale, qi));  // normalised k . q
     }
     __syncthreads();
     // scaled into LDS: k * ki, (q * scale) * qi, v
@@ -252,62 +267,77 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             vvec[e][d0 + q] = __uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16));
     }
     __syncthreads();
-    // The entries in order, each one's operands loaded from LDS one entry ahead. Entry e (decay d, beta b)
-    // on the running state S: kv = k . (d S) = d (k . S), delta = b (v - kv); commit: S <- d S + k delta^T;
-    // verify: out = (d S + k delta^T) . q = d (q . S) + delta (k . q). The column sums of k . S, q . S and
-    // k . q are independent (one exchange chain per entry on the serial path); k . S over the thread's 8
-    // rows in four interleaved accumulators, then ((m0 + m1) + (m2 + m3)), then the column's 16 row groups
-    // (lanes of one residue mod 4): row_ror 8 and 4 inside each row of 16 lanes, then the lane swaps
-    // across rows, so that every lane of the column ends with the same sum.
-    const int Ec = replayed ? E : 0;
-    auto entry_ops = [&](int e, float (&kr)[HRPG], float (&qr)[HRPG], float& vv, float& dd, float& bb, int& pr) {
-        const float4* k4 = reinterpret_cast<const float4*>(kvec[e] + rg * HRPG);
-        const float4* q4 = reinterpret_cast<const float4*>(qvec[max(e - E0, 0)] + rg * HRPG);
-        const float4 ka = k4[0], kb = k4[1], qa = q4[0], qb = q4[1];
-        kr[0] = ka.x, kr[1] = ka.y, kr[2] = ka.z, kr[3] = ka.w, kr[4] = kb.x, kr[5] = kb.y, kr[6] = kb.z, kr[7] = kb.w;
-        qr[0] = qa.x, qr[1] = qa.y, qr[2] = qa.z, qr[3] = qa.w, qr[4] = qb.x, qr[5] = qb.y, qr[6] = qb.z, qr[7] = qb.w;
-        vv = vvec[e][col];
-        dd = egate[e][0], bb = egate[e][1];
-        pr = e >= E0 ? prog[e - E0] : 0;
+    // The entries in order, each one's operands loaded from LDS one entry ahead; the replayed entries
+    // (always committed) first, then the verify entries. Entry e (decay d, beta b) on the running state S:
+    // kv = k . (d S) = d (k . S), delta = b (v - kv); commit: S <- d S + k delta^T; verify: out =
+    // (d S + k delta^T) . q = d (q . S) + delta (k . q). k . S over the thread's 8 rows in four interleaved
+    // accumulators, then ((m0 + m1) + (m2 + m3)), then the column's 16 row groups (lanes of one residue
+    // mod 4): row_ror 8 and 4 inside each row of 16 lanes, then the lane swaps across rows, so that every
+    // lane of the column ends with the same sum; q . S the same way, beside it.
+    const int E0c = replayed ? E0 : 0, Ec = replayed ? E : 0;
+    auto load8 = [&](const float* src, float (&r8)[HRPG]) {
+        const float4* p4 = reinterpret_cast<const float4*>(src + rg * HRPG);
+        const float4 x0 = p4[0], x1 = p4[1];
+        r8[0] = x0.x, r8[1] = x0.y, r8[2] = x0.z, r8[3] = x0.w, r8[4] = x1.x, r8[5] = x1.y, r8[6] = x1.z, r8[7] = x1.w;
     };
-    float kr[HRPG], qr[HRPG], vv = 0.f, decay = 0.f, beta = 0.f;
+    auto dot_col = [&](const float (&r8)[HRPG]) {
+        float m4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m4[r] = __fmul_rn(st[r], r8[r]);
+#pragma unroll
+        for (int r = 4; r < HRPG; ++r) m4[r & 3] = fmaf(st[r], r8[r], m4[r & 3]);
+        return col_sum(__fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3])));
+    };
+    float kr[HRPG], qr[HRPG], vv = 0.f, decay = 0.f, beta = 0.f, kq = 0.f;
     int pr = 0;
-    if (Ec > 0) entry_ops(0, kr, qr, vv, decay, beta, pr);
-    for (int e = 0; e < Ec; ++e) {
-        const bool verify = e >= E0;
-        const bool commit = !verify || (pr & 32);
-        float kn[HRPG], qn[HRPG], vn, dn, bn;
-        int prn;
-        entry_ops(min(e + 1, Ec - 1), kn, qn, vn, dn, bn, prn);
-        float m4[4], r4[4], c4[4];
+    if (E0c > 0) {
+        load8(kvec[0], kr);
+        vv = vvec[0][col], decay = egate[0][0], beta = egate[0][1];
+    }
+#pragma unroll 2
+    for (int e = 0; e < E0c; ++e) {
+        float kn[HRPG];
+        const int en = min(e + 1, E0c - 1);
+        load8(kvec[en], kn);
+        const float vn = vvec[en][col], dn = egate[en][0], bn = egate[en][1];
+        const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, dot_col(kr))), beta);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            m4[r] = __fmul_rn(st[r], kr[r]);
-            r4[r] = __fmul_rn(st[r], qr[r]);
-            c4[r] = __fmul_rn(kr[r], qr[r]);
-        }
+        for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, __fmul_rn(st[r], decay));
 #pragma unroll
-        for (int r = 4; r < HRPG; ++r) {
-            m4[r & 3] = fmaf(st[r], kr[r], m4[r & 3]);
-            r4[r & 3] = fmaf(st[r], qr[r], r4[r & 3]);
-            c4[r & 3] = fmaf(kr[r], qr[r], c4[r & 3]);
-        }
-        // (q . S and k . q of a replayed entry are computed and not used: no branch between the chains)
-        const float ks = col_sum(__fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3])));
-        const float qs = col_sum(__fadd_rn(__fadd_rn(r4[0], r4[1]), __fadd_rn(r4[2], r4[3])));
-        const float kq = col_sum(__fadd_rn(__fadd_rn(c4[0], c4[1]), __fadd_rn(c4[2], c4[3])));
+        for (int r = 0; r < HRPG; ++r) kr[r] = kn[r];
+        vv = vn, decay = dn, beta = bn;
+    }
+    if (E0c > 0)
+#pragma unroll
+        for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
+    // verify entry E0 + j's output is held by row group j of its column (j < R <= 16) and written to LDS
+    // after the loop (no LDS store on the serial path)
+    float held = 0.f;
+    if (Ec > E0c) {
+        load8(kvec[E0c], kr);
+        load8(qvec[0], qr);
+        vv = vvec[E0c][col], decay = egate[E0c][0], beta = egate[E0c][1], kq = ekq[0], pr = prog[0];
+    }
+#pragma unroll 2
+    for (int e = E0c; e < Ec; ++e) {
+        float kn[HRPG], qn[HRPG];
+        const int en = min(e + 1, Ec - 1);
+        load8(kvec[en], kn);
+        load8(qvec[en - E0c], qn);
+        const float vn = vvec[en][col], dn = egate[en][0], bn = egate[en][1], kqn = ekq[en - E0c];
+        const int prn = prog[en - E0c];
+        const float ks = dot_col(kr), qs = dot_col(qr);
         const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, ks)), beta);
-        if (verify && rg == 0) rawc[pr & 15][col] = bfround(fmaf(delta, kq, __fmul_rn(decay, qs)));
-        if (commit)
+        const float o = fmaf(delta, kq, __fmul_rn(decay, qs));
+        held = e - E0c == rg ? o : held;
+        if (pr & 32)  // (uniform) committed
 #pragma unroll
             for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, __fmul_rn(st[r], decay));
-        if (e == E0 - 1)
-#pragma unroll
-            for (int r = 0; r < HRPG; ++r) rs[r * DH] = st[r];
 #pragma unroll
         for (int r = 0; r < HRPG; ++r) kr[r] = kn[r], qr[r] = qn[r];
-        vv = vn, decay = dn, beta = bn, pr = prn;
+        vv = vn, decay = dn, beta = bn, kq = kqn, pr = prn;
     }
+    if (rg < Ec - E0c) rawc[prog[rg] & 15][col] = bfround(held);
     __syncthreads();
     unsigned written = 0;
     for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
