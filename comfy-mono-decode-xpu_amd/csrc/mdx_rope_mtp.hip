@@ -281,6 +281,63 @@ extern "C" int mdx_mtp_prep_verify(const int64_t* st, int64_t* apos, int64_t npo
     return MDX_OK;
 }
 
+namespace mdx {
+namespace {
+
+// mtp_prep_verify's bookkeeping (work-group 0) and the verify rows' inputs: work-group r gathers row r's
+// embedding (token nt[0] for the root row, which it also stores as vtok[0]; vtok[r] for the others) and
+// its RoPE table row (position tree_pos[r] + st[0] + rope_offset, the vpos it also stores). Tokens and
+// positions outside their tables are clamped into them.
+__global__ __launch_bounds__(256) void prep_verify_rows_kernel(const int64_t* st, int64_t* apos, int np, int* aseq,
+                                                               int64_t* vpos, const int64_t* tree_pos, int rows, int* ctl,
+                                                               const int* tree_ctl, int slots, int parity,
+                                                               int64_t rope_offset, const int64_t* nt, int64_t* vtok,
+                                                               const uint16_t* embed, int64_t vocab, int hidden,
+                                                               const float* ftab, int64_t frows, int fcols, uint16_t* x,
+                                                               float* vfreqs) {
+    const int t = threadIdx.x, r = blockIdx.x;
+    const int64_t pos = st[0];
+    if (r == 0) {
+        if (t < np) apos[t] = pos + t;
+        if (t == 0) aseq[0] = int(pos);
+        if (t < rows) vpos[t] = tree_pos[t] + pos + rope_offset;
+        if (t == 0) ctl[1] = parity;
+        if (t < 2 * slots) ctl[2 + slots + t] = tree_ctl[t];
+        if (t == 0) vtok[0] = nt[0];
+    }
+    int64_t tok = r == 0 ? nt[0] : vtok[r];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    int64_t fp = tree_pos[r] + pos + rope_offset;
+    fp = fp < 0 ? 0 : (fp >= frows ? frows - 1 : fp);
+    const uint4* src = reinterpret_cast<const uint4*>(embed + tok * hidden);
+    uint4* dst = reinterpret_cast<uint4*>(x + int64_t(r) * hidden);
+    for (int i = t; i < hidden / 8; i += 256) dst[i] = src[i];
+    for (int i = t; i < fcols; i += 256) vfreqs[int64_t(r) * fcols + i] = ftab[fp * fcols + i];
+}
+
+}  // namespace
+}  // namespace mdx
+
+extern "C" int mdx_mtp_prep_verify_rows(const int64_t* st, int64_t* apos, int64_t npos, int32_t* aseq, int64_t* vpos,
+                                        const int64_t* tree_pos, int64_t rows, int32_t* ctl, const int32_t* tree_ctl,
+                                        int64_t slots, int64_t parity, int64_t rope_offset, const int64_t* nt,
+                                        int64_t* vtok, const uint16_t* embed, int64_t vocab, int64_t hidden,
+                                        const float* ftab, int64_t ftab_rows, int64_t ftab_cols, uint16_t* x,
+                                        float* vfreqs, void* stream) {
+    MDX_CHECK(st && apos && aseq && vpos && tree_pos && ctl && tree_ctl && nt && vtok && embed && ftab && x && vfreqs,
+              "null pointer");
+    MDX_CHECK(slots == 8 || slots == 16, "slots must be 8 or 16");
+    MDX_CHECK(rows >= 1 && rows <= slots && npos >= 0 && npos <= 64, "rows / positions");
+    MDX_CHECK(vocab >= 1 && hidden >= 8 && hidden % 8 == 0 && aligned(embed, 16) && aligned(x, 16) && ftab_rows >= 1 &&
+                  ftab_cols >= 1,
+              "embedding [vocab, hidden % 8 == 0] and RoPE table, 16-byte aligned rows");
+    hipLaunchKernelGGL(mdx::prep_verify_rows_kernel, dim3(unsigned(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       st, apos, int(npos), aseq, vpos, tree_pos, int(rows), ctl, tree_ctl, int(slots), int(parity),
+                       rope_offset, nt, vtok, embed, vocab, int(hidden), ftab, ftab_rows, int(ftab_cols), x, vfreqs);
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
 extern "C" int mdx_mtp_accept(int64_t* st, const int64_t* toks, const int64_t* vtok, const int64_t* cand,
                               const int32_t* children, int64_t rows, int64_t depth, int64_t slots, const uint16_t* x,
                               int64_t hidden, int64_t* nt, uint16_t* hbuf, int32_t* ctl, const int64_t* kv_ptrs,

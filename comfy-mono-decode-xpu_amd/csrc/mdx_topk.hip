@@ -315,13 +315,27 @@ namespace {
 // g_j = -log(-log(clamp(u[r, j], 1e-20, 1))), every operation an fp32 rounding as torch's elementwise
 // kernels round them (a tensor divided by a scalar is multiplied by the scalar's fp32 reciprocal);
 // the first maximal score wins, as torch.argmax picks; out[r] = idx[r, j*]. One wave per row (k <= 64).
+// The uniform of (seed, counter, row r, slot j): the SplitMix64 output (Steele, Lea and Flood 2014: state
+// += 0x9E3779B97F4A7C15, then the two xor-shift-multiply rounds and a final xor-shift) of the state
+// seed + (n + 1) * 0x9E3779B97F4A7C15, n = counter * 1024 + 64 r + j, whose top 23 bits k give
+// (k + 0.5) * 2^-23, in (0, 1) and exact in fp32.
+__device__ __forceinline__ float mix_uniform(uint64_t seed, int64_t counter, int r, int j) {
+    const uint64_t n = uint64_t(counter) * 1024u + uint64_t(r) * 64u + uint64_t(j);
+    uint64_t z = seed + (n + 1u) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float(uint32_t(z >> 41)) + 0.5f) * 1.1920928955078125e-7f;
+}
+
+// u == nullptr: the uniforms are mix_uniform(seed, counter[0], r, j) (counter read on the device)
 __global__ __launch_bounds__(64) void topk_sample_kernel(const float* vals, const int64_t* idx, const float* u, float temp,
-                                                         int64_t k, int64_t* out) {
+                                                         int64_t k, int64_t* out, const int64_t* counter, uint64_t seed) {
     const int r = blockIdx.x, j = threadIdx.x;
     float sc = -INFINITY;
     int at = 64;
     if (j < k) {
-        const float uu = fminf(fmaxf(u[r * k + j], 1e-20f), 1.0f);
+        const float uu = fminf(fmaxf(u ? u[r * k + j] : mix_uniform(seed, counter[0], r, j), 1e-20f), 1.0f);
         const float g = -logf(-logf(uu));
         sc = __fadd_rn(__fmul_rn(vals[r * k + j], __fdiv_rn(1.f, temp)), g);
         at = j;
@@ -435,7 +449,18 @@ extern "C" int mdx_topk_sample(const float* values, const int64_t* indices, cons
     MDX_CHECK(rows >= 1 && rows <= 65535 && k >= 1 && k <= 64, "1 <= rows, 1 <= k <= 64");
     MDX_CHECK(temperature > 0.f, "temperature > 0");
     hipLaunchKernelGGL(mdx::topk_sample_kernel, dim3(unsigned(rows)), dim3(64), 0, static_cast<hipStream_t>(stream),
-                       values, indices, uniform, temperature, k, out);
+                       values, indices, uniform, temperature, k, out, nullptr, uint64_t(0));
+    MDX_LAUNCHED();
+    return MDX_OK;
+}
+
+extern "C" int mdx_topk_sample_seeded(const float* values, const int64_t* indices, uint64_t seed, const int64_t* counter,
+                                      float temperature, int64_t rows, int64_t k, int64_t* out, void* stream) {
+    MDX_CHECK(values && indices && counter && out, "null pointer");
+    MDX_CHECK(rows >= 1 && rows <= 16 && k >= 1 && k <= 64, "1 <= rows <= 16, 1 <= k <= 64");
+    MDX_CHECK(temperature > 0.f, "temperature > 0");
+    hipLaunchKernelGGL(mdx::topk_sample_kernel, dim3(unsigned(rows)), dim3(64), 0, static_cast<hipStream_t>(stream),
+                       values, indices, nullptr, temperature, k, out, counter, seed);
     MDX_LAUNCHED();
     return MDX_OK;
 }

@@ -289,6 +289,30 @@ def mtp_prep_verify(st, apos, aseq, vpos, tree_pos, ctl, tree_ctl, parity, rope_
               _lib.stream_of(st))
 
 
+def mtp_prep_verify_rows(st, apos, aseq, vpos, tree_pos, ctl, tree_ctl, parity, rope_offset, nt, vtok, embed, ftab, x,
+                         vfreqs):
+    """mtp_prep_verify plus the verify rows' inputs in one launch (mdx_mtp_prep_verify_rows): vtok[0] = nt,
+    x[r] = embed[vtok[r]], vfreqs[r] = ftab[vpos[r]]."""
+    for t, n in ((st, "st"), (apos, "attention position"), (vpos, "verify positions"), (tree_pos, "tree positions"),
+                 (nt, "next token"), (vtok, "verify tokens")):
+        _i64(t, n)
+    _check(aseq.dtype == torch.int32, "attention seqlen int32")
+    slots = _slots_of(ctl)
+    _check(tree_ctl.dtype == torch.int32 and tree_ctl.numel() == 2 * slots and tree_ctl.is_contiguous(),
+           "tree program int32 [2 slots]")
+    rows = vpos.numel()
+    _check(tree_pos.numel() == rows and 1 <= rows <= slots and apos.numel() <= 64 and vtok.numel() >= rows, "rows")
+    _check(embed.dtype == torch.bfloat16 and embed.dim() == 2 and embed.is_contiguous(), "embedding bf16 [vocab, H]")
+    _check(ftab.dtype == torch.float32 and ftab.is_contiguous() and ftab.dim() >= 2, "RoPE table f32 [positions, ...]")
+    fcols = ftab[0].numel()
+    _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.numel() == rows * embed.shape[1], "x bf16 [rows, H]")
+    _check(vfreqs.dtype == torch.float32 and vfreqs.is_contiguous() and vfreqs.numel() == rows * fcols, "vfreqs f32")
+    _lib.call("mdx_mtp_prep_verify_rows", _lib.ptr(st), _lib.ptr(apos), apos.numel(), _lib.ptr(aseq), _lib.ptr(vpos),
+              _lib.ptr(tree_pos), rows, _lib.ptr(ctl), _lib.ptr(tree_ctl), slots, int(parity), int(rope_offset),
+              _lib.ptr(nt), _lib.ptr(vtok), _lib.ptr(embed), embed.shape[0], embed.shape[1], _lib.ptr(ftab),
+              ftab.shape[0], fcols, _lib.ptr(x), _lib.ptr(vfreqs), _lib.stream_of(st))
+
+
 def mtp_accept(st, toks, vtok, cand, children, rows, depth, x, nt_buf, h_buf, ctl, kv_ptrs, kv_heads, kv_cap,
                head_dim, result):
     """Reference csrc/mtp_loop.sycl:86-196: the accept walk, record, counters, ctl, next token and
@@ -392,6 +416,22 @@ def topk_sample(values, indices, uniform, temperature, out=None):
     _check(out.dtype == torch.int64 and out.is_contiguous() and out.numel() == R, "out int64 [R]")
     _lib.call("mdx_topk_sample", _lib.ptr(values), _lib.ptr(indices), _lib.ptr(uniform), float(temperature), R, k,
               _lib.ptr(out), _lib.stream_of(values))
+    return out
+
+
+def topk_sample_seeded(values, indices, seed, counter, temperature, out=None):
+    """topk_sample with uniforms drawn on the device (mdx_topk_sample_seeded): SplitMix64 of (seed,
+    counter[0], row, slot); counter int64 on the device (the step's committed position)."""
+    _dev(values, "values")
+    R, k = values.shape
+    _check(values.dtype == torch.float32 and indices.dtype == torch.int64 and values.is_contiguous()
+           and indices.is_contiguous() and indices.shape == values.shape, "values f32 / indices int64 [R, k]")
+    _i64(counter, "counter")
+    if out is None:
+        out = torch.empty(R, dtype=torch.int64, device=values.device)
+    _check(out.dtype == torch.int64 and out.is_contiguous() and out.numel() == R, "out int64 [R]")
+    _lib.call("mdx_topk_sample_seeded", _lib.ptr(values), _lib.ptr(indices), int(seed) & ((1 << 64) - 1), _lib.ptr(counter),
+              float(temperature), R, k, _lib.ptr(out), _lib.stream_of(values))
     return out
 
 

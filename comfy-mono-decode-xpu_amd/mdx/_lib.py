@@ -57,6 +57,10 @@ SIGNATURES = {
                                           c_void_p, c_void_p]),
     "mdx_mtp_prep_verify": (ctypes.c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
                                            c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "mdx_mtp_prep_verify_rows": (ctypes.c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
+                                                c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                                c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p,
+                                                c_void_p, c_void_p]),
     "mdx_mtp_accept": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                       c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                       c_int64, c_int64, c_void_p, c_void_p]),
@@ -99,6 +103,8 @@ SIGNATURES = {
                                              c_void_p]),
     "mdx_topk_sample": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int64, c_int64, c_void_p,
                                        c_void_p]),
+    "mdx_topk_sample_seeded": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_uint64, c_void_p, ctypes.c_float, c_int64,
+                                              c_int64, c_void_p, c_void_p]),
     "mdx_rmsnorm": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_int64, c_int64, c_void_p]),
     "mdx_silu_mul": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "mdx_draft_embed_norm_cat": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,

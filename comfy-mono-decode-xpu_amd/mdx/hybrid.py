@@ -43,6 +43,7 @@ class HybridConfig:
     top_k: int = 20
     temperature: float = 1.0
     greedy: bool = False          # take the top-1 instead of sampling
+    sample_seed: int = 0x5EED5EED  # the sampling uniforms' seed (SplitMix64 of seed, position, row, slot)
     two_stage: bool = False       # drafts: int4 scores + the draft pick instead of the full lm_head
     head: str = "bf16"            # "int8": the int8 ConvRot lm_head (W8A8) for the verify and the drafts
     eps: float = 1e-6
@@ -506,7 +507,7 @@ class HybridModel:
     def draft_part(self):
         """The step's drafts: depth k proposes the children of chain node k."""
         tok, h = self.nt.view(-1), self.hbuf
-        self.vtok[0, 0:1].copy_(self.nt.view(-1))
+        # (the root row's verify token is the next token, stored by the verify's prep launch)
         for k, w in enumerate(self.widths):
             tok, h = self.draft(k, tok, h, w), self.dh[:1]
 
@@ -523,9 +524,9 @@ class HybridModel:
         c, T = self.cfg, self.tree
         R = self.R
         # verify
-        _C.mtp_prep_verify(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0)
-        torch.index_select(self.ftab, 0, self.vpos.view(-1), out=self.vfreqs)
-        torch.index_select(self.embed, 0, self.vtok.view(-1), out=self.x)
+        # positions and control words, the root token, and the rows' embeddings and RoPE rows: one launch
+        _C.mtp_prep_verify_rows(self.st, self.apos, self.aseq, self.vpos, T["tree_pos"], self.ctl, T["tree_ctl"], parity, 0,
+                                self.nt.view(-1), self.vtok, self.embed, self.ftab, self.x, self.vfreqs)
         self._tr("verify.vtok", self.vtok)
         self.verify_layers(self.x, R, T["mask"], self.aseq, self.apos, self.vfreqs)
         if c.head == "int8":
@@ -545,7 +546,8 @@ class HybridModel:
             self.toks.copy_(idx[:, :1].reshape(1, R))
         else:
             # Gumbel-max over the top-k: a sample of softmax(vals / T) restricted to the top k
-            _C.topk_sample(vals, idx, torch.rand(R, c.top_k, device=self.dev), c.temperature, out=self.toks.view(R))
+            # uniforms drawn on the device from the seed and the step's committed position (st[0])
+            _C.topk_sample_seeded(vals, idx, c.sample_seed, self.st, c.temperature, out=self.toks.view(R))
         self._tr("verify.toks", self.toks)
         for i, kv in enumerate(self.kv):
             if kv is not None:

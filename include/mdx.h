@@ -168,6 +168,17 @@ int mdx_mtp_prep_verify(const int64_t* st, int64_t* apos, int64_t npos, int32_t*
                         const int64_t* tree_pos, int64_t rows, int32_t* ctl, const int32_t* tree_ctl, int64_t slots,
                         int64_t parity, int64_t rope_offset, void* stream);
 
+/* mdx_mtp_prep_verify plus the verify rows' inputs, one launch: vtok[0] = nt[0] (the root row's token);
+ * x[r] = embed[vtok[r]] (bf16 [rows, hidden]) and vfreqs[r] = ftab[vpos[r]] (f32 [rows, ftab_cols]),
+ * tokens and positions clamped into their tables. No counterpart in the reference, whose decode loop
+ * gathers these with torch ops around mtp_prep_verify (comfy_mono_decode_xpu/mtp_loop.py:372-373): the
+ * decode step's captured graph carries one launch instead of four. */
+int mdx_mtp_prep_verify_rows(const int64_t* st, int64_t* apos, int64_t npos, int32_t* aseq, int64_t* vpos,
+                             const int64_t* tree_pos, int64_t rows, int32_t* ctl, const int32_t* tree_ctl, int64_t slots,
+                             int64_t parity, int64_t rope_offset, const int64_t* nt, int64_t* vtok,
+                             const uint16_t* embed, int64_t vocab, int64_t hidden, const float* ftab,
+                             int64_t ftab_rows, int64_t ftab_cols, uint16_t* x, float* vfreqs, void* stream);
+
 /* The accept walk of one verify step, on the device.
  * Replaces: _C.mtp_accept, csrc/mtp_loop.sycl:86-196.
  *   path = [0]; extend by the first child c (children[cur][j], -1 terminated) with vtok[c] == toks[cur].
@@ -229,6 +240,14 @@ int mdx_topk_rows_noalloc(const void* x, int32_t x_dtype, int64_t rows, int64_t 
  * sampling.py, upstream torch ops), fused into one launch. */
 int mdx_topk_sample(const float* values, const int64_t* indices, const float* uniform, float temperature, int64_t rows,
                     int64_t k, int64_t* out, void* stream);
+
+/* mdx_topk_sample with uniforms of its own: uniform[r, j] = (k + 0.5) 2^-23, k the top 23 bits of the
+ * SplitMix64 output (Steele, Lea and Flood 2014) for the state seed + (n + 1) 0x9E3779B97F4A7C15,
+ * n = counter[0] 1024 + 64 r + j (counter read on the device: the decode step's committed position, so
+ * a captured graph draws fresh uniforms at every replay). rows <= 16. No counterpart in the reference
+ * (torch's generator there); it keeps the generator's launches out of the decode step. */
+int mdx_topk_sample_seeded(const float* values, const int64_t* indices, uint64_t seed, const int64_t* counter,
+                           float temperature, int64_t rows, int64_t k, int64_t* out, void* stream);
 
 /* Bytes of device workspace mdx_attn_decode needs for H query heads, Hk kv heads, S rows, head_dim D
  * and cache capacity cap. Zero it once when allocated: every launch leaves its counters at zero. */

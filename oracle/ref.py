@@ -912,3 +912,29 @@ def attention_exact(q_bits, key_bits, value_bits, L, xk_bits, xv_bits, mask, sca
                 o = (o + (e[u] * V[u]).astype(f32)).astype(f32)
             out[s, h] = f32_to_bf16((o / parts[0]).astype(f32))
     return out.reshape(S, H * D)
+
+
+# ---------------------------------------------------------------------------------------------
+# Sampling uniforms drawn on the device (mdx_topk_sample_seeded; no counterpart in the reference,
+# which draws them with torch's generator)
+# ---------------------------------------------------------------------------------------------
+
+_M64 = (1 << 64) - 1
+SPLITMIX_GAMMA = 0x9E3779B97F4A7C15
+
+
+def splitmix64_mix(z):
+    """SplitMix64's output function (Steele, Lea and Flood 2014) of a 64-bit state z."""
+    z &= _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def seeded_uniform(seed, counter, r, j):
+    """(k + 0.5) * 2^-23 as float32, k the top 23 bits of splitmix64_mix(seed + (n + 1) * gamma),
+    n = counter * 1024 + 64 r + j."""
+    n = (int(counter) * 1024 + 64 * int(r) + int(j)) & _M64
+    z = splitmix64_mix((int(seed) + (n + 1) * SPLITMIX_GAMMA) & _M64)
+    return np.float32((float(z >> 41) + 0.5) * 2.0 ** -23)
+

@@ -109,3 +109,28 @@ def test_topk_matches_torch_on_distinct_rows():
     v, i = ref.topk_rows(x.numpy(), 20)
     tv, ti = torch.topk(x, 20)
     assert np.array_equal(i, ti.numpy()) and np.array_equal(v, tv.numpy())
+
+
+def test_splitmix64_known_answers():
+    """The sampling uniforms' mixer is SplitMix64's: the generator seeded with 0 (state += gamma, then the
+    output function) gives 0xe220a8397b1dcdaf, 0x6e789e6aa1b965f4, 0x06c45d188009454f."""
+    state, outs = 0, []
+    for _ in range(3):
+        state = (state + ref.SPLITMIX_GAMMA) & ((1 << 64) - 1)
+        outs.append(ref.splitmix64_mix(state))
+    assert outs == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    # seeded_uniform(seed, counter, r, j) is the (n + 1)-th output of the generator seeded with `seed`
+    seed = 12345
+    for n in (0, 1, 1023, 4096 + 64 * 3 + 5):
+        z = ref.splitmix64_mix((seed + (n + 1) * ref.SPLITMIX_GAMMA) & ((1 << 64) - 1))
+        u = ref.seeded_uniform(seed, n // 1024, (n % 1024) // 64, n % 64)
+        assert u == np.float32(((z >> 41) + 0.5) / 2 ** 23) and 0.0 < u < 1.0
+
+
+def test_seeded_uniforms_spread():
+    """The uniforms of consecutive rows, slots and counters fill (0, 1) evenly (a mixing or indexing
+    mistake that repeats whole runs of values or leaves a bias shows here)."""
+    u = np.array([ref.seeded_uniform(7, c, r, j) for c in range(8) for r in range(4) for j in range(64)])
+    assert len(np.unique(u)) >= u.size - 2  # 23-bit values: a birthday collision or two is expected
+    hist = np.histogram(u, bins=8, range=(0.0, 1.0))[0]
+    assert abs(u.mean() - 0.5) < 0.03 and hist.min() > 0.8 * u.size / 8

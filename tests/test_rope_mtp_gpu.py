@@ -183,3 +183,38 @@ def test_mtp_prep_matches_host_prepare(C, dev, slots):
     assert vpos.view(-1).tolist() == [37 + 5 + d for d in tpos.tolist()]
     assert ctl.tolist()[1] == 1 and ctl.tolist()[2 + slots:] == list(range(100, 100 + 2 * slots))
     assert ctl.tolist()[0] == 0 and ctl.tolist()[2:2 + slots] == [0] * slots
+
+
+@pytest.mark.parametrize("slots,rows", [(8, 8), (16, 16), (8, 3)])
+def test_mtp_prep_verify_rows_matches_ops(C, dev, slots, rows):
+    """mtp_prep_verify_rows (one launch) against mtp_prep_verify, the root token's copy and the two
+    index_select gathers of the verify rows, bit for bit; a position past the RoPE table reads its last
+    row."""
+    print(f"case prep_verify_rows slots={slots} rows={rows}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(slots + rows)
+    V, Hd, P = 5000, 4096, 96
+    embed = torch.randn(V, Hd, generator=g, device=dev).bfloat16()
+    ftab = torch.randn(P, 32, 2, 2, generator=g, device=dev)
+    st = torch.tensor([60, 3, 0, 0], dtype=torch.long, device=dev)
+    tpos = torch.tensor(([0, 1, 2, 3, 4, 1, 2, 1] * 2)[:rows], dtype=torch.long, device=dev)
+    tctl = torch.arange(100, 100 + 2 * slots, dtype=torch.int32, device=dev)
+    nt = torch.tensor([4321], dtype=torch.long, device=dev)
+    outs = []
+    for fused in (True, False):
+        apos, aseq = torch.empty(slots, dtype=torch.long, device=dev), torch.empty(1, dtype=torch.int32, device=dev)
+        vpos = torch.empty(1, rows, dtype=torch.long, device=dev)
+        ctl = torch.zeros(2 + 3 * slots, dtype=torch.int32, device=dev)
+        vtok = torch.randint(0, V, (1, rows), generator=torch.Generator(device=dev).manual_seed(1), device=dev)
+        x = torch.empty(rows, Hd, dtype=torch.bfloat16, device=dev)
+        vf = torch.empty(rows, 32, 2, 2, device=dev)
+        if fused:
+            C.mtp_prep_verify_rows(st, apos, aseq, vpos, tpos, ctl, tctl, 1, 34, nt, vtok, embed, ftab, x, vf)
+        else:
+            vtok[0, 0:1].copy_(nt)
+            C.mtp_prep_verify(st, apos, aseq, vpos, tpos, ctl, tctl, 1, 34)
+            torch.index_select(ftab, 0, vpos.view(-1).clamp(max=P - 1), out=vf)
+            torch.index_select(embed, 0, vtok.view(-1), out=x)
+        outs.append((apos, aseq, vpos, ctl, vtok, x, vf))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert outs[0][2].view(-1).max().item() >= P  # some positions ran past the table (clamped to its last row)

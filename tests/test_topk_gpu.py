@@ -142,3 +142,25 @@ def test_topk_sample_matches_torch_expression(C, dev, temperature):
         pick = torch.argmax(vals / temperature + gum, dim=1, keepdim=True)
         want = torch.gather(idx, 1, pick).view(R)
         assert torch.equal(got, want), (got, want)
+
+
+def test_topk_sample_seeded_matches_oracle_uniforms(C, dev):
+    """topk_sample_seeded draws its uniforms on the device from (seed, counter[0], row, slot): the picks
+    equal topk_sample's on the oracle's restatement of those uniforms, for two counters (a captured
+    graph's successive replays), and differ between counters."""
+    from oracle import ref
+    g = torch.Generator(device=dev).manual_seed(9)
+    R, k, seed = 8, 20, 0x5EED5EED
+    vals = torch.randn(R, k, generator=g, device=dev).sort(dim=1, descending=True).values * 0.3
+    idx = torch.randint(0, 151936, (R, k), generator=g, device=dev)
+    picks = []
+    for cnt in (1061, 1062):
+        print(f"case topk_sample_seeded counter={cnt}", flush=True)
+        counter = torch.tensor([cnt, 0, 0, 0], dtype=torch.int64, device=dev)
+        u = torch.tensor([[float(ref.seeded_uniform(seed, cnt, r, j)) for j in range(k)] for r in range(R)],
+                         dtype=torch.float32, device=dev)
+        got = C.topk_sample_seeded(vals, idx, seed, counter, 1.0)
+        want = C.topk_sample(vals, idx, u, 1.0)
+        assert torch.equal(got, want), (got, want)
+        picks.append(got)
+    assert not torch.equal(picks[0], picks[1])
