@@ -141,9 +141,11 @@ def cpu_threads():
 
 def cpu_baseline_mlp(ring0, rows, xb, nwb, lutb, budget_s=25.0):
     """The oracle's operator chain (RMSNorm, quantise, decode + int dot, SiLU, quantise, decode +
-    int dot) on the host, on one set of the same weights: 3 warm-up calls, then the median of >= 10
-    timed calls (fewer only if the budget runs out), with numpy's BLAS threads pinned to the
-    process's CPU affinity count."""
+    int dot) on the host, on one set of the same weights: 3 warm-up calls, then the median of the
+    timed calls (>= 10; up to 100 within the budget). The oracle's C restatement (oracle/cpu_mlp.c, one
+    thread per share of the output channels on every core of the process's affinity; bit-identical to
+    the numpy chain) where it loads, else the numpy chain with its BLAS threads pinned to that count.
+    Returns (median s, calls, CPU model, threads, form)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
     sys.path.insert(0, ROOT)
@@ -154,27 +156,36 @@ def cpu_baseline_mlp(ring0, rows, xb, nwb, lutb, budget_s=25.0):
         q = layout.row_major_codes(w.q).cpu().numpy()
         d.append(dict(packed=q, s=w.s.float().cpu().numpy(), sch=w.sc.cpu().numpy(), cb=None, G=128))
     model, threads = cpu_info()
+    try:
+        from oracle import cpu_port
+        cpu_port.load(build=False)
+        form = "c"
+    except OSError:
+        form = "numpy"
     times = []
     t_end = time.perf_counter() + budget_s
     with threadpool_limits(limits=threads):
-        for i in range(13):
+        for i in range(103 if form == "c" else 13):
             for dd in d:
                 dd.pop("w8", None)  # the decode is part of every call of the chain
             t0 = time.perf_counter()
-            xn = ref.rmsnorm(xb, nwb, 1e-6)
-            ref.mono_mlp(xn, "none", None, lutb, *d)
+            if form == "c":
+                cpu_port.mlp(xb, nwb, 1e-6, lutb, *d, threads=threads)
+            else:
+                xn = ref.rmsnorm(xb, nwb, 1e-6)
+                ref.mono_mlp(xn, "none", None, lutb, *d)
             dt = time.perf_counter() - t0
             if i >= 3:
                 times.append(dt)
-            if time.perf_counter() + dt > t_end and len(times) >= 3:
+            if time.perf_counter() + dt > t_end and len(times) >= 10:
                 break
-    return float(np.median(times)), len(times), model, threads
+    return float(np.median(times)), len(times), model, threads, form
 
 
 def cpu_decode_estimate(mlp_s, mlp_algo_bytes, budget_s=20.0):
-    """Config-5 CPU tok/s, composed from timed pieces of the numpy oracle on the host (a whole 32-layer
-    step on the CPU takes tens of seconds): every W4A8 GEMV of a step at the MLP chain's measured rate
-    per weight byte (the same decode + int dot), the bf16 lm_head (verify + 2 drafts) and the MTP
+    """Config-5 CPU tok/s, composed from timed pieces of the oracle on the host (a whole 32-layer step
+    on the CPU takes tens of seconds): every W4A8 GEMV of a step at the MLP chain's measured rate per
+    weight byte (the CPU baseline's chain: the same decode + int dot), the bf16 lm_head (verify + 2 drafts) and the MTP
     block's bf16 GEMMs at the rate of a timed 8-row slice of the float64 bf16 linear, 24 timed GDN
     steps (8 tree rows) and 8 timed attention calls (8 rows over a 1024-token context); norms,
     RoPE, top-k and the accept walk are left out. One accepted token per step, as in the GPU line."""
@@ -229,7 +240,8 @@ def cpu_decode_estimate(mlp_s, mlp_algo_bytes, budget_s=20.0):
             "ms_per_step": round(step_s * 1e3, 1),
             "components_ms": {"w4a8_gemvs": round(w4_s * 1e3, 1), "bf16_gemms": round(bf_s * 1e3, 1),
                               "gdn_steps": round(24 * gdn_s * 1e3, 1), "attention": round(8 * attn_s * 1e3, 1)},
-            "sample": "composed from timed oracle pieces: W4A8 GEMVs at the MLP chain's rate, one 8-row 16384-row "
+            "sample": "composed from timed oracle pieces: W4A8 GEMVs at the MLP chain's rate (per weight byte, the "
+                      "CPU baseline's MLP chain), one 8-row 16384-row "
                       "slice of the bf16 linear, one GDN step and one attention call (medians of up to 3), "
                       "scaled to a 32-layer step; norms, RoPE and top-k left out"}
 
@@ -346,13 +358,15 @@ def bench_mlp(args, dev):
         xb = x.view(torch.int16).cpu().numpy().view("uint16")
         nwb = nw.view(torch.int16).cpu().numpy().view("uint16")
         lutb = lut.view(torch.int16).cpu().numpy().view("uint16")
-        t_cpu, n, model, threads = cpu_baseline_mlp(cpu_ring, M, xb, nwb, lutb)
+        t_cpu, n, model, threads, form = cpu_baseline_mlp(cpu_ring, M, xb, nwb, lutb)
         res["_cpu_mlp_s"] = t_cpu
+        what = (f"the oracle's C restatement (oracle/cpu_mlp.c: per-group decode tables, int32 dots, {threads} "
+                f"threads over the output channels; bit-identical to the numpy oracle)" if form == "c" else
+                f"the numpy oracle chain (decode + float64 int dot; BLAS threads pinned to {threads})")
         res["cpu_baseline"] = {"value": round(per / t_cpu / 1e9, 4), "unit": "GB/s", "cores": threads,
-                               "kind": "port", "ms_per_step": round(t_cpu * 1e3, 1), "cpu_model": model,
-                               "sample": f"median of {n} MLP calls (after 3 warm-up calls) of the numpy oracle chain "
-                                         f"(decode + float64 int dot) on one weight set of the fp16-faithful form, "
-                                         f"same rows; BLAS threads pinned to {threads}"}
+                               "kind": "port", "ms_per_step": round(t_cpu * 1e3, 2), "cpu_model": model,
+                               "sample": f"median of {n} MLP calls (after 3 warm-up calls) of {what} on one weight "
+                                         f"set of the fp16-faithful form, same rows"}
     return res
 
 
