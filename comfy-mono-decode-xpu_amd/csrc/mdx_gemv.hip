@@ -928,7 +928,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         const int total = a.rows * (Kr / 8), per_row = Kr / 8;
 #pragma unroll
         for (int k = 0; k < HRP; ++k) {
-            const int i = k * nthr + t, r = i / per_row, j = i - r * per_row;
+            // (one or two rows: the row index is a comparison, not a division per piece)
+            const int i = k * nthr + t, r = i >= per_row ? 1 : 0, j = i - r * per_row;
             hraw[k] = make_uint4(0u, 0u, 0u, 0u);
             if (i < total) hraw[k] = *reinterpret_cast<const uint4*>(a.hr + r * K + cu0 * CHUNK_K + 8 * j);
         }
@@ -959,7 +960,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
 #pragma unroll
         for (int p = 0; p < GNP; ++p) {
             if (p >= npass) break;  // (uniform)
-            const int hr = min(p * 2 * nwv + 2 * wave + (lane >> 5), nhr - 1), row = hr / H;
+            const int hr = min(p * 2 * nwv + 2 * wave + (lane >> 5), nhr - 1), row = hr >= H ? 1 : 0;  // (one or two rows)
             const int64_t off = int64_t(row) * K + (hr - row * H) * 128 + 4 * (lane & 31);
             gyr[p] = *reinterpret_cast<const uint2*>(a.gn_y + off);
             gzr[p] = *reinterpret_cast<const uint2*>(a.gn_z + off);
@@ -1114,7 +1115,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         for (int k = 0; k < HRP; ++k) {
             const int i = k * nthr + t;
             if (i < total) {
-                const int r = i / per_row, j = i - r * per_row;
+                const int r = i >= per_row ? 1 : 0, j = i - r * per_row;  // (one or two rows)
                 const float rr = r ? rcp[1] : rcp[0];
                 const uint32_t w[4] = {hraw[k].x, hraw[k].y, hraw[k].z, hraw[k].w};
                 uint32_t o[2] = {0u, 0u};
@@ -1175,7 +1176,7 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, const int wg, const
         for (int p = 0; p < GNP; ++p) {
             const int hr = p * 2 * nwv + 2 * wave + (lane >> 5);
             if (p < npass && hr < nhr) {
-                const int row = hr / H, o = (hr - row * H) * 128 + 4 * (lane & 31);
+                const int row = hr >= H ? 1 : 0, o = (hr - row * H) * 128 + 4 * (lane & 31);  // (one or two rows)
                 *reinterpret_cast<uint32_t*>(xl + row * Kr + o) = quant4(v[p], row ? rr[1] : rr[0]);
                 if (wg == 0 && a.gn_out) *reinterpret_cast<uint2*>(a.gn_out + int64_t(row) * K + o) = pack4(v[p]);
             }
