@@ -133,4 +133,60 @@ __device__ __forceinline__ void gdn_conv_channel(int c, int64_t C, int R, int S,
     }
 }
 
+// The same conv, one row per lane: row ts (< S) of channel c, the channel's rows on lanes of ONE wave.
+// Every lane loads the channel's history and shifts it; the row-0 lane writes it back, an instruction
+// after the wave's loads of it have returned (its data is the store's), so no lane reads the new state.
+// Row ts < R: its ancestry (gdn_ancestry, three LDS reads), its taps and out as above; rows R .. S - 1
+// store zeros. Bit-identical to gdn_conv_channel.
+template <typename ProjAt>
+__device__ __forceinline__ void gdn_conv_row(int c, int64_t C, int ts, int R, int S, int pending, int p,
+                                             const int* acc, const int* parent, ProjAt proj_at,
+                                             const uint16_t* conv_w, uint16_t* conv_state, uint16_t* pb,
+                                             uint16_t* qb) {
+    constexpr int CW = GDN_CW;
+    uint16_t old[CW], prevacc[CW];
+#pragma unroll
+    for (int r = 0; r < CW; ++r) {
+        old[r] = conv_state[c * CW + r];
+        const int j = pending + r - CW;
+        int slot = acc[j < 0 ? 0 : j];
+        slot = slot < 0 ? 0 : (slot >= S ? S - 1 : slot);
+        prevacc[r] = pb[((1 - p) * S + slot) * C + c];
+    }
+    float w[CW + 1];
+#pragma unroll
+    for (int d = 0; d <= CW; ++d) w[d] = bf2f(conv_w[c * (CW + 1) + d]);
+    const bool live = ts < R;
+    // the row's taps from LDS before the history arrives (clamped indices: no branches)
+    const uint32_t code = gdn_ancestry(live ? ts : 0, R, parent);
+    const uint16_t prv = live ? proj_at(ts) : uint16_t(0);
+    uint16_t tap[CW];
+#pragma unroll
+    for (int d = 1; d <= CW; ++d) {
+        const int src = (code >> (8 * (d - 1))) & 0xFF;
+        tap[d - 1] = proj_at(src < 16 ? src : 0);
+    }
+    uint16_t hist[CW];
+#pragma unroll
+    for (int r = 0; r < CW; ++r) {
+        const int j = pending + r;
+        hist[r] = j == 0 ? old[0] : (j == 1 ? old[1] : (j == 2 ? old[2] : prevacc[r]));
+    }
+    if (ts == 0) {
+#pragma unroll
+        for (int r = 0; r < CW; ++r) conv_state[c * CW + r] = hist[r];
+    }
+    float sum = fmaf(bf2f(prv), w[CW], 0.f);
+#pragma unroll
+    for (int d = 1; d <= CW; ++d) {
+        const int src = (code >> (8 * (d - 1))) & 0xFF;
+        const uint16_t hv = src == 16 ? hist[0] : (src == 17 ? hist[1] : hist[2]);
+        sum = fmaf(bf2f(src < 16 ? tap[d - 1] : hv), w[CW - d], sum);
+    }
+    const float y = bfround(sum);
+    const uint16_t out = live ? f2bf(__fdiv_rn(y, __fadd_rn(1.f, expf(-y)))) : uint16_t(0);
+    qb[(p * S + ts) * C + c] = out;
+    pb[(p * S + ts) * C + c] = prv;
+}
+
 }  // namespace mdx

@@ -668,9 +668,10 @@ __device__ void epilogue(const GemvArgs& a, const int wg, const int32_t* red, co
 
 // The Gated-DeltaNet projection epilogue: both matrices' outputs stored (bf16, no residual), matrix 0's
 // also staged in LDS (stage [TPW][rows][16], in the activation region, dead after the loop) with the
-// control words (gctl: thread t's word, loaded in the prologue), then one thread per qkv channel runs
-// the channel's conv (gdn_conv_channel). The channel's tile owns it: no other work-group reads or writes
-// the channel's conv state or buffers in this launch.
+// control words (gctl: thread t's word, loaded in the prologue), then one lane per (qkv channel, row)
+// runs the conv (gdn_conv_row: the rows' LDS taps and the history loads overlap, no row waits on the
+// previous one). The channel's tile owns it: no other work-group reads or writes the channel's conv
+// state or buffers in this launch.
 template <bool MFMA>
 __device__ void gdn_epilogue(const GemvArgs& a, const int wg, const int32_t* red, const float* prml, uint8_t* xl,
                              int gctl) {
@@ -697,16 +698,19 @@ __device__ void gdn_epilogue(const GemvArgs& a, const int wg, const int32_t* red
     if (t < 2 + 3 * S) sctl[t] = gctl;
     __syncthreads();
     const int pending = sctl[0], p = sctl[1];
-    if (!gdn_ctl_ok(pending, p, S) || t >= a.TPW * 16) return;  // (the first, uniform)
-    const int ts = t >> 4, c16 = t & 15;
-    int tile;
-    if (which_mat(a, wg * a.TPW + ts, tile) != 0 || tile >= a.m[0].tiles) return;
-    uint32_t anct[GDN_MAXS];
-#pragma unroll
-    for (int r = 0; r < GDN_MAXS; ++r) anct[r] = r < R ? gdn_ancestry(r, R, sctl + 2 + S) : 0u;
-    const uint16_t* st = stage + ts * R * 16 + c16;
-    gdn_conv_channel(tile * 16 + c16, a.m[0].n, R, S, pending, p, sctl + 2, anct, [&](int r) { return st[r * 16]; },
-                     g.conv_w, g.conv_state, g.pb, g.qb);
+    if (!gdn_ctl_ok(pending, p, S)) return;  // (uniform)
+    // one lane per (channel, row): a channel's rows on the 2^lp >= S consecutive lanes of one wave (2^lp
+    // divides the wave), which gdn_conv_row needs for its state write-back
+    const int lp = S <= 1 ? 0 : (S <= 2 ? 1 : (S <= 4 ? 2 : (S <= 8 ? 3 : 4)));
+    for (int e = t; e < (a.TPW * 16) << lp; e += blockDim.x) {
+        const int row = e & ((1 << lp) - 1), ch = e >> lp;
+        const int ts = ch >> 4, c16 = ch & 15;
+        int tile;
+        if (row >= S || which_mat(a, wg * a.TPW + ts, tile) != 0 || tile >= a.m[0].tiles) continue;
+        const uint16_t* st = stage + ts * R * 16 + c16;
+        gdn_conv_row(tile * 16 + c16, a.m[0].n, row, R, S, pending, p, sctl + 2, sctl + 2 + S,
+                     [&](int r) { return st[r * 16]; }, g.conv_w, g.conv_state, g.pb, g.qb);
+    }
 }
 
 // The RMSNorm of a row-prep launch's one row into LDS (xnl, bf16 [K]) by a gate work-group: the row
