@@ -259,6 +259,8 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
             qvec[e - E0][d0 + q] =
                 __fmul_rn(__fmul_rn(__uint_as_float((q & 1) ? (w[q >> 1] & 0xFFFF0000u) : (w[q >> 1] << 16)), a.qscale), qi);
     }
+    // the step's output rows start as zeros: a row that no verify entry writes stays zero
+    for (int i = t; i < R * SC; i += HT) rawc[i / SC][i % SC] = 0.f;
     if (t < E * VPE) {
         const int e = t / VPE, d0 = (t % VPE) * 8;
         const uint32_t w[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
@@ -288,24 +290,26 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
         for (int r = 4; r < HRPG; ++r) m4[r & 3] = fmaf(st[r], r8[r], m4[r & 3]);
         return col_sum(__fadd_rn(__fadd_rn(m4[0], m4[1]), __fadd_rn(m4[2], m4[3])));
     };
-    float kr[HRPG], qr[HRPG], vv = 0.f, decay = 0.f, beta = 0.f, kq = 0.f;
+    // two register sets per operand, alternating by entry (the loops unrolled by two: no copies of the
+    // prefetched operands into the current ones)
+    float kA[HRPG], kB[HRPG], qA[HRPG], qB[HRPG], vv = 0.f, decay = 0.f, beta = 0.f, kq = 0.f;
     int pr = 0;
     if (E0c > 0) {
-        load8(kvec[0], kr);
+        load8(kvec[0], kA);
         vv = vvec[0][col], decay = egate[0][0], beta = egate[0][1];
     }
-#pragma unroll 2
-    for (int e = 0; e < E0c; ++e) {
-        float kn[HRPG];
+    auto replay = [&](int e, const float (&kc)[HRPG], float (&kn)[HRPG]) {
         const int en = min(e + 1, E0c - 1);
         load8(kvec[en], kn);
         const float vn = vvec[en][col], dn = egate[en][0], bn = egate[en][1];
-        const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, dot_col(kr))), beta);
+        const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, dot_col(kc))), beta);
 #pragma unroll
-        for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, __fmul_rn(st[r], decay));
-#pragma unroll
-        for (int r = 0; r < HRPG; ++r) kr[r] = kn[r];
+        for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kc[r], delta, __fmul_rn(st[r], decay));
         vv = vn, decay = dn, beta = bn;
+    };
+    for (int e = 0; e < E0c; e += 2) {
+        replay(e, kA, kB);
+        if (e + 1 < E0c) replay(e + 1, kB, kA);
     }
     if (E0c > 0)
 #pragma unroll
@@ -314,36 +318,34 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     // after the loop (no LDS store on the serial path)
     float held = 0.f;
     if (Ec > E0c) {
-        load8(kvec[E0c], kr);
-        load8(qvec[0], qr);
+        load8(kvec[E0c], kA);
+        load8(qvec[0], qA);
         vv = vvec[E0c][col], decay = egate[E0c][0], beta = egate[E0c][1], kq = ekq[0], pr = prog[0];
     }
-#pragma unroll 2
-    for (int e = E0c; e < Ec; ++e) {
-        float kn[HRPG], qn[HRPG];
+    auto verify = [&](int e, const float (&kc)[HRPG], const float (&qc)[HRPG], float (&kn)[HRPG], float (&qn)[HRPG]) {
         const int en = min(e + 1, Ec - 1);
         load8(kvec[en], kn);
         load8(qvec[en - E0c], qn);
         const float vn = vvec[en][col], dn = egate[en][0], bn = egate[en][1], kqn = ekq[en - E0c];
         const int prn = prog[en - E0c];
-        const float ks = dot_col(kr), qs = dot_col(qr);
+        const float ks = dot_col(kc), qs = dot_col(qc);
         const float delta = __fmul_rn(__fsub_rn(vv, __fmul_rn(decay, ks)), beta);
         const float o = fmaf(delta, kq, __fmul_rn(decay, qs));
         held = e - E0c == rg ? o : held;
         if (pr & 32)  // (uniform) committed
 #pragma unroll
-            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kr[r], delta, __fmul_rn(st[r], decay));
-#pragma unroll
-        for (int r = 0; r < HRPG; ++r) kr[r] = kn[r], qr[r] = qn[r];
+            for (int r = 0; r < HRPG; ++r) st[r] = fmaf(kc[r], delta, __fmul_rn(st[r], decay));
         vv = vn, decay = dn, beta = bn, kq = kqn, pr = prn;
+    };
+    for (int e = E0c; e < Ec; e += 2) {
+        verify(e, kA, qA, kB, qB);
+        if (e + 1 < Ec) verify(e + 1, kB, qB, kA, qA);
     }
     if (rg < Ec - E0c) rawc[prog[rg] & 15][col] = bfround(held);
     __syncthreads();
-    unsigned written = 0;
-    for (int e = E0; e < E; ++e) written |= 1u << slot_of(e);
     for (int i = t; i < R * SC; i += HT) {
         const int ts = i / SC, c = i % SC;
-        a.core[ts * HV * DH + h * DH + cs * SC + c] = ((written >> ts) & 1) ? f2bf(rawc[ts][c]) : uint16_t(0);
+        a.core[ts * HV * DH + h * DH + cs * SC + c] = f2bf(rawc[ts][c]);
     }
 }
 
