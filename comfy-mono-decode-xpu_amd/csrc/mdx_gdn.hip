@@ -138,13 +138,15 @@ __global__ __launch_bounds__(HT) void gdn_head_kernel(GdnArgs a) {
     const int S = a.slots, R = a.R, HV = a.HV, HK = a.HK, KD = HK * DH;
     const int kh = h / (HV / HK);
     const int64_t C = a.C;
-    // the state of this work-group's columns first (it does not depend on the control words)
+    // the control words' load first, then the state of this work-group's columns (not needed before the
+    // entry loops): the control words' wait (loads return in order) is not a wait for the state
+    const int cw = t < 2 + 3 * S ? a.ctl[t] : 0;
     const int col = (t / 64) * 4 + (lane & 3), rg = lane >> 2;
     float st[HRPG];
     float* rs = a.rec + (int64_t(h) * DH + rg * HRPG) * DH + cs * SC + col;
 #pragma unroll
     for (int r = 0; r < HRPG; ++r) st[r] = rs[r * DH];
-    if (t < 2 + 3 * S) ectl[t] = a.ctl[t];
+    if (t < 2 + 3 * S) ectl[t] = cw;
     __syncthreads();
     const int pending = ectl[0], p = ectl[1];
     if (!(p >= 0 && p <= 1 && pending >= 0 && pending <= S)) return;  // (uniform) invalid control words
