@@ -589,10 +589,10 @@ def w4_bytes(w):
 
 def bench_attn_layer(args, dev):
     """One full-attention decoder layer's mixer for 16 tree-verify rows: RMSNorm + int8 quantisation,
-    W4A8 q/k/v (one launch), Q/K RMSNorm + RoPE (theta 1e7, 64 rotary dims) + the KV cache write, GQA
-    tree-verify attention over `--ctx` cached tokens (32 q / 8 kv heads, head_dim 128), quantisation of
-    its output, W4A8 o_proj with the residual. Weights and KV caches cycle through a ring > 2x the
-    Infinity Cache."""
+    W4A8 q/k/v (one launch), Q/K RMSNorm + RoPE (theta 1e7, 64 rotary dims) + the KV cache write and the GQA
+    tree-verify attention over `--ctx` cached tokens (32 q / 8 kv heads, head_dim 128) in one launch as the
+    decode step runs them (two under MDX_ROPE_ATTN=0), quantisation of its output, W4A8 o_proj with the
+    residual. Weights and KV caches cycle through a ring > 2x the Infinity Cache."""
     import torch
     from mdx import _C, _lib, hybrid
     gen = torch.Generator(device=dev).manual_seed(3)
@@ -633,14 +633,20 @@ def bench_attn_layer(args, dev):
     q2 = torch.empty(S, H * D, dtype=torch.int8, device=dev)
     s2 = torch.empty(S, dtype=torch.float32, device=dev)
 
+    fused = _C.rope_attn_fits(H, Hk, S, D, 64)
+
     def call(i):
         w = ring[i]
         q1, s1 = _C.rms_rot_quant(x, nw, 1e-6, _lib.ROT_NONE, None, xn_out=xn)
         _C.stream_gemv(q1, s1, [w["q"], w["k"], w["v"]], qkv)
         vv = qkv[2].view(1, S, Hk, D)
-        _C.qk_norm_rope_kv(qkv[0].view(1, S, H, D), qkv[1].view(1, S, Hk, D), vv, qn, kn, freqs, w["key"], w["value"],
-                           pos, 1e-6, 1e-6, 64, outs=(qh, kh))
-        _C.attn_dpas(qh, w["key"], w["value"], seq, kh, vv.transpose(1, 2), mask, 0, out=y)
+        if fused:  # the decode step's form: the Q/K norm, RoPE and KV write inside the attention launch
+            _C.qk_norm_rope_attn(qkv[0].view(1, S, H, D), qkv[1].view(1, S, Hk, D), vv, qn, kn, freqs, w["key"],
+                                 w["value"], pos, 1e-6, 1e-6, 64, seq, mask, kh, out=y)
+        else:
+            _C.qk_norm_rope_kv(qkv[0].view(1, S, H, D), qkv[1].view(1, S, Hk, D), vv, qn, kn, freqs, w["key"],
+                               w["value"], pos, 1e-6, 1e-6, 64, outs=(qh, kh))
+            _C.attn_dpas(qh, w["key"], w["value"], seq, kh, vv.transpose(1, 2), mask, 0, out=y)
         _lib.call("mdx_rot_quant", _lib.ptr(y), None, _lib.ROT_NONE, _lib.ptr(q2), _lib.ptr(s2), S, H * D,
                   _lib.stream_of(y))
         _C.stream_gemv(q2, s2, [w["o"]], [xo], residuals=[x])
@@ -652,7 +658,8 @@ def bench_attn_layer(args, dev):
                  {"workload": f"full-attention layer mixer, 16 tree rows, 32q/8kv heads, head_dim 128, ctx={L}, "
                               f"{ring_n}-copy weight + KV ring", "ctx": L, "rows": S,
                   "algorithmic_bytes_per_step": per, "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                  "launches_per_step": 7})
+                  "launches_per_step": 6 if fused else 7,
+                  "rope": "in the attention launch" if fused else "its own launch"})
 
 
 def bench_gdn_layer(args, dev):

@@ -26,10 +26,19 @@
 // into LDS per wave, the next step's K and V prefetched into a second register set (head_dim <= 128);
 // work-group ids dealt so that the row tiles of one (kv head, chunk) share an XCD and re-read the
 // chunk from its L2.
+//
+// The tree-verify form with the Q/K prep (attn2_kernel<.., PREP>, head_dim 128): the launch also does the
+// RoPE/KV kernel's work for these rows (mdx_rope.hpp: per-head RMSNorm, split-half RoPE), so the step
+// needs no launch for it. Every work-group computes its kv head's query rows itself (64 rows x 128, into
+// LDS) while its first ring stages stream in; the tree work-group also computes the tree rows' k, writes
+// them (k_out, and the cache at their positions, which lie past the prefix the chunks read) with the v
+// rows, and only then streams them back as its tree stage. Bit-identical to qk_norm_rope_kv + the
+// streaming form.
 #include <math.h>
 #include <stdlib.h>
 
 #include "mdx_common.hpp"
+#include "mdx_rope.hpp"
 
 namespace mdx {
 namespace {
@@ -61,6 +70,24 @@ struct AttnArgs {
     int min_tpw;             // a chunk gives each wave at least this many tokens
     int p2;                  // the streaming form's token parts per chunk (0: the register form)
     float zscale;            // 1/sqrt(D) * log2(e)
+    // the Q/K prep (PREP launches): raw q / k rows [S][H][D] with strides (row, head), the per-head norm
+    // weights (null: no norm), the rows' rotation matrices [S][rd / 2][2][2] (row stride fs floats), the
+    // caches the tree rows' k / v are written to at pos, k_out = xk [Hk][S][D], q_out [H][S][D] or null
+    const uint16_t* rq;
+    int64_t rqs, rqh;
+    const uint16_t* rk;
+    int64_t rks, rkh;
+    const uint16_t* wq;
+    const uint16_t* wk;
+    float epsq, epsk;
+    const float* freqs;
+    int64_t fs;
+    int rd;
+    uint16_t* kc;
+    uint16_t* vc;
+    const int64_t* pos;
+    uint16_t* k_out;
+    uint16_t* q_out;
 };
 
 __device__ __forceinline__ unsigned bf16pair(float a, float b) { return unsigned(f2bf(a)) | (unsigned(f2bf(b)) << 16); }
@@ -371,7 +398,7 @@ __device__ __forceinline__ void split2(int L, int C, int P, int& T, int& active)
     active = L > 0 ? (L + T - 1) / T : 0;
 }
 
-template <int D, int RTW, int NWV>
+template <int D, int RTW, int NWV, bool PREP = false>
 __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
     constexpr int P = NWV / RTW;
     constexpr int KK = D / 32, DT = D / 16;
@@ -430,12 +457,51 @@ __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
     const int t_last = t_end > t_begin ? t_end - 1 : (tree ? 0 : min(t_begin, L - 1));
     const int t_clamp = t_last < 0 ? 0 : t_last;  // a token every load may read (in bounds)
 
+    // The query rows reach the MFMA operands through LDS, read by inline asm: the compiler waits for every
+    // direct-to-LDS load in flight before it uses a vector register that a load wrote, so query rows loaded
+    // into registers would drain the ring at every stage. Rows D + 8 elements apart with the Q/K prep
+    // (written by asm), D apart otherwise (direct loads of whole rows).
     u32x4 qf[KK];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-        qf[kk] = rvalid ? ld16(a.q + hq * a.qh + sq * a.qs + 32 * kk + 8 * g) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < KK; ++kk) qf[kk] = u32x4{0, 0, 0, 0};
+    static_assert(!PREP || (D == 128 && NWV == 8), "the Q/K prep: head_dim 128, eight waves");
+    constexpr int QROW = D + (PREP ? 8 : 0);
+    __shared__ __align__(16) uint16_t qst[64 * QROW];
+    const uint32_t qbase = lds_addr(reinterpret_cast<const unsigned char*>(qst));
+    if constexpr (!PREP) {
+        // part 0's wave of each row tile brings the tile's 16 rows (D / 32 loads of 1 KiB, ahead of the ring:
+        // the first stage's wait covers them, its barrier every tile's)
+        if (part == 0) {
+            constexpr int LPR = D / 8, RPI = 64 / LPR;  // lanes per row, rows per load
+#pragma unroll
+            for (int j = 0; j < D / 32; ++j) {
+                const int rr_ = min(rt * 16 + j * RPI + lane / LPR, a.rows - 1);  // (clamped: in bounds)
+                const uint16_t* src = a.q + (kh * a.groups + rr_ / a.S) * a.qh + (rr_ % a.S) * a.qs + (lane % LPR) * 8;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)(qst + (rt * 16 + j * RPI) * D),
+                                                 16, 0, 0);
+            }
+        }
+    }
+    auto read_q = [&]() {  // lane (row c16 of tile rt, k-group g): 8 elements at 32 kk + 8 g of its row
+        const uint32_t ar = qbase + uint32_t((rvalid ? r : 0) * QROW + 8 * g) * 2;
+        if constexpr (KK == 4)
+            asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\tds_read_b128 %2, %4 offset:128\n\t"
+                         "ds_read_b128 %3, %4 offset:192\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(qf[0]), "=&v"(qf[1]), "=&v"(qf[2]), "=&v"(qf[3])
+                         : "v"(ar));
+        else
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:64\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(qf[0]), "=&v"(qf[1])
+                         : "v"(ar));
+        if (!rvalid)
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) qf[kk] = u32x4{0, 0, 0, 0};
+    };
 
-    unsigned char* ring = smem + part * NS * 2 * STAGE;
+    // (the tree work-group of a PREP launch writes its one stage itself, into part 0's first slot, which all
+    // of its parts read: the other parts have no tokens there)
+    unsigned char* ring = smem + ((PREP && tree) ? 0 : part) * NS * 2 * STAGE;
     // stage s of this part into ring slot s % NS: the wave's PER instructions of K and of V (instruction
     // i of a matrix writes LDS bytes [1024 i, 1024 i + 1024) of the stage's block in the layouts above;
     // lane -> (token within the stage, byte offset within the token row)). Byte offsets fit 32 bits
@@ -471,16 +537,104 @@ __global__ __launch_bounds__(64 * NWV) void attn2_kernel(AttnArgs a) {
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
 
-    for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+    if constexpr (!PREP) {
+        for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+    } else {
+        // The chunk work-groups issue the ring's first round, then the raw query rows (this wave's rows w,
+        // w + NWV, ...; lane l: elements l and l + 64), their rotation matrices and norm weights: the wait
+        // for these also waits for that round (loads return in order), which the first stage needs
+        // anyway. The compiler waits for every direct-to-LDS load before it uses a vector register that a
+        // load issued after them wrote, so no loaded register may be live into the stage loop: the query
+        // rows go through LDS (inline asm, which the compiler does not track).
+        if (!tree)
+            for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+        constexpr int QPW = 64 / NWV;
+        float rx0[QPW], rx1[QPW];
+        float4 rm[QPW];
+        // the rotation pair of element l (a lane past the rotated elements reads pair 0, unused)
+        const int jj = lane >= a.rd ? 0 : (lane < a.rd / 2 ? lane : lane - a.rd / 2);
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) {
+            const int rc = min(w + NWV * i, a.rows - 1);  // (clamped: every load in bounds)
+            const int s_ = rc % a.S;
+            const uint16_t* src = a.rq + s_ * a.rqs + (kh * a.groups + rc / a.S) * a.rqh;
+            rx0[i] = bf2f(src[lane]);
+            rx1[i] = bf2f(src[lane + 64]);
+            rm[i] = *reinterpret_cast<const float4*>(a.freqs + s_ * a.fs + jj * 4);
+        }
+        const uint16_t* wsrc = a.wq ? a.wq : a.rq;  // (no norm: any valid row, the values unused)
+        const float wq0 = bf2f(wsrc[lane]), wq1 = bf2f(wsrc[lane + 64]);
+        // the query rows into LDS (rows D + 8 elements apart: no bank conflicts)
+        uint16_t qo0[QPW], qo1[QPW];
+        qk_rope128_n<QPW>(rx0, rx1, a.wq != nullptr, wq0, wq1, a.epsq, a.rd, rm, lane, qo0, qo1);
+#pragma unroll
+        for (int i = 0; i < QPW; ++i) {
+            const int r_ = w + NWV * i;
+            if (r_ < a.rows) {  // (uniform)
+                const uint32_t ad = qbase + uint32_t(r_ * QROW + lane) * 2;
+                asm volatile("ds_write_b16 %0, %1\n\tds_write_b16 %0, %2 offset:128" ::"v"(ad), "v"(uint32_t(qo0[i])),
+                             "v"(uint32_t(qo1[i])));
+                if (tree && a.q_out) {
+                    uint16_t* qo = a.q_out + ((kh * a.groups + r_ / a.S) * a.S + r_ % a.S) * D;
+                    qo[lane] = qo0[i];
+                    qo[lane + 64] = qo1[i];
+                }
+            }
+        }
+        if (tree) {
+            // the tree rows' k (normed, rotated) and v straight into the stage this work-group reads, in the
+            // layouts the ring's loads produce (K: block 2 (d / 32) + t / 16, row t % 16, 64 bytes; V: block
+            // d / 16, row t, 32 bytes), and to k_out and the caches (stores nothing waits for); the V rows past
+            // the tree rows zeroed (their P is 0, which a non-finite V would turn into NaN)
+            const uint32_t kl = lds_addr(smem), vl = kl + STAGE;
+            if ((threadIdx.x & 63) / 2 >= a.S)
+                asm volatile("ds_write_b128 %0, %1" ::"v"(vl + threadIdx.x * 16), "v"(u32x4{0u, 0u, 0u, 0u}));
+            for (int s_ = w; s_ < a.S; s_ += NWV) {
+                const uint16_t* src = a.rk + s_ * a.rks + kh * a.rkh;
+                const uint16_t* vsrc = a.xv + kh * a.vh + s_ * a.vs;
+                const float x0 = bf2f(src[lane]), x1 = bf2f(src[lane + 64]);
+                const uint16_t v0 = vsrc[lane], v1 = vsrc[lane + 64];
+                const float4 m = *reinterpret_cast<const float4*>(a.freqs + s_ * a.fs + jj * 4);
+                const float w0 = a.wk ? bf2f(a.wk[lane]) : 1.f, w1 = a.wk ? bf2f(a.wk[lane + 64]) : 1.f;
+                uint16_t o0, o1;
+                qk_rope128(x0, x1, a.wk != nullptr, w0, w1, a.epsk, a.rd, m, lane, o0, o1);
+                asm volatile("ds_write_b16 %0, %1\n\tds_write_b16 %0, %2 offset:4096" ::"v"(
+                                 kl + uint32_t((2 * (lane >> 5)) * 1024 + s_ * 64 + (lane & 31) * 2)),
+                             "v"(uint32_t(o0)), "v"(uint32_t(o1)));
+                asm volatile("ds_write_b16 %0, %1\n\tds_write_b16 %0, %2 offset:4096" ::"v"(
+                                 vl + uint32_t((lane >> 4) * 1024 + s_ * 32 + (lane & 15) * 2)),
+                             "v"(uint32_t(v0)), "v"(uint32_t(v1)));
+                uint16_t* ko = a.k_out + (kh * a.S + s_) * D;
+                ko[lane] = o0;
+                ko[lane + 64] = o1;
+                const int64_t p = a.pos[s_];
+                if (p >= 0 && p < a.cap) {  // (a position outside the cache writes nothing)
+                    uint16_t* kd = a.kc + (int64_t(kh) * a.cap + p) * D;
+                    uint16_t* vd = a.vc + (int64_t(kh) * a.cap + p) * D;
+                    kd[lane] = o0;
+                    kd[lane + 64] = o1;
+                    vd[lane] = v0;
+                    vd[lane + 64] = v1;
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS (the ring stays in flight)
+        __builtin_amdgcn_s_barrier();
+        read_q();
+    }
     for (int s = 0; s < nst; ++s) {
-        // stage s landed (this wave's share), then everyone's share and everyone done with stage s - 1
-        if (s + NS - 2 < nst) {
+        // stage s landed (this wave's share), then everyone's share and everyone done with stage s - 1 (the
+        // PREP tree stage was written to LDS before the barrier that precedes the loop: no wait)
+        if (PREP && tree) {
+        } else if (s + NS - 2 < nst) {
             __builtin_amdgcn_s_waitcnt(((((NS - 2) * 2 * PER) & 15)) | ((((NS - 2) * 2 * PER) >> 4) << 14) | (7 << 4) | (15 << 8));
         } else {
             __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the ring's tail
         }
         // s_barrier alone: __syncthreads' release fence would wait for the whole ring (vmcnt(0))
         __builtin_amdgcn_s_barrier();
+        if constexpr (!PREP)
+            if (s == 0) read_q();
         if (s + NS - 1 < nst) issue(s + NS - 1);
         const unsigned char* kd = ring + (s % NS) * 2 * STAGE;
         const unsigned char* vd = kd + STAGE;
@@ -721,10 +875,10 @@ size_t workspace_bytes(int Hk, int RT, int C, int D) {
     return 256 + size_t(Hk) * RT * (C + 1) * (32 + 16 * size_t(D)) * sizeof(float);
 }
 
-template <int D, int RTW, int NWV>
+template <int D, int RTW, int NWV, bool PREP = false>
 int launch2(const AttnArgs& a, hipStream_t st) {
-    allow_smem(reinterpret_cast<const void*>(&attn2_kernel<D, RTW, NWV>), A2_RING);
-    hipLaunchKernelGGL((attn2_kernel<D, RTW, NWV>), dim3(a.Hk * (a.C + 1)), dim3(64 * NWV), A2_RING, st, a);
+    allow_smem(reinterpret_cast<const void*>(&attn2_kernel<D, RTW, NWV, PREP>), A2_RING);
+    hipLaunchKernelGGL((attn2_kernel<D, RTW, NWV, PREP>), dim3(a.Hk * (a.C + 1)), dim3(64 * NWV), A2_RING, st, a);
     MDX_LAUNCHED();
     hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.Hk * a.RT * 16), dim3(D), 0, st, a);
     MDX_LAUNCHED();
@@ -819,4 +973,77 @@ extern "C" int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t
     if (D == 64) return launch<64>(a, st);
     if (D == 128) return launch<128>(a, st);
     return launch<256>(a, st);
+}
+
+// Tree-verify attention with the RoPE/KV kernel's Q/K prep in the same launch: see the note at the top of
+// this file. Raw rows as mdx_qk_norm_rope_kv takes them, the cache written at position[s] as it writes it,
+// k_out [Hk, S, D] (also the tree rows' k the launch attends), q_out [H, S, D] optional.
+extern "C" int mdx_attn_decode_rope(const uint16_t* q, int64_t q_row_stride, int64_t q_head_stride, const uint16_t* k,
+                                    int64_t k_row_stride, int64_t k_head_stride, const uint16_t* v, int64_t v_row_stride,
+                                    int64_t v_head_stride, const uint16_t* weight_q, const uint16_t* weight_k, float eps_q,
+                                    float eps_k, const float* freqs, int64_t freqs_row_stride, int64_t rd, uint16_t* key,
+                                    uint16_t* value, const int64_t* position, const int32_t* seqlen, const int32_t* mask,
+                                    uint16_t* k_out, uint16_t* q_out, uint16_t* out, int64_t H, int64_t Hk, int64_t S,
+                                    int64_t D, int64_t cap, int64_t chunks_hint, void* workspace, size_t workspace_bytes_,
+                                    void* stream) {
+    MDX_CHECK(q && k && v && freqs && key && value && position && seqlen && mask && k_out && out, "null pointer");
+    MDX_CHECK((weight_q == nullptr) == (weight_k == nullptr), "norm weights: both or neither");
+    MDX_CHECK(D == 128 && use_stream(int(D)), "the Q/K prep form: head_dim 128 (streaming form)");
+    MDX_CHECK(rd == 32 || rd == 64 || rd == 128, "rotary dimension 32, 64 or 128");
+    MDX_CHECK(Hk >= 1 && H % Hk == 0 && S >= 1 && S <= 16, "heads / 1..16 rows");
+    const int64_t rows = H / Hk * S;
+    MDX_CHECK(rows > 16 && rows <= 64, "17..64 query rows per kv head (fewer: the separate launches)");
+    MDX_CHECK(cap >= 1 && cap < (int64_t(1) << 30) / D, "cache capacity");
+    MDX_CHECK(aligned(key, 16) && aligned(value, 16) && aligned(k_out, 16) && aligned(v, 16) && aligned(freqs, 16) &&
+                  v_row_stride % 8 == 0 && v_head_stride % 8 == 0 && freqs_row_stride % 4 == 0,
+              "16-byte aligned cache, k_out, v rows and rotation rows");
+    const int RT = int((rows + 15) / 16);
+    const int C = plan_chunks2(int(Hk), RT, int(D), int(cap), int(chunks_hint));
+    MDX_CHECK(workspace && aligned(workspace, 256) && workspace_bytes_ >= workspace_bytes(int(Hk), RT, C, int(D)),
+              "workspace: %zu bytes, 256-byte aligned, zeroed once", workspace_bytes(int(Hk), RT, C, int(D)));
+    AttnArgs a{};
+    a.key = key;
+    a.value = value;
+    a.seqlen = seqlen;
+    a.xk = k_out;
+    a.xh = S * D;
+    a.xs = D;
+    a.xv = v;
+    a.vh = v_head_stride;
+    a.vs = v_row_stride;
+    a.mask = mask;
+    a.out = out;
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+    a.H = int(H);
+    a.Hk = int(Hk);
+    a.S = int(S);
+    a.cap = int(cap);
+    a.groups = int(H / Hk);
+    a.rows = int(rows);
+    a.RT = RT;
+    a.C = C;
+    a.min_tpw = chunks_hint > 0 ? AT_STEP : min_tpw_default();
+    a.p2 = stream_parts(int(D), RT);
+    a.zscale = float(1.0 / sqrt(double(D)) * 1.4426950408889634);
+    a.rq = q;
+    a.rqs = q_row_stride;
+    a.rqh = q_head_stride;
+    a.rk = k;
+    a.rks = k_row_stride;
+    a.rkh = k_head_stride;
+    a.wq = weight_q;
+    a.wk = weight_k;
+    a.epsq = eps_q;
+    a.epsk = eps_k;
+    a.freqs = freqs;
+    a.fs = freqs_row_stride;
+    a.rd = int(rd);
+    a.kc = key;
+    a.vc = value;
+    a.pos = position;
+    a.k_out = k_out;
+    a.q_out = q_out;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (stream_rtw(RT) == 2) return launch2<128, 2, 8, true>(a, st);
+    return launch2<128, 4, 8, true>(a, st);
 }

@@ -15,6 +15,7 @@
 #include <algorithm>
 
 #include "mdx_common.hpp"
+#include "mdx_rope.hpp"
 
 namespace mdx {
 namespace {
@@ -39,10 +40,6 @@ struct RopeArgs {
     uint16_t* ok;           // [Hk, S, D]
     int S, Hq, Hk, D, rd, cap;
 };
-
-__device__ __forceinline__ float rope_pair(float a, float fa, float b, float fb) {
-    return __fadd_rn(__fmul_rn(a, fa), __fmul_rn(b, fb));
-}
 
 // one wave per (row s, head); heads: q (Hq), then k (Hk), then v (Hk)
 __global__ __launch_bounds__(WAVE) void rope_kv_kernel(RopeArgs a) {

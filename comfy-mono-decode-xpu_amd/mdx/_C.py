@@ -533,6 +533,62 @@ def attn_dpas(q, key, value, seqlen, xk, xv, mask, chunks_hint=0, out=None):
     return out
 
 
+def rope_attn_fits(H, Hk, S, D, rd):
+    """Whether qk_norm_rope_attn takes these tree-verify rows (head_dim 128, rd 32 / 64 / 128, 17..64 query
+    rows per kv head, the streaming attention form). MDX_ROPE_ATTN=0 turns the fused form off (A/B)."""
+    return (_ATTN_MODE[0] != "exact" and D == 128 and rd in (32, 64, 128) and H % Hk == 0
+            and 16 < (H // Hk) * S <= 64 and os.environ.get("MDX_ATTN_V1", "0") != "1"
+            and os.environ.get("MDX_ROPE_ATTN", "1") != "0")
+
+
+def qk_norm_rope_attn(rawq, rawk, vn, weightq, weightk, freqs, key, value, position, epsq, epsk, rd, seqlen, mask,
+                      k_out, out=None, q_out=None, chunks_hint=0):
+    """qk_norm_rope_kv followed by attn_dpas over the tree rows (mask int32 [S]), in one launch plus the merge
+    (this library's own fusion; the reference runs csrc/rope_kv.sycl:120-245 and csrc/attn_dpas.sycl:269-342
+    as two calls). Bit-identical to the pair: the rows' k land in k_out [1, Hk, S, D] and the cache at
+    `position` (past the attended prefix), their q in q_out [1, H, S, D] when given. Returns bf16 [1, S, H * D].
+    rope_attn_fits says which shapes it takes."""
+    qn, kn, vn = (t[0] if t.dim() == 4 else t for t in (rawq, rawk, vn))
+    for t, n in ((qn, "q"), (kn, "k"), (vn, "v")):
+        _bf16_heads(t, n)
+        _check(t.dim() == 3, f"{n}: [S, H, D] or [1, S, H, D]")
+    S, H, D = qn.shape
+    Hk = kn.shape[1]
+    _check(kn.shape == (S, Hk, D) and vn.shape == (S, Hk, D), "k/v shapes")
+    _check(rope_attn_fits(H, Hk, S, D, rd), "shape outside the fused form (use qk_norm_rope_kv + attn_dpas)")
+    _check(key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16 and key.is_contiguous()
+           and value.is_contiguous() and key.dim() == 4 and key.shape[0] == 1 and key.shape[1] == Hk
+           and key.shape[3] == D and value.shape == key.shape, "bf16 [1, Hk, cap, D] cache")
+    _check(freqs.dtype == torch.float32 and freqs.shape[-1] == 2 and freqs.shape[-2] == 2
+           and freqs.shape[-3] == rd // 2 and freqs.stride(-1) == 1 and freqs.stride(-2) == 2
+           and freqs.stride(-3) == 4 and freqs.numel() // (rd // 2 * 4) == S, "freqs [.., S, rd/2, 2, 2] f32")
+    fs = freqs.stride(-4) if freqs.dim() >= 4 else rd // 2 * 4
+    _check(position.dtype == torch.int64 and position.is_contiguous() and position.numel() >= S,
+           "int64 positions [>= S]")
+    _check((weightq is None) == (weightk is None), "norm weights: both or neither")
+    if weightq is not None:
+        _check(epsq > 0 and epsk > 0, "positive eps")
+        for w, n in ((weightq, "weight_q"), (weightk, "weight_k")):
+            _check(w.dtype == torch.bfloat16 and w.is_contiguous() and w.numel() == D, f"{n}: bf16 [D]")
+    _check(seqlen.dtype == torch.int32 and seqlen.numel() >= 1, "int32 seqlen")
+    _check(mask.dtype == torch.int32 and mask.is_contiguous() and mask.numel() == S, "int32 mask [S]")
+    _check(k_out.dtype == torch.bfloat16 and k_out.is_contiguous() and k_out.numel() == Hk * S * D, "k_out bf16 [1, Hk, S, D]")
+    if q_out is not None:
+        _check(q_out.dtype == torch.bfloat16 and q_out.is_contiguous() and q_out.numel() == H * S * D,
+               "q_out bf16 [1, H, S, D]")
+    if out is None:
+        out = torch.empty(1, S, H * D, dtype=torch.bfloat16, device=qn.device)
+    _check(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == S * H * D, "out bf16 [1, S, H * D]")
+    cap = key.shape[2]
+    ws = _attn_ws(qn.device, _lib.lib().mdx_attn_workspace(H, Hk, S, D, cap, int(chunks_hint)))
+    _lib.call("mdx_attn_decode_rope", _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0), kn.stride(1),
+              _lib.ptr(vn), vn.stride(0), vn.stride(1), _lib.ptr(weightq), _lib.ptr(weightk), float(epsq), float(epsk),
+              _lib.ptr(freqs), fs, int(rd), _lib.ptr(key), _lib.ptr(value), _lib.ptr(position), _lib.ptr(seqlen),
+              _lib.ptr(mask), _lib.ptr(k_out), _lib.ptr(q_out), _lib.ptr(out), H, Hk, S, D, cap, int(chunks_hint),
+              _lib.ptr(ws), ws.numel(), _lib.stream_of(qn))
+    return out
+
+
 def bf16_linear(x, w, tiled=True, residual=None, out=None):
     """bf16 decode linear (lm_head / draft block GEMMs; the reference's F.linear at
     comfy_mono_decode_xpu/mtp_loop.py:221-225): bf16(x . W^T) with fp32 accumulation, 1..16 rows.

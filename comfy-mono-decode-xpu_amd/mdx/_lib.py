@@ -75,6 +75,11 @@ SIGNATURES = {
     "mdx_attn_decode": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
                                        c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                        c_int64, c_int64, c_int64, c_int64, c_void_p, c_size_t, c_void_p]),
+    "mdx_attn_decode_rope": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                            c_int64, c_void_p, c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
+                                            c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                            c_int64, c_void_p, c_size_t, c_void_p]),
     "mdx_bf16_linear": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                                        c_void_p]),
     "mdx_attn_exact": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,

@@ -317,8 +317,11 @@ class HybridModel:
         else:
             _C.attn_dpas(q, key, value, seq, xk, xv, mask, 0, out=out)
 
+    def _tracing(self):
+        return self.trace is not None and not torch.cuda.is_current_stream_capturing()
+
     def _tr(self, name, t):
-        if self.trace is not None and not torch.cuda.is_current_stream_capturing():
+        if self._tracing():
             self.trace.append((name, t.detach().clone()))
 
     def _reserve(self, steps):
@@ -348,9 +351,14 @@ class HybridModel:
         vv = qkv[2].view(1, R, c.kv_heads, c.head_dim)
         qo = torch.empty(1, c.heads, R, c.head_dim, dtype=torch.bfloat16, device=self.dev)
         ko = torch.empty(1, c.kv_heads, R, c.head_dim, dtype=torch.bfloat16, device=self.dev)
-        _C.qk_norm_rope_kv(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, outs=(qo, ko))
         y = torch.empty(1, R, qd, dtype=torch.bfloat16, device=self.dev)
-        self._attend(qo, key, value, seq, ko, vv.transpose(1, 2), mask, y)
+        if c.attn != "exact" and _C.rope_attn_fits(c.heads, c.kv_heads, R, c.head_dim, c.rotary):
+            # the Q/K norm, RoPE and KV write inside the attention launch (the same bits as the two calls)
+            _C.qk_norm_rope_attn(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, seq,
+                                 mask, ko, out=y, q_out=qo if self._tracing() else None)
+        else:
+            _C.qk_norm_rope_kv(qv, kv_, vv, L["qn"], L["kn"], freqs, key, value, pos, c.eps, c.eps, c.rotary, outs=(qo, ko))
+            self._attend(qo, key, value, seq, ko, vv.transpose(1, 2), mask, y)
         self._tr(f"L{i}.qo", qo)
         self._tr(f"L{i}.ko", ko)
         self._tr(f"L{i}.y", y)

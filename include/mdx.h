@@ -274,6 +274,24 @@ int mdx_attn_decode(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stri
                     int64_t Hk, int64_t S, int64_t D, int64_t cap, int64_t chunks_hint, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Tree-verify attention with the Q/K RMSNorm + RoPE + KV write of mdx_qk_norm_rope_kv in the same launch
+ * (no counterpart in the reference: it runs csrc/rope_kv.sycl:120-245 and csrc/attn_dpas.sycl:269-342 as
+ * two calls, as mdx_qk_norm_rope_kv + mdx_attn_decode do). For callers that run both back to back on the
+ * tree rows: one launch fewer per attention layer, every output bit-identical to that pair's.
+ *   q, k, v, weight_q/_k, eps_q/_k, freqs, rd, key, value, position: as mdx_qk_norm_rope_kv (the tree
+ *   rows' k / v are written to the cache at position[s]; those positions must lie at or past seqlen[0],
+ *   outside the prefix the launch attends); k_out bf16 [Hk, S, D] receives the rows' k (the tree keys the
+ *   launch attends), q_out bf16 [H, S, D] the rows' q (may be NULL); seqlen, mask, out, chunks_hint,
+ *   workspace (mdx_attn_workspace bytes): as mdx_attn_decode.
+ * D == 128, rd in {32, 64, 128}, mask != NULL, 16 < (H / Hk) * S <= 64 (fewer rows: the two calls). */
+int mdx_attn_decode_rope(const uint16_t* q, int64_t q_row_stride, int64_t q_head_stride, const uint16_t* k,
+                         int64_t k_row_stride, int64_t k_head_stride, const uint16_t* v, int64_t v_row_stride,
+                         int64_t v_head_stride, const uint16_t* weight_q, const uint16_t* weight_k, float eps_q,
+                         float eps_k, const float* freqs, int64_t freqs_row_stride, int64_t rd, uint16_t* key,
+                         uint16_t* value, const int64_t* position, const int32_t* seqlen, const int32_t* mask,
+                         uint16_t* k_out, uint16_t* q_out, uint16_t* out, int64_t H, int64_t Hk, int64_t S, int64_t D,
+                         int64_t cap, int64_t chunks_hint, void* workspace, size_t workspace_bytes, void* stream);
+
 /* bf16 decode linear for 1..16 rows: out = bf16(x . W^T) with fp32 accumulation (MFMA), optional
  * bf16 residual (out = bf16(float(residual) + float(bf16(acc)))).
  * Replaces: the lm_head F.linear of the device loop (comfy_mono_decode_xpu/mtp_loop.py:221-225) and the
