@@ -117,6 +117,17 @@ def ring_time(call, ring_n, steps, warmup):
     return e0.elapsed_time(e1) / 1e3 / steps
 
 
+def fresh_pool():
+    """Hand the caching allocator's unused segments back to the runtime, so the next leg's model is
+    allocated as a fresh serving process would allocate it, not carved out of the segments the previous
+    legs' weight rings left behind."""
+    import gc
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
 def cpu_info():
     """(model name, threads used by the CPU baseline): numpy's BLAS pool is pinned to the process's
     affinity count for the timed leg."""
@@ -503,6 +514,7 @@ def bench_stack(args, dev, tokens=0, two_stage=False, head="bf16"):
     the verify and the drafts instead of the bf16 one."""
     import torch
     from mdx import hybrid
+    fresh_pool()
     steps, warm = args.steps, max(args.warmup, 2)
     per = 3  # at most len(widths) + 1 tokens committed per step
     budget = tokens + 64 if tokens else steps
@@ -552,6 +564,7 @@ def bench_stack_auto(args, dev, tokens=512):
     bookkeeping, its host reads and any new tree's capture included)."""
     import torch
     from mdx import hybrid
+    fresh_pool()
     cap = args.prompt + 8 * (tokens + 64) + 64
     cfg = hybrid.HybridConfig(cap=cap, auto=True, two_stage=args.two_stage, head=args.head,
                               predictable=getattr(args, "predictable", False), scales=args.scales,
@@ -896,6 +909,7 @@ def main():
             lsub.steps, lsub.warmup = 200, 10
             for k, v in kw.items():
                 setattr(lsub, k, v)
+            fresh_pool()
             r = fn(lsub, dev)
             layers[key] = {"value": r["value"], "unit": r["unit"], "us_per_step": round(r["ms_per_step"] * 1e3, 2),
                            "frac_of_peak": round(r["value"] / PEAK_HBM_GBS, 4), "workload": r["config"]["workload"]}
