@@ -1,7 +1,7 @@
 """CPU oracle: a numpy restatement of the reference operator chain of the W4A8 decode path.
 
 TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this module, and only as the checker / the timed CPU baseline -- never as a product path.
+import this module, and only as what results are compared against / the timed CPU baseline -- never as a product path.
 
 Every function cites the reference file:line it restates (comfy-mono-decode-xpu). Floating-point
 steps are single IEEE operations on numpy float32 / float64 scalars or arrays (round to nearest
